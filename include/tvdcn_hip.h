@@ -1,0 +1,136 @@
+/*
+ * tvdcn_hip.h -- C ABI of the MI355X (gfx950) deformable-convolution library
+ * (libtvdcn_hip.so). Plain pointers and sizes only: no torch, no C++ types.
+ *
+ * Every entry point is stateless, re-entrant and stream-ordered: work is
+ * enqueued on `stream` (a hipStream_t passed as void*; NULL = legacy default
+ * stream), nothing is synchronised, no device memory is allocated or freed,
+ * and no pointer is kept after return. Device buffers are dense, contiguous
+ * in the reference's layouts (NC<spatial>, row-major), 16-byte aligned, and of
+ * the element type named by `dtype`. Scratch memory is supplied by the caller
+ * as `workspace` of at least the size returned by the matching *_workspace_size
+ * query. Errors return a non-zero tvdcn_status; tvdcn_last_error() then holds a
+ * thread-local message.
+ *
+ * Reference interface being replaced (tvdcn 1.1.0, paths relative to
+ * tvdcn/csrc/): the twelve `tvdcn::` operator schemas
+ *   deform_conv{1,2,3}d               ops/deform_conv1d.cpp:82-91, ops/deform_conv2d.cpp:117-126,
+ *                                     ops/deform_conv3d.cpp (same block)
+ *   _deform_conv{1,2,3}d_backward     same TORCH_LIBRARY_FRAGMENT blocks
+ *   deform_conv_transpose{1,2,3}d     ops/deform_conv_transpose2d.cpp:125-136 and the 1D/3D twins
+ *   _deform_conv_transpose{1,2,3}d_backward   same blocks
+ * whose CUDA-key kernels are ops/cuda/deform_conv*_kernel.cpp (forward / backward
+ * drivers), and the Python-level mask_softmax{1,2,3}d (ops/activations/mask_softmax.py).
+ */
+#ifndef TVDCN_HIP_H
+#define TVDCN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    TVDCN_DTYPE_FLOAT32 = 0,
+    TVDCN_DTYPE_FLOAT64 = 1,
+    TVDCN_DTYPE_FLOAT16 = 2,
+    TVDCN_DTYPE_BFLOAT16 = 3
+} tvdcn_dtype;
+
+typedef enum {
+    TVDCN_STATUS_SUCCESS = 0,
+    TVDCN_STATUS_INVALID_ARGUMENT = 1,   /* shape / parameter check failed (RuntimeError in the reference) */
+    TVDCN_STATUS_WORKSPACE_TOO_SMALL = 2,
+    TVDCN_STATUS_NOT_SUPPORTED = 3,      /* e.g. a tensor above 2^31 - 1 elements */
+    TVDCN_STATUS_HIP_ERROR = 4           /* a kernel launch failed */
+} tvdcn_status;
+
+/*
+ * Problem descriptor shared by the conv and transposed-conv entry points.
+ * Spatial arrays hold `dim` entries in the reference's axis order ((d,) h, w).
+ *   conv       (transposed = 0): input (batch, in_channels, *in_size),
+ *              weight (out_channels, in_channels / groups, *kernel),
+ *              offset (batch, offset_groups * dim * prod(kernel), *out_size),
+ *              mask   (batch, mask_groups * prod(kernel), *out_size),
+ *              bias   (out_channels), output (batch, out_channels, *out_size)
+ *   transposed (transposed = 1): input (batch, in_channels, *in_size),
+ *              weight (in_channels, out_channels / groups, *kernel),
+ *              offset / mask on the *input* grid (*in_size),
+ *              output (batch, out_channels, *out_size)
+ * offset_groups = 0 means offset is None; mask_groups = 0 means mask is None.
+ * output_padding is used only when transposed = 1.
+ */
+typedef struct {
+    int32_t dim;
+    int32_t transposed;
+    int32_t dtype;            /* tvdcn_dtype */
+    int32_t reserved;
+    int64_t batch;
+    int64_t in_channels;
+    int64_t out_channels;
+    int64_t groups;
+    int64_t offset_groups;
+    int64_t mask_groups;
+    int64_t in_size[3];
+    int64_t kernel[3];
+    int64_t stride[3];
+    int64_t padding[3];
+    int64_t dilation[3];
+    int64_t output_padding[3];
+} tvdcn_conv_desc;
+
+/* Output spatial size (out_size[0..dim)); returns TVDCN_STATUS_SUCCESS or an error
+ * when the descriptor fails the reference's shape checks. */
+tvdcn_status tvdcn_conv_output_size(const tvdcn_conv_desc *desc, int64_t out_size[3]);
+
+/* Bytes of workspace needed by tvdcn_deform_conv_forward / _backward. */
+size_t tvdcn_deform_conv_forward_workspace_size(const tvdcn_conv_desc *desc);
+size_t tvdcn_deform_conv_backward_workspace_size(const tvdcn_conv_desc *desc);
+
+/*
+ * Forward of deform_conv{1,2,3}d / deform_conv_transpose{1,2,3}d.
+ * Replaces the CUDA-key forward drivers ops/cuda/deform_conv2d_kernel.cpp:85-385,
+ * ops/cuda/deform_conv_transpose2d_kernel.cpp:85-372 and their 1D/3D twins,
+ * called through the schemas listed above. offset, mask, bias may be NULL.
+ */
+tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *input, const void *weight,
+                                       const void *offset, const void *mask, const void *bias, void *output,
+                                       void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Backward (the `_..._backward` schemas). Replaces ops/cuda/deform_conv2d_kernel.cpp:387-642,
+ * ops/cuda/deform_conv_transpose2d_kernel.cpp:374-636 and their 1D/3D twins.
+ * grad_offset must be NULL iff offset is NULL, grad_mask iff mask is NULL;
+ * grad_bias may be NULL (not computed). All outputs are overwritten.
+ */
+tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void *grad_out, const void *input,
+                                        const void *weight, const void *offset, const void *mask, void *grad_input,
+                                        void *grad_weight, void *grad_offset, void *grad_mask, void *grad_bias,
+                                        void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * mask_softmax{1,2,3}d (ops/activations/mask_softmax.py:19-126): x viewed as
+ * (batch * groups, kernel_numel, spatial_numel), softmax over the middle axis.
+ * Backward: grad_x = y * (grad_y - sum_k grad_y * y).
+ */
+tvdcn_status tvdcn_mask_softmax_forward(int32_t dtype, int64_t batch, int64_t groups, int64_t kernel_numel,
+                                        int64_t spatial_numel, const void *x, void *y, void *stream);
+tvdcn_status tvdcn_mask_softmax_backward(int32_t dtype, int64_t batch, int64_t groups, int64_t kernel_numel,
+                                         int64_t spatial_numel, const void *y, const void *grad_y, void *grad_x,
+                                         void *stream);
+
+/* Thread-local text of the last error (empty string when none). */
+const char *tvdcn_last_error(void);
+
+/* Library identity (replaces tvdcn/csrc/tvdcn.cpp:24-48 `_cuda_version` /
+ * `_cuda_arch_flags`): HIP runtime version the library was built against
+ * (HIP_VERSION, e.g. 70226015) and the offload targets ("gfx950"). */
+int64_t tvdcn_hip_version(void);
+const char *tvdcn_arch_flags(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TVDCN_HIP_H */

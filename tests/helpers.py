@@ -1,0 +1,54 @@
+"""Shared test helpers: case construction and norm-wise error metrics."""
+import torch
+
+
+def rel_err(a, ref):
+    """max(relative L2 error, max-abs error / max|ref|), computed in float64."""
+    a = a.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    if ref.numel() == 0:
+        return 0.0
+    scale = ref.abs().max().item()
+    if scale == 0:
+        return a.abs().max().item()
+    l2 = ((a - ref).norm() / ref.norm().clamp_min(1e-300)).item()
+    mx = ((a - ref).abs().max() / scale).item()
+    return max(l2, mx)
+
+
+def out_size(dim, transposed, in_size, k, s, p, d, op):
+    if transposed:
+        return [(in_size[i] - 1) * s[i] - 2 * p[i] + d[i] * (k[i] - 1) + 1 + op[i] for i in range(dim)]
+    return [(in_size[i] + 2 * p[i] - (d[i] * (k[i] - 1) + 1)) // s[i] + 1 for i in range(dim)]
+
+
+def make_case(dim, transposed=False, batch=2, cin=4, cout=6, groups=1, og=1, mg=1, deformable=True,
+              modulated=True, bias=True, kernel=None, stride=None, padding=None, dilation=None, out_pad=None,
+              in_size=None, dtype=torch.float64, seed=0, offset_scale=2.0):
+    """Random problem like the reference's DeformConvTestArgs (tests/utils/deform_conv_test_args.py:19-80):
+    returns dict of CPU tensors + params."""
+    g = torch.Generator().manual_seed(seed)
+    kernel = kernel or [2, 3, 2][:dim]
+    stride = stride or [1, 2, 1][:dim]
+    padding = padding or [0, 1, 1][:dim]
+    dilation = dilation or [1, 2, 1][:dim]
+    out_pad = out_pad or [0, 1, 0][:dim] if transposed else [0] * dim
+    in_size = in_size or [5, 6, 7][:dim]
+    o = out_size(dim, transposed, in_size, kernel, stride, padding, dilation, out_pad)
+    grid = in_size if transposed else o
+    kn = 1
+    for k in kernel:
+        kn *= k
+    x = torch.rand(batch, cin, *in_size, generator=g, dtype=torch.float64)
+    if transposed:
+        w = torch.rand(cin, cout // groups, *kernel, generator=g, dtype=torch.float64)
+    else:
+        w = torch.rand(cout, cin // groups, *kernel, generator=g, dtype=torch.float64)
+    off = (torch.rand(batch, og * dim * kn, *grid, generator=g, dtype=torch.float64) - 0.5) * 2 * offset_scale \
+        if deformable else None
+    msk = torch.rand(batch, mg * kn, *grid, generator=g, dtype=torch.float64) if modulated else None
+    b = torch.rand(cout, generator=g, dtype=torch.float64) if bias else None
+    cast = (lambda t: None if t is None else t.to(dtype))
+    return dict(dim=dim, transposed=transposed, input=cast(x), weight=cast(w), offset=cast(off), mask=cast(msk),
+                bias=cast(b), stride=stride, padding=padding, dilation=dilation, output_padding=out_pad,
+                groups=groups, out_shape=[batch, cout] + o)

@@ -1,0 +1,150 @@
+"""GPU parity: tvdcn_amd's HIP kernels against the float64 oracle (a C restatement of
+tvdcn's CPU algorithm, itself pinned to the reference build and the golden fixtures).
+
+Tolerances (norm-wise, see helpers.rel_err): float64 1e-9; float32 forward 1e-5 and
+backward 1e-4 (atomic ordering); float16 / bfloat16 1e-2 against the oracle run on
+the same rounded inputs.
+"""
+import itertools
+
+import pytest
+import torch
+
+import tvdcn_amd
+from oracle import oracle
+from helpers import make_case, rel_err
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {torch.float64: (1e-9, 1e-9), torch.float32: (1e-5, 1e-4), torch.float16: (1e-2, 1e-2),
+       torch.bfloat16: (1e-2, 1e-2)}
+
+
+def run_gpu(case, dtype, grad_out=None):
+    """forward + autograd backward on the GPU; returns (out, [grads...], grad_out used)."""
+    names = ("input", "weight", "offset", "mask", "bias")
+    ts = [case[n].to(DEV, dtype).requires_grad_(True) if case[n] is not None else None for n in names]
+    if case["transposed"]:
+        fn = getattr(tvdcn_amd, f"deform_conv_transpose{case['dim']}d")
+        out = fn(*ts, stride=case["stride"], padding=case["padding"], output_padding=case["output_padding"],
+                 dilation=case["dilation"], groups=case["groups"])
+    else:
+        fn = getattr(tvdcn_amd, f"deform_conv{case['dim']}d")
+        out = fn(*ts, stride=case["stride"], padding=case["padding"], dilation=case["dilation"],
+                 groups=case["groups"])
+    if grad_out is None:
+        g = torch.Generator().manual_seed(7)
+        grad_out = torch.rand(out.shape, generator=g, dtype=torch.float64)
+    out.backward(grad_out.to(DEV, dtype))
+    torch.cuda.synchronize()
+    return out, [t.grad if t is not None else None for t in ts], grad_out
+
+
+def run_oracle(case, grad_out, dtype):
+    cast = (lambda t: None if t is None else t.to(dtype).double())
+    args = [cast(case[n]) for n in ("input", "weight", "offset", "mask", "bias")]
+    kw = dict(stride=case["stride"], padding=case["padding"], dilation=case["dilation"], groups=case["groups"],
+              transposed=case["transposed"], output_padding=case["output_padding"])
+    out = oracle.forward(case["dim"], *args, **kw)
+    grads = oracle.backward(case["dim"], grad_out.to(dtype).double(), *args, **kw)
+    return out, grads
+
+
+def check(case, dtype):
+    out, grads, gout = run_gpu(case, dtype)
+    ref_out, ref_grads = run_oracle(case, gout, dtype)
+    tf, tb = TOL[dtype]
+    assert list(out.shape) == case["out_shape"]
+    e = rel_err(out, ref_out)
+    assert e < tf, f"forward rel err {e}"
+    for name, g, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
+        if r is None:
+            assert g is None
+            continue
+        e = rel_err(g, r)
+        assert e < tb, f"grad_{name} rel err {e}"
+
+
+# flag / group combinations at the reference's test sizes (generic, scalar-channel path)
+COMBOS = list(itertools.product([1, 2, 3], [False, True], [(True, True), (True, False), (False, True),
+                                                              (False, False)]))
+
+
+@pytest.mark.parametrize("dim,transposed,flags", COMBOS)
+def test_small_fp64(dim, transposed, flags):
+    deformable, modulated = flags
+    case = make_case(dim, transposed, cin=4, cout=6, groups=2, og=2, mg=1, deformable=deformable,
+                     modulated=modulated, seed=dim * 10 + int(transposed))
+    check(case, torch.float64)
+
+
+@pytest.mark.parametrize("dim,transposed", list(itertools.product([1, 2, 3], [False, True])))
+def test_small_fp32(dim, transposed):
+    case = make_case(dim, transposed, cin=4, cout=6, groups=2, og=2, mg=2, seed=100 + dim)
+    check(case, torch.float32)
+
+
+@pytest.mark.parametrize("dim,transposed,og,mg,groups", [
+    (2, False, 1, 1, 1), (2, False, 2, 4, 1), (2, False, 4, 2, 2), (1, False, 4, 4, 1), (3, False, 1, 1, 1),
+    (2, True, 2, 2, 1), (2, True, 1, 1, 2), (1, True, 2, 1, 1), (3, True, 1, 1, 1)])
+def test_vector_path_fp32(dim, transposed, og, mg, groups):
+    """channel counts that are multiples of 16/64: exercises the 4-channel vector gather and the
+    wave-reduced offset/mask gradients"""
+    in_size = {1: [40], 2: [12, 11], 3: [5, 6, 7]}[dim]
+    case = make_case(dim, transposed, batch=2, cin=64, cout=128 if not transposed else 64, groups=groups, og=og,
+                     mg=mg, kernel=[3] * dim, stride=[1] * dim, padding=[1] * dim, dilation=[1] * dim,
+                     in_size=in_size, out_pad=[0] * dim, seed=200 + dim)
+    check(case, torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_half_precision(dtype, transposed):
+    case = make_case(2, transposed, batch=2, cin=32, cout=32, og=2, mg=2, kernel=[3, 3], stride=[1, 1],
+                     padding=[1, 1], dilation=[1, 1], in_size=[9, 10], out_pad=[0, 0], seed=300)
+    check(case, dtype)
+
+
+def test_unbatched_and_no_bias():
+    case = make_case(2, False, batch=1, cin=4, cout=4, bias=False, seed=400)
+    x = case["input"][0].to(DEV).requires_grad_(True)
+    w = case["weight"].to(DEV)
+    o = case["offset"][0].to(DEV)
+    m = case["mask"][0].to(DEV)
+    out = tvdcn_amd.deform_conv2d(x, w, o, m, None, case["stride"], case["padding"], case["dilation"])
+    ref = oracle.forward(2, case["input"], case["weight"], case["offset"], case["mask"], None,
+                         case["stride"], case["padding"], case["dilation"])
+    assert out.shape == ref.shape[1:]
+    assert rel_err(out, ref[0]) < 1e-9
+
+
+def test_zero_offset_unit_mask_is_conv2d():
+    """closed form: zero offsets and unit mask reduce to F.conv2d (torch's own GPU convolution)"""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 16, 13, 13, generator=g, dtype=torch.float64).to(DEV)
+    w = torch.randn(32, 8, 3, 3, generator=g, dtype=torch.float64).to(DEV)
+    b = torch.randn(32, generator=g, dtype=torch.float64).to(DEV)
+    off = torch.zeros(2, 2 * 9, 7, 7, dtype=torch.float64, device=DEV)
+    msk = torch.ones(2, 9, 7, 7, dtype=torch.float64, device=DEV)
+    out = tvdcn_amd.deform_conv2d(x, w, off, msk, b, stride=2, padding=1, dilation=1, groups=2)
+    ref = torch.nn.functional.conv2d(x, w, b, stride=2, padding=1, groups=2)
+    assert rel_err(out, ref) < 1e-10
+
+
+def test_mask_softmax_matches_torch_softmax():
+    g = torch.Generator().manual_seed(9)
+    for dim, ks, shape in [(1, (5,), (3, 20, 33)), (2, (4, 4), (2, 32, 6, 7)), (3, (3, 3, 3), (2, 27, 3, 4, 5)),
+                           (2, (7, 7), (1, 98, 5, 5))]:
+        x = torch.randn(*shape, generator=g, dtype=torch.float64).to(DEV).requires_grad_(True)
+        y = getattr(tvdcn_amd, f"mask_softmax{dim}d")(x, ks)
+        kn = 1
+        for k in ks:
+            kn *= k
+        xr = x.detach().clone().requires_grad_(True)
+        yr = torch.softmax(xr.view(shape[0], shape[1] // kn, kn, -1), dim=2).view(shape)
+        assert rel_err(y, yr) < 1e-12
+        gy = torch.randn(*shape, generator=g, dtype=torch.float64).to(DEV)
+        y.backward(gy)
+        yr.backward(gy)
+        assert rel_err(x.grad, xr.grad) < 1e-12

@@ -1,0 +1,366 @@
+// C ABI of libtvdcn_hip.so (declared in include/tvdcn_hip.h).
+//
+// Validates a descriptor with the reference's shape rules, lays out the
+// caller-provided workspace, and enqueues the kernel sequence of each op on the
+// caller's stream. Host-side only: no allocation, no synchronisation.
+#include <string>
+#include <cstring>
+#include <climits>
+
+#include "../../../include/tvdcn_hip.h"
+#include "kernels.h"
+
+using namespace tvdcn_hip;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+tvdcn_status fail(tvdcn_status st, const std::string &msg) {
+    g_last_error = msg;
+    return st;
+}
+
+size_t acc_size(int dtype) { return dtype == TVDCN_DTYPE_FLOAT64 ? 8 : 4; }
+size_t elem_size(int dtype) {
+    switch (dtype) {
+        case TVDCN_DTYPE_FLOAT32: return 4;
+        case TVDCN_DTYPE_FLOAT64: return 8;
+        default: return 2;
+    }
+}
+bool acc_is_storage(int dtype) { return dtype == TVDCN_DTYPE_FLOAT32 || dtype == TVDCN_DTYPE_FLOAT64; }
+
+size_t align_up(size_t v) { return (v + 255) / 256 * 256; }
+
+// Output size: conv per ops/cuda/deform_conv2d_kernel.cpp:167-168, transposed per
+// ops/cuda/deform_conv_transpose2d_kernel.cpp:172-173 (1D/3D files identical in form).
+tvdcn_status output_size(const tvdcn_conv_desc *d, int64_t out[3]) {
+    if (d == nullptr) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null descriptor");
+    if (d->dim < 1 || d->dim > 3) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "dim must be 1, 2 or 3");
+    for (int i = 0; i < d->dim; ++i) {
+        if (d->kernel[i] <= 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "kernel size must be positive");
+        if (d->stride[i] <= 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "stride must be positive");
+        if (d->padding[i] < 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "padding must be non-negative");
+        if (d->dilation[i] <= 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "dilation must be positive");
+        if (d->transposed)
+            out[i] = (d->in_size[i] - 1) * d->stride[i] - 2 * d->padding[i] + d->dilation[i] * (d->kernel[i] - 1) + 1 +
+                     d->output_padding[i];
+        else
+            out[i] = (d->in_size[i] + 2 * d->padding[i] - (d->dilation[i] * (d->kernel[i] - 1) + 1)) / d->stride[i] + 1;
+        if (out[i] <= 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "Calculated output size too small");
+    }
+    return TVDCN_STATUS_SUCCESS;
+}
+
+struct Plan {
+    Geo g;
+    int64_t out_size[3];
+    int dim;
+    bool transposed;
+    int dtype;
+    FwdTiles ft;
+    DataTiles dt;
+    WeightTiles wt;
+};
+
+bool fits_int(int64_t v) { return v >= 0 && v <= (int64_t)INT_MAX; }
+
+tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
+    tvdcn_status st = output_size(d, pl.out_size);
+    if (st) return st;
+    if (d->dtype < 0 || d->dtype > 3) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "unknown dtype");
+    if (d->batch < 0 || d->in_channels <= 0 || d->out_channels <= 0)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "batch must be >= 0 and channels positive");
+    if (d->groups <= 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "groups must be positive");
+    if (d->in_channels % d->groups || d->out_channels % d->groups)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "in_channels and out_channels must be divisible by groups");
+    if (d->offset_groups < 0 || d->mask_groups < 0)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "offset_groups / mask_groups must be >= 0");
+    // Groups of offsets/masks partition the channels of the sampled side (columns).
+    // The reference checks input.size(1) % groups (deform_conv2d_kernel.cpp:205, 233;
+    // transposed :216, :247); for the transposed op the columns are the output
+    // channels, so they must divide those too (the reference indexes past the
+    // offset tensor otherwise).
+    const int64_t C = d->transposed ? d->out_channels : d->in_channels;
+    const int64_t M = d->transposed ? d->in_channels : d->out_channels;
+    if (d->offset_groups && (d->in_channels % d->offset_groups || C % d->offset_groups))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "channels must be divisible by offset_groups");
+    if (d->mask_groups && (d->in_channels % d->mask_groups || C % d->mask_groups))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "channels must be divisible by mask_groups");
+
+    pl.dim = d->dim;
+    pl.transposed = d->transposed != 0;
+    pl.dtype = d->dtype;
+    Geo &g = pl.g;
+    int64_t S3[3] = {1, 1, 1}, P3[3] = {1, 1, 1}, K3[3] = {1, 1, 1}, st3[3] = {1, 1, 1}, pd3[3] = {0, 0, 0},
+            dl3[3] = {1, 1, 1};
+    for (int i = 0; i < d->dim; ++i) {
+        const int e = 3 - d->dim + i;
+        S3[e] = pl.transposed ? pl.out_size[i] : d->in_size[i];
+        P3[e] = pl.transposed ? d->in_size[i] : pl.out_size[i];
+        K3[e] = d->kernel[i];
+        st3[e] = d->stride[i];
+        pd3[e] = d->padding[i];
+        dl3[e] = d->dilation[i];
+    }
+    const int64_t Sn = S3[0] * S3[1] * S3[2], Pn = P3[0] * P3[1] * P3[2], Kn = K3[0] * K3[1] * K3[2];
+    const int64_t B = d->batch;
+    // int32 indexing inside the kernels: every tensor must stay below 2^31 elements
+    const int64_t biggest[] = {B * C * Sn, B * M * Pn, M * (C / d->groups) * Kn,
+                               B * (d->offset_groups ? d->offset_groups : 1) * Kn * d->dim * Pn,
+                               B * (d->mask_groups ? d->mask_groups : 1) * Kn * Pn};
+    for (int64_t v : biggest)
+        if (!fits_int(v)) return fail(TVDCN_STATUS_NOT_SUPPORTED, "tensor too large for 32-bit indexing");
+    for (int i = 0; i < 3; ++i) {
+        g.S[i] = (int)S3[i];
+        g.P[i] = (int)P3[i];
+        g.K[i] = (int)K3[i];
+        g.st[i] = (int)st3[i];
+        g.pad[i] = (int)pd3[i];
+        g.dil[i] = (int)dl3[i];
+    }
+    g.B = (int)B;
+    g.C = (int)C;
+    g.M = (int)M;
+    g.G = (int)d->groups;
+    g.Cg = (int)(C / d->groups);
+    g.Mg = (int)(M / d->groups);
+    g.og = (int)d->offset_groups;
+    g.mg = (int)d->mask_groups;
+    g.cpo = g.og ? g.C / g.og : 1;
+    g.cpm = g.mg ? g.C / g.mg : 1;
+    g.Sn = (int)Sn;
+    g.Pn = (int)Pn;
+    g.Kn = (int)Kn;
+    g.NP = (int)(B * Pn);
+    pl.ft = plan_fwd(g, pl.dtype);
+    pl.dt = plan_data(g, pl.dtype);
+    pl.wt = plan_weight(g, pl.dtype);
+    return TVDCN_STATUS_SUCCESS;
+}
+
+// Workspace sub-buffers (byte offsets into the caller's workspace).
+struct Layout {
+    size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, gw_acc = 0, goff_acc = 0, gmask_acc = 0;
+    size_t total = 0;
+};
+
+Layout layout(const Plan &pl, bool backward) {
+    const Geo &g = pl.g;
+    const size_t a = acc_size(pl.dtype);
+    const size_t cl_bytes = align_up((size_t)g.B * g.Sn * g.C * a);
+    const size_t wf_bytes = align_up((size_t)g.G * g.Kn * pl.ft.Mg_pad * pl.ft.Cg_pad * a);
+    const size_t wd_bytes = align_up((size_t)g.G * g.Kn * pl.dt.Mg_pad * pl.dt.Cg_pad * a);
+    Layout L;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += bytes;
+        return o;
+    };
+    const size_t SENTINEL = (size_t)-1;
+    L.xcl = L.wf = L.wd = L.cl_acc = L.gw_acc = L.goff_acc = L.gmask_acc = SENTINEL;
+    if (!backward) {
+        if (!pl.transposed) {
+            L.xcl = take(cl_bytes);
+            L.wf = take(wf_bytes);
+        } else {
+            L.wd = take(wd_bytes);
+            L.cl_acc = take(cl_bytes);
+        }
+    } else {
+        L.xcl = take(cl_bytes);
+        L.wd = take(wd_bytes);
+        if (pl.transposed)
+            L.wf = take(wf_bytes);
+        else
+            L.cl_acc = take(cl_bytes);
+        if (!acc_is_storage(pl.dtype)) {
+            L.gw_acc = take(align_up((size_t)g.M * g.Cg * g.Kn * a));
+            if (g.og) L.goff_acc = take(align_up((size_t)g.B * g.og * g.Kn * pl.dim * g.Pn * a));
+            if (g.mg) L.gmask_acc = take(align_up((size_t)g.B * g.mg * g.Kn * g.Pn * a));
+        }
+    }
+    L.total = off;
+    return L;
+}
+
+void *at(void *ws, size_t off) { return off == (size_t)-1 ? nullptr : static_cast<char *>(ws) + off; }
+
+#define TVDCN_CHECK_HIP(expr)                                                                     \
+    do {                                                                                          \
+        hipError_t e_ = (expr);                                                                   \
+        if (e_ != hipSuccess)                                                                     \
+            return fail(TVDCN_STATUS_HIP_ERROR, std::string(#expr " failed: ") + hipGetErrorString(e_)); \
+    } while (0)
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+tvdcn_status tvdcn_conv_output_size(const tvdcn_conv_desc *desc, int64_t out_size[3]) {
+    int64_t tmp[3] = {1, 1, 1};
+    tvdcn_status st = output_size(desc, tmp);
+    if (st == TVDCN_STATUS_SUCCESS && out_size)
+        for (int i = 0; i < 3; ++i) out_size[i] = tmp[i];
+    return st;
+}
+
+size_t tvdcn_deform_conv_forward_workspace_size(const tvdcn_conv_desc *desc) {
+    Plan pl;
+    if (make_plan(desc, pl)) return 0;
+    return layout(pl, false).total;
+}
+
+size_t tvdcn_deform_conv_backward_workspace_size(const tvdcn_conv_desc *desc) {
+    Plan pl;
+    if (make_plan(desc, pl)) return 0;
+    return layout(pl, true).total;
+}
+
+tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *input, const void *weight,
+                                       const void *offset, const void *mask, const void *bias, void *output,
+                                       void *workspace, size_t workspace_bytes, void *stream) {
+    Plan pl;
+    tvdcn_status st = make_plan(desc, pl);
+    if (st) return st;
+    const Geo &g = pl.g;
+    if ((desc->offset_groups == 0) != (offset == nullptr))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "offset pointer and offset_groups disagree");
+    if ((desc->mask_groups == 0) != (mask == nullptr))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "mask pointer and mask_groups disagree");
+    const Layout L = layout(pl, false);
+    if (workspace_bytes < L.total) return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
+    if (g.B == 0) return TVDCN_STATUS_SUCCESS;
+    if (!input || !weight || !output) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
+    if (!aligned16(input) || !aligned16(workspace))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "input and workspace must be 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int dt = pl.dtype;
+    g_last_error.clear();
+    if (!pl.transposed) {
+        void *xcl = at(workspace, L.xcl), *wf = at(workspace, L.wf);
+        TVDCN_CHECK_HIP(launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
+        TVDCN_CHECK_HIP(launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
+        TVDCN_CHECK_HIP(launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, bias, output, s));
+    } else {
+        void *wd = at(workspace, L.wd), *ycl = at(workspace, L.cl_acc);
+        TVDCN_CHECK_HIP(launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
+        TVDCN_CHECK_HIP(launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
+        TVDCN_CHECK_HIP(launch_bwd_data(dt, pl.dim, g, pl.dt, true, false, input, wd, nullptr, offset, mask, ycl,
+                                        nullptr, nullptr, s));
+        TVDCN_CHECK_HIP(launch_from_channels_last(dt, ycl, output, bias, g.B, g.C, g.Sn, s));
+    }
+    return TVDCN_STATUS_SUCCESS;
+}
+
+tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void *grad_out, const void *input,
+                                        const void *weight, const void *offset, const void *mask, void *grad_input,
+                                        void *grad_weight, void *grad_offset, void *grad_mask, void *grad_bias,
+                                        void *workspace, size_t workspace_bytes, void *stream) {
+    Plan pl;
+    tvdcn_status st = make_plan(desc, pl);
+    if (st) return st;
+    const Geo &g = pl.g;
+    if ((desc->offset_groups == 0) != (offset == nullptr) || (offset == nullptr) != (grad_offset == nullptr))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "offset / grad_offset pointers and offset_groups disagree");
+    if ((desc->mask_groups == 0) != (mask == nullptr) || (mask == nullptr) != (grad_mask == nullptr))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "mask / grad_mask pointers and mask_groups disagree");
+    const Layout L = layout(pl, true);
+    if (workspace_bytes < L.total) return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
+    if (!grad_out || !input || !weight || !grad_input || !grad_weight)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
+    if (!aligned16(workspace)) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int dt = pl.dtype;
+    const int ab = (int)acc_size(dt);
+    const bool direct = acc_is_storage(dt);
+    g_last_error.clear();
+
+    const size_t n_gw = (size_t)g.M * g.Cg * g.Kn;
+    const size_t n_goff = g.og ? (size_t)g.B * g.og * g.Kn * pl.dim * g.Pn : 0;
+    const size_t n_gmask = g.mg ? (size_t)g.B * g.mg * g.Kn * g.Pn : 0;
+    void *gw = direct ? grad_weight : at(workspace, L.gw_acc);
+    void *goff = direct ? grad_offset : at(workspace, L.goff_acc);
+    void *gmask = direct ? grad_mask : at(workspace, L.gmask_acc);
+    TVDCN_CHECK_HIP(launch_fill_zero(ab, gw, n_gw, s));
+    if (goff) TVDCN_CHECK_HIP(launch_fill_zero(ab, goff, n_goff, s));
+    if (gmask) TVDCN_CHECK_HIP(launch_fill_zero(ab, gmask, n_gmask, s));
+
+    // Z: the GEMM-side tensor (conv: grad_out; transposed: input)
+    // X: the sampled tensor (conv: input; transposed: grad_out)
+    const void *Z = pl.transposed ? input : grad_out;
+    const void *X = pl.transposed ? grad_out : input;
+    if (g.B > 0) {
+        void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
+        TVDCN_CHECK_HIP(launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
+        TVDCN_CHECK_HIP(launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
+        const bool coord = offset != nullptr || mask != nullptr;
+        if (!pl.transposed) {
+            void *gx_cl = at(workspace, L.cl_acc);
+            TVDCN_CHECK_HIP(launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
+            TVDCN_CHECK_HIP(launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask, gx_cl, goff,
+                                            gmask, s));
+            TVDCN_CHECK_HIP(launch_from_channels_last(dt, gx_cl, grad_input, nullptr, g.B, g.C, g.Sn, s));
+        } else {
+            void *wf = at(workspace, L.wf);
+            TVDCN_CHECK_HIP(launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
+            TVDCN_CHECK_HIP(
+                launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, nullptr, grad_input, s));
+            if (coord)
+                TVDCN_CHECK_HIP(launch_bwd_data(dt, pl.dim, g, pl.dt, false, true, Z, wd, xcl, offset, mask, nullptr,
+                                                goff, gmask, s));
+        }
+        TVDCN_CHECK_HIP(launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask, gw, s));
+    }
+    if (!direct) {
+        TVDCN_CHECK_HIP(launch_acc_to_storage(dt, gw, grad_weight, n_gw, s));
+        if (goff) TVDCN_CHECK_HIP(launch_acc_to_storage(dt, goff, grad_offset, n_goff, s));
+        if (gmask) TVDCN_CHECK_HIP(launch_acc_to_storage(dt, gmask, grad_mask, n_gmask, s));
+    }
+    if (grad_bias) {
+        // grad_out is (B, Cout, *out_size): conv Cout = M on the column grid,
+        // transposed Cout = C on the sampled grid
+        const int Cout = pl.transposed ? g.C : g.M;
+        const int So = pl.transposed ? g.Sn : g.Pn;
+        // B == 0 reduces over nothing and writes zeros
+        TVDCN_CHECK_HIP(launch_bias_grad(dt, grad_out, grad_bias, g.B, Cout, So, s));
+    }
+    return TVDCN_STATUS_SUCCESS;
+}
+
+tvdcn_status tvdcn_mask_softmax_forward(int32_t dtype, int64_t batch, int64_t groups, int64_t kernel_numel,
+                                        int64_t spatial_numel, const void *x, void *y, void *stream) {
+    if (dtype < 0 || dtype > 3) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "unknown dtype");
+    if (batch < 0 || groups < 0 || kernel_numel <= 0 || spatial_numel < 0)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "invalid mask_softmax sizes");
+    if (!fits_int(kernel_numel)) return fail(TVDCN_STATUS_NOT_SUPPORTED, "kernel_numel too large");
+    g_last_error.clear();
+    TVDCN_CHECK_HIP(launch_mask_softmax_fwd(dtype, x, y, batch * groups, (int)kernel_numel, spatial_numel,
+                                            static_cast<hipStream_t>(stream)));
+    return TVDCN_STATUS_SUCCESS;
+}
+
+tvdcn_status tvdcn_mask_softmax_backward(int32_t dtype, int64_t batch, int64_t groups, int64_t kernel_numel,
+                                         int64_t spatial_numel, const void *y, const void *grad_y, void *grad_x,
+                                         void *stream) {
+    if (dtype < 0 || dtype > 3) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "unknown dtype");
+    if (batch < 0 || groups < 0 || kernel_numel <= 0 || spatial_numel < 0)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "invalid mask_softmax sizes");
+    if (!fits_int(kernel_numel)) return fail(TVDCN_STATUS_NOT_SUPPORTED, "kernel_numel too large");
+    g_last_error.clear();
+    TVDCN_CHECK_HIP(launch_mask_softmax_bwd(dtype, y, grad_y, grad_x, batch * groups, (int)kernel_numel,
+                                            spatial_numel, static_cast<hipStream_t>(stream)));
+    return TVDCN_STATUS_SUCCESS;
+}
+
+const char *tvdcn_last_error(void) { return g_last_error.c_str(); }
+
+int64_t tvdcn_hip_version(void) { return (int64_t)HIP_VERSION; }
+
+const char *tvdcn_arch_flags(void) { return "gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,298 @@
+// Shared device-side definitions for the gfx950 deformable-convolution kernels.
+//
+// Three kernel families implement every op (conv and transposed, rank 1/2/3):
+//   F  gather-GEMM   Y[b][m][p]   = sum_{c,t} W[m][c][t] * S[c][t][b][p]
+//   D  data-grad     G[c][t][b][p] = sum_m W[m][c][t] * Z[b][m][p], then scatter G*mask
+//                    into the sampled tensor's gradient and/or reduce the offset/mask grads
+//   Wt weight-grad   dW[m][c][t]  = sum_{b,p} Z[b][m][p] * S[c][t][b][p]
+// where S is the bilinear sample (times mask) of the "sampled" tensor X at the
+// deformed tap positions. Conv: X = input, Z = grad_out, M = Cout, C = Cin.
+// Transposed: X = output side (grad_out in backward), Z = input, M = Cin, C = Cout.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+namespace tvdcn_hip {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// Problem geometry, passed by value to every kernel. Spatial shapes are embedded
+// in rank 3 (unused leading axes have extent 1, stride 1, padding 0).
+struct Geo {
+    int B;
+    int C, M, G, Cg, Mg;   // sampled-side channels, GEMM-side channels, groups
+    int og, mg;            // offset / mask groups (0 = absent)
+    int cpo, cpm;          // channels per offset / mask group
+    int S[3];              // sampled grid (conv: input; transposed: output)
+    int P[3];              // column grid (conv: output; transposed: input)
+    int K[3], st[3], pad[3], dil[3];
+    int Sn, Pn, Kn;
+    int NP;                // B * Pn
+};
+
+// ---------------------------------------------------------------------------
+// scalar conversion
+// ---------------------------------------------------------------------------
+template <typename A, typename T> __device__ __forceinline__ A to_acc(T v) { return static_cast<A>(v); }
+template <> __device__ __forceinline__ float to_acc<float, __half>(__half v) { return __half2float(v); }
+template <> __device__ __forceinline__ float to_acc<float, __hip_bfloat16>(__hip_bfloat16 v) {
+    return __bfloat162float(v);
+}
+template <typename T, typename A> __device__ __forceinline__ T from_acc(A v) { return static_cast<T>(v); }
+template <> __device__ __forceinline__ __half from_acc<__half, float>(float v) { return __float2half(v); }
+template <> __device__ __forceinline__ __hip_bfloat16 from_acc<__hip_bfloat16, float>(float v) {
+    return __float2bfloat16(v);
+}
+
+// four consecutive accumulator-typed values (16 B for float, 32 B for double)
+template <typename A> struct Vec4 { A x, y, z, w; };
+
+template <typename A>
+__device__ __forceinline__ Vec4<A> load4(const A *p) {
+    if constexpr (sizeof(A) == 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(p);
+        return {v.x, v.y, v.z, v.w};
+    } else {
+        const double2 a = *reinterpret_cast<const double2 *>(p);
+        const double2 b = *reinterpret_cast<const double2 *>(p + 2);
+        return {a.x, a.y, b.x, b.y};
+    }
+}
+
+template <typename A>
+__device__ __forceinline__ void store4(A *p, Vec4<A> v) {
+    if constexpr (sizeof(A) == 4) {
+        *reinterpret_cast<float4 *>(p) = make_float4(v.x, v.y, v.z, v.w);
+    } else {
+        *reinterpret_cast<double2 *>(p) = make_double2(v.x, v.y);
+        *reinterpret_cast<double2 *>(p + 2) = make_double2(v.z, v.w);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA 16x16x4 (fp32 and fp64). Operand layout, lane l of 64:
+//   A[i][k]: i = l % 16, k = l / 16      B[k][j]: j = l % 16, k = l / 16
+//   D[i][j]: 4 values per lane, i = 4 * (l / 16) + v, j = l % 16
+// ---------------------------------------------------------------------------
+template <typename A> struct Acc4;
+template <> struct Acc4<float> { typedef f32x4 type; };
+template <> struct Acc4<double> { typedef f64x4 type; };
+
+__device__ __forceinline__ f32x4 mfma16x16x4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f64x4 mfma16x16x4(double a, double b, f64x4 c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// atomics: hardware float/double add (global_atomic_add_f32 / _f64)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void atomic_add(float *p, float v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add(double *p, double v) { unsafeAtomicAdd(p, v); }
+
+// ---------------------------------------------------------------------------
+// workgroup -> tile mapping that keeps consecutive tiles on one XCD. The
+// hardware deals workgroups round-robin to the 8 XCDs (each with its own L2);
+// this inverts that so XCD x processes the contiguous tile range
+// [base_x, base_x + count_x), keeping neighbouring pixel tiles (which share
+// input rows) in the same L2.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int xcd_remap(int L, int N) {
+    constexpr int NX = 8;
+    const int q = N / NX, r = N % NX;
+    const int xcd = L % NX, k = L / NX;
+    const int base = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
+    return base + k;
+}
+
+// ---------------------------------------------------------------------------
+// Sampling geometry of one (column pixel, tap, offset group).
+// Restates the reference's per-rank helpers (tvdcn/csrc/ops/cuda/
+// deform_conv2d_common_kernels.cu:25-135 and the 1D/3D twins):
+//   * sample value: 0 if the point is outside (-1, size) on any axis,
+//     else the sum over the in-range corners of (product of axis weights) * x;
+//   * scatter (insert) and coordinate weights: no early-out, each corner
+//     range-checked on both sides.
+// Corner order is the reference's: low/high on the last axis fastest.
+// ---------------------------------------------------------------------------
+template <int DIM> struct Corners {
+    static constexpr int N = 1 << DIM;
+    int idx[N];          // flat spatial index into the sampled grid (0 when invalid)
+    bool valid[N];       // corner inside the grid
+    float frac[3];       // fractional position on each embedded axis used (lo weight = 1-frac)
+    bool inside;         // point inside (-1, size) on every axis (sample early-out rule)
+};
+
+// Axis a of the DIM used axes corresponds to embedded axis 3-DIM+a.
+template <int DIM, typename A>
+struct Point {
+    A pos[DIM];
+    int base[DIM];
+};
+
+template <int DIM>
+__device__ __forceinline__ void decompose_tap(const Geo &g, int t, int kk[DIM]) {
+    if constexpr (DIM == 1) {
+        kk[0] = t;
+    } else if constexpr (DIM == 2) {
+        kk[1] = t % g.K[2];
+        kk[0] = t / g.K[2];
+    } else {
+        kk[2] = t % g.K[2];
+        kk[1] = (t / g.K[2]) % g.K[1];
+        kk[0] = t / (g.K[2] * g.K[1]);
+    }
+}
+
+template <int DIM>
+__device__ __forceinline__ void decompose_pix(const Geo &g, int p, int pp[DIM]) {
+    if constexpr (DIM == 1) {
+        pp[0] = p;
+    } else if constexpr (DIM == 2) {
+        pp[1] = p % g.P[2];
+        pp[0] = p / g.P[2];
+    } else {
+        pp[2] = p % g.P[2];
+        pp[1] = (p / g.P[2]) % g.P[1];
+        pp[0] = p / (g.P[2] * g.P[1]);
+    }
+}
+
+// Integer base point h*stride - pad + i*dilation per axis
+// (deform_conv2d_common_kernels.cu:171-172) plus the offsets of group ogi
+// (offset channel ((ogi*Kn + t)*DIM + axis), deform_conv2d_kernel.cpp:278-286).
+template <int DIM, typename A, typename T>
+__device__ __forceinline__ Point<DIM, A> sample_point(const Geo &g, const T *__restrict__ offset, int b, int p,
+                                                      int t, int ogi) {
+    int kk[DIM], pp[DIM];
+    decompose_tap<DIM>(g, t, kk);
+    decompose_pix<DIM>(g, p, pp);
+    Point<DIM, A> pt;
+#pragma unroll
+    for (int a = 0; a < DIM; ++a) {
+        const int e = 3 - DIM + a;
+        pt.base[a] = pp[a] * g.st[e] - g.pad[e] + kk[a] * g.dil[e];
+        pt.pos[a] = static_cast<A>(pt.base[a]);
+    }
+    if (offset != nullptr) {
+        const T *o = offset + ((size_t)(b * g.og + ogi) * g.Kn + t) * DIM * (size_t)g.Pn + p;
+#pragma unroll
+        for (int a = 0; a < DIM; ++a) pt.pos[a] += to_acc<A>(o[(size_t)a * g.Pn]);
+    }
+    return pt;
+}
+
+// Per-axis decomposition of a (possibly fractional) point.
+template <int DIM, typename A>
+struct AxisW {
+    int lo[DIM];
+    A fh[DIM];           // high-corner weight = pos - floor(pos); low = 1 - fh
+    bool vlo[DIM], vhi[DIM];
+    bool inside;         // sample early-out rule
+};
+
+template <int DIM, typename A>
+__device__ __forceinline__ AxisW<DIM, A> axis_weights(const Geo &g, const Point<DIM, A> &pt, bool deformable) {
+    AxisW<DIM, A> w;
+    w.inside = true;
+#pragma unroll
+    for (int a = 0; a < DIM; ++a) {
+        const int n = g.S[3 - DIM + a];
+        if (deformable) {
+            const A f = floor(pt.pos[a]);
+            w.lo[a] = static_cast<int>(f);
+            w.fh[a] = pt.pos[a] - f;
+            w.inside = w.inside && !(pt.pos[a] <= A(-1) || A(n) <= pt.pos[a]);
+        } else {
+            // integer sampling (offset is None): only the low corner exists
+            // (deform_conv2d_common_kernels.cu:13-22 `sample` / `insert`)
+            w.lo[a] = pt.base[a];
+            w.fh[a] = A(0);
+            w.inside = w.inside && (0 <= pt.base[a] && pt.base[a] < n);
+        }
+        w.vlo[a] = 0 <= w.lo[a] && w.lo[a] < n;
+        w.vhi[a] = deformable && 0 <= w.lo[a] + 1 && w.lo[a] + 1 < n;
+    }
+    return w;
+}
+
+// Corner i (bit a of i, counted from the last axis, selects high on axis a).
+template <int DIM>
+__device__ __forceinline__ int corner_bit(int i, int a) {
+    return (i >> (DIM - 1 - a)) & 1;
+}
+
+// flat index and validity of corner i
+template <int DIM, typename A>
+__device__ __forceinline__ void corner_at(const Geo &g, const AxisW<DIM, A> &w, int i, int &idx, bool &valid) {
+    int flat = 0;
+    valid = true;
+#pragma unroll
+    for (int a = 0; a < DIM; ++a) {
+        const int hi = corner_bit<DIM>(i, a);
+        const int coord = w.lo[a] + hi;
+        valid = valid && (hi ? w.vhi[a] : w.vlo[a]);
+        flat = flat * g.S[3 - DIM + a] + coord;
+    }
+    idx = valid ? flat : 0;
+}
+
+// bilinear product weight of corner i: prod over axes of (hi ? fh : 1 - fh), in the
+// reference's multiplication order (outer axis first).
+template <int DIM, typename A>
+__device__ __forceinline__ A corner_weight(const AxisW<DIM, A> &w, int i) {
+    A r = A(1);
+#pragma unroll
+    for (int a = 0; a < DIM; ++a) {
+        const A f = corner_bit<DIM>(i, a) ? w.fh[a] : A(1) - w.fh[a];
+        r = (a == 0) ? f : r * f;
+    }
+    return r;
+}
+
+// coordinate weight of corner i for derivative axis d: axis d's factor is -1/+1
+// (deform_conv2d_common_kernels.cu:105-135).
+template <int DIM, typename A>
+__device__ __forceinline__ A corner_dweight(const AxisW<DIM, A> &w, int i, int d) {
+    A r = A(1);
+#pragma unroll
+    for (int a = 0; a < DIM; ++a) {
+        const int hi = corner_bit<DIM>(i, a);
+        const A f = (a == d) ? (hi ? A(1) : A(-1)) : (hi ? w.fh[a] : A(1) - w.fh[a]);
+        r = (a == 0) ? f : r * f;
+    }
+    return r;
+}
+
+// Gather-side corner set for the fast paths: flat indices (0 when invalid) and
+// sample weights (0 when invalid or when the sample early-out applies).
+template <int DIM, typename A>
+struct GatherCorners {
+    int idx[1 << DIM];
+    A w[1 << DIM];
+};
+
+template <int DIM, typename A>
+__device__ __forceinline__ GatherCorners<DIM, A> gather_corners(const Geo &g, const AxisW<DIM, A> &aw) {
+    GatherCorners<DIM, A> gc;
+#pragma unroll
+    for (int i = 0; i < (1 << DIM); ++i) {
+        bool v;
+        corner_at<DIM, A>(g, aw, i, gc.idx[i], v);
+        gc.w[i] = (v && aw.inside) ? corner_weight<DIM, A>(aw, i) : A(0);
+    }
+    return gc;
+}
+
+template <typename A, typename T>
+__device__ __forceinline__ A mask_at(const Geo &g, const T *__restrict__ mask, int b, int mgi, int t, int p) {
+    if (mask == nullptr) return A(1);
+    return to_acc<A>(mask[((size_t)(b * g.mg + mgi) * g.Kn + t) * (size_t)g.Pn + p]);
+}
+
+}  // namespace tvdcn_hip

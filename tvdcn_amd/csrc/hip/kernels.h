@@ -1,0 +1,62 @@
+// Host-side launchers of the gfx950 kernels (one definition per .hip file).
+// All launches are asynchronous on `stream`; none allocates or synchronises.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include "common.h"
+
+namespace tvdcn_hip {
+
+enum DType { kF32 = 0, kF64 = 1, kF16 = 2, kBF16 = 3 };
+
+// Tile parameters shared by host and device code.
+struct FwdTiles {
+    int waves;       // 1, 2 or 4 waves along the GEMM-side channels (64 rows each)
+    bool vec4;       // channel quads share offset/mask group (fast gather)
+    int Mg_pad;      // Mg rounded up to 64 * waves
+    int Cg_pad;      // Cg rounded up to 16
+};
+struct DataTiles {
+    int waves;       // taps per workgroup (one 64-channel x 64-pixel tile per wave)
+    int Mg_pad;      // Mg rounded up to 16
+    int Cg_pad;      // Cg rounded up to 64
+};
+struct WeightTiles {
+    int waves;       // 64-row GEMM-side blocks per workgroup
+    bool vec4;
+    int k_chunk;     // column pixels per workgroup (split-K)
+    int k_splits;
+};
+
+FwdTiles plan_fwd(const Geo &g, int dtype);
+DataTiles plan_data(const Geo &g, int dtype);
+WeightTiles plan_weight(const Geo &g, int dtype);
+
+// layout / elementwise helpers (prep.hip)
+hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s);
+hipError_t launch_from_channels_last(int dtype, const void *xcl, void *x, const void *bias, int B, int C, int Sn,
+                                     hipStream_t s);
+hipError_t launch_weight_fwd_layout(int dtype, const Geo &g, const void *w, void *wf, int Mg_pad, int Cg_pad,
+                                    hipStream_t s);
+hipError_t launch_weight_data_layout(int dtype, const Geo &g, const void *w, void *wd, int Mg_pad, int Cg_pad,
+                                     hipStream_t s);
+hipError_t launch_fill_zero(int acc_bytes, void *p, size_t n, hipStream_t s);
+hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n, hipStream_t s);
+hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s);
+
+// the three GEMM families
+hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTiles &t, const void *xcl,
+                                  const void *wf, const void *offset, const void *mask, const void *bias, void *y,
+                                  hipStream_t s);
+hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t, bool scatter, bool coord,
+                           const void *z, const void *wd, const void *xcl, const void *offset, const void *mask,
+                           void *gx_cl, void *goff, void *gmask, hipStream_t s);
+hipError_t launch_bwd_weight(int dtype, int dim, const Geo &g, const WeightTiles &t, const void *z, const void *xcl,
+                             const void *offset, const void *mask, void *gw, hipStream_t s);
+
+// mask_softmax (mask_softmax.hip)
+hipError_t launch_mask_softmax_fwd(int dtype, const void *x, void *y, int64_t BG, int K, int64_t S, hipStream_t s);
+hipError_t launch_mask_softmax_bwd(int dtype, const void *y, const void *gy, void *gx, int64_t BG, int K, int64_t S,
+                                   hipStream_t s);
+
+}  // namespace tvdcn_hip

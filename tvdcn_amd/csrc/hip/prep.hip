@@ -1,0 +1,222 @@
+// Layout and elementwise helpers around the GEMM families (all HBM-bound).
+//   * channels-last conversion of the sampled tensor ([B][C][S] -> [B][S][C]),
+//     so that a bilinear corner fetch of consecutive channels is one coalesced
+//     load; and the inverse (+ optional bias) for gradients / transposed outputs;
+//   * weight re-layouts for the two MFMA operand orders;
+//   * zero fill (a kernel, so it is safe inside captured HIP graphs);
+//   * grad_bias = sum over batch and space of grad_out
+//     (reference: tvdcn/csrc/ops/cuda/deform_conv2d_kernel.cpp:415-417).
+#include "kernels.h"
+
+namespace tvdcn_hip {
+namespace {
+
+constexpr int TT = 64;   // transpose tile
+
+// x [B][C][S] (T) -> xcl [B][S][C] (A); 64 x 64 tile through LDS, 256 threads
+template <typename T, typename A>
+__global__ void __launch_bounds__(256) to_cl_kernel(const T *__restrict__ x, A *__restrict__ xcl, int C, int S) {
+    __shared__ A tile[TT][TT + 1];
+    const int b = blockIdx.z;
+    const int s0 = blockIdx.x * TT, c0 = blockIdx.y * TT;
+    const T *xb = x + (size_t)b * C * S;
+    A *ob = xcl + (size_t)b * C * S;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int r = ty; r < TT; r += 4) {
+        const int c = c0 + r, s = s0 + tx;
+        tile[r][tx] = (c < C && s < S) ? to_acc<A>(xb[(size_t)c * S + s]) : A(0);
+    }
+    __syncthreads();
+    for (int r = ty; r < TT; r += 4) {
+        const int s = s0 + r, c = c0 + tx;
+        if (s < S && c < C) ob[(size_t)s * C + c] = tile[tx][r];
+    }
+}
+
+// xcl [B][S][C] (A) -> x [B][C][S] (T), plus bias[c]
+template <typename T, typename A>
+__global__ void __launch_bounds__(256) from_cl_kernel(const A *__restrict__ xcl, T *__restrict__ x,
+                                                      const T *__restrict__ bias, int C, int S) {
+    __shared__ A tile[TT][TT + 1];
+    const int b = blockIdx.z;
+    const int s0 = blockIdx.x * TT, c0 = blockIdx.y * TT;
+    const A *ib = xcl + (size_t)b * C * S;
+    T *ob = x + (size_t)b * C * S;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int r = ty; r < TT; r += 4) {
+        const int s = s0 + r, c = c0 + tx;
+        tile[r][tx] = (s < S && c < C) ? ib[(size_t)s * C + c] : A(0);
+    }
+    __syncthreads();
+    for (int r = ty; r < TT; r += 4) {
+        const int c = c0 + r, s = s0 + tx;
+        if (c < C && s < S) {
+            A v = tile[tx][r];
+            if (bias != nullptr) v += to_acc<A>(bias[c]);
+            ob[(size_t)c * S + s] = from_acc<T, A>(v);
+        }
+    }
+}
+
+// weight (M, Cg, Kn) -> Wf [G][Kn][Mg_pad][Cg_pad] (zero padded)
+template <typename T, typename A>
+__global__ void weight_f_kernel(const T *__restrict__ w, A *__restrict__ wf, int G, int Mg, int Cg, int Kn,
+                                int Mg_pad, int Cg_pad) {
+    const size_t total = (size_t)G * Kn * Mg_pad * Cg_pad;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i % Cg_pad);
+        const int m = (int)((i / Cg_pad) % Mg_pad);
+        const int t = (int)((i / ((size_t)Cg_pad * Mg_pad)) % Kn);
+        const int g = (int)(i / ((size_t)Cg_pad * Mg_pad * Kn));
+        A v = A(0);
+        if (m < Mg && c < Cg) v = to_acc<A>(w[(((size_t)g * Mg + m) * Cg + c) * Kn + t]);
+        wf[i] = v;
+    }
+}
+
+// weight (M, Cg, Kn) -> Wd [G][Kn][Cg_pad][Mg_pad] (zero padded)
+template <typename T, typename A>
+__global__ void weight_d_kernel(const T *__restrict__ w, A *__restrict__ wd, int G, int Mg, int Cg, int Kn,
+                                int Mg_pad, int Cg_pad) {
+    const size_t total = (size_t)G * Kn * Mg_pad * Cg_pad;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int m = (int)(i % Mg_pad);
+        const int c = (int)((i / Mg_pad) % Cg_pad);
+        const int t = (int)((i / ((size_t)Mg_pad * Cg_pad)) % Kn);
+        const int g = (int)(i / ((size_t)Mg_pad * Cg_pad * Kn));
+        A v = A(0);
+        if (m < Mg && c < Cg) v = to_acc<A>(w[(((size_t)g * Mg + m) * Cg + c) * Kn + t]);
+        wd[i] = v;
+    }
+}
+
+template <typename A>
+__global__ void fill_zero_kernel(A *__restrict__ p, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = A(0);
+}
+
+template <typename T, typename A>
+__global__ void acc_to_storage_kernel(const A *__restrict__ a, T *__restrict__ o, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        o[i] = from_acc<T, A>(a[i]);
+}
+
+// grad_bias[c] = sum_{b, s} gout[b][c][s]; one workgroup per channel
+template <typename T, typename A>
+__global__ void __launch_bounds__(256) bias_grad_kernel(const T *__restrict__ gout, T *__restrict__ gb, int B, int C,
+                                                        int S) {
+    __shared__ A red[256];
+    const int c = blockIdx.x;
+    A acc = A(0);
+    for (int b = 0; b < B; ++b) {
+        const T *row = gout + ((size_t)b * C + c) * S;
+        for (int s = threadIdx.x; s < S; s += 256) acc += to_acc<A>(row[s]);
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) gb[c] = from_acc<T, A>(red[0]);
+}
+
+unsigned grid_for(size_t n) {
+    size_t b = (n + 255) / 256;
+    if (b > 65536) b = 65536;
+    if (b < 1) b = 1;
+    return (unsigned)b;
+}
+
+template <typename F>
+hipError_t by_dtype(int dtype, F &&f) {
+    switch (dtype) {
+        case kF32: return f(float(), float());
+        case kF64: return f(double(), double());
+        case kF16: return f(__half(), float());
+        case kBF16: return f(__hip_bfloat16(), float());
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s) {
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B);
+        hipLaunchKernelGGL((to_cl_kernel<T, A>), grid, dim3(256), 0, s, static_cast<const T *>(x),
+                           static_cast<A *>(xcl), C, Sn);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_from_channels_last(int dtype, const void *xcl, void *x, const void *bias, int B, int C, int Sn,
+                                     hipStream_t s) {
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B);
+        hipLaunchKernelGGL((from_cl_kernel<T, A>), grid, dim3(256), 0, s, static_cast<const A *>(xcl),
+                           static_cast<T *>(x), static_cast<const T *>(bias), C, Sn);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_weight_fwd_layout(int dtype, const Geo &g, const void *w, void *wf, int Mg_pad, int Cg_pad,
+                                    hipStream_t s) {
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        const size_t n = (size_t)g.G * g.Kn * Mg_pad * Cg_pad;
+        hipLaunchKernelGGL((weight_f_kernel<T, A>), dim3(grid_for(n)), dim3(256), 0, s, static_cast<const T *>(w),
+                           static_cast<A *>(wf), g.G, g.Mg, g.Cg, g.Kn, Mg_pad, Cg_pad);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_weight_data_layout(int dtype, const Geo &g, const void *w, void *wd, int Mg_pad, int Cg_pad,
+                                     hipStream_t s) {
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        const size_t n = (size_t)g.G * g.Kn * Mg_pad * Cg_pad;
+        hipLaunchKernelGGL((weight_d_kernel<T, A>), dim3(grid_for(n)), dim3(256), 0, s, static_cast<const T *>(w),
+                           static_cast<A *>(wd), g.G, g.Mg, g.Cg, g.Kn, Mg_pad, Cg_pad);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_fill_zero(int acc_bytes, void *p, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (acc_bytes == 8)
+        hipLaunchKernelGGL((fill_zero_kernel<double>), dim3(grid_for(n)), dim3(256), 0, s, static_cast<double *>(p), n);
+    else
+        hipLaunchKernelGGL((fill_zero_kernel<float>), dim3(grid_for(n)), dim3(256), 0, s, static_cast<float *>(p), n);
+    return hipGetLastError();
+}
+
+hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        hipLaunchKernelGGL((acc_to_storage_kernel<T, A>), dim3(grid_for(n)), dim3(256), 0, s,
+                           static_cast<const A *>(acc), static_cast<T *>(out), n);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s) {
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        hipLaunchKernelGGL((bias_grad_kernel<T, A>), dim3(C), dim3(256), 0, s, static_cast<const T *>(gout),
+                           static_cast<T *>(gbias), B, C, Sn);
+        return hipGetLastError();
+    });
+}
+
+}  // namespace tvdcn_hip

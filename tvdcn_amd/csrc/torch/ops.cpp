@@ -1,0 +1,788 @@
+// PyTorch-ROCm operator layer of tvdcn_amd: the reference's twelve operator
+// schemas (plus mask_softmax), registered under the `tvdcn_amd` namespace with
+// CUDA (= HIP on ROCm), Meta, Autograd and Autocast kernels. The CUDA kernels
+// validate, allocate outputs and workspace from the caching allocator, and call
+// the C ABI of libtvdcn_hip.so on the current HIP stream. There is no CPU
+// kernel: CPU tensors fail in the dispatcher, loudly.
+//
+// Reference interface mirrored (paths relative to tvdcn/csrc/):
+//   schemas        ops/deform_conv{1,2,3}d.cpp, ops/deform_conv_transpose{1,2,3}d.cpp
+//                  (e.g. ops/deform_conv2d.cpp:117-126, ops/deform_conv_transpose2d.cpp:125-136)
+//   validation     ops/cuda/deform_conv2d_kernel.cpp:100-268,
+//                  ops/cuda/deform_conv_transpose2d_kernel.cpp:100-275 and 1D/3D twins
+//   autograd       ops/autograd/deform_conv2d_kernel.cpp:9-203 (saved tensors, returned
+//                  grads, double-backward error) and twins
+//   autocast       ops/autocast/deform_conv2d_kernel.cpp:9-38 and twins
+//   library info   tvdcn.cpp:24-53 (_cuda_version, _cuda_arch_flags)
+#include <ATen/ATen.h>
+#include <ATen/autocast_mode.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/autograd.h>
+#include <torch/library.h>
+
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "tvdcn_hip.h"
+
+namespace tvdcn_amd {
+namespace {
+
+using at::Tensor;
+using c10::optional;
+
+const char *axis_name(int dim, int i) {
+    static const char *n3[] = {"d", "h", "w"};
+    return n3[3 - dim + i];
+}
+
+std::vector<int64_t> ntuple(at::IntArrayRef v, int dim, const char *what) {
+    TORCH_CHECK(v.size() == 1 || (int)v.size() == dim, "Expected a sequence of ", dim, " elements for ", what,
+                ", got ", v.size());
+    std::vector<int64_t> r(dim);
+    for (int i = 0; i < dim; ++i) r[i] = v.size() == 1 ? v[0] : v[i];
+    return r;
+}
+
+std::string join(const std::vector<int64_t> &v) {
+    std::ostringstream os;
+    for (size_t i = 0; i < v.size(); ++i) os << (i ? ", " : "") << v[i];
+    return os.str();
+}
+
+int32_t dtype_code(at::ScalarType t) {
+    switch (t) {
+        case at::kFloat: return TVDCN_DTYPE_FLOAT32;
+        case at::kDouble: return TVDCN_DTYPE_FLOAT64;
+        case at::kHalf: return TVDCN_DTYPE_FLOAT16;
+        case at::kBFloat16: return TVDCN_DTYPE_BFLOAT16;
+        default: TORCH_CHECK(false, "tvdcn_amd: unsupported dtype ", t, " (expected float32/64, float16, bfloat16)");
+    }
+    return -1;
+}
+
+// Parsed and validated problem.
+struct Problem {
+    int dim;
+    bool transposed;
+    bool unbatched;
+    tvdcn_conv_desc desc;
+    std::vector<int64_t> out_size;
+    Tensor input, weight, offset, mask, bias;   // batched, contiguous (offset/mask/bias may be undefined)
+};
+
+// Shape checks of the reference forward drivers, in the same order and with the
+// same wording (rank-generic).
+Problem make_problem(int dim, bool transposed, const Tensor &input, const Tensor &weight,
+                     const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
+                     at::IntArrayRef stride_, at::IntArrayRef padding_, at::IntArrayRef output_padding_,
+                     at::IntArrayRef dilation_, int64_t groups, const char *name) {
+    Problem pr;
+    pr.dim = dim;
+    pr.transposed = transposed;
+    const bool deformable = offset.has_value() && offset->defined();
+    const bool modulated = mask.has_value() && mask->defined();
+    const bool with_bias = bias.has_value() && bias->defined();
+
+    at::CheckedFrom c = name;
+    std::vector<at::TensorArg> args;
+    args.emplace_back(input, "input", 1);
+    args.emplace_back(weight, "weight", 2);
+    if (deformable) args.emplace_back(offset.value(), "offset", 3);
+    if (modulated) args.emplace_back(mask.value(), "mask", 4);
+    if (with_bias) args.emplace_back(bias.value(), "bias", 5);
+    at::checkAllSameType(c, args);
+    for (auto &a : args)
+        TORCH_CHECK(a->device() == input.device(), name, ": expected all tensors on ", input.device(), ", but ",
+                    a.name, " is on ", a->device());
+
+    pr.unbatched = input.dim() == dim + 1;
+    TORCH_CHECK(pr.unbatched || input.dim() == dim + 2, "Expected ", dim + 1, "D (unbatched) or ", dim + 2,
+                "D (batched) input to ", transposed ? "deform_conv_transpose" : "deform_conv", dim,
+                "d, but got input of size: ", input.sizes());
+    TORCH_CHECK(weight.dim() == dim + 2, "Expected ", dim + 2, "D weight");
+    TORCH_CHECK(!deformable || offset->dim() == input.dim(), "Expected ", dim + 1, "D (unbatched) or ", dim + 2,
+                "D (batched) offset, but got offset of size: ", deformable ? offset->sizes() : at::IntArrayRef());
+    TORCH_CHECK(!modulated || mask->dim() == input.dim(), "Expected ", dim + 1, "D (unbatched) or ", dim + 2,
+                "D (batched) mask, but got mask of size: ", modulated ? mask->sizes() : at::IntArrayRef());
+
+    pr.input = input.contiguous();
+    pr.weight = weight.contiguous();
+    pr.offset = deformable ? offset->contiguous() : Tensor();
+    pr.mask = modulated ? mask->contiguous() : Tensor();
+    pr.bias = with_bias ? bias->contiguous() : Tensor();
+    if (pr.unbatched) {
+        pr.input = pr.input.unsqueeze(0);
+        if (deformable) pr.offset = pr.offset.unsqueeze(0);
+        if (modulated) pr.mask = pr.mask.unsqueeze(0);
+    }
+
+    const auto stride = ntuple(stride_, dim, "stride");
+    const auto padding = ntuple(padding_, dim, "padding");
+    const auto dilation = ntuple(dilation_, dim, "dilation");
+    const auto out_pad = transposed ? ntuple(output_padding_, dim, "output_padding") : std::vector<int64_t>(dim, 0);
+
+    const int64_t B = pr.input.size(0), Cin = pr.input.size(1);
+    std::vector<int64_t> ksz(dim), in_size(dim);
+    int64_t kn = 1;
+    for (int i = 0; i < dim; ++i) {
+        ksz[i] = pr.weight.size(2 + i);
+        in_size[i] = pr.input.size(2 + i);
+        kn *= ksz[i];
+    }
+    auto check_pos = [&](const std::vector<int64_t> &v, const char *what, bool allow_zero) {
+        bool ok = true;
+        for (auto x : v) ok = ok && (allow_zero ? x >= 0 : x > 0);
+        if (!ok) {
+            std::ostringstream os;
+            for (int i = 0; i < dim; ++i) os << (i ? " " : "") << what << "_" << axis_name(dim, i) << ": " << v[i];
+            TORCH_CHECK(false, os.str());
+        }
+    };
+    check_pos(ksz, "weight", false);
+    check_pos(stride, "stride", false);
+    check_pos(padding, "pad", true);
+    check_pos(dilation, "dilation", false);
+
+    int64_t Cout;
+    if (!transposed) {
+        Cout = pr.weight.size(0);
+        TORCH_CHECK(pr.weight.size(1) * groups == Cin, "Expected weight.size(1) * groups == in_channels (",
+                    pr.weight.size(1), " * ", groups, " != ", Cin, ")");
+        TORCH_CHECK(pr.weight.size(0) % groups == 0, "Expected weight.size(0) % groups == 0");
+    } else {
+        Cout = pr.weight.size(1) * groups;
+        TORCH_CHECK(pr.weight.size(0) == Cin, "Expected weight.size(0) == in_channels (", pr.weight.size(0),
+                    " != ", Cin, ")");
+        TORCH_CHECK(pr.weight.size(0) % groups == 0, "Expected weight.size(0) % groups == 0");
+    }
+
+    std::vector<int64_t> out(dim);
+    for (int i = 0; i < dim; ++i)
+        out[i] = transposed ? (in_size[i] - 1) * stride[i] - 2 * padding[i] + dilation[i] * (ksz[i] - 1) + 1 + out_pad[i]
+                            : (in_size[i] + 2 * padding[i] - (dilation[i] * (ksz[i] - 1) + 1)) / stride[i] + 1;
+    // offsets / masks live on the column grid: conv output grid, transposed input grid
+    const std::vector<int64_t> &grid = transposed ? in_size : out;
+    const char *grid_name = transposed ? "input" : "output";
+    std::string kprod;
+    for (int i = 0; i < dim; ++i) kprod += std::string(i ? " * " : "") + "weight.size(" + std::to_string(2 + i) + ")";
+
+    int64_t og = 0, mg = 0;
+    if (deformable) {
+        og = pr.offset.size(1) / (dim * kn);
+        TORCH_CHECK(pr.offset.size(0) == B, "invalid batch size of offset");
+        TORCH_CHECK(og > 0, "The shape of the offset tensor at dimension 1 is not valid. It should be a multiple of ",
+                    dim, " * ", kprod, ".\nGot offset.size(1)=", pr.offset.size(1), ", while ", dim, " * ", kprod, "=",
+                    dim * kn);
+        TORCH_CHECK(Cin % og == 0, "Expected in_channels % offset_groups == 0");
+        TORCH_CHECK(pr.offset.size(1) == og * dim * kn, "offset.shape[1] is not valid. got: ", pr.offset.size(1),
+                    " expected: ", og * dim * kn);
+        std::vector<int64_t> got(pr.offset.sizes().begin() + 2, pr.offset.sizes().end());
+        TORCH_CHECK(got == grid, "offset ", grid_name, " dims: (", join(got), ") - computed ", grid_name, " dims: (",
+                    join(grid), ")");
+        if (transposed)
+            TORCH_CHECK(Cout % og == 0, "Expected out_channels % offset_groups == 0 (offset groups partition the ",
+                        "output channels of a transposed deformable convolution)");
+    }
+    if (modulated) {
+        mg = pr.mask.size(1) / kn;
+        TORCH_CHECK(pr.mask.size(0) == B, "invalid batch size of mask");
+        TORCH_CHECK(mg > 0, "The shape of the mask tensor at dimension 1 is not valid. It should be a multiple of ",
+                    kprod, ".\nGot mask.size(1)=", pr.mask.size(1), ", while ", kprod, "=", kn);
+        TORCH_CHECK(Cin % mg == 0, "Expected in_channels % mask_groups == 0");
+        TORCH_CHECK(pr.mask.size(1) == mg * kn, "mask.shape[1] is not valid. got: ", pr.mask.size(1), " expected: ",
+                    mg * kn);
+        std::vector<int64_t> got(pr.mask.sizes().begin() + 2, pr.mask.sizes().end());
+        TORCH_CHECK(got == grid, "mask ", grid_name, " dims: (", join(got), ") - computed ", grid_name, " dims: (",
+                    join(grid), ")");
+        if (transposed)
+            TORCH_CHECK(Cout % mg == 0, "Expected out_channels % mask_groups == 0 (mask groups partition the ",
+                        "output channels of a transposed deformable convolution)");
+    }
+    {
+        bool ok = true;
+        std::ostringstream os;
+        for (int i = 0; i < dim; ++i) {
+            ok = ok && out[i] > 0;
+            os << (i ? " " : "") << "out_" << axis_name(dim, i) << ": " << out[i];
+        }
+        TORCH_CHECK(ok, "Calculated output size too small - ", os.str());
+    }
+    if (with_bias) TORCH_CHECK(pr.bias.numel() == Cout, "Expected bias of ", Cout, " elements");
+
+    tvdcn_conv_desc &d = pr.desc;
+    std::memset(&d, 0, sizeof(d));
+    d.dim = dim;
+    d.transposed = transposed;
+    d.dtype = -1;
+    d.batch = B;
+    d.in_channels = Cin;
+    d.out_channels = Cout;
+    d.groups = groups;
+    d.offset_groups = og;
+    d.mask_groups = mg;
+    for (int i = 0; i < 3; ++i) {
+        d.kernel[i] = d.stride[i] = d.dilation[i] = d.in_size[i] = 1;
+        d.padding[i] = d.output_padding[i] = 0;
+    }
+    for (int i = 0; i < dim; ++i) {
+        d.in_size[i] = in_size[i];
+        d.kernel[i] = ksz[i];
+        d.stride[i] = stride[i];
+        d.padding[i] = padding[i];
+        d.dilation[i] = dilation[i];
+        d.output_padding[i] = out_pad[i];
+    }
+    pr.out_size = out;
+    return pr;
+}
+
+std::vector<int64_t> out_shape(const Problem &pr) {
+    std::vector<int64_t> s = {pr.desc.batch, pr.desc.out_channels};
+    s.insert(s.end(), pr.out_size.begin(), pr.out_size.end());
+    return s;
+}
+
+void check_status(tvdcn_status st, const char *what) {
+    TORCH_CHECK(st == TVDCN_STATUS_SUCCESS, what, " failed (status ", (int)st, "): ", tvdcn_last_error());
+}
+
+const void *ptr_or_null(const Tensor &t) { return t.defined() ? t.data_ptr() : nullptr; }
+void *mut_ptr_or_null(const Tensor &t) { return t.defined() ? t.data_ptr() : nullptr; }
+
+// The C ABI wants 16-byte aligned operands; tensors that are contiguous views at
+// an odd offset are copied.
+Tensor aligned(const Tensor &t) {
+    if (!t.defined()) return t;
+    if ((reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0) return t;
+    return t.clone(at::MemoryFormat::Contiguous);
+}
+
+hipStream_t current_stream(const Tensor &t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
+
+// ---------------------------------------------------------------------------
+// forward / backward, CUDA (HIP) key
+// ---------------------------------------------------------------------------
+Tensor forward_hip(int dim, bool transposed, const Tensor &input, const Tensor &weight,
+                   const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
+                   at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding,
+                   at::IntArrayRef dilation, int64_t groups, const char *name) {
+    TORCH_CHECK(input.is_cuda(), name, ": expected a GPU (HIP) tensor");
+    c10::DeviceGuard guard(input.device());
+    Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
+                              dilation, groups, name);
+    pr.desc.dtype = dtype_code(pr.input.scalar_type());
+    Tensor output = at::empty(out_shape(pr), pr.input.options());
+    if (output.numel() > 0) {
+        const size_t ws_bytes = tvdcn_deform_conv_forward_workspace_size(&pr.desc);
+        TORCH_CHECK(ws_bytes > 0 || pr.desc.batch == 0, name, ": ", tvdcn_last_error());
+        Tensor ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 1)}, pr.input.options().dtype(at::kByte));
+        Tensor x = aligned(pr.input), w = aligned(pr.weight), o = aligned(pr.offset), m = aligned(pr.mask),
+               b = aligned(pr.bias);
+        check_status(tvdcn_deform_conv_forward(&pr.desc, x.data_ptr(), w.data_ptr(), ptr_or_null(o), ptr_or_null(m),
+                                               ptr_or_null(b), output.data_ptr(), ws.data_ptr(), ws_bytes,
+                                               current_stream(output)),
+                     name);
+    } else {
+        output.zero_();
+    }
+    if (pr.unbatched) output = output.squeeze(0);
+    return output;
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_hip(
+    int dim, bool transposed, const Tensor &grad, const Tensor &input, const Tensor &weight,
+    const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
+    at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding, at::IntArrayRef dilation,
+    int64_t groups, const char *name) {
+    TORCH_CHECK(input.is_cuda(), name, ": expected a GPU (HIP) tensor");
+    c10::DeviceGuard guard(input.device());
+    Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
+                              dilation, groups, name);
+    pr.desc.dtype = dtype_code(pr.input.scalar_type());
+    Tensor g = grad.contiguous();
+    if (pr.unbatched) g = g.unsqueeze(0);
+    TORCH_CHECK(g.sizes() == at::IntArrayRef(out_shape(pr)), name, ": grad has shape ", g.sizes(), ", expected ",
+                at::IntArrayRef(out_shape(pr)));
+    TORCH_CHECK(g.scalar_type() == pr.input.scalar_type(), name, ": grad dtype must match input dtype");
+
+    Tensor grad_input = at::empty_like(pr.input);
+    Tensor grad_weight = at::empty_like(pr.weight);
+    Tensor grad_offset = pr.offset.defined() ? at::empty_like(pr.offset) : Tensor();
+    Tensor grad_mask = pr.mask.defined() ? at::empty_like(pr.mask) : Tensor();
+    Tensor grad_bias = pr.bias.defined() ? at::empty({pr.desc.out_channels}, pr.input.options()) : Tensor();
+    const size_t ws_bytes = tvdcn_deform_conv_backward_workspace_size(&pr.desc);
+    TORCH_CHECK(ws_bytes > 0, name, ": ", tvdcn_last_error());
+    Tensor ws = at::empty({(int64_t)ws_bytes}, pr.input.options().dtype(at::kByte));
+    Tensor ga = aligned(g), x = aligned(pr.input), w = aligned(pr.weight), o = aligned(pr.offset),
+           m = aligned(pr.mask);
+    check_status(tvdcn_deform_conv_backward(&pr.desc, ga.data_ptr(), x.data_ptr(), w.data_ptr(), ptr_or_null(o),
+                                            ptr_or_null(m), grad_input.data_ptr(), grad_weight.data_ptr(),
+                                            mut_ptr_or_null(grad_offset), mut_ptr_or_null(grad_mask),
+                                            mut_ptr_or_null(grad_bias), ws.data_ptr(), ws_bytes,
+                                            current_stream(grad_input)),
+                 name);
+    if (pr.unbatched) {
+        grad_input = grad_input.squeeze(0);
+        if (grad_offset.defined()) grad_offset = grad_offset.squeeze(0);
+        if (grad_mask.defined()) grad_mask = grad_mask.squeeze(0);
+    }
+    return {grad_input, grad_weight, grad_offset, grad_mask, grad_bias};
+}
+
+// ---------------------------------------------------------------------------
+// Meta key: same validation, shapes only (no data, no compute)
+// ---------------------------------------------------------------------------
+Tensor forward_meta(int dim, bool transposed, const Tensor &input, const Tensor &weight,
+                    const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
+                    at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding,
+                    at::IntArrayRef dilation, int64_t groups, const char *name) {
+    Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
+                              dilation, groups, name);
+    dtype_code(pr.input.scalar_type());
+    Tensor output = at::empty(out_shape(pr), pr.input.options());
+    if (pr.unbatched) output = output.squeeze(0);
+    return output;
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_meta(
+    int dim, bool transposed, const Tensor &grad, const Tensor &input, const Tensor &weight,
+    const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
+    at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding, at::IntArrayRef dilation,
+    int64_t groups, const char *name) {
+    Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
+                              dilation, groups, name);
+    (void)grad;
+    return {at::empty_like(input), at::empty_like(weight),
+            pr.offset.defined() ? at::empty_like(offset.value()) : Tensor(),
+            pr.mask.defined() ? at::empty_like(mask.value()) : Tensor(),
+            pr.bias.defined() ? at::empty({pr.desc.out_channels}, input.options()) : Tensor()};
+}
+
+// ---------------------------------------------------------------------------
+// autograd (ops/autograd/deform_conv2d_kernel.cpp:9-203): save the five tensors,
+// backward calls the `_..._backward` op, which itself refuses double backward.
+// ---------------------------------------------------------------------------
+struct OpNames {
+    const char *fwd;
+    const char *bwd;
+};
+
+template <int DIM, bool TR>
+struct Names;
+#define TVDCN_NAMES(D, TRV, F, Bw)                               \
+    template <>                                                  \
+    struct Names<D, TRV> {                                       \
+        static constexpr const char *fwd = "tvdcn_amd::" F;      \
+        static constexpr const char *bwd = "tvdcn_amd::" Bw;     \
+        static constexpr const char *short_name = F;             \
+    };
+TVDCN_NAMES(1, false, "deform_conv1d", "_deform_conv1d_backward")
+TVDCN_NAMES(2, false, "deform_conv2d", "_deform_conv2d_backward")
+TVDCN_NAMES(3, false, "deform_conv3d", "_deform_conv3d_backward")
+TVDCN_NAMES(1, true, "deform_conv_transpose1d", "_deform_conv_transpose1d_backward")
+TVDCN_NAMES(2, true, "deform_conv_transpose2d", "_deform_conv_transpose2d_backward")
+TVDCN_NAMES(3, true, "deform_conv_transpose3d", "_deform_conv_transpose3d_backward")
+#undef TVDCN_NAMES
+
+using FwdSig = Tensor(const Tensor &, const Tensor &, const optional<Tensor> &, const optional<Tensor> &,
+                      const optional<Tensor> &, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef,
+                      int64_t);
+using BwdSig = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor>(
+    const Tensor &, const Tensor &, const Tensor &, const optional<Tensor> &, const optional<Tensor> &,
+    const optional<Tensor> &, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t);
+// conv schemas have no output_padding: their typed signatures differ
+using FwdSigC = Tensor(const Tensor &, const Tensor &, const optional<Tensor> &, const optional<Tensor> &,
+                       const optional<Tensor> &, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t);
+using BwdSigC = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor>(
+    const Tensor &, const Tensor &, const Tensor &, const optional<Tensor> &, const optional<Tensor> &,
+    const optional<Tensor> &, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t);
+
+template <int DIM, bool TR>
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> call_backward(const Tensor &grad, const Tensor &input,
+                                                                 const Tensor &weight, const optional<Tensor> &offset,
+                                                                 const optional<Tensor> &mask,
+                                                                 const optional<Tensor> &bias, at::IntArrayRef stride,
+                                                                 at::IntArrayRef padding, at::IntArrayRef out_pad,
+                                                                 at::IntArrayRef dilation, int64_t groups) {
+    if constexpr (TR) {
+        static auto op = c10::Dispatcher::singleton().findSchemaOrThrow(Names<DIM, TR>::bwd, "").template typed<BwdSig>();
+        return op.call(grad, input, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups);
+    } else {
+        static auto op =
+            c10::Dispatcher::singleton().findSchemaOrThrow(Names<DIM, TR>::bwd, "").template typed<BwdSigC>();
+        return op.call(grad, input, weight, offset, mask, bias, stride, padding, dilation, groups);
+    }
+}
+
+template <int DIM, bool TR>
+Tensor call_forward(const Tensor &input, const Tensor &weight, const optional<Tensor> &offset,
+                    const optional<Tensor> &mask, const optional<Tensor> &bias, at::IntArrayRef stride,
+                    at::IntArrayRef padding, at::IntArrayRef out_pad, at::IntArrayRef dilation, int64_t groups) {
+    if constexpr (TR) {
+        static auto op = c10::Dispatcher::singleton().findSchemaOrThrow(Names<DIM, TR>::fwd, "").template typed<FwdSig>();
+        return op.call(input, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups);
+    } else {
+        static auto op =
+            c10::Dispatcher::singleton().findSchemaOrThrow(Names<DIM, TR>::fwd, "").template typed<FwdSigC>();
+        return op.call(input, weight, offset, mask, bias, stride, padding, dilation, groups);
+    }
+}
+
+optional<Tensor> opt(const Tensor &t) { return t.defined() ? optional<Tensor>(t) : optional<Tensor>(); }
+
+template <int DIM, bool TR>
+class DeformFunction : public torch::autograd::Function<DeformFunction<DIM, TR>> {
+   public:
+    static torch::autograd::Variable forward(torch::autograd::AutogradContext *ctx, const Tensor &input,
+                                             const Tensor &weight, const optional<Tensor> &offset,
+                                             const optional<Tensor> &mask, const optional<Tensor> &bias,
+                                             at::IntArrayRef stride, at::IntArrayRef padding,
+                                             at::IntArrayRef out_pad, at::IntArrayRef dilation, int64_t groups) {
+        at::AutoDispatchBelowADInplaceOrView guard;
+        Tensor output = call_forward<DIM, TR>(input, weight, offset, mask, bias, stride, padding, out_pad, dilation,
+                                              groups);
+        ctx->save_for_backward({input, weight, offset.value_or(Tensor()), mask.value_or(Tensor()),
+                                bias.value_or(Tensor())});
+        ctx->saved_data["stride"] = stride.vec();
+        ctx->saved_data["padding"] = padding.vec();
+        ctx->saved_data["output_padding"] = out_pad.vec();
+        ctx->saved_data["dilation"] = dilation.vec();
+        ctx->saved_data["groups"] = groups;
+        return output;
+    }
+
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext *ctx,
+                                                   const torch::autograd::variable_list &grad_output) {
+        auto saved = ctx->get_saved_variables();
+        const auto stride = ctx->saved_data["stride"].toIntVector();
+        const auto padding = ctx->saved_data["padding"].toIntVector();
+        const auto out_pad = ctx->saved_data["output_padding"].toIntVector();
+        const auto dilation = ctx->saved_data["dilation"].toIntVector();
+        const int64_t groups = ctx->saved_data["groups"].toInt();
+        auto grads = call_backward<DIM, TR>(grad_output[0], saved[0], saved[1], opt(saved[2]), opt(saved[3]),
+                                            opt(saved[4]), stride, padding, out_pad, dilation, groups);
+        return {std::get<0>(grads), std::get<1>(grads), std::get<2>(grads), std::get<3>(grads), std::get<4>(grads),
+                Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// Autograd kernel of the backward op: runs it below autograd; when any input
+// still requires grad, the outputs get a node that raises on use
+// (ops/autograd/deform_conv2d_kernel.cpp:96-144: "double backwards on ... not supported").
+template <int DIM, bool TR>
+class DeformBackwardFunction : public torch::autograd::Function<DeformBackwardFunction<DIM, TR>> {
+   public:
+    static torch::autograd::variable_list forward(torch::autograd::AutogradContext *ctx, const Tensor &grad,
+                                                  const Tensor &input, const Tensor &weight,
+                                                  const optional<Tensor> &offset, const optional<Tensor> &mask,
+                                                  const optional<Tensor> &bias, at::IntArrayRef stride,
+                                                  at::IntArrayRef padding, at::IntArrayRef out_pad,
+                                                  at::IntArrayRef dilation, int64_t groups) {
+        at::AutoDispatchBelowADInplaceOrView guard;
+        auto r = call_backward<DIM, TR>(grad, input, weight, offset, mask, bias, stride, padding, out_pad, dilation,
+                                        groups);
+        // undefined gradients (absent offset / mask / bias) are returned as
+        // empty placeholders here and turned back into undefined by the caller
+        ctx->saved_data["defined"] = std::vector<int64_t>{std::get<2>(r).defined(), std::get<3>(r).defined(),
+                                                          std::get<4>(r).defined()};
+        auto ph = [&](const Tensor &t) { return t.defined() ? t : at::empty({0}, input.options()); };
+        return {std::get<0>(r), std::get<1>(r), ph(std::get<2>(r)), ph(std::get<3>(r)), ph(std::get<4>(r))};
+    }
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext *,
+                                                   const torch::autograd::variable_list &) {
+        TORCH_CHECK(false, "double backwards on ", Names<DIM, TR>::short_name, " not supported");
+        return {};
+    }
+};
+
+template <int DIM, bool TR>
+Tensor forward_autograd(const Tensor &input, const Tensor &weight, const optional<Tensor> &offset,
+                        const optional<Tensor> &mask, const optional<Tensor> &bias, at::IntArrayRef stride,
+                        at::IntArrayRef padding, at::IntArrayRef out_pad, at::IntArrayRef dilation, int64_t groups) {
+    return DeformFunction<DIM, TR>::apply(input, weight, offset, mask, bias, stride, padding, out_pad, dilation,
+                                          groups);
+}
+
+template <int DIM, bool TR>
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_autograd(
+    const Tensor &grad, const Tensor &input, const Tensor &weight, const optional<Tensor> &offset,
+    const optional<Tensor> &mask, const optional<Tensor> &bias, at::IntArrayRef stride, at::IntArrayRef padding,
+    at::IntArrayRef out_pad, at::IntArrayRef dilation, int64_t groups) {
+    auto r = DeformBackwardFunction<DIM, TR>::apply(grad, input, weight, offset, mask, bias, stride, padding, out_pad,
+                                                    dilation, groups);
+    const bool has_off = offset.has_value() && offset->defined();
+    const bool has_mask = mask.has_value() && mask->defined();
+    const bool has_bias = bias.has_value() && bias->defined();
+    return {r[0], r[1], has_off ? r[2] : Tensor(), has_mask ? r[3] : Tensor(), has_bias ? r[4] : Tensor()};
+}
+
+// ---------------------------------------------------------------------------
+// autocast (ops/autocast/deform_conv2d_kernel.cpp:9-38): run in fp32, cast back
+// ---------------------------------------------------------------------------
+template <int DIM, bool TR>
+Tensor forward_autocast(const Tensor &input, const Tensor &weight, const optional<Tensor> &offset,
+                        const optional<Tensor> &mask, const optional<Tensor> &bias, at::IntArrayRef stride,
+                        at::IntArrayRef padding, at::IntArrayRef out_pad, at::IntArrayRef dilation, int64_t groups) {
+    c10::impl::ExcludeDispatchKeyGuard no_autocast(c10::DispatchKey::Autocast);
+    auto f32 = [](const optional<Tensor> &t) -> optional<Tensor> {
+        if (!t.has_value() || !t->defined()) return t;
+        return at::autocast::cached_cast(at::kFloat, *t, c10::DeviceType::CUDA);
+    };
+    return call_forward<DIM, TR>(at::autocast::cached_cast(at::kFloat, input, c10::DeviceType::CUDA),
+                                 at::autocast::cached_cast(at::kFloat, weight, c10::DeviceType::CUDA), f32(offset),
+                                 f32(mask), f32(bias), stride, padding, out_pad, dilation, groups)
+        .to(input.scalar_type());
+}
+
+// ---------------------------------------------------------------------------
+// kernel adapters with the exact schema signatures
+// ---------------------------------------------------------------------------
+template <int DIM, bool TR>
+struct Kernels {
+    // conv signature (no output_padding) adapters
+    static Tensor fwd_hip_c(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                            const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef d,
+                            int64_t g) {
+        return forward_hip(DIM, TR, i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g, Names<DIM, TR>::short_name);
+    }
+    static Tensor fwd_hip_t(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                            const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                            at::IntArrayRef d, int64_t g) {
+        return forward_hip(DIM, TR, i, w, o, m, b, s, p, op, d, g, Names<DIM, TR>::short_name);
+    }
+    static Tensor fwd_meta_c(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                             const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef d,
+                             int64_t g) {
+        return forward_meta(DIM, TR, i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g, Names<DIM, TR>::short_name);
+    }
+    static Tensor fwd_meta_t(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                             const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                             at::IntArrayRef d, int64_t g) {
+        return forward_meta(DIM, TR, i, w, o, m, b, s, p, op, d, g, Names<DIM, TR>::short_name);
+    }
+    using G5 = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor>;
+    static G5 bwd_hip_c(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
+                        const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
+                        at::IntArrayRef d, int64_t g) {
+        return backward_hip(DIM, TR, gr, i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g, Names<DIM, TR>::short_name);
+    }
+    static G5 bwd_hip_t(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
+                        const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
+                        at::IntArrayRef op, at::IntArrayRef d, int64_t g) {
+        return backward_hip(DIM, TR, gr, i, w, o, m, b, s, p, op, d, g, Names<DIM, TR>::short_name);
+    }
+    static G5 bwd_meta_c(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
+                         const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
+                         at::IntArrayRef d, int64_t g) {
+        return backward_meta(DIM, TR, gr, i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g,
+                             Names<DIM, TR>::short_name);
+    }
+    static G5 bwd_meta_t(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
+                         const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
+                         at::IntArrayRef op, at::IntArrayRef d, int64_t g) {
+        return backward_meta(DIM, TR, gr, i, w, o, m, b, s, p, op, d, g, Names<DIM, TR>::short_name);
+    }
+    static Tensor fwd_ag_c(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                           const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef d,
+                           int64_t g) {
+        return forward_autograd<DIM, TR>(i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g);
+    }
+    static Tensor fwd_ag_t(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                           const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                           at::IntArrayRef d, int64_t g) {
+        return forward_autograd<DIM, TR>(i, w, o, m, b, s, p, op, d, g);
+    }
+    static G5 bwd_ag_c(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
+                       const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
+                       at::IntArrayRef d, int64_t g) {
+        return backward_autograd<DIM, TR>(gr, i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g);
+    }
+    static G5 bwd_ag_t(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
+                       const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
+                       at::IntArrayRef op, at::IntArrayRef d, int64_t g) {
+        return backward_autograd<DIM, TR>(gr, i, w, o, m, b, s, p, op, d, g);
+    }
+    static Tensor fwd_ac_c(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                           const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef d,
+                           int64_t g) {
+        return forward_autocast<DIM, TR>(i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g);
+    }
+    static Tensor fwd_ac_t(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                           const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                           at::IntArrayRef d, int64_t g) {
+        return forward_autocast<DIM, TR>(i, w, o, m, b, s, p, op, d, g);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// mask_softmax: x viewed as (B, groups, K, S), softmax over K
+// ---------------------------------------------------------------------------
+void softmax_dims(const Tensor &x, int64_t K, int64_t &B, int64_t &G, int64_t &S) {
+    TORCH_CHECK(x.dim() >= 2, "mask_softmax: expected a (batch, groups * kernel_numel, *spatial) tensor");
+    TORCH_CHECK(K > 0, "mask_softmax: kernel_numel must be positive");
+    B = x.size(0);
+    G = x.size(1) / K;
+    TORCH_CHECK(G > 0 && G * K == x.size(1), "The shape of the mask tensor at dimension 1 is not valid. It should ",
+                "be a multiple of the kernel size.\nGot mask.size(1)=", x.size(1), ", while kernel_numel=", K);
+    S = 1;
+    for (int64_t i = 2; i < x.dim(); ++i) S *= x.size(i);
+}
+
+Tensor mask_softmax_hip(const Tensor &x, int64_t K) {
+    TORCH_CHECK(x.is_cuda(), "mask_softmax: expected a GPU (HIP) tensor");
+    c10::DeviceGuard guard(x.device());
+    int64_t B, G, S;
+    softmax_dims(x, K, B, G, S);
+    Tensor xc = x.contiguous();
+    Tensor y = at::empty_like(xc);
+    check_status(tvdcn_mask_softmax_forward(dtype_code(xc.scalar_type()), B, G, K, S, xc.data_ptr(), y.data_ptr(),
+                                            current_stream(y)),
+                 "mask_softmax");
+    return y;
+}
+
+Tensor mask_softmax_backward_hip(const Tensor &grad, const Tensor &y, int64_t K) {
+    TORCH_CHECK(y.is_cuda(), "mask_softmax: expected a GPU (HIP) tensor");
+    c10::DeviceGuard guard(y.device());
+    int64_t B, G, S;
+    softmax_dims(y, K, B, G, S);
+    Tensor yc = y.contiguous(), gc = grad.contiguous();
+    TORCH_CHECK(gc.sizes() == yc.sizes() && gc.scalar_type() == yc.scalar_type(),
+                "mask_softmax backward: grad must match the output");
+    Tensor gx = at::empty_like(yc);
+    check_status(tvdcn_mask_softmax_backward(dtype_code(yc.scalar_type()), B, G, K, S, yc.data_ptr(), gc.data_ptr(),
+                                             gx.data_ptr(), current_stream(gx)),
+                 "mask_softmax backward");
+    return gx;
+}
+
+Tensor mask_softmax_meta(const Tensor &x, int64_t K) {
+    int64_t B, G, S;
+    softmax_dims(x, K, B, G, S);
+    return at::empty_like(x, at::MemoryFormat::Contiguous);
+}
+
+Tensor mask_softmax_backward_meta(const Tensor &grad, const Tensor &y, int64_t K) {
+    int64_t B, G, S;
+    softmax_dims(y, K, B, G, S);
+    (void)grad;
+    return at::empty_like(y, at::MemoryFormat::Contiguous);
+}
+
+class MaskSoftmaxFunction : public torch::autograd::Function<MaskSoftmaxFunction> {
+   public:
+    static Tensor forward(torch::autograd::AutogradContext *ctx, const Tensor &x, int64_t K) {
+        at::AutoDispatchBelowADInplaceOrView guard;
+        static auto op = c10::Dispatcher::singleton()
+                             .findSchemaOrThrow("tvdcn_amd::mask_softmax", "")
+                             .typed<Tensor(const Tensor &, int64_t)>();
+        Tensor y = op.call(x, K);
+        ctx->save_for_backward({y});
+        ctx->saved_data["K"] = K;
+        return y;
+    }
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext *ctx,
+                                                   const torch::autograd::variable_list &g) {
+        static auto op = c10::Dispatcher::singleton()
+                             .findSchemaOrThrow("tvdcn_amd::_mask_softmax_backward", "")
+                             .typed<Tensor(const Tensor &, const Tensor &, int64_t)>();
+        auto saved = ctx->get_saved_variables();
+        return {op.call(g[0], saved[0], ctx->saved_data["K"].toInt()), Tensor()};
+    }
+};
+
+Tensor mask_softmax_autograd(const Tensor &x, int64_t K) { return MaskSoftmaxFunction::apply(x, K); }
+
+int64_t hip_version() { return tvdcn_hip_version(); }
+std::string arch_flags() { return tvdcn_arch_flags(); }
+
+}  // namespace
+}  // namespace tvdcn_amd
+
+// ---------------------------------------------------------------------------
+// registration
+// ---------------------------------------------------------------------------
+#define TVDCN_CONV_SCHEMA(D)                                                                                   \
+    "deform_conv" #D "d(Tensor input, Tensor weight, Tensor? offset=None, Tensor? mask=None, Tensor? bias=None, " \
+    "SymInt[" #D "] stride=1, SymInt[" #D "] padding=0, SymInt[" #D "] dilation=1, SymInt groups=1) -> Tensor"
+#define TVDCN_CONV_BWD_SCHEMA(D)                                                                                 \
+    "_deform_conv" #D "d_backward(Tensor grad, Tensor input, Tensor weight, Tensor? offset=None, "               \
+    "Tensor? mask=None, Tensor? bias=None, SymInt[" #D "] stride=1, SymInt[" #D "] padding=0, SymInt[" #D        \
+    "] dilation=1, SymInt groups=1) -> (Tensor, Tensor, Tensor, Tensor, Tensor)"
+#define TVDCN_TR_SCHEMA(D)                                                                                     \
+    "deform_conv_transpose" #D "d(Tensor input, Tensor weight, Tensor? offset=None, Tensor? mask=None, "        \
+    "Tensor? bias=None, SymInt[" #D "] stride=1, SymInt[" #D "] padding=0, SymInt[" #D "] output_padding=0, "   \
+    "SymInt[" #D "] dilation=1, SymInt groups=1) -> Tensor"
+#define TVDCN_TR_BWD_SCHEMA(D)                                                                                 \
+    "_deform_conv_transpose" #D "d_backward(Tensor grad, Tensor input, Tensor weight, Tensor? offset=None, "    \
+    "Tensor? mask=None, Tensor? bias=None, SymInt[" #D "] stride=1, SymInt[" #D "] padding=0, SymInt[" #D      \
+    "] output_padding=0, SymInt[" #D "] dilation=1, SymInt groups=1) -> (Tensor, Tensor, Tensor, Tensor, Tensor)"
+
+TORCH_LIBRARY(tvdcn_amd, m) {
+    m.def(TVDCN_CONV_SCHEMA(1));
+    m.def(TVDCN_CONV_BWD_SCHEMA(1));
+    m.def(TVDCN_CONV_SCHEMA(2));
+    m.def(TVDCN_CONV_BWD_SCHEMA(2));
+    m.def(TVDCN_CONV_SCHEMA(3));
+    m.def(TVDCN_CONV_BWD_SCHEMA(3));
+    m.def(TVDCN_TR_SCHEMA(1));
+    m.def(TVDCN_TR_BWD_SCHEMA(1));
+    m.def(TVDCN_TR_SCHEMA(2));
+    m.def(TVDCN_TR_BWD_SCHEMA(2));
+    m.def(TVDCN_TR_SCHEMA(3));
+    m.def(TVDCN_TR_BWD_SCHEMA(3));
+    m.def("mask_softmax(Tensor mask, int kernel_numel) -> Tensor");
+    m.def("_mask_softmax_backward(Tensor grad, Tensor output, int kernel_numel) -> Tensor");
+    m.def("_cuda_version", &tvdcn_amd::hip_version);
+    m.def("_cuda_arch_flags", &tvdcn_amd::arch_flags);
+}
+
+namespace tvdcn_amd {
+using Conv1 = Kernels<1, false>;
+using Conv2 = Kernels<2, false>;
+using Conv3 = Kernels<3, false>;
+using Tr1 = Kernels<1, true>;
+using Tr2 = Kernels<2, true>;
+using Tr3 = Kernels<3, true>;
+}  // namespace tvdcn_amd
+
+#define TVDCN_IMPL_CONV(D, KEYFN_F, KEYFN_B)                                                  \
+    m.impl("deform_conv" #D "d", TORCH_FN(tvdcn_amd::Conv##D::KEYFN_F##_c));                  \
+    m.impl("_deform_conv" #D "d_backward", TORCH_FN(tvdcn_amd::Conv##D::KEYFN_B##_c));        \
+    m.impl("deform_conv_transpose" #D "d", TORCH_FN(tvdcn_amd::Tr##D::KEYFN_F##_t));          \
+    m.impl("_deform_conv_transpose" #D "d_backward", TORCH_FN(tvdcn_amd::Tr##D::KEYFN_B##_t));
+
+TORCH_LIBRARY_IMPL(tvdcn_amd, CUDA, m) {
+    TVDCN_IMPL_CONV(1, fwd_hip, bwd_hip)
+    TVDCN_IMPL_CONV(2, fwd_hip, bwd_hip)
+    TVDCN_IMPL_CONV(3, fwd_hip, bwd_hip)
+    m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_hip));
+    m.impl("_mask_softmax_backward", TORCH_FN(tvdcn_amd::mask_softmax_backward_hip));
+}
+
+TORCH_LIBRARY_IMPL(tvdcn_amd, Meta, m) {
+    TVDCN_IMPL_CONV(1, fwd_meta, bwd_meta)
+    TVDCN_IMPL_CONV(2, fwd_meta, bwd_meta)
+    TVDCN_IMPL_CONV(3, fwd_meta, bwd_meta)
+    m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_meta));
+    m.impl("_mask_softmax_backward", TORCH_FN(tvdcn_amd::mask_softmax_backward_meta));
+}
+
+TORCH_LIBRARY_IMPL(tvdcn_amd, Autograd, m) {
+    TVDCN_IMPL_CONV(1, fwd_ag, bwd_ag)
+    TVDCN_IMPL_CONV(2, fwd_ag, bwd_ag)
+    TVDCN_IMPL_CONV(3, fwd_ag, bwd_ag)
+    m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_autograd));
+}
+
+TORCH_LIBRARY_IMPL(tvdcn_amd, Autocast, m) {
+    m.impl("deform_conv1d", TORCH_FN(tvdcn_amd::Conv1::fwd_ac_c));
+    m.impl("deform_conv2d", TORCH_FN(tvdcn_amd::Conv2::fwd_ac_c));
+    m.impl("deform_conv3d", TORCH_FN(tvdcn_amd::Conv3::fwd_ac_c));
+    m.impl("deform_conv_transpose1d", TORCH_FN(tvdcn_amd::Tr1::fwd_ac_t));
+    m.impl("deform_conv_transpose2d", TORCH_FN(tvdcn_amd::Tr2::fwd_ac_t));
+    m.impl("deform_conv_transpose3d", TORCH_FN(tvdcn_amd::Tr3::fwd_ac_t));
+}

@@ -1,0 +1,63 @@
+"""Loader for the native operator library and the capability queries.
+
+Mirrors tvdcn/extension.py (``has_ops``, ``with_cuda``, ``cuda_version``,
+``cuda_arch_list``, ``_assert_has_ops``; tvdcn/extension.py:61-188). The library
+is ``tvdcn_amd/_C.so``, built in-tree by ``tvdcn_amd/_build.py``; it registers the
+``torch.ops.tvdcn_amd`` operators and links ``libtvdcn_hip.so`` (the gfx950 HIP
+kernels behind the C ABI in ``include/tvdcn_hip.h``). There is no fallback: if
+the library is missing every op raises.
+"""
+import os
+from typing import List
+
+import torch
+
+_LIB_DIR = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_LIB_DIR, "_C.so")
+HIP_LIB_PATH = os.path.join(_LIB_DIR, "libtvdcn_hip.so")
+
+_HAS_OPS = False
+_LOAD_ERROR = None
+
+try:
+    if os.path.exists(_LIB_PATH):
+        torch.ops.load_library(_LIB_PATH)
+        _HAS_OPS = True
+    else:
+        _LOAD_ERROR = f"{_LIB_PATH} does not exist"
+except (ImportError, OSError, RuntimeError) as e:  # pragma: no cover - reported by _assert_has_ops
+    _LOAD_ERROR = str(e)
+
+
+def _assert_has_ops():
+    if not _HAS_OPS:
+        raise RuntimeError(
+            "Couldn't load the tvdcn_amd native ops (" + str(_LOAD_ERROR) + "). Build them with:\n"
+            "\tpython -m tvdcn_amd._build")
+
+
+def has_ops() -> bool:
+    """True when the native operator library is loaded."""
+    return _HAS_OPS
+
+
+def cuda_version() -> int:
+    """HIP runtime version the kernels were built against (HIP_VERSION), -1 without ops.
+
+    Named after the reference's ``cuda_version`` (on ROCm, torch's "cuda" device is HIP).
+    """
+    if not _HAS_OPS:
+        return -1
+    return torch.ops.tvdcn_amd._cuda_version()
+
+
+def with_cuda() -> bool:
+    """True when the library carries GPU kernels (always, once loaded)."""
+    return cuda_version() != -1
+
+
+def cuda_arch_list() -> List[str]:
+    """Offload targets the kernels were compiled for (``['gfx950']``)."""
+    if not _HAS_OPS:
+        return []
+    return torch.ops.tvdcn_amd._cuda_arch_flags().split()
