@@ -1,0 +1,236 @@
+#!/usr/bin/env python3
+"""Benchmark of the deformable-convolution hot path on one MI355X.
+
+Default workload (the north-star metric): deform_conv2d
+DCNv2 backbone layer, fp32, input (8,256,64,64), weight (256,256,3,3), stride 1,
+pad 1, dilation 1, one offset/mask group, offset N(0, 2^2) px, mask sigmoid(N(0,1)),
+forward + backward with upstream gradient N(0,1). One "step" = forward + backward
+through autograd on inputs already resident in HBM.
+
+Printed JSON line (rank 0): the driver contract plus
+  roofline      -- the kernel family with the most time in the timed region: its
+                   algorithmic flops per launch / its average launch duration, the
+                   duration measured with HIP events recorded on the launch stream
+                   (tvdcn_kernel_timer_* in the C ABI), against MI355X peak;
+  cpu_baseline  -- the reference's own CPU path (oracle/_ref, compiled from the
+                   reference sources) timed on this host on a bounded sample;
+  kernels       -- every kernel family's average launch time and roofline fraction.
+"""
+import argparse
+import ctypes
+import hashlib
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "deform_conv2d fwd+bwd ms and % HBM/MFMA roofline, B8 C256 64x64 k3 fp32"
+PEAK_FP32_MFMA = 157.3e12      # MI355X dense fp32 matrix, FLOP/s
+PEAK_HBM = 8.0e12              # MI355X HBM3E, B/s
+FAMILIES = ["layout", "gather_gemm", "data_grad", "weight_grad", "bias_grad", "mask_softmax"]
+
+
+def make_inputs(batch=8, seed=1002):
+    """cfg2 tensors in the order input, weight, offset, mask-logits, bias, grad_out (CPU, fp32)."""
+    g = torch.Generator().manual_seed(seed)
+    C, H, W, K = 256, 64, 64, 3
+    x = torch.randn(batch, C, H, W, generator=g)
+    w = torch.randn(C, C, K, K, generator=g) * (2.0 / (C * K * K)) ** 0.5   # Kaiming normal, fan_in 2304
+    off = torch.randn(batch, 2 * K * K, H, W, generator=g) * 2.0
+    mask = torch.sigmoid(torch.randn(batch, K * K, H, W, generator=g))
+    bias = torch.zeros(C)
+    gout = torch.randn(batch, C, H, W, generator=g)
+    return dict(input=x, weight=w, offset=off, mask=mask, bias=bias, grad_out=gout)
+
+
+def sha(t):
+    return hashlib.sha256(t.contiguous().numpy().tobytes()).hexdigest()[:16]
+
+
+def flops_fwd(batch=8):
+    return 2.0 * batch * 256 * 256 * 9 * 64 * 64
+
+
+def gpu_bench(inp, steps, warmup):
+    import tvdcn_amd
+    lib = ctypes.CDLL(tvdcn_amd.extension.HIP_LIB_PATH)
+    lib.tvdcn_kernel_timer_enable.argtypes = [ctypes.c_int32]
+    lib.tvdcn_kernel_timer_read.argtypes = [ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(ctypes.c_int64)]
+    dev = torch.device("cuda:0")
+    params = [inp[k].to(dev).requires_grad_(True) for k in ("input", "weight", "offset", "mask", "bias")]
+    gout = inp["grad_out"].to(dev)
+
+    def fwd():
+        return tvdcn_amd.deform_conv2d(*params, stride=1, padding=1, dilation=1, groups=1)
+
+    def step():
+        for p in params:
+            p.grad = None
+        fwd().backward(gout)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # forward only
+    with torch.no_grad():
+        for _ in range(2):
+            fwd()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fwd()
+        torch.cuda.synchronize()
+        fwd_ms = (time.perf_counter() - t0) * 1e3 / steps
+
+    # forward + backward: the metric
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / steps
+
+    # per-kernel durations from HIP events on the launch stream
+    lib.tvdcn_kernel_timer_enable(1)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    kern = {}
+    for i, name in enumerate(FAMILIES):
+        tot, n = ctypes.c_double(0), ctypes.c_int64(0)
+        lib.tvdcn_kernel_timer_read(i, ctypes.byref(tot), ctypes.byref(n))
+        if n.value:
+            kern[name] = dict(total_ms=tot.value, launches=n.value, avg_ms=tot.value / n.value)
+    lib.tvdcn_kernel_timer_enable(0)
+    return fwd_ms, step_ms, kern
+
+
+def kernel_rooflines(kern, batch=8):
+    """Algorithmic work per launch (cfg2) for each family, against the bound that applies."""
+    F = flops_fwd(batch)
+    e = 4
+    n_in = batch * 256 * 64 * 64
+    n_off, n_mask = batch * 18 * 64 * 64, batch * 9 * 64 * 64
+    work = {
+        # each of the three MFMA families performs one cfg2-sized contraction per launch
+        "gather_gemm": ("mfma", F, PEAK_FP32_MFMA, "TFLOP/s"),
+        "data_grad": ("mfma", F, PEAK_FP32_MFMA, "TFLOP/s"),
+        "weight_grad": ("mfma", F, PEAK_FP32_MFMA, "TFLOP/s"),
+        # grad_bias reads grad_out once
+        "bias_grad": ("hbm", e * n_in, PEAK_HBM, "GB/s"),
+    }
+    out = {}
+    for name, k in kern.items():
+        if name in work:
+            bound, amount, peak, unit = work[name]
+            achieved = amount / (k["avg_ms"] * 1e-3)
+            scale = 1e12 if unit == "TFLOP/s" else 1e9
+            out[name] = dict(avg_ms=round(k["avg_ms"], 4), launches=k["launches"], bound=bound,
+                             achieved=round(achieved / scale, 2), peak=round(peak / scale, 1), unit=unit,
+                             frac=round(achieved / peak, 4))
+        else:
+            # layout family: several small launches (channels-last copies, weight re-layouts, zero fills)
+            out[name] = dict(avg_ms=round(k["avg_ms"], 4), launches=k["launches"], total_ms=round(k["total_ms"], 4))
+    return out
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary, or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_cfg2.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(inp, batch):
+    """The reference's CPU implementation (oracle/_ref) on `batch` images of the same tensors."""
+    from oracle import oracle
+    if not oracle.load_reference():
+        return None
+    x, o, m, g = (inp[k][:batch] for k in ("input", "offset", "mask", "grad_out"))
+    w, b = inp["weight"], inp["bias"]
+    ops = torch.ops.tvdcn
+
+    def run():
+        with torch.inference_mode():
+            ops.deform_conv2d(x, w, o, m, b, [1, 1], [1, 1], [1, 1], 1)
+            ops._deform_conv2d_backward(g, x, w, o, m, b, [1, 1], [1, 1], [1, 1], 1)
+
+    t0 = time.perf_counter()
+    run()   # warm-up
+    first = time.perf_counter() - t0
+    reps = 3 if first < 8.0 else 1
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    ms = statistics.median(times) * 1e3 * (8 / batch)
+    cores = len(os.sched_getaffinity(0))
+    return dict(value=round(ms, 1), unit="ms", cores=cores, kind="reference",
+                sample=f"reference CPU path (oracle/_ref: tvdcn 1.1.0 cpu/ kernels + ATen addmm_), forward+backward "
+                       f"of {batch} of the 8 images, median of {reps} after 1 warm-up, scaled x{8 // batch} to the "
+                       f"full batch; torch threads {torch.get_num_threads()}, reference OpenMP loops 32 threads")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-batch", type=int, default=2, help="images of the workload timed on the CPU (divides 8)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
+              f"(the path would shard over the batch, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    inp = make_inputs()
+    hashes = {k: sha(v) for k, v in inp.items()}
+    print(f"[bench] inputs sha256/16: {hashes}", file=sys.stderr, flush=True)
+    fwd_ms, step_ms, kern = gpu_bench(inp, args.steps, args.warmup)
+    print(f"[bench] fwd {fwd_ms:.3f} ms, fwd+bwd {step_ms:.3f} ms", file=sys.stderr, flush=True)
+    roof = kernel_rooflines(kern)
+    mfma = {k: v for k, v in roof.items() if "frac" in v}
+    dom = max(mfma, key=lambda k: kern[k]["total_ms"])
+    d = roof[dom]
+    roofline = dict(kernel=dom, bound=d["bound"], achieved=d["achieved"], peak=d["peak"], unit=d["unit"],
+                    frac=d["frac"], traffic=load_traffic(dom))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(inp, args.cpu_batch)
+        if cpu:
+            print(f"[bench] cpu baseline {cpu['value']} ms ({cpu['cores']} cores)", file=sys.stderr, flush=True)
+
+    total_flops = 3 * flops_fwd()
+    line = {
+        "metric": METRIC, "value": round(step_ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "deform_conv2d DCNv2 layer fwd+bwd (BASELINE configs[1])", "batch": 8,
+                   "channels": 256, "spatial": [64, 64], "kernel": [3, 3], "stride": 1, "padding": 1,
+                   "offset_groups": 1, "mask_groups": 1, "parallelism": "none (1 GPU)"},
+        "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(step_ms - fwd_ms, 4),
+        "fwd_bwd_tflops": round(total_flops / (step_ms * 1e-3) / 1e12, 2),
+        "roofline": roofline, "cpu_baseline": cpu, "kernels": roof,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

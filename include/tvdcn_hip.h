@@ -130,6 +130,26 @@ const char *tvdcn_last_error(void);
 int64_t tvdcn_hip_version(void);
 const char *tvdcn_arch_flags(void);
 
+/*
+ * Optional kernel timing (no counterpart in the reference; used by bench.py).
+ * When enabled, every kernel launch of the entry points above is bracketed by
+ * two HIP events recorded on its launch stream. tvdcn_kernel_timer_read waits
+ * for the recorded events and returns the summed elapsed time and launch count
+ * of one kernel family since the last enable call. Enabling (or disabling)
+ * clears the totals. Off by default; costs two event records per launch when on.
+ */
+enum {
+    TVDCN_KERNEL_LAYOUT = 0,        /* channels-last / weight re-layouts, fills, casts */
+    TVDCN_KERNEL_GATHER_GEMM = 1,   /* fused deformable gather + MFMA contraction */
+    TVDCN_KERNEL_DATA_GRAD = 2,     /* MFMA grad-columns + scatter / offset-mask grads */
+    TVDCN_KERNEL_WEIGHT_GRAD = 3,   /* re-gather + MFMA weight gradient */
+    TVDCN_KERNEL_BIAS_GRAD = 4,
+    TVDCN_KERNEL_MASK_SOFTMAX = 5,
+    TVDCN_KERNEL_FAMILIES = 6
+};
+void tvdcn_kernel_timer_enable(int32_t enable);
+tvdcn_status tvdcn_kernel_timer_read(int32_t family, double *total_ms, int64_t *launches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,7 +14,7 @@
 //
 // Tile: 64 column pixels (rows) x WAVES taps x 64 sampled-side channels; each
 // wave owns one tap and accumulates 4 x 4 MFMA 16x16x4 blocks. Output layout
-// per lane: 4 consecutive pixels x 1 channel per block, so every atomic
+// per lane: 4 pixels x 1 channel per block, so every atomic
 // instruction covers 4 pixels x 16 consecutive channels of the channels-last
 // gradient (4 x 64 B segments). Offset/mask partial sums are reduced across the
 // 16 channel lanes with cross-lane shuffles and across the wave's 4 channel
@@ -151,7 +151,7 @@ bwd_data_kernel(const Geo g, const T *__restrict__ z, const A *__restrict__ wd, 
     for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int n = n0 + pb * 16 + 4 * (lane >> 4) + v;
+            const int n = n0 + pb * 16 + mfma_row<A>(lane, v);
             const bool n_ok = n < g.NP;
             const int b = n_ok ? n / g.Pn : 0;
             const int p = n_ok ? n - b * g.Pn : 0;

@@ -189,7 +189,7 @@ bwd_weight_kernel(const Geo g, const T *__restrict__ z, const A *__restrict__ xc
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int m = mrow0 + mb * 16 + 4 * (lane >> 4) + v;
+                const int m = mrow0 + mb * 16 + mfma_row<A>(lane, v);
                 if (m < g.Mg) atomic_add(gw + (((size_t)grp * g.Mg + m) * g.Cg + cc) * g.Kn + t, acc[mb][cb][v]);
             }
     }

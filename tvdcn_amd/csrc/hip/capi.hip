@@ -6,6 +6,8 @@
 #include <string>
 #include <cstring>
 #include <climits>
+#include <mutex>
+#include <vector>
 
 #include "../../../include/tvdcn_hip.h"
 #include "kernels.h"
@@ -197,6 +199,80 @@ void *at(void *ws, size_t off) { return off == (size_t)-1 ? nullptr : static_cas
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// ---------------------------------------------------------------------------
+// Optional per-kernel timing: HIP events recorded on the launch stream around
+// each kernel family (off by default; see tvdcn_kernel_timer_enable).
+// ---------------------------------------------------------------------------
+struct KernelTimer {
+    std::mutex mu;
+    bool enabled = false;
+    struct Rec {
+        int family;
+        hipEvent_t start, stop;
+    };
+    std::vector<Rec> pending;
+    std::vector<hipEvent_t> pool;
+    double total_ms[TVDCN_KERNEL_FAMILIES] = {};
+    int64_t count[TVDCN_KERNEL_FAMILIES] = {};
+
+    hipEvent_t get_event() {
+        if (!pool.empty()) {
+            hipEvent_t e = pool.back();
+            pool.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+    void drain() {
+        for (auto &r : pending) {
+            float ms = 0.f;
+            if (hipEventSynchronize(r.stop) == hipSuccess && hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess) {
+                total_ms[r.family] += ms;
+                count[r.family] += 1;
+            }
+            pool.push_back(r.start);
+            pool.push_back(r.stop);
+        }
+        pending.clear();
+    }
+};
+
+KernelTimer &timer() {
+    static KernelTimer t;
+    return t;
+}
+
+struct TimedScope {
+    int family;
+    hipStream_t stream;
+    hipEvent_t start = nullptr;
+    TimedScope(int fam, hipStream_t s) : family(fam), stream(s) {
+        KernelTimer &t = timer();
+        std::lock_guard<std::mutex> lk(t.mu);
+        if (!t.enabled) return;
+        start = t.get_event();
+        if (start && hipEventRecord(start, stream) != hipSuccess) start = nullptr;
+    }
+    ~TimedScope() {
+        if (!start) return;
+        KernelTimer &t = timer();
+        std::lock_guard<std::mutex> lk(t.mu);
+        hipEvent_t stop = t.get_event();
+        if (stop && hipEventRecord(stop, stream) == hipSuccess)
+            t.pending.push_back({family, start, stop});
+        else
+            t.pool.push_back(start);
+    }
+};
+
+#define TVDCN_LAUNCH(fam, stream, expr)     \
+    do {                                    \
+        TimedScope ts_((fam), (stream));    \
+        TVDCN_CHECK_HIP(expr);              \
+    } while (0)
+
 }  // namespace
 
 extern "C" {
@@ -243,16 +319,16 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
     g_last_error.clear();
     if (!pl.transposed) {
         void *xcl = at(workspace, L.xcl), *wf = at(workspace, L.wf);
-        TVDCN_CHECK_HIP(launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
-        TVDCN_CHECK_HIP(launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
-        TVDCN_CHECK_HIP(launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, bias, output, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s, launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, bias, output, s));
     } else {
         void *wd = at(workspace, L.wd), *ycl = at(workspace, L.cl_acc);
-        TVDCN_CHECK_HIP(launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
-        TVDCN_CHECK_HIP(launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
-        TVDCN_CHECK_HIP(launch_bwd_data(dt, pl.dim, g, pl.dt, true, false, input, wd, nullptr, offset, mask, ycl,
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, false, input, wd, nullptr, offset, mask, ycl,
                                         nullptr, nullptr, s));
-        TVDCN_CHECK_HIP(launch_from_channels_last(dt, ycl, output, bias, g.B, g.C, g.Sn, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_from_channels_last(dt, ycl, output, bias, g.B, g.C, g.Sn, s));
     }
     return TVDCN_STATUS_SUCCESS;
 }
@@ -286,9 +362,9 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     void *gw = direct ? grad_weight : at(workspace, L.gw_acc);
     void *goff = direct ? grad_offset : at(workspace, L.goff_acc);
     void *gmask = direct ? grad_mask : at(workspace, L.gmask_acc);
-    TVDCN_CHECK_HIP(launch_fill_zero(ab, gw, n_gw, s));
-    if (goff) TVDCN_CHECK_HIP(launch_fill_zero(ab, goff, n_goff, s));
-    if (gmask) TVDCN_CHECK_HIP(launch_fill_zero(ab, gmask, n_gmask, s));
+    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gw, n_gw, s));
+    if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, goff, n_goff, s));
+    if (gmask) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gmask, n_gmask, s));
 
     // Z: the GEMM-side tensor (conv: grad_out; transposed: input)
     // X: the sampled tensor (conv: input; transposed: grad_out)
@@ -296,30 +372,30 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     const void *X = pl.transposed ? grad_out : input;
     if (g.B > 0) {
         void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
-        TVDCN_CHECK_HIP(launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
-        TVDCN_CHECK_HIP(launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
         const bool coord = offset != nullptr || mask != nullptr;
         if (!pl.transposed) {
             void *gx_cl = at(workspace, L.cl_acc);
-            TVDCN_CHECK_HIP(launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
-            TVDCN_CHECK_HIP(launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask, gx_cl, goff,
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask, gx_cl, goff,
                                             gmask, s));
-            TVDCN_CHECK_HIP(launch_from_channels_last(dt, gx_cl, grad_input, nullptr, g.B, g.C, g.Sn, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_from_channels_last(dt, gx_cl, grad_input, nullptr, g.B, g.C, g.Sn, s));
         } else {
             void *wf = at(workspace, L.wf);
-            TVDCN_CHECK_HIP(launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
             TVDCN_CHECK_HIP(
                 launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, nullptr, grad_input, s));
             if (coord)
-                TVDCN_CHECK_HIP(launch_bwd_data(dt, pl.dim, g, pl.dt, false, true, Z, wd, xcl, offset, mask, nullptr,
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, false, true, Z, wd, xcl, offset, mask, nullptr,
                                                 goff, gmask, s));
         }
-        TVDCN_CHECK_HIP(launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask, gw, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask, gw, s));
     }
     if (!direct) {
-        TVDCN_CHECK_HIP(launch_acc_to_storage(dt, gw, grad_weight, n_gw, s));
-        if (goff) TVDCN_CHECK_HIP(launch_acc_to_storage(dt, goff, grad_offset, n_goff, s));
-        if (gmask) TVDCN_CHECK_HIP(launch_acc_to_storage(dt, gmask, grad_mask, n_gmask, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, gw, grad_weight, n_gw, s));
+        if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, goff, grad_offset, n_goff, s));
+        if (gmask) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, gmask, grad_mask, n_gmask, s));
     }
     if (grad_bias) {
         // grad_out is (B, Cout, *out_size): conv Cout = M on the column grid,
@@ -327,7 +403,7 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
         const int Cout = pl.transposed ? g.C : g.M;
         const int So = pl.transposed ? g.Sn : g.Pn;
         // B == 0 reduces over nothing and writes zeros
-        TVDCN_CHECK_HIP(launch_bias_grad(dt, grad_out, grad_bias, g.B, Cout, So, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_BIAS_GRAD, s, launch_bias_grad(dt, grad_out, grad_bias, g.B, Cout, So, s));
     }
     return TVDCN_STATUS_SUCCESS;
 }
@@ -339,8 +415,9 @@ tvdcn_status tvdcn_mask_softmax_forward(int32_t dtype, int64_t batch, int64_t gr
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "invalid mask_softmax sizes");
     if (!fits_int(kernel_numel)) return fail(TVDCN_STATUS_NOT_SUPPORTED, "kernel_numel too large");
     g_last_error.clear();
-    TVDCN_CHECK_HIP(launch_mask_softmax_fwd(dtype, x, y, batch * groups, (int)kernel_numel, spatial_numel,
-                                            static_cast<hipStream_t>(stream)));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    TVDCN_LAUNCH(TVDCN_KERNEL_MASK_SOFTMAX, s,
+                 launch_mask_softmax_fwd(dtype, x, y, batch * groups, (int)kernel_numel, spatial_numel, s));
     return TVDCN_STATUS_SUCCESS;
 }
 
@@ -352,8 +429,9 @@ tvdcn_status tvdcn_mask_softmax_backward(int32_t dtype, int64_t batch, int64_t g
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "invalid mask_softmax sizes");
     if (!fits_int(kernel_numel)) return fail(TVDCN_STATUS_NOT_SUPPORTED, "kernel_numel too large");
     g_last_error.clear();
-    TVDCN_CHECK_HIP(launch_mask_softmax_bwd(dtype, y, grad_y, grad_x, batch * groups, (int)kernel_numel,
-                                            spatial_numel, static_cast<hipStream_t>(stream)));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    TVDCN_LAUNCH(TVDCN_KERNEL_MASK_SOFTMAX, s, launch_mask_softmax_bwd(dtype, y, grad_y, grad_x, batch * groups,
+                                                                      (int)kernel_numel, spatial_numel, s));
     return TVDCN_STATUS_SUCCESS;
 }
 
@@ -362,5 +440,27 @@ const char *tvdcn_last_error(void) { return g_last_error.c_str(); }
 int64_t tvdcn_hip_version(void) { return (int64_t)HIP_VERSION; }
 
 const char *tvdcn_arch_flags(void) { return "gfx950"; }
+
+void tvdcn_kernel_timer_enable(int32_t enable) {
+    KernelTimer &t = timer();
+    std::lock_guard<std::mutex> lk(t.mu);
+    t.drain();
+    t.enabled = enable != 0;
+    for (int i = 0; i < TVDCN_KERNEL_FAMILIES; ++i) {
+        t.total_ms[i] = 0.0;
+        t.count[i] = 0;
+    }
+}
+
+tvdcn_status tvdcn_kernel_timer_read(int32_t family, double *total_ms, int64_t *launches) {
+    if (family < 0 || family >= TVDCN_KERNEL_FAMILIES)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "unknown kernel family");
+    KernelTimer &t = timer();
+    std::lock_guard<std::mutex> lk(t.mu);
+    t.drain();
+    if (total_ms) *total_ms = t.total_ms[family];
+    if (launches) *launches = t.count[family];
+    return TVDCN_STATUS_SUCCESS;
+}
 
 }  // extern "C"

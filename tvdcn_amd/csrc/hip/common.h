@@ -76,11 +76,22 @@ __device__ __forceinline__ void store4(A *p, Vec4<A> v) {
 // ---------------------------------------------------------------------------
 // MFMA 16x16x4 (fp32 and fp64). Operand layout, lane l of 64:
 //   A[i][k]: i = l % 16, k = l / 16      B[k][j]: j = l % 16, k = l / 16
-//   D[i][j]: 4 values per lane, i = 4 * (l / 16) + v, j = l % 16
+//   D[i][j]: 4 values per lane v = 0..3, j = l % 16 and
+//            fp32: i = 4 * (l / 16) + v        fp64: i = l / 16 + 4 * v
+// (both measured on gfx950 with one-hot operands)
 // ---------------------------------------------------------------------------
 template <typename A> struct Acc4;
 template <> struct Acc4<float> { typedef f32x4 type; };
 template <> struct Acc4<double> { typedef f64x4 type; };
+
+// row of the 16x16 output block held by lane `lane` in accumulator slot v
+template <typename A>
+__device__ __forceinline__ int mfma_row(int lane, int v) {
+    if constexpr (sizeof(A) == 8)
+        return (lane >> 4) + 4 * v;
+    else
+        return 4 * (lane >> 4) + v;
+}
 
 __device__ __forceinline__ f32x4 mfma16x16x4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);

@@ -210,7 +210,7 @@ fwd_gather_gemm_kernel(const Geo g, const A *__restrict__ xcl, const A *__restri
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int m = mrow0 + mb * 16 + 4 * (lane >> 4) + v;
+                const int m = mrow0 + mb * 16 + mfma_row<A>(lane, v);
                 if (m < g.Mg) {
                     const int mg_glob = grp * g.Mg + m;
                     A r = acc[mb][nb][v];
