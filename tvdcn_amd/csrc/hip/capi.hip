@@ -136,6 +136,11 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     g.Pn = (int)Pn;
     g.Kn = (int)Kn;
     g.NP = (int)(B * Pn);
+    g.dPn = make_fastdiv((uint32_t)g.Pn);
+    g.dP2 = make_fastdiv((uint32_t)g.P[2]);
+    g.dP12 = make_fastdiv((uint32_t)(g.P[1] * g.P[2]));
+    g.dK2 = make_fastdiv((uint32_t)g.K[2]);
+    g.dK12 = make_fastdiv((uint32_t)(g.K[1] * g.K[2]));
     pl.ft = plan_fwd(g, pl.dtype);
     pl.dt = plan_data(g, pl.dtype);
     pl.wt = plan_weight(g, pl.dtype);
@@ -144,7 +149,7 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
 
 // Workspace sub-buffers (byte offsets into the caller's workspace).
 struct Layout {
-    size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, gw_acc = 0, goff_acc = 0, gmask_acc = 0;
+    size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, wpart = 0, goff_acc = 0, gmask_acc = 0;
     size_t total = 0;
 };
 
@@ -162,7 +167,7 @@ Layout layout(const Plan &pl, bool backward) {
         return o;
     };
     const size_t SENTINEL = (size_t)-1;
-    L.xcl = L.wf = L.wd = L.cl_acc = L.gw_acc = L.goff_acc = L.gmask_acc = SENTINEL;
+    L.xcl = L.wf = L.wd = L.cl_acc = L.wpart = L.goff_acc = L.gmask_acc = SENTINEL;
     if (!backward) {
         if (!pl.transposed) {
             L.xcl = take(cl_bytes);
@@ -178,8 +183,8 @@ Layout layout(const Plan &pl, bool backward) {
             L.wf = take(wf_bytes);
         else
             L.cl_acc = take(cl_bytes);
+        L.wpart = take(align_up(pl.wt.part_elems * a));
         if (!acc_is_storage(pl.dtype)) {
-            L.gw_acc = take(align_up((size_t)g.M * g.Cg * g.Kn * a));
             if (g.og) L.goff_acc = take(align_up((size_t)g.B * g.og * g.Kn * pl.dim * g.Pn * a));
             if (g.mg) L.gmask_acc = take(align_up((size_t)g.B * g.mg * g.Kn * g.Pn * a));
         }
@@ -356,13 +361,10 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     const bool direct = acc_is_storage(dt);
     g_last_error.clear();
 
-    const size_t n_gw = (size_t)g.M * g.Cg * g.Kn;
     const size_t n_goff = g.og ? (size_t)g.B * g.og * g.Kn * pl.dim * g.Pn : 0;
     const size_t n_gmask = g.mg ? (size_t)g.B * g.mg * g.Kn * g.Pn : 0;
-    void *gw = direct ? grad_weight : at(workspace, L.gw_acc);
     void *goff = direct ? grad_offset : at(workspace, L.goff_acc);
     void *gmask = direct ? grad_mask : at(workspace, L.gmask_acc);
-    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gw, n_gw, s));
     if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, goff, n_goff, s));
     if (gmask) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gmask, n_gmask, s));
 
@@ -370,6 +372,9 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     // X: the sampled tensor (conv: input; transposed: grad_out)
     const void *Z = pl.transposed ? input : grad_out;
     const void *X = pl.transposed ? grad_out : input;
+    if (g.B == 0)   // empty batch: the reference returns zeros
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                     launch_fill_zero((int)elem_size(dt), grad_weight, (size_t)g.M * g.Cg * g.Kn, s));
     if (g.B > 0) {
         void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
@@ -390,10 +395,10 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, false, true, Z, wd, xcl, offset, mask, nullptr,
                                                 goff, gmask, s));
         }
-        TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask, gw, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,
+                                                                    at(workspace, L.wpart), grad_weight, s));
     }
     if (!direct) {
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, gw, grad_weight, n_gw, s));
         if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, goff, grad_offset, n_goff, s));
         if (gmask) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, gmask, grad_mask, n_gmask, s));
     }

@@ -14,11 +14,32 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
 #include <stdint.h>
+#include <type_traits>
 
 namespace tvdcn_hip {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// Division by a run-time-invariant positive divisor with one multiply-high, an add
+// and a shift (Granlund & Montgomery, "Division by Invariant Integers using
+// Multiplication", PLDI 1994): s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1,
+// q = (mulhi(n, m) + n) >> s, exact for 0 <= n < 2^31 (the sum cannot overflow).
+struct FastDiv {
+    uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t s = 0;
+    while ((uint64_t(1) << s) < d) ++s;
+    const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1;
+    return FastDiv{d, (uint32_t)m, s};
+}
+
+__device__ __forceinline__ int fdiv(const FastDiv &f, int n) {
+    const uint32_t t = __umulhi((uint32_t)n, f.m);
+    return (int)((t + (uint32_t)n) >> f.s);
+}
 
 // Problem geometry, passed by value to every kernel. Spatial shapes are embedded
 // in rank 3 (unused leading axes have extent 1, stride 1, padding 0).
@@ -32,6 +53,7 @@ struct Geo {
     int K[3], st[3], pad[3], dil[3];
     int Sn, Pn, Kn;
     int NP;                // B * Pn
+    FastDiv dPn, dP2, dP12, dK2, dK12;   // divisors Pn, P[2], P[1]*P[2], K[2], K[1]*K[2]
 };
 
 // ---------------------------------------------------------------------------
@@ -70,6 +92,20 @@ __device__ __forceinline__ void store4(A *p, Vec4<A> v) {
     } else {
         *reinterpret_cast<double2 *>(p) = make_double2(v.x, v.y);
         *reinterpret_cast<double2 *>(p + 2) = make_double2(v.z, v.w);
+    }
+}
+
+// four consecutive storage-typed values converted to the accumulator type, with
+// one vector load (16 B fp32, 2 x 16 B fp64, 8 B fp16/bf16); p must be aligned
+// to 4 elements
+template <typename A, typename T>
+__device__ __forceinline__ Vec4<A> load4_t(const T *p) {
+    if constexpr (sizeof(T) == sizeof(A)) {
+        return load4<A>(reinterpret_cast<const A *>(p));
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2 *>(p);
+        const T *h = reinterpret_cast<const T *>(&u);
+        return {to_acc<A>(h[0]), to_acc<A>(h[1]), to_acc<A>(h[2]), to_acc<A>(h[3])};
     }
 }
 
@@ -151,12 +187,13 @@ __device__ __forceinline__ void decompose_tap(const Geo &g, int t, int kk[DIM]) 
     if constexpr (DIM == 1) {
         kk[0] = t;
     } else if constexpr (DIM == 2) {
-        kk[1] = t % g.K[2];
-        kk[0] = t / g.K[2];
+        kk[0] = fdiv(g.dK2, t);
+        kk[1] = t - kk[0] * g.K[2];
     } else {
-        kk[2] = t % g.K[2];
-        kk[1] = (t / g.K[2]) % g.K[1];
-        kk[0] = t / (g.K[2] * g.K[1]);
+        kk[0] = fdiv(g.dK12, t);
+        const int r = t - kk[0] * g.K[1] * g.K[2];
+        kk[1] = fdiv(g.dK2, r);
+        kk[2] = r - kk[1] * g.K[2];
     }
 }
 
@@ -165,12 +202,13 @@ __device__ __forceinline__ void decompose_pix(const Geo &g, int p, int pp[DIM]) 
     if constexpr (DIM == 1) {
         pp[0] = p;
     } else if constexpr (DIM == 2) {
-        pp[1] = p % g.P[2];
-        pp[0] = p / g.P[2];
+        pp[0] = fdiv(g.dP2, p);
+        pp[1] = p - pp[0] * g.P[2];
     } else {
-        pp[2] = p % g.P[2];
-        pp[1] = (p / g.P[2]) % g.P[1];
-        pp[0] = p / (g.P[2] * g.P[1]);
+        pp[0] = fdiv(g.dP12, p);
+        const int r = p - pp[0] * g.P[1] * g.P[2];
+        pp[1] = fdiv(g.dP2, r);
+        pp[2] = r - pp[1] * g.P[2];
     }
 }
 

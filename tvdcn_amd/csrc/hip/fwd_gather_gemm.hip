@@ -65,7 +65,7 @@ fwd_gather_gemm_kernel(const Geo g, const A *__restrict__ xcl, const A *__restri
         const int n = n0 + s_nl[i];
         s_ok[i] = n < g.NP;
         const int nn = s_ok[i] ? n : 0;
-        s_b[i] = nn / g.Pn;
+        s_b[i] = fdiv(g.dPn, nn);
         s_p[i] = nn - s_b[i] * g.Pn;
     }
     // fast-path corner cache (one set per slot)
@@ -204,7 +204,7 @@ fwd_gather_gemm_kernel(const Geo g, const A *__restrict__ xcl, const A *__restri
     for (int nb = 0; nb < 4; ++nb) {
         const int n = n0 + nb * 16 + (lane & 15);
         if (n >= g.NP) continue;
-        const int b = n / g.Pn;
+        const int b = fdiv(g.dPn, n);
         const int p = n - b * g.Pn;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb)

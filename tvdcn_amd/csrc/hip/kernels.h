@@ -20,12 +20,14 @@ struct DataTiles {
     int waves;       // taps per workgroup (one 64-channel x 64-pixel tile per wave)
     int Mg_pad;      // Mg rounded up to 16
     int Cg_pad;      // Cg rounded up to 64
+    bool uniform;    // every 64-channel tile lies in one offset group and one mask group
 };
 struct WeightTiles {
     int waves;       // 64-row GEMM-side blocks per workgroup
     bool vec4;
     int k_chunk;     // column pixels per workgroup (split-K)
     int k_splits;
+    size_t part_elems;   // workspace elements for the split partials
 };
 
 FwdTiles plan_fwd(const Geo &g, int dtype);
@@ -40,7 +42,7 @@ hipError_t launch_weight_fwd_layout(int dtype, const Geo &g, const void *w, void
                                     hipStream_t s);
 hipError_t launch_weight_data_layout(int dtype, const Geo &g, const void *w, void *wd, int Mg_pad, int Cg_pad,
                                      hipStream_t s);
-hipError_t launch_fill_zero(int acc_bytes, void *p, size_t n, hipStream_t s);
+hipError_t launch_fill_zero(int elem_bytes, void *p, size_t n, hipStream_t s);   // elem_bytes 2, 4 or 8
 hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n, hipStream_t s);
 hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s);
 
@@ -51,8 +53,10 @@ hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTil
 hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t, bool scatter, bool coord,
                            const void *z, const void *wd, const void *xcl, const void *offset, const void *mask,
                            void *gx_cl, void *goff, void *gmask, hipStream_t s);
+// writes split partials to `part` (WeightTiles::part_elems accumulator elements),
+// then reduces them into gw (storage type, layout (M, Cg, Kn))
 hipError_t launch_bwd_weight(int dtype, int dim, const Geo &g, const WeightTiles &t, const void *z, const void *xcl,
-                             const void *offset, const void *mask, void *gw, hipStream_t s);
+                             const void *offset, const void *mask, void *part, void *gw, hipStream_t s);
 
 // mask_softmax (mask_softmax.hip)
 hipError_t launch_mask_softmax_fwd(int dtype, const void *x, void *y, int64_t BG, int K, int64_t S, hipStream_t s);

@@ -189,12 +189,17 @@ hipError_t launch_weight_data_layout(int dtype, const Geo &g, const void *w, voi
     });
 }
 
-hipError_t launch_fill_zero(int acc_bytes, void *p, size_t n, hipStream_t s) {
+hipError_t launch_fill_zero(int elem_bytes, void *p, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    if (acc_bytes == 8)
+    if (elem_bytes == 8)
         hipLaunchKernelGGL((fill_zero_kernel<double>), dim3(grid_for(n)), dim3(256), 0, s, static_cast<double *>(p), n);
-    else
+    else if (elem_bytes == 4)
         hipLaunchKernelGGL((fill_zero_kernel<float>), dim3(grid_for(n)), dim3(256), 0, s, static_cast<float *>(p), n);
+    else if (elem_bytes == 2)
+        hipLaunchKernelGGL((fill_zero_kernel<uint16_t>), dim3(grid_for(n)), dim3(256), 0, s, static_cast<uint16_t *>(p),
+                           n);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
