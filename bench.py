@@ -190,7 +190,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-batch", type=int, default=2, help="images of the workload timed on the CPU (divides 8)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB 5 times (reference for the rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE scale) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        src = torch.empty(args.copy_calibration * 2**20 // 4, dtype=torch.float32, device="cuda").uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": args.copy_calibration * 2**20}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               f"(the path would shard over the batch, see DESIGN.md)", file=sys.stderr)

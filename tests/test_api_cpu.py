@@ -1,0 +1,349 @@
+"""CPU tests of the drop-in boundary and the host logic (no GPU compute).
+
+* the C ABI library loads and exports every function declared in include/tvdcn_hip.h;
+  its host-only entry points (output size, workspace queries, argument checks) work;
+* the operator schemas match the reference's (names, argument order, defaults);
+* shape inference and validation run on meta tensors, with the reference's error
+  texts (checked side by side with the reference build when oracle/_ref exists);
+* autograd and double-backward behaviour, on meta tensors;
+* CPU tensors are refused loudly (no CPU fallback);
+* the nn.Module wrappers and mask activations keep the reference's API and errors.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import tvdcn_amd
+from tvdcn_amd import extension
+from oracle import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tvdcn_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tvdcn_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return ctypes.CDLL(extension.HIP_LIB_PATH)
+
+
+def test_native_library_loaded():
+    assert tvdcn_amd.has_ops()
+    assert tvdcn_amd.with_cuda()
+    assert tvdcn_amd.cuda_arch_list() == ["gfx950"]
+    assert tvdcn_amd.cuda_version() > 60000000
+
+
+def test_c_abi_exports_every_declared_function(lib):
+    names = declared_functions()
+    assert len(names) >= 11
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+class Desc(ctypes.Structure):
+    _fields_ = [("dim", ctypes.c_int32), ("transposed", ctypes.c_int32), ("dtype", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("batch", ctypes.c_int64), ("in_channels", ctypes.c_int64),
+                ("out_channels", ctypes.c_int64), ("groups", ctypes.c_int64), ("offset_groups", ctypes.c_int64),
+                ("mask_groups", ctypes.c_int64), ("in_size", ctypes.c_int64 * 3), ("kernel", ctypes.c_int64 * 3),
+                ("stride", ctypes.c_int64 * 3), ("padding", ctypes.c_int64 * 3), ("dilation", ctypes.c_int64 * 3),
+                ("output_padding", ctypes.c_int64 * 3)]
+
+
+def cfg2_desc(**over):
+    d = Desc(dim=2, transposed=0, dtype=0, batch=8, in_channels=256, out_channels=256, groups=1, offset_groups=1,
+             mask_groups=1)
+    for i in range(3):
+        d.in_size[i], d.kernel[i], d.stride[i], d.padding[i], d.dilation[i], d.output_padding[i] = 64, 3, 1, 1, 1, 0
+    for k, v in over.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_c_abi_host_queries(lib):
+    lib.tvdcn_conv_output_size.restype = ctypes.c_int
+    lib.tvdcn_deform_conv_forward_workspace_size.restype = ctypes.c_size_t
+    lib.tvdcn_deform_conv_backward_workspace_size.restype = ctypes.c_size_t
+    lib.tvdcn_last_error.restype = ctypes.c_char_p
+    d = cfg2_desc()
+    out = (ctypes.c_int64 * 3)()
+    assert lib.tvdcn_conv_output_size(ctypes.byref(d), out) == 0
+    assert list(out)[:2] == [64, 64]
+    fw = lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(d))
+    bw = lib.tvdcn_deform_conv_backward_workspace_size(ctypes.byref(d))
+    # forward: channels-last copy of the input (33.5 MB) + the re-laid-out weight
+    assert 8 * 256 * 64 * 64 * 4 <= fw < 8 * 256 * 64 * 64 * 4 + 4 * 2**20
+    assert bw > fw
+    # transposed output size (cfg5): 32 -> 64 with k4 s2 p1
+    t = cfg2_desc(transposed=1, in_channels=256, out_channels=128, offset_groups=2, mask_groups=2)
+    for i in range(2):
+        t.in_size[i], t.kernel[i], t.stride[i] = 32, 4, 2
+    assert lib.tvdcn_conv_output_size(ctypes.byref(t), out) == 0
+    assert list(out)[:2] == [64, 64]
+
+
+def test_c_abi_argument_errors(lib):
+    lib.tvdcn_conv_output_size.restype = ctypes.c_int
+    lib.tvdcn_deform_conv_forward.restype = ctypes.c_int
+    lib.tvdcn_last_error.restype = ctypes.c_char_p
+    out = (ctypes.c_int64 * 3)()
+    bad = cfg2_desc()
+    bad.stride[0] = 0
+    assert lib.tvdcn_conv_output_size(ctypes.byref(bad), out) == 1
+    assert b"stride" in lib.tvdcn_last_error()
+    small = cfg2_desc()
+    small.in_size[0] = 1
+    small.padding[0] = 0
+    assert lib.tvdcn_conv_output_size(ctypes.byref(small), out) == 1
+    assert b"too small" in lib.tvdcn_last_error()
+    # argument checks fail before any device work: workspace too small, mismatched offset pointer
+    d = cfg2_desc()
+    st = lib.tvdcn_deform_conv_forward(ctypes.byref(d), None, None, None, None, None, None, None,
+                                       ctypes.c_size_t(0), None)
+    assert st == 1 and b"offset" in lib.tvdcn_last_error()
+    d = cfg2_desc(offset_groups=0, mask_groups=0)
+    st = lib.tvdcn_deform_conv_forward(ctypes.byref(d), None, None, None, None, None, None, None,
+                                       ctypes.c_size_t(16), None)
+    assert st == 2
+    d = cfg2_desc(offset_groups=3)
+    assert lib.tvdcn_conv_output_size(ctypes.byref(d), out) == 0
+    st = lib.tvdcn_deform_conv_forward(ctypes.byref(d), None, None, ctypes.c_void_p(16), ctypes.c_void_p(16), None,
+                                       None, None, ctypes.c_size_t(0), None)
+    assert st == 1 and b"offset_groups" in lib.tvdcn_last_error()
+
+
+REF_SCHEMAS = {
+    "deform_conv1d": "(Tensor input, Tensor weight, Tensor? offset=None, Tensor? mask=None, Tensor? bias=None, "
+                     "SymInt[1] stride=[1], SymInt[1] padding=[0], SymInt[1] dilation=[1], SymInt groups=1) -> Tensor",
+    "deform_conv2d": "(Tensor input, Tensor weight, Tensor? offset=None, Tensor? mask=None, Tensor? bias=None, "
+                     "SymInt[2] stride=[1, 1], SymInt[2] padding=[0, 0], SymInt[2] dilation=[1, 1], "
+                     "SymInt groups=1) -> Tensor",
+    "deform_conv_transpose2d": "(Tensor input, Tensor weight, Tensor? offset=None, Tensor? mask=None, "
+                               "Tensor? bias=None, SymInt[2] stride=[1, 1], SymInt[2] padding=[0, 0], "
+                               "SymInt[2] output_padding=[0, 0], SymInt[2] dilation=[1, 1], SymInt groups=1) -> Tensor",
+}
+
+
+@pytest.mark.parametrize("name", sorted(REF_SCHEMAS))
+def test_schemas_match_reference(name):
+    schema = str(getattr(torch.ops.tvdcn_amd, name).default._schema)
+    assert schema == f"tvdcn_amd::{name}{REF_SCHEMAS[name]}"
+
+
+def test_all_twelve_ops_and_backward_schemas_exist():
+    for dim in (1, 2, 3):
+        for base in (f"deform_conv{dim}d", f"deform_conv_transpose{dim}d"):
+            fwd = str(getattr(torch.ops.tvdcn_amd, base).default._schema)
+            bwd = str(getattr(torch.ops.tvdcn_amd, f"_{base}_backward").default._schema)
+            assert "-> Tensor" in fwd
+            assert bwd.endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
+            if oracle.load_reference():
+                ref_f = str(getattr(torch.ops.tvdcn, base).default._schema).split("::", 1)[1]
+                ref_b = str(getattr(torch.ops.tvdcn, f"_{base}_backward").default._schema).split("::", 1)[1]
+                assert fwd.split("::", 1)[1] == ref_f
+                assert bwd.split("::", 1)[1] == ref_b
+
+
+def meta(*shape):
+    return torch.empty(*shape, device="meta")
+
+
+@pytest.mark.parametrize("dim", [1, 2, 3])
+def test_meta_shapes(dim):
+    sz = [9, 10, 11][:dim]
+    k = [3, 2, 3][:dim]
+    kn = 1
+    for kk in k:
+        kn *= kk
+    out = [s - kk + 1 for s, kk in zip(sz, k)]
+    y = getattr(tvdcn_amd, f"deform_conv{dim}d")(meta(2, 4, *sz), meta(6, 2, *k), meta(2, 2 * dim * kn, *out),
+                                                 meta(2, 3 * kn, *out)[:, :kn], meta(6), groups=2)
+    assert list(y.shape) == [2, 6] + out
+    yt = getattr(tvdcn_amd, f"deform_conv_transpose{dim}d")(meta(2, 4, *sz), meta(4, 3, *k), meta(2, dim * kn, *sz),
+                                                            None, meta(6), stride=2, padding=1, output_padding=1,
+                                                            groups=2)
+    assert list(yt.shape) == [2, 6] + [(s - 1) * 2 - 2 + kk + 1 for s, kk in zip(sz, k)]
+    # unbatched
+    y1 = getattr(tvdcn_amd, f"deform_conv{dim}d")(meta(4, *sz), meta(6, 4, *k), meta(dim * kn, *out))
+    assert list(y1.shape) == [6] + out
+
+
+def reference_error(fn_name, *args):
+    """message raised by the reference build for the same (CPU) arguments, or None"""
+    if not oracle.load_reference():
+        return None
+    cpu = [torch.zeros(a.shape) if isinstance(a, torch.Tensor) else a for a in args]
+    try:
+        with torch.inference_mode():
+            getattr(torch.ops.tvdcn, fn_name)(*cpu)
+    except RuntimeError as e:
+        return str(e)
+    return ""
+
+
+INVALID = [
+    ("offset channels", (meta(2, 4, 8, 8), meta(5, 4, 3, 3), meta(2, 17, 6, 6), None, None),
+     "The shape of the offset tensor at dimension 1 is not valid"),
+    ("offset multiple", (meta(2, 4, 8, 8), meta(5, 4, 3, 3), meta(2, 36 + 18, 6, 6), None, None),
+     "% offset_groups == 0"),
+    ("offset batch", (meta(2, 4, 8, 8), meta(5, 4, 3, 3), meta(3, 18, 6, 6), None, None),
+     "invalid batch size of offset"),
+    ("offset grid", (meta(2, 4, 8, 8), meta(5, 4, 3, 3), meta(2, 18, 5, 6), None, None), "offset output dims"),
+    ("mask channels", (meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, meta(2, 8, 6, 6), None),
+     "The shape of the mask tensor at dimension 1 is not valid"),
+    ("mask batch", (meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, meta(1, 9, 6, 6), None), "invalid batch size of mask"),
+    ("mask grid", (meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, meta(2, 9, 6, 7), None), "mask output dims"),
+    ("input ndim", (meta(2, 4, 8, 8, 1), meta(5, 4, 3, 3), None, None, None), "Expected 3D (unbatched) or 4D"),
+    ("weight ndim", (meta(2, 4, 8, 8), meta(5, 4, 3), None, None, None), "Expected 4D weight"),
+    ("too small", (meta(2, 4, 2, 2), meta(5, 4, 3, 3), None, None, None), "Calculated output size too small"),
+]
+
+
+@pytest.mark.parametrize("label,args,msg", INVALID, ids=[c[0] for c in INVALID])
+def test_validation_errors_match_reference(label, args, msg):
+    with pytest.raises(RuntimeError) as ei:
+        torch.ops.tvdcn_amd.deform_conv2d(*args, [1, 1], [0, 0], [1, 1], 1)
+    assert msg in str(ei.value)
+    ref = reference_error("deform_conv2d", *args, [1, 1], [0, 0], [1, 1], 1)
+    if ref is not None:
+        assert msg in ref, ref
+
+
+@pytest.mark.parametrize("what", ["stride", "pad", "dilation"])
+def test_parameter_errors(what):
+    s, p, d = [1, 1], [0, 0], [1, 1]
+    {"stride": s, "pad": p, "dilation": d}[what][0] = -1 if what == "pad" else 0
+    with pytest.raises(RuntimeError, match=what + "_h"):
+        torch.ops.tvdcn_amd.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, None, None, s, p, d, 1)
+
+
+def test_groups_error():
+    with pytest.raises(RuntimeError, match="groups"):
+        torch.ops.tvdcn_amd.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, None, None, [1, 1], [0, 0],
+                                          [1, 1], 2)
+
+
+def test_dtype_mismatch_error():
+    with pytest.raises(RuntimeError):
+        torch.ops.tvdcn_amd.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3).double(), None, None, None, [1, 1],
+                                          [0, 0], [1, 1], 1)
+
+
+def test_cpu_tensors_are_refused():
+    with pytest.raises(NotImplementedError, match="CPU"):
+        tvdcn_amd.deform_conv2d(torch.rand(1, 2, 5, 5), torch.rand(2, 2, 3, 3), torch.rand(1, 18, 3, 3))
+    with pytest.raises(NotImplementedError, match="CPU"):
+        tvdcn_amd.mask_softmax2d(torch.rand(1, 9, 3, 3), (3, 3))
+
+
+def test_meta_autograd_and_double_backward():
+    x = meta(2, 4, 8, 8).requires_grad_(True)
+    w = meta(5, 4, 3, 3).requires_grad_(True)
+    o = meta(2, 18, 6, 6).requires_grad_(True)
+    m = meta(2, 9, 6, 6).requires_grad_(True)
+    b = meta(5).requires_grad_(True)
+    y = tvdcn_amd.deform_conv2d(x, w, o, m, b)
+    gx, gw, go, gm, gb = torch.autograd.grad(y.sum(), (x, w, o, m, b), create_graph=True)
+    assert gx.shape == x.shape and gw.shape == w.shape and go.shape == o.shape and gm.shape == m.shape
+    assert gb.shape == b.shape
+    with pytest.raises(RuntimeError, match="double backwards on deform_conv2d not supported"):
+        gx.sum().backward()
+
+
+def test_meta_autograd_without_offset_mask_bias():
+    x = meta(2, 4, 8, 8).requires_grad_(True)
+    w = meta(5, 4, 3, 3).requires_grad_(True)
+    y = tvdcn_amd.deform_conv2d(x, w)
+    y.sum().backward()
+    assert x.grad.shape == x.shape and w.grad.shape == w.shape
+    gs = torch.ops.tvdcn_amd._deform_conv2d_backward(meta(2, 5, 6, 6), meta(2, 4, 8, 8), meta(5, 4, 3, 3), None,
+                                                     None, None, [1, 1], [0, 0], [1, 1], 1)
+    assert gs[2] is None and gs[3] is None and gs[4] is None
+
+
+def test_modules_api():
+    m = tvdcn_amd.DeformConv2d(4, 6, 3, padding=1, groups=2, bias=False)
+    assert m.weight.shape == (6, 2, 3, 3) and m.bias is None
+    assert "bias=False" in repr(m) and "groups=2" in repr(m)
+    p = tvdcn_amd.PackedDeformConv2d(4, 8, 3, padding=1, offset_groups=2, mask_groups=4, modulated=True,
+                                     mask_activation="softmax")
+    assert p.offset_generator.weight.shape == (2 * 9 * 2, 2, 3, 3)
+    assert p.mask_generator.weight.shape == (9 * 4, 1, 3, 3)
+    assert float(p.offset_generator.weight.detach().abs().sum()) == 0.0
+    assert isinstance(p.mask_activation, tvdcn_amd.MaskSoftmax2d)
+    t = tvdcn_amd.PackedDeformConvTranspose2d(4, 6, 4, stride=2, padding=1, modulated=True)
+    assert t.offset_generator.kernel_size == (1, 1) and t.mask_generator.out_channels == 16
+    assert isinstance(t.mask_activation, tvdcn_amd.MaskSigmoid) and t.mask_activation.scale == 2.0
+    for cls in (tvdcn_amd.PackedDeformConv1d, tvdcn_amd.PackedDeformConv3d, tvdcn_amd.PackedDeformConvTranspose1d,
+                tvdcn_amd.PackedDeformConvTranspose3d):
+        assert cls(4, 4, 3).deformable
+    with pytest.raises(ValueError, match="in_channels must be divisible by offset_groups"):
+        tvdcn_amd.PackedDeformConv2d(4, 8, 3, offset_groups=3)
+    with pytest.raises(ValueError, match="out_channels must be divisible by mask_groups"):
+        tvdcn_amd.PackedDeformConv2d(4, 6, 3, mask_groups=4)
+    with pytest.raises(ValueError, match="no activation is supported for offset"):
+        tvdcn_amd.PackedDeformConv2d(4, 8, 3, offset_activation="tanh")
+    with pytest.raises(ValueError, match="only"):
+        tvdcn_amd.PackedDeformConv2d(4, 8, 3, mask_activation="relu")
+
+
+def test_module_forward_on_meta():
+    m = tvdcn_amd.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True, device="meta")
+    assert m(meta(2, 4, 8, 8)).shape == (2, 6, 8, 8)
+    r = tvdcn_amd.DeformConv2d(4, 6, 3, padding=1, padding_mode="reflect", device="meta")
+    assert r(meta(2, 4, 8, 8), meta(2, 18, 8, 8)).shape == (2, 6, 8, 8)
+    t = tvdcn_amd.DeformConvTranspose2d(4, 6, 3, stride=2, padding=1, device="meta")
+    assert t(meta(2, 4, 5, 5), None, output_size=[10, 10]).shape == (2, 6, 10, 10)
+    with pytest.raises(ValueError, match="requested an output size"):
+        t(meta(2, 4, 5, 5), None, output_size=[20, 20])
+    bad = tvdcn_amd.DeformConvTranspose2d(4, 6, 3, padding_mode="reflect", device="meta")
+    with pytest.raises(ValueError, match="zeros"):
+        bad(meta(2, 4, 5, 5), None)
+
+
+def test_output_padding_matches_torch_rule():
+    ours = tvdcn_amd.DeformConvTranspose2d(4, 6, 3, stride=3, padding=1, dilation=2)
+    ref = torch.nn.ConvTranspose2d(4, 6, 3, stride=3, padding=1, dilation=2)
+    x = torch.empty(1, 4, 7, 5)
+    for size in ([21, 15], [22, 16], [23, 17]):
+        assert ours._output_padding(x, size, [3, 3], [1, 1], [3, 3], 2, [2, 2]) == \
+            ref._output_padding(x, size, [3, 3], [1, 1], [3, 3], 2, [2, 2])
+
+
+def test_mask_activation_errors():
+    with pytest.raises(ValueError, match="scale must be positive"):
+        tvdcn_amd.mask_sigmoid(torch.zeros(2), scale=0.0)
+    assert torch.allclose(tvdcn_amd.mask_sigmoid(torch.zeros(3)), torch.ones(3))
+    with pytest.raises(RuntimeError, match="mask tensor at dimension 1 is not valid"):
+        tvdcn_amd.mask_softmax2d(meta(2, 5, 3, 3), (3, 3))
+    y = tvdcn_amd.mask_softmax3d(meta(2, 54, 2, 3, 4), 3)
+    assert y.shape == (2, 54, 2, 3, 4)
+    assert tvdcn_amd.MaskSoftmax1d(5)(meta(2, 10, 7)).shape == (2, 10, 7)
+
+
+def fastdiv(n, d):
+    """Python restatement of FastDiv (tvdcn_amd/csrc/hip/common.h) for checking the constants"""
+    s = 0
+    while (1 << s) < d:
+        s += 1
+    m = ((1 << 32) * ((1 << s) - d)) // d + 1
+    t = (n * m) >> 32
+    return (t + n) >> s
+
+
+def test_fastdiv_constants_are_exact():
+    import random
+    rng = random.Random(0)
+    for d in list(range(1, 300)) + [4096, 4097, 12544, 50176, 65536, 1 << 20, (1 << 31) - 1]:
+        for n in [0, 1, d - 1, d, d + 1, 2 * d - 1, (1 << 31) - 1, (1 << 31) - 2] + \
+                 [rng.randrange(0, 1 << 31) for _ in range(200)]:
+            if 0 <= n < (1 << 31):
+                assert fastdiv(n, d) == n // d, (n, d)

@@ -309,13 +309,13 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
     tvdcn_status st = make_plan(desc, pl);
     if (st) return st;
     const Geo &g = pl.g;
+    if (g.B == 0) return TVDCN_STATUS_SUCCESS;   // empty batch: empty output, nothing to do
     if ((desc->offset_groups == 0) != (offset == nullptr))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "offset pointer and offset_groups disagree");
     if ((desc->mask_groups == 0) != (mask == nullptr))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "mask pointer and mask_groups disagree");
     const Layout L = layout(pl, false);
     if (workspace_bytes < L.total) return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
-    if (g.B == 0) return TVDCN_STATUS_SUCCESS;
     if (!input || !weight || !output) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
     if (!aligned16(input) || !aligned16(workspace))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "input and workspace must be 16-byte aligned");
@@ -346,6 +346,20 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     tvdcn_status st = make_plan(desc, pl);
     if (st) return st;
     const Geo &g = pl.g;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int dt = pl.dtype;
+    if (g.B == 0) {
+        // empty batch: the reference returns zero weight / bias gradients; the
+        // batch-sized tensors are empty (their pointers may be null)
+        if (!grad_weight) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
+        g_last_error.clear();
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                     launch_fill_zero((int)elem_size(dt), grad_weight, (size_t)g.M * g.Cg * g.Kn, s));
+        if (grad_bias)
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                         launch_fill_zero((int)elem_size(dt), grad_bias, (size_t)desc->out_channels, s));
+        return TVDCN_STATUS_SUCCESS;
+    }
     if ((desc->offset_groups == 0) != (offset == nullptr) || (offset == nullptr) != (grad_offset == nullptr))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "offset / grad_offset pointers and offset_groups disagree");
     if ((desc->mask_groups == 0) != (mask == nullptr) || (mask == nullptr) != (grad_mask == nullptr))
@@ -355,8 +369,6 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     if (!grad_out || !input || !weight || !grad_input || !grad_weight)
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
     if (!aligned16(workspace)) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const int dt = pl.dtype;
     const int ab = (int)acc_size(dt);
     const bool direct = acc_is_storage(dt);
     g_last_error.clear();
@@ -372,10 +384,7 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     // X: the sampled tensor (conv: input; transposed: grad_out)
     const void *Z = pl.transposed ? input : grad_out;
     const void *X = pl.transposed ? grad_out : input;
-    if (g.B == 0)   // empty batch: the reference returns zeros
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
-                     launch_fill_zero((int)elem_size(dt), grad_weight, (size_t)g.M * g.Cg * g.Kn, s));
-    if (g.B > 0) {
+    {
         void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
@@ -407,7 +416,6 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
         // transposed Cout = C on the sampled grid
         const int Cout = pl.transposed ? g.C : g.M;
         const int So = pl.transposed ? g.Sn : g.Pn;
-        // B == 0 reduces over nothing and writes zeros
         TVDCN_LAUNCH(TVDCN_KERNEL_BIAS_GRAD, s, launch_bias_grad(dt, grad_out, grad_bias, g.B, Cout, So, s));
     }
     return TVDCN_STATUS_SUCCESS;
