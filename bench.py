@@ -142,14 +142,25 @@ def kernel_rooflines(kern, batch=8):
     return out
 
 
-def load_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary, or None."""
-    path = os.path.join(ROOT, "profiles", "traffic_cfg2.json")
+TRAFFIC_KERNELS = {"gather_gemm": "fwd_gather_gemm_kernel<2, float, float,",
+                   "data_grad": "bwd_data_kernel<2, float, float,",
+                   "weight_grad": "bwd_weight_kernel<2, float, float,"}
+
+
+def load_traffic(family):
+    """HBM bytes per launch of `family`'s kernel, read from the committed rocprofv3 --pmc summary
+    (profiles/traffic_deform_conv2d_cfg2.md: calibrated FETCH_SIZE + WRITE_SIZE per dispatch), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_deform_conv2d_cfg2.md")
+    prefix = TRAFFIC_KERNELS.get(family)
     try:
         with open(path) as f:
-            return json.load(f).get(kernel, {}).get("hbm_bytes_per_launch")
+            for row in f:
+                cells = [c.strip() for c in row.strip().strip("|").split("|")]
+                if len(cells) == 4 and prefix and cells[0].strip("`").startswith(prefix):
+                    return int(round(float(cells[3]) * 1e6))
     except (OSError, ValueError):
-        return None
+        pass
+    return None
 
 
 def cpu_baseline(inp, batch):
