@@ -19,14 +19,25 @@ HIP_LIB_PATH = os.path.join(_LIB_DIR, "libtvdcn_hip.so")
 _HAS_OPS = False
 _LOAD_ERROR = None
 
-try:
-    if os.path.exists(_LIB_PATH):
-        torch.ops.load_library(_LIB_PATH)
-        _HAS_OPS = True
-    else:
-        _LOAD_ERROR = f"{_LIB_PATH} does not exist"
-except (ImportError, OSError, RuntimeError) as e:  # pragma: no cover - reported by _assert_has_ops
-    _LOAD_ERROR = str(e)
+
+def _load() -> bool:
+    """Loads ``_C.so`` once it exists; safe to call again (e.g. right after a build)."""
+    global _HAS_OPS, _LOAD_ERROR
+    if _HAS_OPS:
+        return True
+    try:
+        if os.path.exists(_LIB_PATH):
+            torch.ops.load_library(_LIB_PATH)
+            _HAS_OPS = True
+            _LOAD_ERROR = None
+        else:
+            _LOAD_ERROR = f"{_LIB_PATH} does not exist"
+    except (ImportError, OSError, RuntimeError) as e:  # pragma: no cover - reported by _assert_has_ops
+        _LOAD_ERROR = str(e)
+    return _HAS_OPS
+
+
+_load()
 
 
 def _assert_has_ops():
