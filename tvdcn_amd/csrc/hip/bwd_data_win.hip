@@ -1,0 +1,609 @@
+// Family D, windowed variant: grad-columns on MFMA with the bilinear scatter
+// pre-accumulated in an LDS window of the sampled grid.
+//
+//   G[c][t][p] = sum_{m in group} W[m][c][t] * Z[b][m][p]             (MFMA, never stored)
+//   SCATTER: dX[b][s][c] += w_corner(s) * mask * G                       (bilinear insert)
+//   COORD:   dOffset[b][og][t][a][p] += mask * G * d(sample)/d(pos_a)    (summed over c in og)
+//            dMask[b][mg][t][p]      += G * sample                        (summed over c in mg)
+//
+// Replaces the reference's grad-columns addmm_ + col2im + compute_grad_offset +
+// compute_grad_mask per batch block (tvdcn/csrc/ops/cuda/deform_conv2d_kernel.cpp:518-598,
+// kernels deform_conv2d_common_kernels.cu:258-624, and the 1D/3D twins).
+//
+// Workgroup = one tile: a box of 256 column pixels of one image (16x16 in 2D,
+// 256 in 1D, 4x8x8 in 3D) x 16 sampled-side channels x every tap; eight waves
+// (two per SIMD, so one wave's loads overlap the other's MFMAs), each owning 32
+// pixels; one workgroup per CU (the window takes most of the 160 KB of LDS).
+//   * K loop over the GEMM-side channels m, 16 per step, operands straight from
+//     global memory into registers (next step prefetched while the MFMAs of the
+//     current one run): wave w computes Gt[c][px] for its 32 pixels, so each lane
+//     holds four consecutive channels of one pixel per (tap, 16-pixel block).
+//   * Epilogue per tap: the geometry of the 256 pixels (one per thread) goes to an
+//     LDS table. The offset/mask gradients are formed in the MFMA layout (4
+//     channels in-lane, two shuffles across the channel quads, one atomic per
+//     pixel and quantity).
+//   * The scatter accumulates in the LDS window in 32-bit fixed point with
+//     integer LDS atomics (ds_add_u32 measured at ~5 cycles per wave instruction
+//     on gfx950, ds_add_f32 at ~190). Channel c of a pass uses the scale
+//     2^s_c, s_c = 29 - ceil(log2 B_c), B_c = sum over the pass's (pixel, tap) of
+//     |G * mask|: a bilinear corner weight is at most 1 and each (pixel, tap)
+//     reaches a cell through at most one corner, so every cell sum stays below
+//     2^29 (no overflow) and is rounded at B_c * 2^-29 per term (~1e-9 B_c).
+//     Integer sums are also order independent. A non-finite B_c sends the pass
+//     to global float atomics so that inf/nan propagate as in the reference.
+//     Corners outside the window go to global float atomics.
+//   * The window (sampled-grid box around the tile's undeformed footprint plus a
+//     margin R per axis) is flushed after each pass: one float atomic per
+//     non-zero (cell, channel), 16 consecutive channels per cell.
+#include "kernels.h"
+
+namespace tvdcn_hip {
+namespace {
+
+constexpr int NW = 8;             // waves per workgroup (two per SIMD)
+constexpr int NT = 64 * NW;       // threads per workgroup
+constexpr int PB = 2;             // 16-pixel blocks per wave
+constexpr int BPX = NW * PB * 16; // column pixels per tile (256)
+constexpr int BC = 16;            // sampled-side channels per tile
+constexpr int BM = 16;            // GEMM-side channels per K step
+constexpr int CS = BC + 1;        // window cell stride (odd: spreads the LDS banks)
+constexpr int FIX_BITS = 29;      // fixed-point headroom: |cell sum| * 2^s_c < 2^29
+
+template <int DIM> struct Rec {
+    static constexpr int NC = 1 << DIM;
+    // gidx[NC] | loc[NC] | w[NC] | fh[DIM] | mask | inside, padded to 4 words
+    static constexpr int RAW = 3 * NC + DIM + 2;
+    static constexpr int SIZE = (RAW + 3) / 4 * 4;
+};
+
+// LDS words ahead of the window: geometry table, per-wave channel bounds, scales
+template <int DIM> constexpr int fixed_floats() { return BPX * Rec<DIM>::SIZE + NW * BC + BC + 4; }
+
+template <int DIM, typename T, bool SCATTER, bool COORD>
+__global__ void __launch_bounds__(NT)
+bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, const float *__restrict__ wchunks,
+                    const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
+                    float *__restrict__ gx_cl, float *__restrict__ goff, float *__restrict__ gmask) {
+    constexpr int NC = 1 << DIM;
+    constexpr int RS = Rec<DIM>::SIZE;
+    constexpr int TMAX = WIN_TMAX;
+    typedef f32x4 acc4;
+
+    extern __shared__ float smem[];
+    float *recs = smem;                                        // [BPX][RS]
+    float *bsum = smem + BPX * RS;                             // [NW][BC] partial bounds
+    int *scl = reinterpret_cast<int *>(bsum + NW * BC);        // [BC] scale exponents, [BC] = non-finite flag
+    int *win = reinterpret_cast<int *>(smem + fixed_floats<DIM>());   // [cells][CS] fixed point
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int q = lane >> 4;
+    const int mq = 4 * q;
+
+    // ---- tile coordinates ------------------------------------------------------
+    int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int ct = L % wt.c_tiles;
+    L /= wt.c_tiles;
+    int tcoord[3];
+    tcoord[2] = L % wt.ntile[2];
+    L /= wt.ntile[2];
+    tcoord[1] = L % wt.ntile[1];
+    L /= wt.ntile[1];
+    tcoord[0] = L % wt.ntile[0];
+    L /= wt.ntile[0];
+    const int b = L % g.B;
+    const int grp = L / g.B;
+    int p0[3], org[3];
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+        p0[e] = tcoord[e] * wt.box[e];
+        org[e] = p0[e] * g.st[e] - g.pad[e] - wt.R[e];
+    }
+    const int c0 = ct * BC;                      // first channel of the tile within the group
+    const int cg0 = grp * g.Cg + c0;             // first global sampled-side channel
+    const int ogu = g.og ? cg0 / g.cpo : 0;      // the tile's offset / mask group (uniform)
+    const int mgu = g.mg ? cg0 / g.cpm : 0;
+    const bool deformable = offset != nullptr;
+    const bool cq_ok = c0 + mq < g.Cg;           // Cg % 4 == 0: a channel quad is all in or all out
+
+    // pixel `i` of the tile (0..255) -> column pixel index p (or -1 outside the grid)
+    auto tile_pixel = [&](int i) {
+        const int iz = i >> wt.lbxy;
+        const int iy = (i >> wt.lbx) & (wt.box[1] - 1);
+        const int ix = i & (wt.box[2] - 1);
+        const int pz = p0[0] + iz, py = p0[1] + iy, px = p0[2] + ix;
+        if (pz >= g.P[0] || py >= g.P[1] || px >= g.P[2]) return -1;
+        return (pz * g.P[1] + py) * g.P[2] + px;
+    };
+
+    if constexpr (SCATTER) {
+        for (int i = tid; i < wt.cells * CS; i += NT) win[i] = 0;
+    }
+
+    // ---- K-loop operands, straight to registers ---------------------------------
+    // B = Z[m][px]: pixel wave * 32 + pb * 16 + lane % 16, m = 4 * (lane / 16) + kk
+    // A = W[c][m]:  channel c0 + lane % 16, same m; the K order is permuted the same
+    //               way on both operands, which leaves the sum unchanged
+    int zp[PB];
+    const T *zb[PB];
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+        zp[pb] = tile_pixel(wave * (PB * 16) + pb * 16 + (lane & 15));
+        zb[pb] = z + ((size_t)b * g.M + (size_t)grp * g.Mg) * g.Pn + (zp[pb] < 0 ? 0 : zp[pb]);
+    }
+    auto load_z = [&](int ms, float (&zr)[PB][4]) {
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb)
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int m = ms * BM + mq + kk;
+                zr[pb][kk] = (zp[pb] >= 0 && m < g.Mg) ? to_acc<float>(zb[pb][(size_t)m * g.Pn]) : 0.f;
+            }
+    };
+    // weight chunks [G][c_tiles][m_steps][Kn][16 c][16 m]
+    const float *wbase =
+        wchunks + ((size_t)grp * wt.c_tiles + ct) * wt.m_steps * g.Kn * (BC * BM) + (lane & 15) * BM + mq;
+    auto load_w = [&](int ms, int t0, int ntaps, acc4 (&wr)[TMAX]) {
+        const float *p = wbase + ((size_t)ms * g.Kn + t0) * (BC * BM);
+#pragma unroll
+        for (int tp = 0; tp < TMAX; ++tp)
+            wr[tp] = tp < ntaps ? *reinterpret_cast<const acc4 *>(p + tp * (BC * BM)) : acc4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
+        const int ntaps = min(wt.tpp, g.Kn - t0);
+
+        acc4 acc[TMAX][PB];
+#pragma unroll
+        for (int tp = 0; tp < TMAX; ++tp)
+#pragma unroll
+            for (int pb = 0; pb < PB; ++pb) acc[tp][pb] = acc4{0.f, 0.f, 0.f, 0.f};
+
+        // ---- K loop: ping-pong register buffers, two steps per iteration -----------
+        auto kloop = [&](auto full_tag) {
+            constexpr bool FULL = decltype(full_tag)::value;   // every tap slot in use: no guards
+            float za[PB][4], zbb[PB][4];
+            acc4 wa[TMAX], wb[TMAX];
+            auto step = [&](const float (&zr)[PB][4], const acc4 (&wr)[TMAX]) {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                    for (int tp = 0; tp < TMAX; ++tp) {
+                        if (FULL || tp < ntaps) {
+#pragma unroll
+                            for (int pb = 0; pb < PB; ++pb)
+                                acc[tp][pb] = mfma16x16x4(wr[tp][kk], zr[pb][kk], acc[tp][pb]);
+                        }
+                    }
+            };
+            load_z(0, za);
+            load_w(0, t0, ntaps, wa);
+            for (int ms = 0; ms < wt.m_steps; ms += 2) {
+                const bool has1 = ms + 1 < wt.m_steps;
+                if (has1) {
+                    load_z(ms + 1, zbb);
+                    load_w(ms + 1, t0, ntaps, wb);
+                }
+                step(za, wa);
+                if (has1) {
+                    if (ms + 2 < wt.m_steps) {
+                        load_z(ms + 2, za);
+                        load_w(ms + 2, t0, ntaps, wa);
+                    }
+                    step(zbb, wb);
+                }
+            }
+        };
+        if (ntaps == TMAX)
+            kloop(std::true_type());
+        else
+            kloop(std::false_type());
+
+        // ---- fixed-point scale per channel of this pass -------------------------------
+        int sexp[4] = {0, 0, 0, 0};   // scale exponents of this lane's channels c0 + mq + v
+        bool use_window = false;
+        if constexpr (SCATTER) {
+            float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int pb = 0; pb < PB; ++pb) {
+                const int p = zp[pb];
+#pragma unroll
+                for (int tp = 0; tp < TMAX; ++tp) {
+                    if (tp < ntaps && p >= 0) {
+                        const float mk = fabsf(mask_at<float, T>(g, mask, b, mgu, t0 + tp, p));
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) part[v] += fabsf(acc[tp][pb][v]) * mk;
+                    }
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+#pragma unroll
+                for (int m = 1; m < 16; m <<= 1) part[v] += __shfl_xor(part[v], m);
+            }
+            if ((lane & 15) == 0) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) bsum[wave * BC + mq + v] = part[v];
+            }
+            __syncthreads();
+            if (tid < BC) {
+                float bc = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) bc += bsum[w * BC + tid];
+                int e = 0;
+                if (bc > 0.f && isfinite(bc)) frexpf(bc, &e);   // bc < 2^e
+                scl[tid] = FIX_BITS - e;
+                // the pass uses the window only if every bound is finite (ballot over 16 lanes)
+                const unsigned long long bad = __ballot(!isfinite(bc));
+                if (tid == 0) scl[BC] = bad != 0ull;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sexp[v] = scl[mq + v];
+            use_window = wt.cells > 0 && scl[BC] == 0;
+        }
+
+        // ---- epilogue, one tap at a time ------------------------------------------
+        for (int tl = 0; tl < ntaps; ++tl) {
+            const int t = t0 + tl;
+            // geometry of pixel tid (threads 0..255)
+            if (tid < BPX) {
+                const int p = tile_pixel(tid);
+                float *rec = recs + tid * RS;
+                const bool ok = p >= 0;
+                const AxisW<DIM, float> aw =
+                    axis_weights<DIM, float>(g, sample_point<DIM, float, T>(g, offset, b, ok ? p : 0, t, ogu),
+                                             deformable);
+#pragma unroll
+                for (int k = 0; k < NC; ++k) {
+                    int idx;
+                    bool v;
+                    corner_at<DIM, float>(g, aw, k, idx, v);
+                    v = v && ok;
+                    int loc = -1;
+                    if (SCATTER && v && wt.cells > 0) {
+                        bool in = true;
+                        int lin = 0;
+#pragma unroll
+                        for (int a = 0; a < DIM; ++a) {
+                            const int e = 3 - DIM + a;
+                            const int l = aw.lo[a] + corner_bit<DIM>(k, a) - org[e];
+                            in = in && l >= 0 && l < wt.WE[e];
+                            lin = lin * wt.WE[e] + l;
+                        }
+                        loc = in ? lin : -1;
+                    }
+                    rec[k] = __int_as_float(v ? idx : -1);
+                    rec[NC + k] = __int_as_float(loc);
+                    rec[2 * NC + k] = v ? corner_weight<DIM, float>(aw, k) : 0.f;
+                }
+#pragma unroll
+                for (int a = 0; a < DIM; ++a) rec[3 * NC + a] = aw.fh[a];
+                rec[3 * NC + DIM] = ok ? mask_at<float, T>(g, mask, b, mgu, t, p) : 0.f;
+                rec[3 * NC + DIM + 1] = aw.inside ? 1.f : 0.f;
+            }
+            acc4 gt[PB];
+            switch (tl) {
+#define TVDCN_SEL(K)                                          \
+    case K:                                                   \
+        if constexpr (K < TMAX) {                             \
+            _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) gt[pb] = acc[K][pb]; \
+        }                                                     \
+        break;
+                TVDCN_SEL(0) TVDCN_SEL(1) TVDCN_SEL(2) TVDCN_SEL(3) TVDCN_SEL(4)
+                TVDCN_SEL(5) TVDCN_SEL(6) TVDCN_SEL(7) TVDCN_SEL(8)
+#undef TVDCN_SEL
+                default:
+#pragma unroll
+                    for (int pb = 0; pb < PB; ++pb) gt[pb] = acc4{0.f, 0.f, 0.f, 0.f};
+            }
+            __syncthreads();
+
+#pragma unroll
+            for (int pb = 0; pb < PB; ++pb) {
+                const int i = wave * (PB * 16) + pb * 16 + (lane & 15);
+                const float *rec = recs + i * RS;
+                int gidx[NC];
+                float w[NC];
+#pragma unroll
+                for (int k = 0; k < NC; ++k) {
+                    gidx[k] = __float_as_int(rec[k]);
+                    w[k] = rec[2 * NC + k];
+                }
+                const float mk = rec[3 * NC + DIM];
+                const acc4 gv = gt[pb];
+
+                if constexpr (COORD) {
+                    AxisW<DIM, float> aw;
+#pragma unroll
+                    for (int a = 0; a < DIM; ++a) aw.fh[a] = rec[3 * NC + a];
+                    const bool inside = rec[3 * NC + DIM + 1] != 0.f;
+                    Vec4<float> xv[NC];
+#pragma unroll
+                    for (int k = 0; k < NC; ++k) {
+                        if (gidx[k] >= 0 && cq_ok)
+                            xv[k] = load4<float>(xcl + ((size_t)b * g.Sn + gidx[k]) * g.C + cg0 + mq);
+                        else
+                            xv[k] = {0.f, 0.f, 0.f, 0.f};
+                    }
+                    float qv[DIM + 1];
+#pragma unroll
+                    for (int a = 0; a < DIM; ++a) {
+                        Vec4<float> d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int k = 0; k < NC; ++k) {
+                            const float dw = corner_dweight<DIM, float>(aw, k, a);
+                            d.x += dw * xv[k].x;
+                            d.y += dw * xv[k].y;
+                            d.z += dw * xv[k].z;
+                            d.w += dw * xv[k].w;
+                        }
+                        qv[a] = mk * (gv[0] * d.x + gv[1] * d.y + gv[2] * d.z + gv[3] * d.w);
+                    }
+                    {
+                        Vec4<float> sv = {0.f, 0.f, 0.f, 0.f};
+                        if (inside) {
+#pragma unroll
+                            for (int k = 0; k < NC; ++k) {
+                                sv.x += w[k] * xv[k].x;
+                                sv.y += w[k] * xv[k].y;
+                                sv.z += w[k] * xv[k].z;
+                                sv.w += w[k] * xv[k].w;
+                            }
+                        }
+                        qv[DIM] = gv[0] * sv.x + gv[1] * sv.y + gv[2] * sv.z + gv[3] * sv.w;
+                    }
+#pragma unroll
+                    for (int a = 0; a <= DIM; ++a) {
+                        qv[a] += __shfl_xor(qv[a], 16);
+                        qv[a] += __shfl_xor(qv[a], 32);
+                    }
+                    const int p = tile_pixel(i);
+                    if (q == 0 && p >= 0) {
+                        if (deformable) {
+#pragma unroll
+                            for (int a = 0; a < DIM; ++a)
+                                atomic_add(goff + ((((size_t)b * g.og + ogu) * g.Kn + t) * DIM + a) * g.Pn + p, qv[a]);
+                        }
+                        if (mask != nullptr)
+                            atomic_add(gmask + (((size_t)b * g.mg + mgu) * g.Kn + t) * g.Pn + p, qv[DIM]);
+                    }
+                }
+
+                if constexpr (SCATTER) {
+                    if (cq_ok) {
+                        float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+#pragma unroll
+                        for (int k = 0; k < NC; ++k) {
+                            if (gidx[k] < 0) continue;
+                            const int loc = use_window ? __float_as_int(rec[NC + k]) : -1;
+                            const float s = mk * w[k];
+                            if (loc >= 0) {
+                                unsigned int *dst = reinterpret_cast<unsigned int *>(win + loc * CS + mq);
+#pragma unroll
+                                for (int v = 0; v < 4; ++v)
+                                    atomicAdd(dst + v, (unsigned int)__float2int_rn(ldexpf(s * gv[v], sexp[v])));
+                            } else {
+                                float *dst = gdst + (size_t)gidx[k] * g.C;
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) atomic_add(dst + v, s * gv[v]);
+                            }
+                        }
+                    }
+                }
+            }
+            __syncthreads();   // the geometry table is rewritten for the next tap
+        }
+
+        // ---- flush the window: one float atomic per non-zero (cell, channel) ----------
+        if (SCATTER && use_window) {
+            const int c = tid & 15;
+            const int se = scl[c];
+            float *gbase = gx_cl + (size_t)b * g.Sn * g.C + cg0 + c;
+            for (int cell = tid >> 4; cell < wt.cells; cell += NT / 16) {
+                const int iv = win[cell * CS + c];
+                if (iv == 0) continue;
+                win[cell * CS + c] = 0;   // ready for the next pass
+                if (c0 + c >= g.Cg) continue;
+                const float v = ldexpf((float)iv, -se);
+                const int lx = cell % wt.WE[2];
+                const int r = cell / wt.WE[2];
+                const int ly = r % wt.WE[1];
+                const int lz = r / wt.WE[1];
+                const int sz = org[0] + lz, sy = org[1] + ly, sx = org[2] + lx;
+                // only valid corners write the window, so a non-zero cell lies inside the grid
+                if (sz < 0 || sz >= g.S[0] || sy < 0 || sy >= g.S[1] || sx < 0 || sx >= g.S[2]) continue;
+                atomic_add(gbase + (size_t)((sz * g.S[1] + sy) * g.S[2] + sx) * g.C, v);
+            }
+            __syncthreads();   // window cleared before the next pass scatters into it
+        }
+    }
+}
+
+// weight (M, Cg, Kn) -> chunks [G][c_tiles][m_steps][Kn][16 c][16 m], zero padded
+template <typename T>
+__global__ void weight_win_kernel(const T *__restrict__ w, float *__restrict__ out, int G, int Mg, int Cg, int Kn,
+                                  int c_tiles, int m_steps) {
+    const size_t total = (size_t)G * c_tiles * m_steps * Kn * BC * BM;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int mi = (int)(i % BM);
+        const int ci = (int)((i / BM) % BC);
+        size_t r = i / (BM * BC);
+        const int t = (int)(r % Kn);
+        r /= Kn;
+        const int ms = (int)(r % m_steps);
+        r /= m_steps;
+        const int ct = (int)(r % c_tiles);
+        const int grp = (int)(r / c_tiles);
+        const int m = ms * BM + mi, c = ct * BC + ci;
+        float v = 0.f;
+        if (m < Mg && c < Cg) v = to_acc<float>(w[(((size_t)grp * Mg + m) * Cg + c) * Kn + t]);
+        out[i] = v;
+    }
+}
+
+template <int DIM> size_t lds_bytes(const WinTiles &t) {
+    return ((size_t)fixed_floats<DIM>() + (size_t)t.cells * CS) * sizeof(float);
+}
+
+template <int DIM, typename T, bool SCATTER, bool COORD>
+hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void *wchunks, const void *xcl,
+                    const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
+    auto kern = bwd_data_win_kernel<DIM, T, SCATTER, COORD>;
+    const size_t lds = lds_bytes<DIM>(tl);
+    static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)WIN_LDS_TARGET);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const long long blocks = (long long)g.G * g.B * tl.ntile[0] * tl.ntile[1] * tl.ntile[2] * tl.c_tiles;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, tl, static_cast<const T *>(z),
+                       static_cast<const float *>(wchunks), static_cast<const float *>(xcl),
+                       static_cast<const T *>(offset), static_cast<const T *>(mask), static_cast<float *>(gx_cl),
+                       static_cast<float *>(goff), static_cast<float *>(gmask));
+    return hipGetLastError();
+}
+
+template <int DIM, typename T>
+hipError_t launch_f(const Geo &g, const WinTiles &tl, bool scatter, bool coord, const void *z, const void *wc,
+                    const void *xcl, const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask,
+                    hipStream_t s) {
+    if (scatter && coord) return launch_k<DIM, T, true, true>(g, tl, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
+    if (scatter) return launch_k<DIM, T, true, false>(g, tl, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
+    if (coord) return launch_k<DIM, T, false, true>(g, tl, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
+    return hipSuccess;
+}
+
+template <typename T>
+hipError_t launch_d(int dim, const Geo &g, const WinTiles &tl, bool scatter, bool coord, const void *z,
+                    const void *wc, const void *xcl, const void *offset, const void *mask, void *gx_cl, void *goff,
+                    void *gmask, hipStream_t s) {
+    switch (dim) {
+        case 1: return launch_f<1, T>(g, tl, scatter, coord, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
+        case 2: return launch_f<2, T>(g, tl, scatter, coord, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
+        case 3: return launch_f<3, T>(g, tl, scatter, coord, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+int ilog2(int v) {
+    int r = 0;
+    while ((1 << r) < v) ++r;
+    return r;
+}
+
+}  // namespace
+
+WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter) {
+    WinTiles t{};
+    t.ok = false;
+    if (dtype == kF64) return t;
+    if (g.C % 4 || g.Cg % 4) return t;
+    // every 16-channel tile must lie inside one offset group and one mask group
+    for (int grp = 0; grp < g.G; ++grp)
+        for (int c0 = 0; c0 < g.Cg; c0 += BC) {
+            const int first = grp * g.Cg + c0, last = grp * g.Cg + (c0 + BC < g.Cg ? c0 + BC : g.Cg) - 1;
+            if ((g.og && first / g.cpo != last / g.cpo) || (g.mg && first / g.cpm != last / g.cpm)) return t;
+        }
+    // tile box: powers of two per used axis, product 256, no wider than the grid needs
+    int box[3] = {1, 1, 1};
+    auto p2 = [](int v, int cap) {
+        int r = 1;
+        while (r < v && r < cap) r <<= 1;
+        return r;
+    };
+    if (dim == 1) {
+        box[2] = 256;
+    } else if (dim == 2) {
+        box[2] = p2(g.P[2], 16);
+        box[1] = 256 / box[2];
+    } else {
+        box[2] = p2(g.P[2], 8);
+        box[1] = p2(g.P[1], 8);
+        box[0] = 256 / (box[1] * box[2]);
+    }
+    for (int e = 0; e < 3; ++e) {
+        t.box[e] = box[e];
+        t.ntile[e] = (g.P[e] + box[e] - 1) / box[e];
+    }
+    t.lbx = ilog2(box[2]);
+    t.lbxy = ilog2(box[1] * box[2]);
+    t.c_tiles = (g.Cg + BC - 1) / BC;
+    t.m_steps = (g.Mg + BM - 1) / BM;
+    // window: undeformed footprint of the box (low and high corners) plus a margin
+    // R per used axis, shrunk until it fits the LDS budget
+    int need[3] = {1, 1, 1};
+    for (int e = 3 - dim; e < 3; ++e) need[e] = (box[e] - 1) * g.st[e] + (g.K[e] - 1) * g.dil[e] + 2;
+    const size_t fixed_bytes = (dim == 3 ? (size_t)fixed_floats<3>()
+                                         : (dim == 2 ? (size_t)fixed_floats<2>() : (size_t)fixed_floats<1>())) *
+                               sizeof(float);
+    const long long max_cells = scatter ? (long long)((WIN_LDS_TARGET - fixed_bytes) / (CS * sizeof(float))) : 0;
+    int R = 0;
+    t.cells = 0;
+    if (max_cells > 0) {
+        for (R = dim == 1 ? 32 : 8; R > -64; --R) {
+            long long cells = 1;
+            bool degenerate = false;
+            for (int e = 3 - dim; e < 3; ++e) {
+                const int ext = need[e] + 2 * R;
+                if (ext < 1) degenerate = true;
+                cells *= ext;
+            }
+            if (degenerate) break;
+            if (cells <= max_cells) {
+                t.cells = (int)cells;
+                break;
+            }
+        }
+    }
+    for (int e = 0; e < 3; ++e) {
+        const bool used = e >= 3 - dim;
+        t.R[e] = (used && t.cells) ? R : 0;
+        t.WE[e] = (used && t.cells) ? need[e] + 2 * R : 1;
+    }
+    if (!t.cells) {
+        for (int e = 0; e < 3; ++e) t.WE[e] = 1;
+    }
+    const int npass = (g.Kn + WIN_TMAX - 1) / WIN_TMAX;
+    t.tpp = (g.Kn + npass - 1) / npass;
+    t.chunk_elems = (size_t)g.G * t.c_tiles * t.m_steps * g.Kn * BC * BM;
+    t.ok = true;
+    return t;
+}
+
+hipError_t launch_weight_win_layout(int dtype, const Geo &g, const WinTiles &t, const void *w, void *chunks,
+                                    hipStream_t s) {
+    const size_t n = t.chunk_elems;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+#define TVDCN_WW(T)                                                                                             \
+    hipLaunchKernelGGL((weight_win_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, s, static_cast<const T *>(w), \
+                       static_cast<float *>(chunks), g.G, g.Mg, g.Cg, g.Kn, t.c_tiles, t.m_steps);               \
+    return hipGetLastError();
+    switch (dtype) {
+        case kF32: { TVDCN_WW(float) }
+        case kF16: { TVDCN_WW(__half) }
+        case kBF16: { TVDCN_WW(__hip_bfloat16) }
+    }
+#undef TVDCN_WW
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
+                               const void *z, const void *wchunks, const void *xcl, const void *offset,
+                               const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
+    switch (dtype) {
+        case kF32: return launch_d<float>(dim, g, t, scatter, coord, z, wchunks, xcl, offset, mask, gx_cl, goff, gmask, s);
+        case kF16: return launch_d<__half>(dim, g, t, scatter, coord, z, wchunks, xcl, offset, mask, gx_cl, goff, gmask, s);
+        case kBF16:
+            return launch_d<__hip_bfloat16>(dim, g, t, scatter, coord, z, wchunks, xcl, offset, mask, gx_cl, goff, gmask,
+                                            s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace tvdcn_hip

@@ -63,6 +63,8 @@ struct Plan {
     int dtype;
     FwdTiles ft;
     DataTiles dt;
+    WinTiles wn_s;   // windowed data-gradient plan with the scatter (conv backward, transposed forward)
+    WinTiles wn_c;   // the same without the scatter (transposed backward: offset/mask gradients only)
     WeightTiles wt;
 };
 
@@ -143,6 +145,8 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     g.dK12 = make_fastdiv((uint32_t)(g.K[1] * g.K[2]));
     pl.ft = plan_fwd(g, pl.dtype);
     pl.dt = plan_data(g, pl.dtype);
+    pl.wn_s = plan_data_win(g, pl.dtype, pl.dim, true);
+    pl.wn_c = plan_data_win(g, pl.dtype, pl.dim, false);
     pl.wt = plan_weight(g, pl.dtype);
     return TVDCN_STATUS_SUCCESS;
 }
@@ -158,7 +162,9 @@ Layout layout(const Plan &pl, bool backward) {
     const size_t a = acc_size(pl.dtype);
     const size_t cl_bytes = align_up((size_t)g.B * g.Sn * g.C * a);
     const size_t wf_bytes = align_up((size_t)g.G * g.Kn * pl.ft.Mg_pad * pl.ft.Cg_pad * a);
-    const size_t wd_bytes = align_up((size_t)g.G * g.Kn * pl.dt.Mg_pad * pl.dt.Cg_pad * a);
+    // data-gradient weight: windowed-kernel chunks when eligible, else the [G][Kn][Cg][Mg] layout
+    const size_t wd_bytes = pl.wn_s.ok ? align_up(pl.wn_s.chunk_elems * sizeof(float))
+                                       : align_up((size_t)g.G * g.Kn * pl.dt.Mg_pad * pl.dt.Cg_pad * a);
     Layout L;
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -330,9 +336,15 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
     } else {
         void *wd = at(workspace, L.wd), *ycl = at(workspace, L.cl_acc);
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
-        TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, false, input, wd, nullptr, offset, mask, ycl,
-                                        nullptr, nullptr, s));
+        if (pl.wn_s.ok) {
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_s, true, false, input, wd, nullptr,
+                                                                        offset, mask, ycl, nullptr, nullptr, s));
+        } else {
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, false, input, wd, nullptr, offset,
+                                                                    mask, ycl, nullptr, nullptr, s));
+        }
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_from_channels_last(dt, ycl, output, bias, g.B, g.C, g.Sn, s));
     }
     return TVDCN_STATUS_SUCCESS;
@@ -387,22 +399,32 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     {
         void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
         const bool coord = offset != nullptr || mask != nullptr;
+        if (pl.wn_s.ok)
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
+        else
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
         if (!pl.transposed) {
             void *gx_cl = at(workspace, L.cl_acc);
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
-            TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask, gx_cl, goff,
-                                            gmask, s));
+            if (pl.wn_s.ok)
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_s, true, coord, Z, wd, xcl, offset,
+                                                                            mask, gx_cl, goff, gmask, s));
+            else
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask,
+                                                                        gx_cl, goff, gmask, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_from_channels_last(dt, gx_cl, grad_input, nullptr, g.B, g.C, g.Sn, s));
         } else {
             void *wf = at(workspace, L.wf);
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
             TVDCN_CHECK_HIP(
                 launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, nullptr, grad_input, s));
-            if (coord)
-                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, false, true, Z, wd, xcl, offset, mask, nullptr,
-                                                goff, gmask, s));
+            if (coord && pl.wn_c.ok)
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_c, false, true, Z, wd, xcl, offset,
+                                                                            mask, nullptr, goff, gmask, s));
+            else if (coord)
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, false, true, Z, wd, xcl, offset, mask,
+                                                                        nullptr, goff, gmask, s));
         }
         TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,
                                                                     at(workspace, L.wpart), grad_weight, s));

@@ -30,7 +30,25 @@ struct WeightTiles {
     size_t part_elems;   // workspace elements for the split partials
 };
 
+// Windowed data-gradient kernel (bwd_data_win.hip): 256-pixel box x 16 channels x
+// up to WIN_TMAX taps per pass, bilinear scatter pre-accumulated in LDS.
+constexpr int WIN_TMAX = 9;                   // taps held in accumulators per pass
+constexpr size_t WIN_LDS_TARGET = 156 * 1024; // bytes of LDS per workgroup (gfx950: 160 KB per CU)
+struct WinTiles {
+    bool ok;             // eligible: fp32/fp16/bf16, C % 4 == 0, 16-channel tiles group-uniform
+    int box[3];          // tile box (embedded axes), product 256, powers of two
+    int lbx, lbxy;       // log2(box[2]), log2(box[1] * box[2])
+    int ntile[3];        // tiles per axis
+    int R[3];            // window margin per axis
+    int WE[3];           // window extent per axis (1 on unused axes)
+    int cells;           // window cells (0 = no window: scatter goes straight to global)
+    int c_tiles, m_steps;
+    int tpp;             // taps per pass (<= WIN_TMAX)
+    size_t chunk_elems;  // floats of the re-laid-out weight
+};
+
 FwdTiles plan_fwd(const Geo &g, int dtype);
+WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter);
 DataTiles plan_data(const Geo &g, int dtype);
 WeightTiles plan_weight(const Geo &g, int dtype);
 
@@ -53,6 +71,11 @@ hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTil
 hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t, bool scatter, bool coord,
                            const void *z, const void *wd, const void *xcl, const void *offset, const void *mask,
                            void *gx_cl, void *goff, void *gmask, hipStream_t s);
+hipError_t launch_weight_win_layout(int dtype, const Geo &g, const WinTiles &t, const void *w, void *chunks,
+                                    hipStream_t s);
+hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
+                               const void *z, const void *wchunks, const void *xcl, const void *offset,
+                               const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s);
 // writes split partials to `part` (WeightTiles::part_elems accumulator elements),
 // then reduces them into gw (storage type, layout (M, Cg, Kn))
 hipError_t launch_bwd_weight(int dtype, int dim, const Geo &g, const WeightTiles &t, const void *z, const void *xcl,
