@@ -46,18 +46,14 @@ constexpr int PB = 2;             // 16-pixel blocks per wave
 constexpr int BPX = NW * PB * 16; // column pixels per tile (256)
 constexpr int BC = 16;            // sampled-side channels per tile
 constexpr int BM = 16;            // GEMM-side channels per K step
-constexpr int CS = BC + 1;        // window cell stride (odd: spreads the LDS banks)
+constexpr int CS = BC + 1;        // fixed-point window cell stride (odd: spreads the LDS banks)
+constexpr int XS = BC + 4;        // X window cell stride (16-byte quads)
 constexpr int FIX_BITS = 29;      // fixed-point headroom: |cell sum| * 2^s_c < 2^29
 
-template <int DIM> struct Rec {
-    static constexpr int NC = 1 << DIM;
-    // gidx[NC] | loc[NC] | w[NC] | fh[DIM] | mask | inside, padded to 4 words
-    static constexpr int RAW = 3 * NC + DIM + 2;
-    static constexpr int SIZE = (RAW + 3) / 4 * 4;
-};
-
-// LDS words ahead of the window: geometry table, per-wave channel bounds, scales
-template <int DIM> constexpr int fixed_floats() { return BPX * Rec<DIM>::SIZE + NW * BC + BC + 4; }
+// LDS words ahead of the windows: geometry table [WIN_TMAX][BPX] x (position, mask),
+// per-wave channel bounds, scale exponents
+constexpr int GEO_WORDS = WIN_TMAX * BPX * 4;
+constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + BC + 4;
 
 template <int DIM, typename T, bool SCATTER, bool COORD>
 __global__ void __launch_bounds__(NT)
@@ -65,15 +61,15 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                     const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
                     float *__restrict__ gx_cl, float *__restrict__ goff, float *__restrict__ gmask) {
     constexpr int NC = 1 << DIM;
-    constexpr int RS = Rec<DIM>::SIZE;
     constexpr int TMAX = WIN_TMAX;
     typedef f32x4 acc4;
 
     extern __shared__ float smem[];
-    float *recs = smem;                                        // [BPX][RS]
-    float *bsum = smem + BPX * RS;                             // [NW][BC] partial bounds
+    acc4 *geo = reinterpret_cast<acc4 *>(smem);                // [TMAX][BPX]: pos[0..DIM), mask in .w
+    float *bsum = smem + GEO_WORDS;                            // [NW][BC] partial bounds
     int *scl = reinterpret_cast<int *>(bsum + NW * BC);        // [BC] scale exponents, [BC] = non-finite flag
-    int *win = reinterpret_cast<int *>(smem + fixed_floats<DIM>());   // [cells][CS] fixed point
+    float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X values (COORD)
+    int *iwin = reinterpret_cast<int *>(xwin + (COORD ? wt.cells * XS : 0));   // [cells][CS] fixed point
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -106,6 +102,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
     const int mgu = g.mg ? cg0 / g.cpm : 0;
     const bool deformable = offset != nullptr;
     const bool cq_ok = c0 + mq < g.Cg;           // Cg % 4 == 0: a channel quad is all in or all out
+    const float *xb = xcl + (size_t)b * g.Sn * g.C + cg0;
 
     // pixel `i` of the tile (0..255) -> column pixel index p (or -1 outside the grid)
     auto tile_pixel = [&](int i) {
@@ -116,9 +113,30 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
         if (pz >= g.P[0] || py >= g.P[1] || px >= g.P[2]) return -1;
         return (pz * g.P[1] + py) * g.P[2] + px;
     };
+    // window cell -> flat sampled-grid index (or -1 outside the grid)
+    auto cell_index = [&](int cell) {
+        const int lx = cell % wt.WE[2];
+        const int r = cell / wt.WE[2];
+        const int ly = r % wt.WE[1];
+        const int lz = r / wt.WE[1];
+        const int sz = org[0] + lz, sy = org[1] + ly, sx = org[2] + lx;
+        if (sz < 0 || sz >= g.S[0] || sy < 0 || sy >= g.S[1] || sx < 0 || sx >= g.S[2]) return -1;
+        return (sz * g.S[1] + sy) * g.S[2] + sx;
+    };
 
+    // ---- per-tile LDS state: X window (read by the offset/mask gradients), zeroed
+    //      fixed-point window (scatter)
+    if constexpr (COORD) {
+        for (int e = tid; e < wt.cells * 4; e += NT) {
+            const int cell = e >> 2, qd = e & 3;
+            const int si = cell_index(cell);
+            acc4 v = acc4{0.f, 0.f, 0.f, 0.f};
+            if (si >= 0 && c0 + 4 * qd < g.Cg) v = *reinterpret_cast<const acc4 *>(xb + (size_t)si * g.C + 4 * qd);
+            *reinterpret_cast<acc4 *>(xwin + cell * XS + 4 * qd) = v;
+        }
+    }
     if constexpr (SCATTER) {
-        for (int i = tid; i < wt.cells * CS; i += NT) win[i] = 0;
+        for (int i = tid; i < wt.cells * CS; i += NT) iwin[i] = 0;
     }
 
     // ---- K-loop operands, straight to registers ---------------------------------
@@ -132,13 +150,19 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
         zp[pb] = tile_pixel(wave * (PB * 16) + pb * 16 + (lane & 15));
         zb[pb] = z + ((size_t)b * g.M + (size_t)grp * g.Mg) * g.Pn + (zp[pb] < 0 ? 0 : zp[pb]);
     }
+    // Loads are unconditional, from clamped (valid) addresses, so that a prefetch is
+    // only waited for where its data is consumed. Pixels outside the grid stage some
+    // value of a valid pixel: their G is never read (their geometry has no valid
+    // corner, no offset/mask output, and the scale bound skips them). Rows m >= Mg
+    // meet zero weights; when Mg % 16 != 0 they are zeroed at use (MPAD) so that a
+    // non-finite value there cannot leak into the sum.
     auto load_z = [&](int ms, float (&zr)[PB][4]) {
 #pragma unroll
         for (int pb = 0; pb < PB; ++pb)
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 const int m = ms * BM + mq + kk;
-                zr[pb][kk] = (zp[pb] >= 0 && m < g.Mg) ? to_acc<float>(zb[pb][(size_t)m * g.Pn]) : 0.f;
+                zr[pb][kk] = to_acc<float>(zb[pb][(size_t)min(m, g.Mg - 1) * g.Pn]);
             }
     };
     // weight chunks [G][c_tiles][m_steps][Kn][16 c][16 m]
@@ -147,12 +171,28 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
     auto load_w = [&](int ms, int t0, int ntaps, acc4 (&wr)[TMAX]) {
         const float *p = wbase + ((size_t)ms * g.Kn + t0) * (BC * BM);
 #pragma unroll
-        for (int tp = 0; tp < TMAX; ++tp)
-            wr[tp] = tp < ntaps ? *reinterpret_cast<const acc4 *>(p + tp * (BC * BM)) : acc4{0.f, 0.f, 0.f, 0.f};
+        for (int tp = 0; tp < TMAX; ++tp) {
+            // taps past the pass re-read its last tap (in bounds); their products are never used
+            wr[tp] = *reinterpret_cast<const acc4 *>(p + min(tp, ntaps - 1) * (BC * BM));
+        }
     };
 
     for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
         const int ntaps = min(wt.tpp, g.Kn - t0);
+
+        // ---- sampling positions and masks of the pass, one (tap, pixel) per thread ----
+        for (int e = tid; e < ntaps * BPX; e += NT) {
+            const int tl = e / BPX, i = e % BPX;
+            const int p = tile_pixel(i);
+            acc4 r = acc4{-4.f, -4.f, -4.f, 0.f};   // outside the grid: no valid corner, mask 0
+            if (p >= 0) {
+                const Point<DIM, float> pt = sample_point<DIM, float, T>(g, offset, b, p, t0 + tl, ogu);
+#pragma unroll
+                for (int a = 0; a < DIM; ++a) r[a] = pt.pos[a];
+                r[3] = mask_at<float, T>(g, mask, b, mgu, t0 + tl, p);
+            }
+            geo[tl * BPX + i] = r;
+        }
 
         acc4 acc[TMAX][PB];
 #pragma unroll
@@ -160,45 +200,57 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
 #pragma unroll
             for (int pb = 0; pb < PB; ++pb) acc[tp][pb] = acc4{0.f, 0.f, 0.f, 0.f};
 
-        // ---- K loop: ping-pong register buffers, two steps per iteration -----------
-        auto kloop = [&](auto full_tag) {
+        // ---- K loop: Z ping-pong, W rolling reload ----------------------------------
+        auto kloop = [&](auto full_tag, auto mpad_tag) {
             constexpr bool FULL = decltype(full_tag)::value;   // every tap slot in use: no guards
+            constexpr bool MPAD = decltype(mpad_tag)::value;   // Mg % 16 != 0: zero rows m >= Mg
+            // Z: ping-pong pair; W: one register set, each tap's fragment reloaded for
+            // the next step as soon as this step's MFMAs on it are issued (the last step
+            // re-reads itself, so the step is one straight-line block)
             float za[PB][4], zbb[PB][4];
-            acc4 wa[TMAX], wb[TMAX];
-            auto step = [&](const float (&zr)[PB][4], const acc4 (&wr)[TMAX]) {
+            acc4 wr[TMAX];
+            auto step = [&](int ms, const float (&zr)[PB][4]) {
+                const int msn = min(ms + 1, wt.m_steps - 1);
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk)
+                for (int tp = 0; tp < TMAX; ++tp) {
+                    if (FULL || tp < ntaps) {
 #pragma unroll
-                    for (int tp = 0; tp < TMAX; ++tp) {
-                        if (FULL || tp < ntaps) {
+                        for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-                            for (int pb = 0; pb < PB; ++pb)
-                                acc[tp][pb] = mfma16x16x4(wr[tp][kk], zr[pb][kk], acc[tp][pb]);
-                        }
+                            for (int pb = 0; pb < PB; ++pb) {
+                                const float zv = (!MPAD || ms * BM + mq + kk < g.Mg) ? zr[pb][kk] : 0.f;
+                                acc[tp][pb] = mfma16x16x4(wr[tp][kk], zv, acc[tp][pb]);
+                            }
                     }
+                    const int tq = FULL ? tp : min(tp, ntaps - 1);
+                    wr[tp] = *reinterpret_cast<const acc4 *>(wbase + ((size_t)msn * g.Kn + t0 + tq) * (BC * BM));
+                    // issue order: this tap's MFMAs, then its reload (a full step ahead of use)
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             };
             load_z(0, za);
-            load_w(0, t0, ntaps, wa);
+            load_w(0, t0, ntaps, wr);
             for (int ms = 0; ms < wt.m_steps; ms += 2) {
                 const bool has1 = ms + 1 < wt.m_steps;
+                load_z(min(ms + 1, wt.m_steps - 1), zbb);
+                // keep the prefetch ahead of this step's MFMAs (the scheduler would sink it)
+                __builtin_amdgcn_sched_barrier(0);
+                step(ms, za);
                 if (has1) {
-                    load_z(ms + 1, zbb);
-                    load_w(ms + 1, t0, ntaps, wb);
-                }
-                step(za, wa);
-                if (has1) {
-                    if (ms + 2 < wt.m_steps) {
-                        load_z(ms + 2, za);
-                        load_w(ms + 2, t0, ntaps, wa);
-                    }
-                    step(zbb, wb);
+                    load_z(min(ms + 2, wt.m_steps - 1), za);
+                    __builtin_amdgcn_sched_barrier(0);
+                    step(ms + 1, zbb);
                 }
             }
         };
-        if (ntaps == TMAX)
-            kloop(std::true_type());
+        const bool mpad = g.Mg % BM != 0;
+        if (ntaps == TMAX && !mpad)
+            kloop(std::true_type(), std::false_type());
+        else if (!mpad)
+            kloop(std::false_type(), std::false_type());
         else
-            kloop(std::false_type());
+            kloop(std::false_type(), std::true_type());
+        __syncthreads();   // geometry table (and X window) written
 
         // ---- fixed-point scale per channel of this pass -------------------------------
         int sexp[4] = {0, 0, 0, 0};   // scale exponents of this lane's channels c0 + mq + v
@@ -207,11 +259,11 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
             float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int pb = 0; pb < PB; ++pb) {
-                const int p = zp[pb];
+                const int i = wave * (PB * 16) + pb * 16 + (lane & 15);
 #pragma unroll
                 for (int tp = 0; tp < TMAX; ++tp) {
-                    if (tp < ntaps && p >= 0) {
-                        const float mk = fabsf(mask_at<float, T>(g, mask, b, mgu, t0 + tp, p));
+                    if (tp < ntaps && zp[pb] >= 0) {
+                        const float mk = fabsf(geo[tp * BPX + i][3]);
 #pragma unroll
                         for (int v = 0; v < 4; ++v) part[v] += fabsf(acc[tp][pb][v]) * mk;
                     }
@@ -244,52 +296,16 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
             use_window = wt.cells > 0 && scl[BC] == 0;
         }
 
-        // ---- epilogue, one tap at a time ------------------------------------------
+        // ---- epilogue: every wave walks its own pixels tap by tap, no barriers -------
         for (int tl = 0; tl < ntaps; ++tl) {
             const int t = t0 + tl;
-            // geometry of pixel tid (threads 0..255)
-            if (tid < BPX) {
-                const int p = tile_pixel(tid);
-                float *rec = recs + tid * RS;
-                const bool ok = p >= 0;
-                const AxisW<DIM, float> aw =
-                    axis_weights<DIM, float>(g, sample_point<DIM, float, T>(g, offset, b, ok ? p : 0, t, ogu),
-                                             deformable);
-#pragma unroll
-                for (int k = 0; k < NC; ++k) {
-                    int idx;
-                    bool v;
-                    corner_at<DIM, float>(g, aw, k, idx, v);
-                    v = v && ok;
-                    int loc = -1;
-                    if (SCATTER && v && wt.cells > 0) {
-                        bool in = true;
-                        int lin = 0;
-#pragma unroll
-                        for (int a = 0; a < DIM; ++a) {
-                            const int e = 3 - DIM + a;
-                            const int l = aw.lo[a] + corner_bit<DIM>(k, a) - org[e];
-                            in = in && l >= 0 && l < wt.WE[e];
-                            lin = lin * wt.WE[e] + l;
-                        }
-                        loc = in ? lin : -1;
-                    }
-                    rec[k] = __int_as_float(v ? idx : -1);
-                    rec[NC + k] = __int_as_float(loc);
-                    rec[2 * NC + k] = v ? corner_weight<DIM, float>(aw, k) : 0.f;
-                }
-#pragma unroll
-                for (int a = 0; a < DIM; ++a) rec[3 * NC + a] = aw.fh[a];
-                rec[3 * NC + DIM] = ok ? mask_at<float, T>(g, mask, b, mgu, t, p) : 0.f;
-                rec[3 * NC + DIM + 1] = aw.inside ? 1.f : 0.f;
-            }
             acc4 gt[PB];
             switch (tl) {
-#define TVDCN_SEL(K)                                          \
-    case K:                                                   \
-        if constexpr (K < TMAX) {                             \
+#define TVDCN_SEL(K)                                                            \
+    case K:                                                                     \
+        if constexpr (K < TMAX) {                                               \
             _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) gt[pb] = acc[K][pb]; \
-        }                                                     \
+        }                                                                       \
         break;
                 TVDCN_SEL(0) TVDCN_SEL(1) TVDCN_SEL(2) TVDCN_SEL(3) TVDCN_SEL(4)
                 TVDCN_SEL(5) TVDCN_SEL(6) TVDCN_SEL(7) TVDCN_SEL(8)
@@ -298,68 +314,73 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
 #pragma unroll
                     for (int pb = 0; pb < PB; ++pb) gt[pb] = acc4{0.f, 0.f, 0.f, 0.f};
             }
-            __syncthreads();
 
 #pragma unroll
             for (int pb = 0; pb < PB; ++pb) {
                 const int i = wave * (PB * 16) + pb * 16 + (lane & 15);
-                const float *rec = recs + i * RS;
-                int gidx[NC];
+                const acc4 r = geo[tl * BPX + i];
+                Point<DIM, float> pt;
+#pragma unroll
+                for (int a = 0; a < DIM; ++a) {
+                    pt.pos[a] = r[a];
+                    pt.base[a] = (int)r[a];   // exact: without offsets the position is an integer
+                }
+                const AxisW<DIM, float> aw = axis_weights<DIM, float>(g, pt, deformable);
+                const float mk = r[3];
+                int gidx[NC], loc[NC];
                 float w[NC];
 #pragma unroll
                 for (int k = 0; k < NC; ++k) {
-                    gidx[k] = __float_as_int(rec[k]);
-                    w[k] = rec[2 * NC + k];
+                    int idx;
+                    bool v;
+                    corner_at<DIM, float>(g, aw, k, idx, v);
+                    gidx[k] = v ? idx : -1;
+                    w[k] = v ? corner_weight<DIM, float>(aw, k) : 0.f;
+                    bool in = v && wt.cells > 0;
+                    int lin = 0;
+#pragma unroll
+                    for (int a = 0; a < DIM; ++a) {
+                        const int e = 3 - DIM + a;
+                        const int l = aw.lo[a] + corner_bit<DIM>(k, a) - org[e];
+                        in = in && l >= 0 && l < wt.WE[e];
+                        lin = lin * wt.WE[e] + l;
+                    }
+                    loc[k] = in ? lin : -1;
                 }
-                const float mk = rec[3 * NC + DIM];
                 const acc4 gv = gt[pb];
 
                 if constexpr (COORD) {
-                    AxisW<DIM, float> aw;
-#pragma unroll
-                    for (int a = 0; a < DIM; ++a) aw.fh[a] = rec[3 * NC + a];
-                    const bool inside = rec[3 * NC + DIM + 1] != 0.f;
-                    Vec4<float> xv[NC];
+                    acc4 xv[NC];
 #pragma unroll
                     for (int k = 0; k < NC; ++k) {
-                        if (gidx[k] >= 0 && cq_ok)
-                            xv[k] = load4<float>(xcl + ((size_t)b * g.Sn + gidx[k]) * g.C + cg0 + mq);
-                        else
-                            xv[k] = {0.f, 0.f, 0.f, 0.f};
+                        xv[k] = acc4{0.f, 0.f, 0.f, 0.f};
+                        if (loc[k] >= 0)
+                            xv[k] = *reinterpret_cast<const acc4 *>(xwin + loc[k] * XS + mq);
+                        else if (gidx[k] >= 0 && cq_ok)
+                            xv[k] = *reinterpret_cast<const acc4 *>(xb + (size_t)gidx[k] * g.C + mq);
                     }
                     float qv[DIM + 1];
 #pragma unroll
                     for (int a = 0; a < DIM; ++a) {
-                        Vec4<float> d = {0.f, 0.f, 0.f, 0.f};
+                        acc4 d = acc4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                        for (int k = 0; k < NC; ++k) {
-                            const float dw = corner_dweight<DIM, float>(aw, k, a);
-                            d.x += dw * xv[k].x;
-                            d.y += dw * xv[k].y;
-                            d.z += dw * xv[k].z;
-                            d.w += dw * xv[k].w;
-                        }
-                        qv[a] = mk * (gv[0] * d.x + gv[1] * d.y + gv[2] * d.z + gv[3] * d.w);
+                        for (int k = 0; k < NC; ++k) d += corner_dweight<DIM, float>(aw, k, a) * xv[k];
+                        qv[a] = mk * (gv[0] * d[0] + gv[1] * d[1] + gv[2] * d[2] + gv[3] * d[3]);
                     }
                     {
-                        Vec4<float> sv = {0.f, 0.f, 0.f, 0.f};
-                        if (inside) {
+                        acc4 sv = acc4{0.f, 0.f, 0.f, 0.f};
+                        if (aw.inside) {
 #pragma unroll
-                            for (int k = 0; k < NC; ++k) {
-                                sv.x += w[k] * xv[k].x;
-                                sv.y += w[k] * xv[k].y;
-                                sv.z += w[k] * xv[k].z;
-                                sv.w += w[k] * xv[k].w;
-                            }
+                            for (int k = 0; k < NC; ++k) sv += w[k] * xv[k];
                         }
-                        qv[DIM] = gv[0] * sv.x + gv[1] * sv.y + gv[2] * sv.z + gv[3] * sv.w;
+                        qv[DIM] = gv[0] * sv[0] + gv[1] * sv[1] + gv[2] * sv[2] + gv[3] * sv[3];
                     }
 #pragma unroll
                     for (int a = 0; a <= DIM; ++a) {
                         qv[a] += __shfl_xor(qv[a], 16);
                         qv[a] += __shfl_xor(qv[a], 32);
                     }
-                    const int p = tile_pixel(i);
+                    const int p = zp[pb];
                     if (q == 0 && p >= 0) {
                         if (deformable) {
 #pragma unroll
@@ -377,10 +398,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
 #pragma unroll
                         for (int k = 0; k < NC; ++k) {
                             if (gidx[k] < 0) continue;
-                            const int loc = use_window ? __float_as_int(rec[NC + k]) : -1;
                             const float s = mk * w[k];
-                            if (loc >= 0) {
-                                unsigned int *dst = reinterpret_cast<unsigned int *>(win + loc * CS + mq);
+                            if (use_window && loc[k] >= 0) {
+                                unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + loc[k] * CS + mq);
 #pragma unroll
                                 for (int v = 0; v < 4; ++v)
                                     atomicAdd(dst + v, (unsigned int)__float2int_rn(ldexpf(s * gv[v], sexp[v])));
@@ -393,8 +413,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                     }
                 }
             }
-            __syncthreads();   // the geometry table is rewritten for the next tap
         }
+        __syncthreads();   // all waves done with the geometry table and the window
 
         // ---- flush the window: one float atomic per non-zero (cell, channel) ----------
         if (SCATTER && use_window) {
@@ -402,19 +422,14 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
             const int se = scl[c];
             float *gbase = gx_cl + (size_t)b * g.Sn * g.C + cg0 + c;
             for (int cell = tid >> 4; cell < wt.cells; cell += NT / 16) {
-                const int iv = win[cell * CS + c];
+                const int iv = iwin[cell * CS + c];
                 if (iv == 0) continue;
-                win[cell * CS + c] = 0;   // ready for the next pass
+                iwin[cell * CS + c] = 0;   // ready for the next pass
                 if (c0 + c >= g.Cg) continue;
-                const float v = ldexpf((float)iv, -se);
-                const int lx = cell % wt.WE[2];
-                const int r = cell / wt.WE[2];
-                const int ly = r % wt.WE[1];
-                const int lz = r / wt.WE[1];
-                const int sz = org[0] + lz, sy = org[1] + ly, sx = org[2] + lx;
                 // only valid corners write the window, so a non-zero cell lies inside the grid
-                if (sz < 0 || sz >= g.S[0] || sy < 0 || sy >= g.S[1] || sx < 0 || sx >= g.S[2]) continue;
-                atomic_add(gbase + (size_t)((sz * g.S[1] + sy) * g.S[2] + sx) * g.C, v);
+                const int si = cell_index(cell);
+                if (si < 0) continue;
+                atomic_add(gbase + (size_t)si * g.C, ldexpf((float)iv, -se));
             }
             __syncthreads();   // window cleared before the next pass scatters into it
         }
@@ -443,15 +458,15 @@ __global__ void weight_win_kernel(const T *__restrict__ w, float *__restrict__ o
     }
 }
 
-template <int DIM> size_t lds_bytes(const WinTiles &t) {
-    return ((size_t)fixed_floats<DIM>() + (size_t)t.cells * CS) * sizeof(float);
+template <bool SCATTER, bool COORD> size_t lds_bytes(const WinTiles &t) {
+    return ((size_t)FIXED_WORDS + (size_t)t.cells * ((SCATTER ? CS : 0) + (COORD ? XS : 0))) * sizeof(float);
 }
 
 template <int DIM, typename T, bool SCATTER, bool COORD>
 hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void *wchunks, const void *xcl,
                     const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
     auto kern = bwd_data_win_kernel<DIM, T, SCATTER, COORD>;
-    const size_t lds = lds_bytes<DIM>(tl);
+    const size_t lds = lds_bytes<SCATTER, COORD>(tl);
     static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -537,10 +552,10 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter) {
     // R per used axis, shrunk until it fits the LDS budget
     int need[3] = {1, 1, 1};
     for (int e = 3 - dim; e < 3; ++e) need[e] = (box[e] - 1) * g.st[e] + (g.K[e] - 1) * g.dil[e] + 2;
-    const size_t fixed_bytes = (dim == 3 ? (size_t)fixed_floats<3>()
-                                         : (dim == 2 ? (size_t)fixed_floats<2>() : (size_t)fixed_floats<1>())) *
-                               sizeof(float);
-    const long long max_cells = scatter ? (long long)((WIN_LDS_TARGET - fixed_bytes) / (CS * sizeof(float))) : 0;
+    // per window cell: the fixed-point accumulators (scatter) and the X values (offset/mask
+    // gradients); the plan is sized for both so that one plan serves every launch
+    (void)scatter;
+    const long long max_cells = (long long)((WIN_LDS_TARGET - FIXED_WORDS * sizeof(float)) / ((CS + XS) * sizeof(float)));
     int R = 0;
     t.cells = 0;
     if (max_cells > 0) {
