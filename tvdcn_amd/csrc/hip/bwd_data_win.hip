@@ -35,20 +35,20 @@
 //   * The window (sampled-grid box around the tile's undeformed footprint plus a
 //     margin R per axis) is flushed after each pass: one float atomic per
 //     non-zero (cell, channel), 16 consecutive channels per cell.
-#include "kernels.h"
+#include "window.h"
 
 namespace tvdcn_hip {
 namespace {
 
+using namespace win;
+
 constexpr int NW = 8;             // waves per workgroup (two per SIMD)
 constexpr int NT = 64 * NW;       // threads per workgroup
-constexpr int PB = 2;             // 16-pixel blocks per wave
-constexpr int BPX = NW * PB * 16; // column pixels per tile (256)
-constexpr int BC = 16;            // sampled-side channels per tile
+constexpr int PB = 2;             // 16-pixel blocks per wave (NW * PB * 16 = BPX)
 constexpr int BM = 16;            // GEMM-side channels per K step
 constexpr int CS = BC + 1;        // fixed-point window cell stride (odd: spreads the LDS banks)
-constexpr int XS = BC + 4;        // X window cell stride (16-byte quads)
 constexpr int FIX_BITS = 29;      // fixed-point headroom: |cell sum| * 2^s_c < 2^29
+static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
 
 // LDS words ahead of the windows: geometry table [WIN_TMAX][BPX] x (position, mask),
 // per-wave channel bounds, scale exponents
@@ -62,13 +62,12 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                     float *__restrict__ gx_cl, float *__restrict__ goff, float *__restrict__ gmask) {
     constexpr int NC = 1 << DIM;
     constexpr int TMAX = WIN_TMAX;
-    typedef f32x4 acc4;
 
     extern __shared__ float smem[];
-    acc4 *geo = reinterpret_cast<acc4 *>(smem);                // [TMAX][BPX]: pos[0..DIM), mask in .w
+    acc4 *geo = reinterpret_cast<acc4 *>(smem);                // [TMAX][BPX] sampling table (window.h)
     float *bsum = smem + GEO_WORDS;                            // [NW][BC] partial bounds
     int *scl = reinterpret_cast<int *>(bsum + NW * BC);        // [BC] scale exponents, [BC] = non-finite flag
-    float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X values (COORD)
+    float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X window (COORD)
     int *iwin = reinterpret_cast<int *>(xwin + (COORD ? wt.cells * XS : 0));   // [cells][CS] fixed point
 
     const int tid = threadIdx.x;
@@ -77,64 +76,21 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
     const int q = lane >> 4;
     const int mq = 4 * q;
 
-    // ---- tile coordinates ------------------------------------------------------
+    // ---- tile: one spatial box x one 16-channel slice --------------------------------
     int L = xcd_remap(blockIdx.x, gridDim.x);
     const int ct = L % wt.c_tiles;
     L /= wt.c_tiles;
-    int tcoord[3];
-    tcoord[2] = L % wt.ntile[2];
-    L /= wt.ntile[2];
-    tcoord[1] = L % wt.ntile[1];
-    L /= wt.ntile[1];
-    tcoord[0] = L % wt.ntile[0];
-    L /= wt.ntile[0];
-    const int b = L % g.B;
-    const int grp = L / g.B;
-    int p0[3], org[3];
-#pragma unroll
-    for (int e = 0; e < 3; ++e) {
-        p0[e] = tcoord[e] * wt.box[e];
-        org[e] = p0[e] * g.st[e] - g.pad[e] - wt.R[e];
-    }
-    const int c0 = ct * BC;                      // first channel of the tile within the group
-    const int cg0 = grp * g.Cg + c0;             // first global sampled-side channel
-    const int ogu = g.og ? cg0 / g.cpo : 0;      // the tile's offset / mask group (uniform)
-    const int mgu = g.mg ? cg0 / g.cpm : 0;
+    const int n_sp = g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2];
+    Tile tile;
+    tile.init(g, wt, L % n_sp, ct, L / n_sp);
+    const int b = tile.b, grp = tile.grp, c0 = tile.c0, cg0 = tile.cg0, ogu = tile.ogu, mgu = tile.mgu;
     const bool deformable = offset != nullptr;
     const bool cq_ok = c0 + mq < g.Cg;           // Cg % 4 == 0: a channel quad is all in or all out
     const float *xb = xcl + (size_t)b * g.Sn * g.C + cg0;
 
-    // pixel `i` of the tile (0..255) -> column pixel index p (or -1 outside the grid)
-    auto tile_pixel = [&](int i) {
-        const int iz = i >> wt.lbxy;
-        const int iy = (i >> wt.lbx) & (wt.box[1] - 1);
-        const int ix = i & (wt.box[2] - 1);
-        const int pz = p0[0] + iz, py = p0[1] + iy, px = p0[2] + ix;
-        if (pz >= g.P[0] || py >= g.P[1] || px >= g.P[2]) return -1;
-        return (pz * g.P[1] + py) * g.P[2] + px;
-    };
-    // window cell -> flat sampled-grid index (or -1 outside the grid)
-    auto cell_index = [&](int cell) {
-        const int lx = cell % wt.WE[2];
-        const int r = cell / wt.WE[2];
-        const int ly = r % wt.WE[1];
-        const int lz = r / wt.WE[1];
-        const int sz = org[0] + lz, sy = org[1] + ly, sx = org[2] + lx;
-        if (sz < 0 || sz >= g.S[0] || sy < 0 || sy >= g.S[1] || sx < 0 || sx >= g.S[2]) return -1;
-        return (sz * g.S[1] + sy) * g.S[2] + sx;
-    };
-
     // ---- per-tile LDS state: X window (read by the offset/mask gradients), zeroed
     //      fixed-point window (scatter)
-    if constexpr (COORD) {
-        for (int e = tid; e < wt.cells * 4; e += NT) {
-            const int cell = e >> 2, qd = e & 3;
-            const int si = cell_index(cell);
-            acc4 v = acc4{0.f, 0.f, 0.f, 0.f};
-            if (si >= 0 && c0 + 4 * qd < g.Cg) v = *reinterpret_cast<const acc4 *>(xb + (size_t)si * g.C + 4 * qd);
-            *reinterpret_cast<acc4 *>(xwin + cell * XS + 4 * qd) = v;
-        }
-    }
+    if constexpr (COORD) fill_xwin(g, wt, tile, xb, xwin, tid, NT);
     if constexpr (SCATTER) {
         for (int i = tid; i < wt.cells * CS; i += NT) iwin[i] = 0;
     }
@@ -147,7 +103,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
     const T *zb[PB];
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
-        zp[pb] = tile_pixel(wave * (PB * 16) + pb * 16 + (lane & 15));
+        zp[pb] = tile.pixel(g, wt, wave * (PB * 16) + pb * 16 + (lane & 15));
         zb[pb] = z + ((size_t)b * g.M + (size_t)grp * g.Mg) * g.Pn + (zp[pb] < 0 ? 0 : zp[pb]);
     }
     // Loads are unconditional, from clamped (valid) addresses, so that a prefetch is
@@ -180,19 +136,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
     for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
         const int ntaps = min(wt.tpp, g.Kn - t0);
 
-        // ---- sampling positions and masks of the pass, one (tap, pixel) per thread ----
-        for (int e = tid; e < ntaps * BPX; e += NT) {
-            const int tl = e / BPX, i = e % BPX;
-            const int p = tile_pixel(i);
-            acc4 r = acc4{-4.f, -4.f, -4.f, 0.f};   // outside the grid: no valid corner, mask 0
-            if (p >= 0) {
-                const Point<DIM, float> pt = sample_point<DIM, float, T>(g, offset, b, p, t0 + tl, ogu);
-#pragma unroll
-                for (int a = 0; a < DIM; ++a) r[a] = pt.pos[a];
-                r[3] = mask_at<float, T>(g, mask, b, mgu, t0 + tl, p);
-            }
-            geo[tl * BPX + i] = r;
-        }
+        // ---- sampling table of the pass, one (tap, pixel) per thread ------------------
+        fill_geo<DIM, T>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
 
         acc4 acc[TMAX][PB];
 #pragma unroll
@@ -263,7 +208,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
 #pragma unroll
                 for (int tp = 0; tp < TMAX; ++tp) {
                     if (tp < ntaps && zp[pb] >= 0) {
-                        const float mk = fabsf(geo[tp * BPX + i][3]);
+                        const float mk = fabsf(rec_mask<DIM>(geo[tp * BPX + i]));
 #pragma unroll
                         for (int v = 0; v < 4; ++v) part[v] += fabsf(acc[tp][pb][v]) * mk;
                     }
@@ -319,55 +264,95 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
             for (int pb = 0; pb < PB; ++pb) {
                 const int i = wave * (PB * 16) + pb * 16 + (lane & 15);
                 const acc4 r = geo[tl * BPX + i];
-                Point<DIM, float> pt;
-#pragma unroll
-                for (int a = 0; a < DIM; ++a) {
-                    pt.pos[a] = r[a];
-                    pt.base[a] = (int)r[a];   // exact: without offsets the position is an integer
-                }
-                const AxisW<DIM, float> aw = axis_weights<DIM, float>(g, pt, deformable);
-                const float mk = r[3];
-                int gidx[NC], loc[NC];
-                float w[NC];
-#pragma unroll
-                for (int k = 0; k < NC; ++k) {
-                    int idx;
-                    bool v;
-                    corner_at<DIM, float>(g, aw, k, idx, v);
-                    gidx[k] = v ? idx : -1;
-                    w[k] = v ? corner_weight<DIM, float>(aw, k) : 0.f;
-                    bool in = v && wt.cells > 0;
-                    int lin = 0;
-#pragma unroll
-                    for (int a = 0; a < DIM; ++a) {
-                        const int e = 3 - DIM + a;
-                        const int l = aw.lo[a] + corner_bit<DIM>(k, a) - org[e];
-                        in = in && l >= 0 && l < wt.WE[e];
-                        lin = lin * wt.WE[e] + l;
-                    }
-                    loc[k] = in ? lin : -1;
-                }
+                const float mk = rec_mask<DIM>(r);
                 const acc4 gv = gt[pb];
-
-                if constexpr (COORD) {
-                    acc4 xv[NC];
+                const int fc = rec_fast_cell<DIM>(r);
+                float qv[DIM + 1];
+                if (DIM < 3 && fc >= 0 && (!SCATTER || use_window)) {
+                    // fast path: every corner cell is in the window (zeros / dropped
+                    // outside the grid), plain bilinear formulas
+                    const float fx = r[DIM - 1] - floorf(r[DIM - 1]);
+                    const float fy = DIM == 2 ? r[0] - floorf(r[0]) : 0.f;
+                    constexpr int NF = DIM == 2 ? 4 : 2;
+                    int cell[NF];
+                    float w[NF];
+                    cell[0] = fc;
+                    cell[1] = fc + 1;
+                    if constexpr (DIM == 2) {
+                        cell[2] = fc + wt.WE[2];
+                        cell[3] = fc + wt.WE[2] + 1;
+                        w[0] = (1.f - fy) * (1.f - fx);
+                        w[1] = (1.f - fy) * fx;
+                        w[2] = fy * (1.f - fx);
+                        w[3] = fy * fx;
+                    } else {
+                        w[0] = 1.f - fx;
+                        w[1] = fx;
+                    }
+                    if constexpr (COORD) {
+                        acc4 x[NF];
+#pragma unroll
+                        for (int k = 0; k < NF; ++k) x[k] = *reinterpret_cast<const acc4 *>(xwin + cell[k] * XS + mq);
+                        acc4 sv = w[0] * x[0];
+#pragma unroll
+                        for (int k = 1; k < NF; ++k) sv += w[k] * x[k];
+                        acc4 d[DIM];
+                        if constexpr (DIM == 2) {
+                            d[0] = (1.f - fx) * (x[2] - x[0]) + fx * (x[3] - x[1]);   // d/dy
+                            d[1] = (1.f - fy) * (x[1] - x[0]) + fy * (x[3] - x[2]);   // d/dx
+                        } else {
+                            d[0] = x[1] - x[0];
+                        }
+#pragma unroll
+                        for (int a = 0; a < DIM; ++a)
+                            qv[a] = mk * (gv[0] * d[a][0] + gv[1] * d[a][1] + gv[2] * d[a][2] + gv[3] * d[a][3]);
+                        qv[DIM] = gv[0] * sv[0] + gv[1] * sv[1] + gv[2] * sv[2] + gv[3] * sv[3];
+                    }
+                    if constexpr (SCATTER) {
+                        if (cq_ok) {
+#pragma unroll
+                            for (int k = 0; k < NF; ++k) {
+                                const float s = mk * w[k];
+                                unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + cell[k] * CS + mq);
+#pragma unroll
+                                for (int v = 0; v < 4; ++v)
+                                    atomicAdd(dst + v, (unsigned int)__float2int_rn(ldexpf(s * gv[v], sexp[v])));
+                            }
+                        }
+                    }
+                } else {
+                    // general path: per-corner validity, window membership and global fallback
+                    const AxisW<DIM, float> aw = record_weights<DIM>(g, r, deformable);
+                    int gidx[NC], loc[NC];
+                    float w[NC];
 #pragma unroll
                     for (int k = 0; k < NC; ++k) {
-                        xv[k] = acc4{0.f, 0.f, 0.f, 0.f};
-                        if (loc[k] >= 0)
-                            xv[k] = *reinterpret_cast<const acc4 *>(xwin + loc[k] * XS + mq);
-                        else if (gidx[k] >= 0 && cq_ok)
-                            xv[k] = *reinterpret_cast<const acc4 *>(xb + (size_t)gidx[k] * g.C + mq);
+                        int idx;
+                        bool v;
+                        corner_at<DIM, float>(g, aw, k, idx, v);
+                        gidx[k] = v ? idx : -1;
+                        w[k] = v ? corner_weight<DIM, float>(aw, k) : 0.f;
+                        loc[k] = v ? tile.corner_cell<DIM>(wt, aw, k) : -1;
                     }
-                    float qv[DIM + 1];
+                    if constexpr (COORD) {
+                        acc4 xv[NC];
 #pragma unroll
-                    for (int a = 0; a < DIM; ++a) {
-                        acc4 d = acc4{0.f, 0.f, 0.f, 0.f};
+                        for (int k = 0; k < NC; ++k) {
+                            // LDS read unconditional (clamped), global read in its own branch
+                            xv[k] = *reinterpret_cast<const acc4 *>(xwin + max(loc[k], 0) * XS + mq);
+                            if (loc[k] < 0) {
+                                xv[k] = acc4{0.f, 0.f, 0.f, 0.f};
+                                if (gidx[k] >= 0 && cq_ok)
+                                    xv[k] = *reinterpret_cast<const acc4 *>(xb + (size_t)gidx[k] * g.C + mq);
+                            }
+                        }
 #pragma unroll
-                        for (int k = 0; k < NC; ++k) d += corner_dweight<DIM, float>(aw, k, a) * xv[k];
-                        qv[a] = mk * (gv[0] * d[0] + gv[1] * d[1] + gv[2] * d[2] + gv[3] * d[3]);
-                    }
-                    {
+                        for (int a = 0; a < DIM; ++a) {
+                            acc4 d = acc4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int k = 0; k < NC; ++k) d += corner_dweight<DIM, float>(aw, k, a) * xv[k];
+                            qv[a] = mk * (gv[0] * d[0] + gv[1] * d[1] + gv[2] * d[2] + gv[3] * d[3]);
+                        }
                         acc4 sv = acc4{0.f, 0.f, 0.f, 0.f};
                         if (aw.inside) {
 #pragma unroll
@@ -375,6 +360,29 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                         }
                         qv[DIM] = gv[0] * sv[0] + gv[1] * sv[1] + gv[2] * sv[2] + gv[3] * sv[3];
                     }
+                    if constexpr (SCATTER) {
+                        if (cq_ok) {
+                            float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+#pragma unroll
+                            for (int k = 0; k < NC; ++k) {
+                                if (gidx[k] < 0) continue;
+                                const float s = mk * w[k];
+                                if (use_window && loc[k] >= 0) {
+                                    unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + loc[k] * CS + mq);
+#pragma unroll
+                                    for (int v = 0; v < 4; ++v)
+                                        atomicAdd(dst + v, (unsigned int)__float2int_rn(ldexpf(s * gv[v], sexp[v])));
+                                } else {
+                                    float *dst = gdst + (size_t)gidx[k] * g.C;
+#pragma unroll
+                                    for (int v = 0; v < 4; ++v) atomic_add(dst + v, s * gv[v]);
+                                }
+                            }
+                        }
+                    }
+                }
+
+                if constexpr (COORD) {
 #pragma unroll
                     for (int a = 0; a <= DIM; ++a) {
                         qv[a] += __shfl_xor(qv[a], 16);
@@ -389,27 +397,6 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                         }
                         if (mask != nullptr)
                             atomic_add(gmask + (((size_t)b * g.mg + mgu) * g.Kn + t) * g.Pn + p, qv[DIM]);
-                    }
-                }
-
-                if constexpr (SCATTER) {
-                    if (cq_ok) {
-                        float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
-#pragma unroll
-                        for (int k = 0; k < NC; ++k) {
-                            if (gidx[k] < 0) continue;
-                            const float s = mk * w[k];
-                            if (use_window && loc[k] >= 0) {
-                                unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + loc[k] * CS + mq);
-#pragma unroll
-                                for (int v = 0; v < 4; ++v)
-                                    atomicAdd(dst + v, (unsigned int)__float2int_rn(ldexpf(s * gv[v], sexp[v])));
-                            } else {
-                                float *dst = gdst + (size_t)gidx[k] * g.C;
-#pragma unroll
-                                for (int v = 0; v < 4; ++v) atomic_add(dst + v, s * gv[v]);
-                            }
-                        }
                     }
                 }
             }
@@ -427,7 +414,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                 iwin[cell * CS + c] = 0;   // ready for the next pass
                 if (c0 + c >= g.Cg) continue;
                 // only valid corners write the window, so a non-zero cell lies inside the grid
-                const int si = cell_index(cell);
+                const int si = tile.cell_index(g, wt, cell);
                 if (si < 0) continue;
                 atomic_add(gbase + (size_t)si * g.C, ldexpf((float)iv, -se));
             }

@@ -298,6 +298,15 @@ __global__ void __launch_bounds__(256) weight_reduce_kernel(const A *__restrict_
     }
 }
 
+template <typename T, typename A>
+hipError_t launch_reduce(const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s) {
+    const size_t n = (size_t)g.G * g.Kn * g.Mg * g.Cg;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL((weight_reduce_kernel<T, A>), dim3(blocks), dim3(256), 0, s, static_cast<const A *>(part),
+                       static_cast<T *>(gw), k_splits, g.G, g.Kn, g.Mg, g.Cg);
+    return hipGetLastError();
+}
+
 template <int DIM, typename T, typename A, int WAVES, bool VEC4>
 hipError_t launch_t(const Geo &g, const WeightTiles &tl, const void *z, const void *xcl, const void *offset,
                     const void *mask, void *part, hipStream_t s) {
@@ -340,11 +349,7 @@ hipError_t launch_d(int dim, const Geo &g, const WeightTiles &tl, const void *z,
         case 3: e = launch_w<3, T, A>(g, tl, z, xcl, offset, mask, part, s); break;
     }
     if (e != hipSuccess) return e;
-    const size_t n = (size_t)g.G * g.Kn * g.Mg * g.Cg;
-    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
-    hipLaunchKernelGGL((weight_reduce_kernel<T, A>), dim3(blocks), dim3(256), 0, s, static_cast<const A *>(part),
-                       static_cast<T *>(gw), tl.k_splits, g.G, g.Kn, g.Mg, g.Cg);
-    return hipGetLastError();
+    return launch_reduce<T, A>(g, tl.k_splits, part, gw, s);
 }
 
 }  // namespace
@@ -370,6 +375,16 @@ WeightTiles plan_weight(const Geo &g, int dtype) {
     t.k_splits = g.NP > 0 ? (int)((g.NP + chunk - 1) / chunk) : 1;
     t.part_elems = (size_t)t.k_splits * g.G * g.Kn * g.Mg * g.Cg;
     return t;
+}
+
+hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s) {
+    switch (dtype) {
+        case kF32: return launch_reduce<float, float>(g, k_splits, part, gw, s);
+        case kF64: return launch_reduce<double, double>(g, k_splits, part, gw, s);
+        case kF16: return launch_reduce<__half, float>(g, k_splits, part, gw, s);
+        case kBF16: return launch_reduce<__hip_bfloat16, float>(g, k_splits, part, gw, s);
+    }
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_bwd_weight(int dtype, int dim, const Geo &g, const WeightTiles &t, const void *z, const void *xcl,

@@ -1,0 +1,286 @@
+// Family Wt, windowed variant: weight gradient over tiles whose sampled values are
+// formed from an LDS window.
+//
+//   dW[m][c][t] = sum_{b,p} Z[b][m][p] * mask * bilinear(X[b][c], pos(b, og(c), t, p))
+//
+// Replaces the reference's im2col recompute + grad_weight addmm_
+// (tvdcn/csrc/ops/cuda/deform_conv2d_kernel.cpp:600-626; transposed
+// deform_conv_transpose2d_kernel.cpp:586-613; 1D/3D twins).
+//
+// Workgroup = (group, 16-channel slice, up to 256 GEMM-side rows, a run of spatial
+// tiles); eight waves, wave w owning 32 rows. The dW block [rows][16 c][taps of the
+// pass] stays in accumulators (72 registers per lane) across the whole run of tiles.
+// Per tile (a box of 256 column pixels of one image, see window.h) the sampling
+// table and the X window are filled once; then the tile is walked in 16-pixel
+// chunks: the sampled columns S[tap][c][px] of the next chunk are formed from the
+// window (LDS reads only, global loads for the rare corners outside it) into a
+// double-buffered LDS tile while the MFMAs of the current chunk run:
+//   A = Z[m][px] (4 consecutive pixels per lane, one 16-byte load when contiguous),
+//   B = S[px][c] of one tap, D = dW[m][c] of that tap.
+// At the end of the run the block is stored to a split slot of the workspace and
+// the splits are summed in a fixed order (deterministic).
+#include "window.h"
+
+namespace tvdcn_hip {
+namespace {
+
+using namespace win;
+
+constexpr int NW = 8;               // waves per workgroup
+constexpr int NT = 64 * NW;
+constexpr int MB = 2;               // 16-row blocks per wave
+constexpr int BMW = NW * MB * 16;   // rows per workgroup (256)
+constexpr int KP = 16;              // pixels per chunk
+constexpr int NCH = BPX / KP;       // chunks per tile
+constexpr int SS = KP + 4;          // S tile row stride (rows = (tap, channel))
+constexpr int TM = WIN_TMAX;
+
+constexpr int GEO_WORDS = TM * BPX * 4;
+constexpr int SBUF_WORDS = 2 * TM * BC * SS;
+
+template <int DIM, typename T>
+__global__ void __launch_bounds__(NT)
+bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const T *__restrict__ z,
+                      const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
+                      float *__restrict__ part) {
+    constexpr int NC = 1 << DIM;
+    extern __shared__ float smem[];
+    acc4 *geo = reinterpret_cast<acc4 *>(smem);         // [TM][BPX]
+    float *sbuf = smem + GEO_WORDS;                     // [2][TM * BC][SS]
+    float *xwin = smem + GEO_WORDS + SBUF_WORDS;        // [cells][XS]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int q = lane >> 4;
+
+    int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int ct = L % wt.c_tiles;
+    L /= wt.c_tiles;
+    const int mt = L % ww.m_tiles;
+    L /= ww.m_tiles;
+    const int split = L % ww.n_split;
+    const int grp = L / ww.n_split;
+    const int s_beg = split * ww.tiles_per_split;
+    const int s_end = min(ww.n_spatial, s_beg + ww.tiles_per_split);
+    const bool deformable = offset != nullptr;
+    const int mrow = mt * BMW + wave * (MB * 16);    // first row of this wave
+
+    // S-builder item of this thread: chunk pixel j, channel quad sq, taps st, st + 8, ...
+    const int sj = tid & 15, sq = (tid >> 4) & 3, st0 = tid >> 6;
+
+    for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
+        const int ntaps = min(wt.tpp, g.Kn - t0);
+
+        acc4 acc[MB][TM];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int tp = 0; tp < TM; ++tp) acc[mb][tp] = acc4{0.f, 0.f, 0.f, 0.f};
+
+        for (int s = s_beg; s < s_end; ++s) {
+            Tile tile;
+            tile.init(g, wt, s, ct, grp);
+            const float *xb = xcl + (size_t)tile.b * g.Sn * g.C + tile.cg0;
+            const bool cq_ok = tile.c0 + 4 * sq < g.Cg;
+            __syncthreads();   // previous tile done with the tables
+            fill_geo<DIM, T>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
+            fill_xwin(g, wt, tile, xb, xwin, tid, NT);
+            __syncthreads();
+
+            // S[tap][c][px] of chunk k into buffer bf
+            auto build_s = [&](int k, int bf) {
+                float *dst = sbuf + bf * (TM * BC * SS);
+                const int i = k * KP + sj;
+                for (int tl = st0; tl < ntaps; tl += NW) {
+                    const acc4 r = geo[tl * BPX + i];
+                    const int fc = rec_fast_cell<DIM>(r);
+                    acc4 sv;
+                    if (fc >= 0) {
+                        // every corner cell is in the window (zeros outside the grid)
+                        const float *xc = xwin + fc * XS + 4 * sq;
+                        const float fx = r[DIM - 1] - floorf(r[DIM - 1]);
+                        const acc4 x00 = *reinterpret_cast<const acc4 *>(xc);
+                        const acc4 x01 = *reinterpret_cast<const acc4 *>(xc + XS);
+                        if constexpr (DIM == 2) {
+                            const float fy = r[0] - floorf(r[0]);
+                            const acc4 x10 = *reinterpret_cast<const acc4 *>(xc + wt.WE[2] * XS);
+                            const acc4 x11 = *reinterpret_cast<const acc4 *>(xc + (wt.WE[2] + 1) * XS);
+                            sv = (1.f - fy) * ((1.f - fx) * x00 + fx * x01) + fy * ((1.f - fx) * x10 + fx * x11);
+                        } else {
+                            sv = (1.f - fx) * x00 + fx * x01;
+                        }
+                    } else {
+                        const AxisW<DIM, float> aw = record_weights<DIM>(g, r, deformable);
+                        sv = acc4{0.f, 0.f, 0.f, 0.f};
+                        if (aw.inside) {
+#pragma unroll
+                            for (int kk = 0; kk < NC; ++kk) {
+                                int idx;
+                                bool v;
+                                corner_at<DIM, float>(g, aw, kk, idx, v);
+                                if (!v) continue;
+                                const int cell = tile.corner_cell<DIM>(wt, aw, kk);
+                                // LDS read unconditional (clamped), global read in its own branch:
+                                // the two address spaces are never merged into one pointer
+                                acc4 x = *reinterpret_cast<const acc4 *>(xwin + max(cell, 0) * XS + 4 * sq);
+                                if (cell < 0) {
+                                    x = acc4{0.f, 0.f, 0.f, 0.f};
+                                    if (cq_ok) x = *reinterpret_cast<const acc4 *>(xb + (size_t)idx * g.C + 4 * sq);
+                                }
+                                sv += corner_weight<DIM, float>(aw, kk) * x;
+                            }
+                        }
+                    }
+                    sv *= rec_mask<DIM>(r);
+                    float *row = dst + (tl * BC + 4 * sq) * SS + sj;
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) row[v * SS] = sv[v];
+                }
+            };
+
+            // A operand: Z[m][4 consecutive chunk pixels], m = mrow + mb * 16 + lane % 16
+            int zp4[4];   // pixel of the lane's 4 chunk positions for the current chunk
+            auto load_a = [&](int k, acc4 (&za)[MB]) {
+                const int i0 = k * KP + 4 * q;
+                int p[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) p[u] = tile.pixel(g, wt, i0 + u);
+                const bool contig = ww.z_vec && p[0] >= 0 && p[3] == p[0] + 3;
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    const int m = min(mrow + mb * 16 + (lane & 15), g.Mg - 1);
+                    const T *zr = z + ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
+                    if (contig) {
+                        const Vec4<float> v = load4_t<float, T>(zr + p[0]);
+                        za[mb] = acc4{v.x, v.y, v.z, v.w};
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) za[mb][u] = p[u] >= 0 ? to_acc<float>(zr[p[u]]) : 0.f;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) zp4[u] = p[u];
+            };
+
+            acc4 za[MB], zn[MB];
+            load_a(0, za);
+            build_s(0, 0);
+            __syncthreads();
+            for (int k = 0; k < NCH; ++k) {
+                const int bf = k & 1;
+                const bool more = k + 1 < NCH;
+                // pixels outside the grid contribute nothing (their S is 0; Z is zeroed
+                // so that a non-finite value there cannot leak)
+                acc4 zc[MB];
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) zc[mb][u] = zp4[u] >= 0 ? za[mb][u] : 0.f;
+                }
+                if (more) load_a(k + 1, zn);
+                const float *sb = sbuf + bf * (TM * BC * SS) + (lane & 15) * SS + 4 * q;
+#pragma unroll
+                for (int tp = 0; tp < TM; ++tp) {
+                    if (tp < ntaps) {
+                        const acc4 bv = *reinterpret_cast<const acc4 *>(sb + tp * BC * SS);
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                            for (int mb = 0; mb < MB; ++mb) acc[mb][tp] = mfma16x16x4(zc[mb][kk], bv[kk], acc[mb][tp]);
+                    }
+                }
+                if (more) {
+                    build_s(k + 1, bf ^ 1);
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) za[mb] = zn[mb];
+                }
+                __syncthreads();
+            }
+        }
+
+        // this split's block: part[split][grp][t][m][c]
+#pragma unroll
+        for (int tp = 0; tp < TM; ++tp) {
+            if (tp >= ntaps) continue;
+            float *dst = part + (((size_t)split * g.G + grp) * g.Kn + t0 + tp) * g.Mg * (size_t)g.Cg;
+            const int c = ct * BC + (lane & 15);
+            if (c >= g.Cg) continue;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int m = mrow + mb * 16 + 4 * q + v;
+                    if (m < g.Mg) dst[(size_t)m * g.Cg + c] = acc[mb][tp][v];
+                }
+        }
+    }
+}
+
+template <int DIM, typename T>
+hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
+                    const void *offset, const void *mask, void *part, hipStream_t s) {
+    auto kern = bwd_weight_win_kernel<DIM, T>;
+    const size_t lds = ((size_t)GEO_WORDS + SBUF_WORDS + (size_t)wt.cells * XS) * sizeof(float);
+    static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)WIN_LDS_TARGET);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const long long blocks = (long long)g.G * ww.n_split * ww.m_tiles * wt.c_tiles;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, wt, ww, static_cast<const T *>(z),
+                       static_cast<const float *>(xcl), static_cast<const T *>(offset), static_cast<const T *>(mask),
+                       static_cast<float *>(part));
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
+                    const void *offset, const void *mask, void *part, hipStream_t s) {
+    switch (dim) {
+        case 1: return launch_k<1, T>(g, wt, ww, z, xcl, offset, mask, part, s);
+        case 2: return launch_k<2, T>(g, wt, ww, z, xcl, offset, mask, part, s);
+        case 3: return launch_k<3, T>(g, wt, ww, z, xcl, offset, mask, part, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+WeightWin plan_weight_win(const Geo &g, const WinTiles &wt) {
+    WeightWin w{};
+    w.ok = false;
+    // needs the windowed tiling and enough rows to keep the eight waves busy
+    if (!wt.ok || g.Mg < 128 || (size_t)GEO_WORDS * 4 + SBUF_WORDS * 4 + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
+        return w;
+    w.m_tiles = (g.Mg + BMW - 1) / BMW;
+    w.n_spatial = g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2];
+    const long long per_split_groups = (long long)g.G * w.m_tiles * wt.c_tiles;
+    // one workgroup per CU, about one wave of workgroups
+    long long splits = (256 + per_split_groups - 1) / per_split_groups;
+    if (splits > w.n_spatial) splits = w.n_spatial;
+    if (splits < 1) splits = 1;
+    w.tiles_per_split = (int)((w.n_spatial + splits - 1) / splits);
+    w.n_split = (w.n_spatial + w.tiles_per_split - 1) / w.tiles_per_split;
+    w.z_vec = g.P[2] % 4 == 0 && wt.box[2] >= 4;
+    w.part_elems = (size_t)w.n_split * g.G * g.Kn * g.Mg * g.Cg;
+    w.ok = g.B > 0;
+    return w;
+}
+
+hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
+                                 const void *z, const void *xcl, const void *offset, const void *mask, void *part,
+                                 void *gw, hipStream_t s) {
+    hipError_t e = hipErrorInvalidValue;
+    switch (dtype) {
+        case kF32: e = launch_d<float>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
+        case kF16: e = launch_d<__half>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
+        case kBF16: e = launch_d<__hip_bfloat16>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
+    }
+    if (e != hipSuccess) return e;
+    return launch_weight_reduce(dtype, g, ww.n_split, part, gw, s);
+}
+
+}  // namespace tvdcn_hip

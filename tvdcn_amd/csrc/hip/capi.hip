@@ -66,6 +66,7 @@ struct Plan {
     WinTiles wn_s;   // windowed data-gradient plan with the scatter (conv backward, transposed forward)
     WinTiles wn_c;   // the same without the scatter (transposed backward: offset/mask gradients only)
     WeightTiles wt;
+    WeightWin ww;    // windowed weight-gradient plan (over the wn_s tiling)
 };
 
 bool fits_int(int64_t v) { return v >= 0 && v <= (int64_t)INT_MAX; }
@@ -148,6 +149,7 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     pl.wn_s = plan_data_win(g, pl.dtype, pl.dim, true);
     pl.wn_c = plan_data_win(g, pl.dtype, pl.dim, false);
     pl.wt = plan_weight(g, pl.dtype);
+    pl.ww = plan_weight_win(g, pl.wn_s);
     return TVDCN_STATUS_SUCCESS;
 }
 
@@ -189,7 +191,7 @@ Layout layout(const Plan &pl, bool backward) {
             L.wf = take(wf_bytes);
         else
             L.cl_acc = take(cl_bytes);
-        L.wpart = take(align_up(pl.wt.part_elems * a));
+        L.wpart = take(align_up(pl.ww.ok ? pl.ww.part_elems * sizeof(float) : pl.wt.part_elems * a));
         if (!acc_is_storage(pl.dtype)) {
             if (g.og) L.goff_acc = take(align_up((size_t)g.B * g.og * g.Kn * pl.dim * g.Pn * a));
             if (g.mg) L.gmask_acc = take(align_up((size_t)g.B * g.mg * g.Kn * g.Pn * a));
@@ -426,8 +428,12 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, false, true, Z, wd, xcl, offset, mask,
                                                                         nullptr, goff, gmask, s));
         }
-        TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,
-                                                                    at(workspace, L.wpart), grad_weight, s));
+        if (pl.ww.ok)
+            TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight_win(dt, pl.dim, g, pl.wn_s, pl.ww, Z, xcl, offset,
+                                                                            mask, at(workspace, L.wpart), grad_weight, s));
+        else
+            TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,
+                                                                        at(workspace, L.wpart), grad_weight, s));
     }
     if (!direct) {
         if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, goff, grad_offset, n_goff, s));

@@ -47,7 +47,19 @@ struct WinTiles {
     size_t chunk_elems;  // floats of the re-laid-out weight
 };
 
+// Windowed weight-gradient kernel (bwd_weight_win.hip): workgroups own (group,
+// 16-channel slice, 256 rows) and a run of spatial tiles of the WinTiles tiling.
+struct WeightWin {
+    bool ok;
+    int m_tiles;         // 256-row blocks of the GEMM side
+    int n_spatial;       // spatial tiles (B x ntile0 x ntile1 x ntile2)
+    int tiles_per_split, n_split;
+    bool z_vec;          // 4 consecutive tile pixels are contiguous and 16-byte aligned
+    size_t part_elems;   // workspace floats for the split partials
+};
+
 FwdTiles plan_fwd(const Geo &g, int dtype);
+WeightWin plan_weight_win(const Geo &g, const WinTiles &wt);
 WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter);
 DataTiles plan_data(const Geo &g, int dtype);
 WeightTiles plan_weight(const Geo &g, int dtype);
@@ -76,6 +88,11 @@ hipError_t launch_weight_win_layout(int dtype, const Geo &g, const WinTiles &t, 
 hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
                                const void *z, const void *wchunks, const void *xcl, const void *offset,
                                const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s);
+hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
+                                 const void *z, const void *xcl, const void *offset, const void *mask, void *part,
+                                 void *gw, hipStream_t s);
+// gw (storage type, layout (M, Cg, Kn)) = sum over k_splits of part[ks][G][Kn][Mg][Cg]
+hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s);
 // writes split partials to `part` (WeightTiles::part_elems accumulator elements),
 // then reduces them into gw (storage type, layout (M, Cg, Kn))
 hipError_t launch_bwd_weight(int dtype, int dim, const Geo &g, const WeightTiles &t, const void *z, const void *xcl,
