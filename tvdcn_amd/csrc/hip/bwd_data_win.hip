@@ -407,17 +407,15 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
         if (SCATTER && use_window) {
             const int c = tid & 15;
             const int se = scl[c];
+            const bool c_ok = c0 + c < g.Cg;
             float *gbase = gx_cl + (size_t)b * g.Sn * g.C + cg0 + c;
-            for (int cell = tid >> 4; cell < wt.cells; cell += NT / 16) {
+            for_cells(g, wt, tile, tid >> 4, NT / 16, [&](int cell, int si) {
                 const int iv = iwin[cell * CS + c];
-                if (iv == 0) continue;
+                if (iv == 0) return;
                 iwin[cell * CS + c] = 0;   // ready for the next pass
-                if (c0 + c >= g.Cg) continue;
-                // only valid corners write the window, so a non-zero cell lies inside the grid
-                const int si = tile.cell_index(g, wt, cell);
-                if (si < 0) continue;
-                atomic_add(gbase + (size_t)si * g.C, ldexpf((float)iv, -se));
-            }
+                // window cells outside the grid hold only contributions of corners outside it
+                if (si >= 0 && c_ok) atomic_add(gbase + (size_t)si * g.C, ldexpf((float)iv, -se));
+            });
             __syncthreads();   // window cleared before the next pass scatters into it
         }
     }

@@ -147,16 +147,44 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
     }
 }
 
+// Walks window cells first, first + step, ... keeping (lz, ly, lx) incrementally (no
+// divisions per cell); f(cell, flat index in the sampled grid or -1 outside it).
+template <typename F>
+__device__ __forceinline__ void for_cells(const Geo &g, const WinTiles &wt, const Tile &tile, int first, int step, F &&f) {
+    int lx = first % wt.WE[2];
+    int r = first / wt.WE[2];
+    int ly = r % wt.WE[1];
+    int lz = r / wt.WE[1];
+    const int sx_step = step % wt.WE[2], sy_step = (step / wt.WE[2]) % wt.WE[1], sz_step = step / (wt.WE[2] * wt.WE[1]);
+    for (int cell = first; cell < wt.cells; cell += step) {
+        const int sz = tile.org[0] + lz, sy = tile.org[1] + ly, sx = tile.org[2] + lx;
+        const bool in = sz >= 0 && sz < g.S[0] && sy >= 0 && sy < g.S[1] && sx >= 0 && sx < g.S[2];
+        f(cell, in ? (sz * g.S[1] + sy) * g.S[2] + sx : -1);
+        lx += sx_step;
+        ly += sy_step;
+        lz += sz_step;
+        if (lx >= wt.WE[2]) {
+            lx -= wt.WE[2];
+            ++ly;
+        }
+        if (ly >= wt.WE[1]) {
+            ly -= wt.WE[1];
+            ++lz;
+        }
+    }
+}
+
 // X window: xwin[cell * XS + 4 * quad .. + 3] = channels c0 + 4 * quad .. of the cell
+// (threads take (cell, quad) pairs: nthreads must be a multiple of 4)
 __device__ __forceinline__ void fill_xwin(const Geo &g, const WinTiles &wt, const Tile &tile, const float *__restrict__ xb,
                                           float *xwin, int tid, int nthreads) {
-    for (int e = tid; e < wt.cells * 4; e += nthreads) {
-        const int cell = e >> 2, qd = e & 3;
-        const int si = tile.cell_index(g, wt, cell);
+    const int qd = tid & 3;
+    const bool q_ok = tile.c0 + 4 * qd < g.Cg;
+    for_cells(g, wt, tile, tid >> 2, nthreads >> 2, [&](int cell, int si) {
         acc4 v = acc4{0.f, 0.f, 0.f, 0.f};
-        if (si >= 0 && tile.c0 + 4 * qd < g.Cg) v = *reinterpret_cast<const acc4 *>(xb + (size_t)si * g.C + 4 * qd);
+        if (si >= 0 && q_ok) v = *reinterpret_cast<const acc4 *>(xb + (size_t)si * g.C + 4 * qd);
         *reinterpret_cast<acc4 *>(xwin + cell * XS + 4 * qd) = v;
-    }
+    });
 }
 
 // The sampling geometry of a geo record: the point (integer base for offset-free
