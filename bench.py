@@ -143,8 +143,8 @@ def kernel_rooflines(kern, batch=8):
 
 
 TRAFFIC_KERNELS = {"gather_gemm": "fwd_gather_gemm_kernel<2, float, float,",
-                   "data_grad": "bwd_data_kernel<2, float, float,",
-                   "weight_grad": "bwd_weight_kernel<2, float, float,"}
+                   "data_grad": "bwd_data_win_kernel<2, float, true, true>",
+                   "weight_grad": "bwd_weight_win_kernel<2, float>"}
 
 
 def load_traffic(family):

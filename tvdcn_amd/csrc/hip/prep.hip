@@ -102,24 +102,37 @@ __global__ void acc_to_storage_kernel(const A *__restrict__ a, T *__restrict__ o
         o[i] = from_acc<T, A>(a[i]);
 }
 
-// grad_bias[c] = sum_{b, s} gout[b][c][s]; one workgroup per channel
+// grad_bias[c] = sum_{b, s} gout[b][c][s]; one 1024-thread workgroup per channel,
+// four consecutive positions per load when rows are 4-aligned; per-thread partial sums
+// in a fixed order, then a fixed reduction tree (deterministic)
 template <typename T, typename A>
-__global__ void __launch_bounds__(256) bias_grad_kernel(const T *__restrict__ gout, T *__restrict__ gb, int B, int C,
-                                                        int S) {
-    __shared__ A red[256];
+__global__ void __launch_bounds__(1024) bias_grad_kernel(const T *__restrict__ gout, T *__restrict__ gb, int B, int C,
+                                                         int S) {
+    __shared__ A red[16];
     const int c = blockIdx.x;
+    const int tid = threadIdx.x;
+    const bool vec = sizeof(T) <= 4 && S % 4 == 0;
     A acc = A(0);
     for (int b = 0; b < B; ++b) {
         const T *row = gout + ((size_t)b * C + c) * S;
-        for (int s = threadIdx.x; s < S; s += 256) acc += to_acc<A>(row[s]);
+        if (vec) {
+            for (int s4 = tid; s4 < S / 4; s4 += 1024) {
+                const Vec4<A> v = load4_t<A, T>(row + 4 * s4);
+                acc += (v.x + v.y) + (v.z + v.w);
+            }
+        } else {
+            for (int s = tid; s < S; s += 1024) acc += to_acc<A>(row[s]);
+        }
     }
-    red[threadIdx.x] = acc;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) acc += __shfl_xor(acc, m);
+    if ((tid & 63) == 0) red[tid >> 6] = acc;
     __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-        __syncthreads();
+    if (tid == 0) {
+        A sum = A(0);
+        for (int w = 0; w < 16; ++w) sum += red[w];
+        gb[c] = from_acc<T, A>(sum);
     }
-    if (threadIdx.x == 0) gb[c] = from_acc<T, A>(red[0]);
 }
 
 unsigned grid_for(size_t n) {
@@ -218,7 +231,7 @@ hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int
     return by_dtype(dtype, [&](auto tv, auto av) {
         using T = decltype(tv);
         using A = decltype(av);
-        hipLaunchKernelGGL((bias_grad_kernel<T, A>), dim3(C), dim3(256), 0, s, static_cast<const T *>(gout),
+        hipLaunchKernelGGL((bias_grad_kernel<T, A>), dim3(C), dim3(1024), 0, s, static_cast<const T *>(gout),
                            static_cast<T *>(gbias), B, C, Sn);
         return hipGetLastError();
     });
