@@ -142,7 +142,7 @@ def kernel_rooflines(kern, batch=8):
     return out
 
 
-TRAFFIC_KERNELS = {"gather_gemm": "fwd_gather_gemm_kernel<2, float, float,",
+TRAFFIC_KERNELS = {"gather_gemm": "fwd_win_kernel<2, float>",
                    "data_grad": "bwd_data_win_kernel<2, float, true, true>",
                    "weight_grad": "bwd_weight_win_kernel<2, float>"}
 

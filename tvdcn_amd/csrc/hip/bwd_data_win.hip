@@ -497,6 +497,43 @@ int ilog2(int v) {
 
 }  // namespace
 
+WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_bytes, size_t cell_bytes,
+                    long long cell_cap) {
+    // window = undeformed footprint of the box (low and high corners) plus a margin R per
+    // used axis, the largest R (up to 8, 32 in 1D) whose LDS fits beside fixed_bytes and
+    // whose cell count stays within cell_cap (0: no cap)
+    WinTiles t = base;
+    int need[3] = {1, 1, 1};
+    for (int e = 3 - dim; e < 3; ++e) need[e] = (t.box[e] - 1) * g.st[e] + (g.K[e] - 1) * g.dil[e] + 2;
+    long long max_cells =
+        WIN_LDS_TARGET > fixed_bytes ? (long long)((WIN_LDS_TARGET - fixed_bytes) / cell_bytes) : 0;
+    if (cell_cap > 0 && max_cells > cell_cap) max_cells = cell_cap;
+    int R = 0;
+    t.cells = 0;
+    if (max_cells > 0) {
+        for (R = dim == 1 ? 32 : 8; R > -64; --R) {
+            long long cells = 1;
+            bool degenerate = false;
+            for (int e = 3 - dim; e < 3; ++e) {
+                const int ext = need[e] + 2 * R;
+                if (ext < 1) degenerate = true;
+                cells *= ext;
+            }
+            if (degenerate) break;
+            if (cells <= max_cells) {
+                t.cells = (int)cells;
+                break;
+            }
+        }
+    }
+    for (int e = 0; e < 3; ++e) {
+        const bool used = e >= 3 - dim;
+        t.R[e] = (used && t.cells) ? R : 0;
+        t.WE[e] = (used && t.cells) ? need[e] + 2 * R : 1;
+    }
+    return t;
+}
+
 WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter) {
     WinTiles t{};
     t.ok = false;
@@ -533,40 +570,10 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter) {
     t.lbxy = ilog2(box[1] * box[2]);
     t.c_tiles = (g.Cg + BC - 1) / BC;
     t.m_steps = (g.Mg + BM - 1) / BM;
-    // window: undeformed footprint of the box (low and high corners) plus a margin
-    // R per used axis, shrunk until it fits the LDS budget
-    int need[3] = {1, 1, 1};
-    for (int e = 3 - dim; e < 3; ++e) need[e] = (box[e] - 1) * g.st[e] + (g.K[e] - 1) * g.dil[e] + 2;
+    (void)scatter;
     // per window cell: the fixed-point accumulators (scatter) and the X values (offset/mask
     // gradients); the plan is sized for both so that one plan serves every launch
-    (void)scatter;
-    const long long max_cells = (long long)((WIN_LDS_TARGET - FIXED_WORDS * sizeof(float)) / ((CS + XS) * sizeof(float)));
-    int R = 0;
-    t.cells = 0;
-    if (max_cells > 0) {
-        for (R = dim == 1 ? 32 : 8; R > -64; --R) {
-            long long cells = 1;
-            bool degenerate = false;
-            for (int e = 3 - dim; e < 3; ++e) {
-                const int ext = need[e] + 2 * R;
-                if (ext < 1) degenerate = true;
-                cells *= ext;
-            }
-            if (degenerate) break;
-            if (cells <= max_cells) {
-                t.cells = (int)cells;
-                break;
-            }
-        }
-    }
-    for (int e = 0; e < 3; ++e) {
-        const bool used = e >= 3 - dim;
-        t.R[e] = (used && t.cells) ? R : 0;
-        t.WE[e] = (used && t.cells) ? need[e] + 2 * R : 1;
-    }
-    if (!t.cells) {
-        for (int e = 0; e < 3; ++e) t.WE[e] = 1;
-    }
+    t = win_resize(t, g, dim, FIXED_WORDS * sizeof(float), (CS + XS) * sizeof(float));
     const int npass = (g.Kn + WIN_TMAX - 1) / WIN_TMAX;
     t.tpp = (g.Kn + npass - 1) / npass;
     t.chunk_elems = (size_t)g.G * t.c_tiles * t.m_steps * g.Kn * BC * BM;

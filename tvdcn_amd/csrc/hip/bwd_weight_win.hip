@@ -249,6 +249,8 @@ hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &
 
 }  // namespace
 
+size_t weight_win_fixed_bytes() { return (size_t)(GEO_WORDS + SBUF_WORDS) * sizeof(float); }
+
 WeightWin plan_weight_win(const Geo &g, const WinTiles &wt) {
     WeightWin w{};
     w.ok = false;

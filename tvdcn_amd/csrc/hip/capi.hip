@@ -66,7 +66,10 @@ struct Plan {
     WinTiles wn_s;   // windowed data-gradient plan with the scatter (conv backward, transposed forward)
     WinTiles wn_c;   // the same without the scatter (transposed backward: offset/mask gradients only)
     WeightTiles wt;
-    WeightWin ww;    // windowed weight-gradient plan (over the wn_s tiling)
+    WinTiles wn_w;   // the wn_s tiling with the weight-gradient kernel's window margin
+    WinTiles wn_f;   // the wn_s tiling with the forward kernel's window margin
+    WeightWin ww;    // windowed weight-gradient plan (over wn_w)
+    FwdWin fw;       // windowed forward plan (over wn_f)
 };
 
 bool fits_int(int64_t v) { return v >= 0 && v <= (int64_t)INT_MAX; }
@@ -149,7 +152,10 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     pl.wn_s = plan_data_win(g, pl.dtype, pl.dim, true);
     pl.wn_c = plan_data_win(g, pl.dtype, pl.dim, false);
     pl.wt = plan_weight(g, pl.dtype);
-    pl.ww = plan_weight_win(g, pl.wn_s);
+    pl.wn_w = win_resize(pl.wn_s, g, pl.dim, weight_win_fixed_bytes(), x_window_cell_bytes());
+    pl.wn_f = win_resize(pl.wn_s, g, pl.dim, fwd_win_fixed_bytes(), x_window_cell_bytes(), fwd_win_max_cells());
+    pl.ww = plan_weight_win(g, pl.wn_w);
+    pl.fw = plan_fwd_win(g, pl.wn_f);
     return TVDCN_STATUS_SUCCESS;
 }
 
@@ -163,7 +169,9 @@ Layout layout(const Plan &pl, bool backward) {
     const Geo &g = pl.g;
     const size_t a = acc_size(pl.dtype);
     const size_t cl_bytes = align_up((size_t)g.B * g.Sn * g.C * a);
-    const size_t wf_bytes = align_up((size_t)g.G * g.Kn * pl.ft.Mg_pad * pl.ft.Cg_pad * a);
+    // forward weight layout Wf[G][Kn][Mg_pad][Cg_pad], padded for whichever forward kernel runs
+    const size_t wf_bytes = pl.fw.ok ? align_up((size_t)g.G * g.Kn * pl.fw.Mg_pad * pl.fw.Cg_pad * sizeof(float))
+                                     : align_up((size_t)g.G * g.Kn * pl.ft.Mg_pad * pl.ft.Cg_pad * a);
     // data-gradient weight: windowed-kernel chunks when eligible, else the [G][Kn][Cg][Mg] layout
     const size_t wd_bytes = pl.wn_s.ok ? align_up(pl.wn_s.chunk_elems * sizeof(float))
                                        : align_up((size_t)g.G * g.Kn * pl.dt.Mg_pad * pl.dt.Cg_pad * a);
@@ -333,8 +341,15 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
     if (!pl.transposed) {
         void *xcl = at(workspace, L.xcl), *wf = at(workspace, L.wf);
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
-        TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s, launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, bias, output, s));
+        if (pl.fw.ok) {
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.fw.Mg_pad, pl.fw.Cg_pad, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
+                         launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, bias, output, s));
+        } else {
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
+                         launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, bias, output, s));
+        }
     } else {
         void *wd = at(workspace, L.wd), *ycl = at(workspace, L.cl_acc);
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
@@ -418,9 +433,15 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_from_channels_last(dt, gx_cl, grad_input, nullptr, g.B, g.C, g.Sn, s));
         } else {
             void *wf = at(workspace, L.wf);
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
-            TVDCN_CHECK_HIP(
-                launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, nullptr, grad_input, s));
+            if (pl.fw.ok) {
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.fw.Mg_pad, pl.fw.Cg_pad, s));
+                TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
+                             launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, nullptr, grad_input, s));
+            } else {
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
+                TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
+                             launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, nullptr, grad_input, s));
+            }
             if (coord && pl.wn_c.ok)
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_c, false, true, Z, wd, xcl, offset,
                                                                             mask, nullptr, goff, gmask, s));
@@ -429,7 +450,7 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
                                                                         nullptr, goff, gmask, s));
         }
         if (pl.ww.ok)
-            TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight_win(dt, pl.dim, g, pl.wn_s, pl.ww, Z, xcl, offset,
+            TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight_win(dt, pl.dim, g, pl.wn_w, pl.ww, Z, xcl, offset,
                                                                             mask, at(workspace, L.wpart), grad_weight, s));
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,

@@ -1,0 +1,312 @@
+// Family F, windowed variant: the forward gather-GEMM with the sampled columns formed
+// from an LDS window of the sampled tensor.
+//
+//   Y[b][m][p] = bias[m] + sum_{t, c in group} W[m][c][t] * mask * bilinear(X[b][c], pos(b, og(c), t, p))
+//
+// Replaces the reference's im2col kernel + addmm_ pair
+// (tvdcn/csrc/ops/cuda/deform_conv2d_common_kernels.cu:138-256 and
+// deform_conv2d_kernel.cpp:341-380; 1D/3D twins); the columns are never written
+// to HBM. Also computes the transposed op's input gradient.
+//
+// Workgroup = (spatial tile of 256 column pixels, 128 GEMM-side rows); eight waves,
+// wave w owning 32 pixels x 128 rows (64 accumulators per lane). The reduction runs
+// over 16-channel slices x taps; per step (slice, tap) every lane forms its own MFMA
+// B fragment -- the sampled values of 4 channels of one of its pixels -- straight from
+// the X window (LDS) and the sampling table, one step ahead, while the MFMAs of the
+// current step run with A = W[m][c] (16-byte fragments of the re-laid-out weight, each
+// reloaded for the next step right after its last use). Waves own disjoint pixels, so
+// nothing is exchanged between them inside a slice: barriers only where the X window
+// of the next slice (prefetched into registers during the last step of the current
+// one) replaces the current one, and where the sampling table is rebuilt (when the
+// offset / mask group changes). See window.h for the tile / window machinery.
+#include "window.h"
+
+namespace tvdcn_hip {
+namespace {
+
+using namespace win;
+
+constexpr int NW = 8;               // waves per workgroup
+constexpr int NT = 64 * NW;
+constexpr int PB = 2;               // 16-pixel blocks per wave
+constexpr int MB = 8;               // 16-row blocks per wave (128 rows)
+constexpr int BMR = MB * 16;        // rows per workgroup
+constexpr int TM = WIN_TMAX;
+constexpr int XQ = 8;               // X window quads prefetched per thread (cells * 4 <= XQ * NT)
+static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
+
+constexpr int GEO_WORDS = TM * BPX * 4;
+
+template <int DIM, typename T>
+__global__ void __launch_bounds__(NT)
+fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__restrict__ xcl,
+               const float *__restrict__ wf, const T *__restrict__ offset, const T *__restrict__ mask,
+               const T *__restrict__ bias, T *__restrict__ y) {
+    constexpr int NC = 1 << DIM;
+    extern __shared__ float smem[];
+    acc4 *geo = reinterpret_cast<acc4 *>(smem);     // [TM][BPX]
+    float *xwin = smem + GEO_WORDS;                 // [cells][XS]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int q = lane >> 4;
+
+    int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int mt = L % fw.m_tiles;
+    L /= fw.m_tiles;
+    const int n_sp = g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2];
+    const int sp = L % n_sp;
+    const int grp = L / n_sp;
+    const bool deformable = offset != nullptr;
+    const int slices = (g.Cg + BC - 1) / BC;
+
+    Tile tile;
+    tile.init(g, wt, sp, 0, grp);
+    const float *xg = xcl + (size_t)tile.b * g.Sn * g.C + (size_t)grp * g.Cg;   // group's channel 0
+
+
+    // X window prefetch: quad e = tid + j * NT of the window (cell e / 4, quad e % 4). The
+    // cells (and their grid indices) are the same for every slice: resolved once.
+    int xsi[XQ];   // flat sampled-grid index of the thread's cells (-1: outside the grid / window)
+#pragma unroll
+    for (int j = 0; j < XQ; ++j) {
+        const int e = tid + j * NT;
+        xsi[j] = e < wt.cells * 4 ? tile.cell_index(g, wt, e >> 2) : -1;
+    }
+    acc4 xpre[XQ];
+    auto prefetch_x = [&](int cs) {
+        const float *xb = xg + cs * BC + 4 * (tid & 3);
+        const bool q_ok = cs * BC + 4 * (tid & 3) < g.Cg;   // quad of thread tid + j * NT is tid % 4
+#pragma unroll
+        for (int j = 0; j < XQ; ++j) {
+            xpre[j] = acc4{0.f, 0.f, 0.f, 0.f};
+            if (xsi[j] >= 0 && q_ok) xpre[j] = *reinterpret_cast<const acc4 *>(xb + (size_t)xsi[j] * g.C);
+        }
+    };
+    auto store_x = [&]() {
+#pragma unroll
+        for (int j = 0; j < XQ; ++j) {
+            const int e = tid + j * NT;
+            if (e < wt.cells * 4) *reinterpret_cast<acc4 *>(xwin + (e >> 2) * XS + 4 * (e & 3)) = xpre[j];
+        }
+    };
+
+    // B fragment of pixel block pb for (slice cs, tap tl of the pass): the sampled values of
+    // channels cs * 16 + 4 * (lane / 16) .. + 3 at pixel wave * 32 + pb * 16 + lane % 16
+    auto build_b = [&](int cs, int tl, acc4 (&bv)[PB]) {
+        const int qd = q;
+        const bool q_ok = cs * BC + 4 * qd < g.Cg;
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb) {
+            const acc4 r = geo[tl * BPX + wave * (PB * 16) + pb * 16 + (lane & 15)];
+            const int fc = rec_fast_cell<DIM>(r);
+            const float mk = rec_mask<DIM>(r);
+            acc4 sv;
+            if (fc >= 0) {
+                const float fx = r[DIM - 1] - floorf(r[DIM - 1]);
+                const float *xc = xwin + fc * XS + 4 * qd;
+                const acc4 x00 = *reinterpret_cast<const acc4 *>(xc);
+                const acc4 x01 = *reinterpret_cast<const acc4 *>(xc + XS);
+                if constexpr (DIM == 2) {
+                    const float fy = r[0] - floorf(r[0]);
+                    const acc4 x10 = *reinterpret_cast<const acc4 *>(xc + wt.WE[2] * XS);
+                    const acc4 x11 = *reinterpret_cast<const acc4 *>(xc + (wt.WE[2] + 1) * XS);
+                    sv = (1.f - fy) * ((1.f - fx) * x00 + fx * x01) + fy * ((1.f - fx) * x10 + fx * x11);
+                } else {
+                    sv = (1.f - fx) * x00 + fx * x01;
+                }
+            } else {
+                Point<DIM, float> pt;
+#pragma unroll
+                for (int a = 0; a < DIM; ++a) {
+                    pt.pos[a] = r[a];
+                    pt.base[a] = (int)r[a];
+                }
+                const AxisW<DIM, float> aw = axis_weights<DIM, float>(g, pt, deformable);
+                sv = acc4{0.f, 0.f, 0.f, 0.f};
+                if (aw.inside) {
+#pragma unroll
+                    for (int kk = 0; kk < NC; ++kk) {
+                        int idx;
+                        bool v;
+                        corner_at<DIM, float>(g, aw, kk, idx, v);
+                        if (!v) continue;
+                        const int cell = tile.corner_cell<DIM>(wt, aw, kk);
+                        // LDS read unconditional (clamped), global read in its own branch: the two
+                        // address spaces are never merged into one pointer
+                        acc4 x = *reinterpret_cast<const acc4 *>(xwin + max(cell, 0) * XS + 4 * qd);
+                        if (cell < 0) {
+                            x = acc4{0.f, 0.f, 0.f, 0.f};
+                            if (q_ok) x = *reinterpret_cast<const acc4 *>(xg + cs * BC + (size_t)idx * g.C + 4 * qd);
+                        }
+                        sv += corner_weight<DIM, float>(aw, kk) * x;
+                    }
+                }
+            }
+            bv[pb] = mk * sv;
+        }
+    };
+
+    // A operand: W[m][c] fragments, rows m = mt * 128 + mb * 16 + lane % 16, 4 channels of
+    // the slice at 4 * (lane / 16); layout Wf[grp][t][m][c] with padded rows / channels
+    const float *wrow = wf + ((size_t)grp * g.Kn * fw.Mg_pad + mt * BMR + (lane & 15)) * fw.Cg_pad + 4 * q;
+    auto load_w = [&](int cs, int t, acc4 (&wr)[MB]) {
+        const float *p = wrow + (size_t)t * fw.Mg_pad * fw.Cg_pad + cs * BC;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) wr[mb] = *reinterpret_cast<const acc4 *>(p + (size_t)mb * 16 * fw.Cg_pad);
+    };
+
+    acc4 acc[MB][PB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb) acc[mb][pb] = acc4{0.f, 0.f, 0.f, 0.f};
+
+    // MFMAs of one step with B fragments bv and A fragments wr; each row block's fragment
+    // is reloaded for step (csn, tn) right after its last use (issue order pinned)
+    auto mfma_step = [&](const acc4 (&bv)[PB], acc4 (&wr)[MB], bool more, int csn, int tn) {
+        const float *pn = wrow + (size_t)tn * fw.Mg_pad * fw.Cg_pad + csn * BC;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int pb = 0; pb < PB; ++pb) acc[mb][pb] = mfma16x16x4(wr[mb][kk], bv[pb][kk], acc[mb][pb]);
+            if (more) wr[mb] = *reinterpret_cast<const acc4 *>(pn + (size_t)mb * 16 * fw.Cg_pad);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // switch the tables to slice cs: X window from the prefetch registers, sampling
+    // table rebuilt when the slice's offset / mask group differs from the last one
+    int geo_og = -1, geo_mg = -1;
+    auto open_slice = [&](int cs, int t0, int ntaps) {
+        store_x();
+        const int c_first = grp * g.Cg + cs * BC;
+        const int og_s = g.og ? c_first / g.cpo : 0, mg_s = g.mg ? c_first / g.cpm : 0;
+        if (og_s != geo_og || mg_s != geo_mg) {
+            tile.ogu = og_s;
+            tile.mgu = mg_s;
+            fill_geo<DIM, T>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
+            geo_og = og_s;
+            geo_mg = mg_s;
+        }
+    };
+
+    for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
+        const int ntaps = min(wt.tpp, g.Kn - t0);
+        const int nsteps = slices * ntaps;
+        geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
+
+        // step k = (slice k / ntaps, tap k % ntaps). Invariant at the top of step k: its
+        // B fragments are in bcur, its weight fragments in wa.
+        acc4 wa[MB], bcur[PB], bnxt[PB];
+        prefetch_x(0);
+        load_w(0, t0, wa);
+        __syncthreads();   // previous pass done with the tables
+        open_slice(0, t0, ntaps);
+        __syncthreads();
+        build_b(0, 0, bcur);
+        for (int k = 0; k < nsteps; ++k) {
+            const bool more = k + 1 < nsteps;
+            const int kn = k + 1, csn = kn / ntaps, tln = kn - csn * ntaps;
+            const bool new_slice = more && tln == 0;
+            if (new_slice)
+                prefetch_x(csn);   // in flight during this step's MFMAs
+            else if (more)
+                build_b(csn, tln, bnxt);
+            mfma_step(bcur, wa, more, csn, t0 + tln);
+            if (new_slice) {
+                __syncthreads();   // every wave done reading the current window
+                open_slice(csn, t0, ntaps);
+                __syncthreads();
+                build_b(csn, 0, bnxt);
+            }
+#pragma unroll
+            for (int pb = 0; pb < PB; ++pb) bcur[pb] = bnxt[pb];
+        }
+    }
+
+    // ---- epilogue: + bias, store NC<spatial> ---------------------------------------
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+        const int p = tile.pixel(g, wt, wave * (PB * 16) + pb * 16 + (lane & 15));
+        if (p < 0) continue;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = mt * BMR + mb * 16 + 4 * q + v;
+                if (m < g.Mg) {
+                    const int mg_glob = grp * g.Mg + m;
+                    float r = acc[mb][pb][v];
+                    if (bias != nullptr) r += to_acc<float>(bias[mg_glob]);
+                    y[((size_t)tile.b * g.M + mg_glob) * g.Pn + p] = from_acc<T, float>(r);
+                }
+            }
+    }
+}
+
+template <int DIM, typename T>
+hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
+                    const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
+    auto kern = fwd_win_kernel<DIM, T>;
+    const size_t lds = ((size_t)GEO_WORDS + (size_t)wt.cells * XS) * sizeof(float);
+    static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)WIN_LDS_TARGET);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const long long blocks = (long long)g.G * g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2] * fw.m_tiles;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, wt, fw, static_cast<const float *>(xcl),
+                       static_cast<const float *>(wf), static_cast<const T *>(offset), static_cast<const T *>(mask),
+                       static_cast<const T *>(bias), static_cast<T *>(y));
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
+                    const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
+    switch (dim) {
+        case 1: return launch_k<1, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case 2: return launch_k<2, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case 3: return launch_k<3, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+size_t x_window_cell_bytes() { return XS * sizeof(float); }
+
+size_t fwd_win_fixed_bytes() { return (size_t)GEO_WORDS * sizeof(float); }
+
+long long fwd_win_max_cells() { return (long long)XQ * NT / 4; }
+
+FwdWin plan_fwd_win(const Geo &g, const WinTiles &wt) {
+    FwdWin f{};
+    f.ok = false;
+    const size_t lds = ((size_t)GEO_WORDS + (size_t)wt.cells * XS) * sizeof(float);
+    if (!wt.ok || g.Mg < 64 || lds > WIN_LDS_TARGET || (size_t)wt.cells * 4 > (size_t)XQ * NT) return f;
+    f.m_tiles = (g.Mg + BMR - 1) / BMR;
+    f.Mg_pad = f.m_tiles * BMR;
+    f.Cg_pad = (g.Cg + BC - 1) / BC * BC;
+    f.ok = true;
+    return f;
+}
+
+hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,
+                          const void *wf, const void *offset, const void *mask, const void *bias, void *y,
+                          hipStream_t s) {
+    switch (dtype) {
+        case kF32: return launch_d<float>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case kF16: return launch_d<__half>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case kBF16: return launch_d<__hip_bfloat16>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace tvdcn_hip

@@ -58,9 +58,26 @@ struct WeightWin {
     size_t part_elems;   // workspace floats for the split partials
 };
 
+// Windowed forward kernel (fwd_win.hip): workgroups own (spatial tile, 128 rows) of the
+// WinTiles tiling and reduce over 16-channel slices x taps.
+struct FwdWin {
+    bool ok;
+    int m_tiles;         // 128-row blocks of the GEMM side
+    int Mg_pad, Cg_pad;  // padded weight layout Wf[G][Kn][Mg_pad][Cg_pad]
+};
+
 FwdTiles plan_fwd(const Geo &g, int dtype);
+FwdWin plan_fwd_win(const Geo &g, const WinTiles &wt);
 WeightWin plan_weight_win(const Geo &g, const WinTiles &wt);
 WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter);
+// the same tiling with the window margin re-sized for another kernel's LDS budget
+// (cell_cap > 0: at most that many window cells)
+WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_bytes, size_t cell_bytes,
+                    long long cell_cap = 0);
+size_t fwd_win_fixed_bytes();      // LDS of the windowed forward besides its X window
+long long fwd_win_max_cells();     // X window cells the windowed forward can stage
+size_t weight_win_fixed_bytes();   // LDS of the windowed weight gradient besides its X window
+size_t x_window_cell_bytes();
 DataTiles plan_data(const Geo &g, int dtype);
 WeightTiles plan_weight(const Geo &g, int dtype);
 
@@ -80,6 +97,9 @@ hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int
 hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTiles &t, const void *xcl,
                                   const void *wf, const void *offset, const void *mask, const void *bias, void *y,
                                   hipStream_t s);
+hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,
+                          const void *wf, const void *offset, const void *mask, const void *bias, void *y,
+                          hipStream_t s);
 hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t, bool scatter, bool coord,
                            const void *z, const void *wd, const void *xcl, const void *offset, const void *mask,
                            void *gx_cl, void *goff, void *gmask, hipStream_t s);
