@@ -57,18 +57,20 @@ def flops_fwd(batch=8):
     return 2.0 * batch * 256 * 256 * 9 * 64 * 64
 
 
-def gpu_bench(inp, steps, warmup):
+def _kernel_lib():
     import tvdcn_amd
     lib = ctypes.CDLL(tvdcn_amd.extension.HIP_LIB_PATH)
     lib.tvdcn_kernel_timer_enable.argtypes = [ctypes.c_int32]
     lib.tvdcn_kernel_timer_read.argtypes = [ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_int64)]
-    dev = torch.device("cuda:0")
-    params = [inp[k].to(dev).requires_grad_(True) for k in ("input", "weight", "offset", "mask", "bias")]
-    gout = inp["grad_out"].to(dev)
+    return lib
 
-    def fwd():
-        return tvdcn_amd.deform_conv2d(*params, stride=1, padding=1, dilation=1, groups=1)
+
+def time_path(params, fwd, gout, steps, warmup):
+    """Times fwd() alone and fwd().backward(gout) (grads of `params` cleared each step) with host
+    clocks around synchronised loops, then per-kernel-family durations from HIP events on the
+    launch stream. Returns (fwd_ms, step_ms, {family: totals})."""
+    lib = _kernel_lib()
 
     def step():
         for p in params:
@@ -90,7 +92,7 @@ def gpu_bench(inp, steps, warmup):
         torch.cuda.synchronize()
         fwd_ms = (time.perf_counter() - t0) * 1e3 / steps
 
-    # forward + backward: the metric
+    # forward + backward
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -113,23 +115,33 @@ def gpu_bench(inp, steps, warmup):
     return fwd_ms, step_ms, kern
 
 
-def kernel_rooflines(kern, batch=8):
-    """Algorithmic work per launch (cfg2) for each family, against the bound that applies."""
-    F = flops_fwd(batch)
-    e = 4
-    n_in = batch * 256 * 64 * 64
-    n_off, n_mask = batch * 18 * 64 * 64, batch * 9 * 64 * 64
+def gpu_bench(inp, steps, warmup):
+    import tvdcn_amd
+    dev = torch.device("cuda:0")
+    params = [inp[k].to(dev).requires_grad_(True) for k in ("input", "weight", "offset", "mask", "bias")]
+    gout = inp["grad_out"].to(dev)
+
+    def fwd():
+        return tvdcn_amd.deform_conv2d(*params, stride=1, padding=1, dilation=1, groups=1)
+
+    return time_path(params, fwd, gout, steps, warmup)
+
+
+def family_rooflines(kern, contraction_flops, grad_out_bytes, mask_bytes=0):
+    """Algorithmic work per launch of each kernel family against the bound that applies: each of
+    the three MFMA families performs one contraction of `contraction_flops` per launch; the bias
+    gradient reads grad_out once; mask_softmax reads + writes the mask (forward) or reads two
+    tensors and writes one (backward): 2.5 passes over `mask_bytes` on average."""
     work = {
-        # each of the three MFMA families performs one cfg2-sized contraction per launch
-        "gather_gemm": ("mfma", F, PEAK_FP32_MFMA, "TFLOP/s"),
-        "data_grad": ("mfma", F, PEAK_FP32_MFMA, "TFLOP/s"),
-        "weight_grad": ("mfma", F, PEAK_FP32_MFMA, "TFLOP/s"),
-        # grad_bias reads grad_out once
-        "bias_grad": ("hbm", e * n_in, PEAK_HBM, "GB/s"),
+        "gather_gemm": ("mfma", contraction_flops, PEAK_FP32_MFMA, "TFLOP/s"),
+        "data_grad": ("mfma", contraction_flops, PEAK_FP32_MFMA, "TFLOP/s"),
+        "weight_grad": ("mfma", contraction_flops, PEAK_FP32_MFMA, "TFLOP/s"),
+        "bias_grad": ("hbm", grad_out_bytes, PEAK_HBM, "GB/s"),
+        "mask_softmax": ("hbm", 2.5 * mask_bytes, PEAK_HBM, "GB/s"),
     }
     out = {}
     for name, k in kern.items():
-        if name in work:
+        if name in work and work[name][1] > 0:
             bound, amount, peak, unit = work[name]
             achieved = amount / (k["avg_ms"] * 1e-3)
             scale = 1e12 if unit == "TFLOP/s" else 1e9
@@ -140,6 +152,106 @@ def kernel_rooflines(kern, batch=8):
             # layout family: several small launches (channels-last copies, weight re-layouts, zero fills)
             out[name] = dict(avg_ms=round(k["avg_ms"], 4), launches=k["launches"], total_ms=round(k["total_ms"], 4))
     return out
+
+
+def kernel_rooflines(kern, batch=8):
+    """cfg2 work per launch for each family."""
+    return family_rooflines(kern, flops_fwd(batch), 4 * batch * 256 * 64 * 64)
+
+
+# ---- per-config suite (BASELINE.json configs 2-5) ------------------------------------------
+
+def _kaiming(shape, fan_in, g):
+    return torch.randn(*shape, generator=g) * (2.0 / fan_in) ** 0.5
+
+
+def suite_case(n):
+    """Tensors (CPU, fp32) and parameters of BASELINE.json configs[n - 1], n = 2..5, with that
+    config's distributions. For configs 3 and 5 the mask is the op's mask_softmax of N(0,1)
+    logits, applied inside the timed layer (it is part of the path)."""
+    g = torch.Generator().manual_seed(3000 + n)
+    if n == 2:
+        t = make_inputs()
+        return dict(name="cfg2 deform_conv2d B8 C256 64x64 k3", op="deform_conv2d", tr=False,
+                    x=t["input"], w=t["weight"], o=t["offset"], m=t["mask"], b=t["bias"], logits=None, ks=None,
+                    kw=dict(stride=1, padding=1, dilation=1, groups=1))
+    if n == 3:
+        return dict(name="cfg3 deform_conv1d B16 C512 L4096 k5 og4 mg4", op="deform_conv1d", tr=False,
+                    x=torch.randn(16, 512, 4096, generator=g), w=_kaiming((512, 512, 5), 2560, g),
+                    o=torch.randn(16, 20, 4096, generator=g) * 3, m=None, b=None,
+                    logits=torch.randn(16, 20, 4096, generator=g), ks=(5,),
+                    kw=dict(stride=1, padding=2, dilation=1, groups=1))
+    if n == 4:
+        return dict(name="cfg4 deform_conv3d B2 C64 16x56x56 k3", op="deform_conv3d", tr=False,
+                    x=torch.randn(2, 64, 16, 56, 56, generator=g), w=_kaiming((64, 64, 3, 3, 3), 1728, g),
+                    o=torch.randn(2, 81, 16, 56, 56, generator=g) * 1.5,
+                    m=torch.sigmoid(torch.randn(2, 27, 16, 56, 56, generator=g)), b=None, logits=None, ks=None,
+                    kw=dict(stride=1, padding=1, dilation=1, groups=1))
+    if n == 5:
+        # offsets / masks on the input grid (32 x 32), where the transposed op defines them
+        return dict(name="cfg5 deform_conv_transpose2d B8 C256->128 32x32->64x64 k4 s2 og2 mg2",
+                    op="deform_conv_transpose2d", tr=True,
+                    x=torch.randn(8, 256, 32, 32, generator=g), w=_kaiming((256, 128, 4, 4), 128 * 16, g),
+                    o=torch.randn(8, 64, 32, 32, generator=g), m=None, b=None,
+                    logits=torch.randn(8, 32, 32, 32, generator=g), ks=(4, 4),
+                    kw=dict(stride=2, padding=1, output_padding=0, dilation=1, groups=1))
+    raise ValueError(n)
+
+
+def suite_flops(c):
+    """Algorithmic flops of one contraction (= the forward's GEMM work)."""
+    x, w = c["x"], c["w"]
+    kn = 1
+    for k in w.shape[2:]:
+        kn *= k
+    B, groups = x.shape[0], c["kw"]["groups"]
+    if c["tr"]:
+        # columns over the input pixels: (Cin) x (Cout/groups * Kn) per group
+        return 2.0 * B * x[0, 0].numel() * x.shape[1] * w.shape[1] * kn
+    out_px = 1
+    for i, S in enumerate(x.shape[2:]):
+        K = w.shape[2 + i]
+        out_px *= (S + 2 * c["kw"]["padding"] - (c["kw"]["dilation"] * (K - 1) + 1)) // c["kw"]["stride"] + 1
+    return 2.0 * B * out_px * w.shape[0] * (x.shape[1] // groups) * kn
+
+
+def run_suite_case(n, dtype, steps, warmup):
+    import tvdcn_amd
+    c = suite_case(n)
+    dev = torch.device("cuda:0")
+    mk = lambda t: None if t is None else t.to(dev, dtype).requires_grad_(True)
+    x, w, o, m, b, logits = (mk(c[k]) for k in ("x", "w", "o", "m", "b", "logits"))
+    params = [t for t in (x, w, o, m, b, logits) if t is not None]
+    op = getattr(tvdcn_amd, c["op"])
+    dim = x.dim() - 2
+    softmax = getattr(tvdcn_amd, f"mask_softmax{dim}d")
+
+    def fwd():
+        mask = softmax(logits, c["ks"]) if logits is not None else m
+        return op(x, w, o, mask, b, **c["kw"])
+
+    with torch.no_grad():
+        out_shape = fwd().shape
+    gout = torch.randn(out_shape, generator=torch.Generator().manual_seed(4000 + n)).to(dev, dtype)
+    fwd_ms, step_ms, kern = time_path(params, fwd, gout, steps, warmup)
+    F = suite_flops(c)
+    es = torch.finfo(dtype).bits // 8
+    mask_bytes = es * (logits.numel() if logits is not None else 0)
+    roof = family_rooflines(kern, F, es * gout.numel(), mask_bytes)
+    return {
+        "case": c["name"], "dtype": str(dtype).replace("torch.", ""), "compute": "f32 (fp32 MFMA, fp32 accumulate)",
+        "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(step_ms - fwd_ms, 4), "fwd_bwd_ms": round(step_ms, 4),
+        "gflop_fwd": round(F / 1e9, 3), "gflop_fwd_bwd": round(3 * F / 1e9, 3),
+        "fwd_tflops": round(F / (fwd_ms * 1e-3) / 1e12, 2),
+        "fwd_frac_mfma_fp32": round(F / (fwd_ms * 1e-3) / PEAK_FP32_MFMA, 4),
+        "fwd_bwd_tflops": round(3 * F / (step_ms * 1e-3) / 1e12, 2),
+        "fwd_bwd_frac_mfma_fp32": round(3 * F / (step_ms * 1e-3) / PEAK_FP32_MFMA, 4),
+        "kernels": roof,
+    }
+
+
+SUITE = [(2, torch.float32), (3, torch.float32), (4, torch.float32), (5, torch.float32), (5, torch.float16),
+         (5, torch.bfloat16)]
 
 
 TRAFFIC_KERNELS = {"gather_gemm": "fwd_win_kernel<2, float>",
@@ -201,6 +313,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-batch", type=int, default=2, help="images of the workload timed on the CPU (divides 8)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the metric line, print one JSON line per BASELINE config 2-5 (cfg5 also in "
+                         "fp16 / bf16): forward and forward+backward ms, TFLOP/s, fraction of fp32 MFMA peak and "
+                         "per-kernel-family rooflines")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 5 times (reference for the rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scale) and exit")
@@ -220,6 +336,13 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+
+    if args.configs:
+        for n, dt in SUITE:
+            print(f"[bench] suite cfg{n} {dt}", file=sys.stderr, flush=True)
+            print(json.dumps(run_suite_case(n, dt, args.steps, args.warmup)), flush=True)
+            torch.cuda.empty_cache()
+        return
 
     inp = make_inputs()
     hashes = {k: sha(v) for k, v in inp.items()}

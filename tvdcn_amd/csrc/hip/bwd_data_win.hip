@@ -534,7 +534,7 @@ WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_by
     return t;
 }
 
-WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter) {
+WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coord) {
     WinTiles t{};
     t.ok = false;
     if (dtype == kF64) return t;
@@ -570,10 +570,9 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter) {
     t.lbxy = ilog2(box[1] * box[2]);
     t.c_tiles = (g.Cg + BC - 1) / BC;
     t.m_steps = (g.Mg + BM - 1) / BM;
-    (void)scatter;
-    // per window cell: the fixed-point accumulators (scatter) and the X values (offset/mask
-    // gradients); the plan is sized for both so that one plan serves every launch
-    t = win_resize(t, g, dim, FIXED_WORDS * sizeof(float), (CS + XS) * sizeof(float));
+    // per window cell: the fixed-point accumulators (scatter) and / or the X values
+    // (offset/mask gradients), as the launches this plan serves need them
+    t = win_resize(t, g, dim, FIXED_WORDS * sizeof(float), ((scatter ? CS : 0) + (coord ? XS : 0)) * sizeof(float));
     const int npass = (g.Kn + WIN_TMAX - 1) / WIN_TMAX;
     t.tpp = (g.Kn + npass - 1) / npass;
     t.chunk_elems = (size_t)g.G * t.c_tiles * t.m_steps * g.Kn * BC * BM;

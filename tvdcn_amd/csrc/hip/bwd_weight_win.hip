@@ -94,22 +94,11 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                 const int i = k * KP + sj;
                 for (int tl = st0; tl < ntaps; tl += NW) {
                     const acc4 r = geo[tl * BPX + i];
-                    const int fc = rec_fast_cell<DIM>(r);
+                    const int fc = fast_cell<DIM>(r);
                     acc4 sv;
                     if (fc >= 0) {
                         // every corner cell is in the window (zeros outside the grid)
-                        const float *xc = xwin + fc * XS + 4 * sq;
-                        const float fx = r[DIM - 1] - floorf(r[DIM - 1]);
-                        const acc4 x00 = *reinterpret_cast<const acc4 *>(xc);
-                        const acc4 x01 = *reinterpret_cast<const acc4 *>(xc + XS);
-                        if constexpr (DIM == 2) {
-                            const float fy = r[0] - floorf(r[0]);
-                            const acc4 x10 = *reinterpret_cast<const acc4 *>(xc + wt.WE[2] * XS);
-                            const acc4 x11 = *reinterpret_cast<const acc4 *>(xc + (wt.WE[2] + 1) * XS);
-                            sv = (1.f - fy) * ((1.f - fx) * x00 + fx * x01) + fy * ((1.f - fx) * x10 + fx * x11);
-                        } else {
-                            sv = (1.f - fx) * x00 + fx * x01;
-                        }
+                        sv = window_sample<DIM>(wt, xwin, fc, 4 * sq, r);
                     } else {
                         const AxisW<DIM, float> aw = record_weights<DIM>(g, r, deformable);
                         sv = acc4{0.f, 0.f, 0.f, 0.f};

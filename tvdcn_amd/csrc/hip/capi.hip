@@ -63,8 +63,11 @@ struct Plan {
     int dtype;
     FwdTiles ft;
     DataTiles dt;
-    WinTiles wn_s;   // windowed data-gradient plan with the scatter (conv backward, transposed forward)
-    WinTiles wn_c;   // the same without the scatter (transposed backward: offset/mask gradients only)
+    WinTiles wn_s;   // windowed data-gradient plan, scatter + offset/mask gradients (conv backward)
+    WinTiles wn_x;   // the same tiling, scatter only (transposed forward): a larger window
+    WinTiles wn_c;   // the same tiling, offset/mask gradients only (transposed backward)
+    bool data_split; // conv backward: scatter (wn_x) and offset/mask gradients (wn_c) as two
+                     // launches, when the shared window of wn_s would be too small
     WeightTiles wt;
     WinTiles wn_w;   // the wn_s tiling with the weight-gradient kernel's window margin
     WinTiles wn_f;   // the wn_s tiling with the forward kernel's window margin
@@ -149,13 +152,17 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     g.dK12 = make_fastdiv((uint32_t)(g.K[1] * g.K[2]));
     pl.ft = plan_fwd(g, pl.dtype);
     pl.dt = plan_data(g, pl.dtype);
-    pl.wn_s = plan_data_win(g, pl.dtype, pl.dim, true);
-    pl.wn_c = plan_data_win(g, pl.dtype, pl.dim, false);
+    pl.wn_s = plan_data_win(g, pl.dtype, pl.dim, true, true);
+    pl.wn_x = plan_data_win(g, pl.dtype, pl.dim, true, false);
+    pl.wn_c = plan_data_win(g, pl.dtype, pl.dim, false, true);
+    // a margin under 2 cells loses a large share of the corners to global atomics
+    // (3D: the window grows with the cube of its extent); two launches recompute the
+    // grad-columns contraction but each gets about twice the window
+    pl.data_split = pl.wn_s.ok && pl.wn_s.R[2] < 2 && pl.wn_x.R[2] > pl.wn_s.R[2] && pl.wn_c.R[2] > pl.wn_s.R[2];
     pl.wt = plan_weight(g, pl.dtype);
     pl.wn_w = win_resize(pl.wn_s, g, pl.dim, weight_win_fixed_bytes(), x_window_cell_bytes());
-    pl.wn_f = win_resize(pl.wn_s, g, pl.dim, fwd_win_fixed_bytes(), x_window_cell_bytes(), fwd_win_max_cells());
     pl.ww = plan_weight_win(g, pl.wn_w);
-    pl.fw = plan_fwd_win(g, pl.wn_f);
+    pl.fw = plan_fwd_win(g, pl.wn_s, pl.dim, pl.wn_f);
     return TVDCN_STATUS_SUCCESS;
 }
 
@@ -355,7 +362,7 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
         if (pl.wn_s.ok) {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
-            TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_s, true, false, input, wd, nullptr,
+            TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, input, wd, nullptr,
                                                                         offset, mask, ycl, nullptr, nullptr, s));
         } else {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
@@ -424,9 +431,15 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
         if (!pl.transposed) {
             void *gx_cl = at(workspace, L.cl_acc);
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
-            if (pl.wn_s.ok)
-                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_s, true, coord, Z, wd, xcl, offset,
-                                                                            mask, gx_cl, goff, gmask, s));
+            if (pl.wn_s.ok && coord && pl.data_split) {
+                // two launches, each with the larger window its LDS share allows
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, Z, wd, xcl, offset,
+                                                                            mask, gx_cl, nullptr, nullptr, s));
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_c, false, true, Z, wd, xcl, offset,
+                                                                            mask, nullptr, goff, gmask, s));
+            } else if (pl.wn_s.ok)
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, coord ? pl.wn_s : pl.wn_x, true, coord,
+                                                                            Z, wd, xcl, offset, mask, gx_cl, goff, gmask, s));
             else
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask,
                                                                         gx_cl, goff, gmask, s));

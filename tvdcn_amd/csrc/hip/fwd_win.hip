@@ -8,8 +8,9 @@
 // deform_conv2d_kernel.cpp:341-380; 1D/3D twins); the columns are never written
 // to HBM. Also computes the transposed op's input gradient.
 //
-// Workgroup = (spatial tile of 256 column pixels, 128 GEMM-side rows); eight waves,
-// wave w owning 32 pixels x 128 rows (64 accumulators per lane). The reduction runs
+// Workgroup = (spatial tile of 256 column pixels, 128 or 64 GEMM-side rows); eight
+// waves, wave w owning 32 pixels x all rows (64 or 32 accumulators per lane; 64-row
+// tiles serve small GEMM sides and grids too small to fill the chip). The reduction runs
 // over 16-channel slices x taps; per step (slice, tap) every lane forms its own MFMA
 // B fragment -- the sampled values of 4 channels of one of its pixels -- straight from
 // the X window (LDS) and the sampling table, one step ahead, while the MFMAs of the
@@ -29,20 +30,23 @@ using namespace win;
 constexpr int NW = 8;               // waves per workgroup
 constexpr int NT = 64 * NW;
 constexpr int PB = 2;               // 16-pixel blocks per wave
-constexpr int MB = 8;               // 16-row blocks per wave (128 rows)
-constexpr int BMR = MB * 16;        // rows per workgroup
 constexpr int TM = WIN_TMAX;
-constexpr int XQ = 8;               // X window quads prefetched per thread (cells * 4 <= XQ * NT)
+// MB = 16-row blocks per wave (rows per workgroup 16 * MB); XQ = X window quads
+// prefetched per thread (cells * 4 <= XQ * NT): the 64-row variant spends the
+// registers its smaller accumulator frees on a larger window
+constexpr int xq_of(int mb) { return mb == 8 ? 8 : 12; }
 static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
 
 constexpr int GEO_WORDS = TM * BPX * 4;
 
-template <int DIM, typename T>
+template <int DIM, typename T, int MB>
 __global__ void __launch_bounds__(NT)
 fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__restrict__ xcl,
                const float *__restrict__ wf, const T *__restrict__ offset, const T *__restrict__ mask,
                const T *__restrict__ bias, T *__restrict__ y) {
     constexpr int NC = 1 << DIM;
+    constexpr int BMR = MB * 16;
+    constexpr int XQ = xq_of(MB);
     extern __shared__ float smem[];
     acc4 *geo = reinterpret_cast<acc4 *>(smem);     // [TM][BPX]
     float *xwin = smem + GEO_WORDS;                 // [cells][XS]
@@ -100,22 +104,11 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
 #pragma unroll
         for (int pb = 0; pb < PB; ++pb) {
             const acc4 r = geo[tl * BPX + wave * (PB * 16) + pb * 16 + (lane & 15)];
-            const int fc = rec_fast_cell<DIM>(r);
+            const int fc = fast_cell<DIM>(r);
             const float mk = rec_mask<DIM>(r);
             acc4 sv;
             if (fc >= 0) {
-                const float fx = r[DIM - 1] - floorf(r[DIM - 1]);
-                const float *xc = xwin + fc * XS + 4 * qd;
-                const acc4 x00 = *reinterpret_cast<const acc4 *>(xc);
-                const acc4 x01 = *reinterpret_cast<const acc4 *>(xc + XS);
-                if constexpr (DIM == 2) {
-                    const float fy = r[0] - floorf(r[0]);
-                    const acc4 x10 = *reinterpret_cast<const acc4 *>(xc + wt.WE[2] * XS);
-                    const acc4 x11 = *reinterpret_cast<const acc4 *>(xc + (wt.WE[2] + 1) * XS);
-                    sv = (1.f - fy) * ((1.f - fx) * x00 + fx * x01) + fy * ((1.f - fx) * x10 + fx * x11);
-                } else {
-                    sv = (1.f - fx) * x00 + fx * x01;
-                }
+                sv = window_sample<DIM>(wt, xwin, fc, 4 * qd, r);
             } else {
                 Point<DIM, float> pt;
 #pragma unroll
@@ -248,10 +241,10 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     }
 }
 
-template <int DIM, typename T>
+template <int DIM, typename T, int MB>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
                     const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
-    auto kern = fwd_win_kernel<DIM, T>;
+    auto kern = fwd_win_kernel<DIM, T, MB>;
     const size_t lds = ((size_t)GEO_WORDS + (size_t)wt.cells * XS) * sizeof(float);
     static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
     if (!attr_set) {
@@ -267,13 +260,21 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const vo
     return hipGetLastError();
 }
 
+template <int DIM, typename T>
+hipError_t launch_m(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
+                    const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
+    if (fw.mb == 8) return launch_k<DIM, T, 8>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+    if (fw.mb == 4) return launch_k<DIM, T, 4>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+    return hipErrorInvalidValue;
+}
+
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
                     const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
     switch (dim) {
-        case 1: return launch_k<1, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
-        case 2: return launch_k<2, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
-        case 3: return launch_k<3, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case 1: return launch_m<1, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case 2: return launch_m<2, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case 3: return launch_m<3, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
     }
     return hipErrorInvalidValue;
 }
@@ -282,17 +283,22 @@ hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw,
 
 size_t x_window_cell_bytes() { return XS * sizeof(float); }
 
-size_t fwd_win_fixed_bytes() { return (size_t)GEO_WORDS * sizeof(float); }
-
-long long fwd_win_max_cells() { return (long long)XQ * NT / 4; }
-
-FwdWin plan_fwd_win(const Geo &g, const WinTiles &wt) {
+FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     FwdWin f{};
     f.ok = false;
+    wt = base;
+    if (!base.ok || g.Mg < 16) return f;
+    // 128-row tiles unless the GEMM side is small or the grid would leave CUs idle
+    // (one workgroup per CU at a time: the window takes most of the LDS)
+    const long long spatial = (long long)g.G * g.B * base.ntile[0] * base.ntile[1] * base.ntile[2];
+    f.mb = (g.Mg <= 64 || spatial * ((g.Mg + 127) / 128) < 256) ? 4 : 8;
+    const int rows = 16 * f.mb;
+    const long long max_cells = (long long)xq_of(f.mb) * NT / 4;
+    wt = win_resize(base, g, dim, (size_t)GEO_WORDS * sizeof(float), XS * sizeof(float), max_cells);
     const size_t lds = ((size_t)GEO_WORDS + (size_t)wt.cells * XS) * sizeof(float);
-    if (!wt.ok || g.Mg < 64 || lds > WIN_LDS_TARGET || (size_t)wt.cells * 4 > (size_t)XQ * NT) return f;
-    f.m_tiles = (g.Mg + BMR - 1) / BMR;
-    f.Mg_pad = f.m_tiles * BMR;
+    if (lds > WIN_LDS_TARGET || wt.cells > max_cells) return f;
+    f.m_tiles = (g.Mg + rows - 1) / rows;
+    f.Mg_pad = f.m_tiles * rows;
     f.Cg_pad = (g.Cg + BC - 1) / BC * BC;
     f.ok = true;
     return f;

@@ -62,20 +62,21 @@ struct WeightWin {
 // WinTiles tiling and reduce over 16-channel slices x taps.
 struct FwdWin {
     bool ok;
-    int m_tiles;         // 128-row blocks of the GEMM side
+    int mb;              // 16-row blocks per workgroup (8 or 4)
+    int m_tiles;         // (16 * mb)-row blocks of the GEMM side
     int Mg_pad, Cg_pad;  // padded weight layout Wf[G][Kn][Mg_pad][Cg_pad]
 };
 
 FwdTiles plan_fwd(const Geo &g, int dtype);
-FwdWin plan_fwd_win(const Geo &g, const WinTiles &wt);
+// windowed forward plan over the base tiling; wt receives the tiling with the forward's
+// own window margin
+FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt);
 WeightWin plan_weight_win(const Geo &g, const WinTiles &wt);
-WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter);
+WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coord);
 // the same tiling with the window margin re-sized for another kernel's LDS budget
 // (cell_cap > 0: at most that many window cells)
 WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_bytes, size_t cell_bytes,
                     long long cell_cap = 0);
-size_t fwd_win_fixed_bytes();      // LDS of the windowed forward besides its X window
-long long fwd_win_max_cells();     // X window cells the windowed forward can stage
 size_t weight_win_fixed_bytes();   // LDS of the windowed weight gradient besides its X window
 size_t x_window_cell_bytes();
 DataTiles plan_data(const Geo &g, int dtype);

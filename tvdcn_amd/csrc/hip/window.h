@@ -105,6 +105,35 @@ template <int DIM> __device__ __forceinline__ int rec_fast_cell(const acc4 &r) {
     return DIM == 3 ? -1 : __float_as_int(r[3]);
 }
 
+// Fast cell of a record (DIM <= 2; none for DIM = 3: the 3D windows that fit in LDS
+// have margins of at most one cell, where most waves hold a lane outside the window
+// and the extra fast path measured slower than the general path alone).
+template <int DIM>
+__device__ __forceinline__ int fast_cell(const acc4 &r) {
+    if constexpr (DIM < 3) return rec_fast_cell<DIM>(r);
+    return -1;
+}
+
+// Sampled value of one channel quad (offset xq within the cell) at a record whose fast
+// cell is fc (DIM <= 2): every corner cell lies in the window (zeros outside the
+// grid), so the plain bilinear formulas apply.
+template <int DIM>
+__device__ __forceinline__ acc4 window_sample(const WinTiles &wt, const float *xwin, int fc, int xq, const acc4 &r) {
+    const float *xc = xwin + fc * XS + xq;
+    const float fx = r[DIM - 1] - floorf(r[DIM - 1]);
+    auto row = [&](int off) {
+        const acc4 x0 = *reinterpret_cast<const acc4 *>(xc + off * XS);
+        const acc4 x1 = *reinterpret_cast<const acc4 *>(xc + (off + 1) * XS);
+        return (1.f - fx) * x0 + fx * x1;
+    };
+    if constexpr (DIM == 1) {
+        return row(0);
+    } else {
+        const float fy = r[0] - floorf(r[0]);
+        return (1.f - fy) * row(0) + fy * row(wt.WE[2]);
+    }
+}
+
 template <int DIM, typename T>
 __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const Tile &tile, const T *__restrict__ offset,
                                          const T *__restrict__ mask, int t0, int ntaps, acc4 *geo, int tid, int nthreads) {
