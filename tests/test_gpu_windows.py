@@ -1,0 +1,50 @@
+"""GPU parity of the windowed kernels' less common paths, against the float64 oracle.
+
+* offsets far larger than the window margin: bilinear corners outside the LDS window
+  take the general path (global reads in the forward and weight gradient, global
+  atomics in the data gradient);
+* a GEMM side that is not a multiple of 16 rows (zero-padded rows in the data gradient);
+* a non-finite upstream gradient: the data gradient's fixed-point window cannot bound
+  the pass and falls back to global float atomics, so inf / nan propagate as in the
+  reference.
+"""
+import pytest
+import torch
+
+from helpers import make_case, rel_err
+from test_gpu_parity import TOL, check, run_gpu, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dim,transposed", [(2, False), (2, True), (1, False), (3, False)])
+def test_offsets_beyond_window_fp32(dim, transposed):
+    in_size = {1: [300], 2: [40, 36], 3: [6, 12, 12]}[dim]
+    case = make_case(dim, transposed, batch=2, cin=32, cout=64, kernel=[3] * dim, stride=[1] * dim,
+                     padding=[1] * dim, dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim, seed=500 + dim,
+                     offset_scale=12.0)
+    check(case, torch.float32)
+
+
+def test_gemm_side_not_multiple_of_16_fp32():
+    case = make_case(2, False, batch=2, cin=32, cout=40, kernel=[3, 3], stride=[1, 1], padding=[1, 1],
+                     dilation=[1, 1], in_size=[20, 18], out_pad=[0, 0], seed=510)
+    check(case, torch.float32)
+
+
+def test_nonfinite_grad_out_fp32():
+    case = make_case(2, False, batch=2, cin=32, cout=64, kernel=[3, 3], stride=[1, 1], padding=[1, 1],
+                     dilation=[1, 1], in_size=[20, 18], out_pad=[0, 0], seed=520)
+    g = torch.Generator().manual_seed(521)
+    gout = torch.rand(case["out_shape"], generator=g, dtype=torch.float64)
+    gout[1, 5, 7, 9] = float("nan")
+    _, grads, _ = run_gpu(case, torch.float32, grad_out=gout)
+    _, ref_grads = run_oracle(case, gout, torch.float32)
+    for name, gr, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
+        gr = gr.detach().double().cpu()
+        assert torch.equal(torch.isnan(gr), torch.isnan(r)), f"grad_{name}: nan pattern differs"
+        assert torch.equal(torch.isinf(gr), torch.isinf(r)), f"grad_{name}: inf pattern differs"
+        fin = torch.isfinite(r)
+        if fin.any():
+            e = rel_err(gr[fin], r[fin])
+            assert e < TOL[torch.float32][1], f"grad_{name} rel err {e}"

@@ -271,8 +271,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                 if (DIM < 3 && fc >= 0 && (!SCATTER || use_window)) {
                     // fast path: every corner cell is in the window (zeros / dropped
                     // outside the grid), plain bilinear formulas
-                    const float fx = r[DIM - 1] - floorf(r[DIM - 1]);
-                    const float fy = DIM == 2 ? r[0] - floorf(r[0]) : 0.f;
+                    const float fx = r[DIM - 1];   // fast records hold the fractional parts
+                    const float fy = DIM == 2 ? r[0] : 0.f;
                     constexpr int NF = DIM == 2 ? 4 : 2;
                     int cell[NF];
                     float w[NF];
@@ -322,7 +322,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                     }
                 } else {
                     // general path: per-corner validity, window membership and global fallback
-                    const AxisW<DIM, float> aw = record_weights<DIM>(g, r, deformable);
+                    // (also taken by fast records when the pass scatters to global memory)
+                    const AxisW<DIM, float> aw = record_weights<DIM>(g, record_position<DIM>(wt, tile, r), deformable);
                     int gidx[NC], loc[NC];
                     float w[NC];
 #pragma unroll

@@ -95,10 +95,11 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                 for (int tl = st0; tl < ntaps; tl += NW) {
                     const acc4 r = geo[tl * BPX + i];
                     const int fc = fast_cell<DIM>(r);
+                    const float mk = rec_mask<DIM>(r);
                     acc4 sv;
                     if (fc >= 0) {
                         // every corner cell is in the window (zeros outside the grid)
-                        sv = window_sample<DIM>(wt, xwin, fc, 4 * sq, r);
+                        sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * sq, r, mk);
                     } else {
                         const AxisW<DIM, float> aw = record_weights<DIM>(g, r, deformable);
                         sv = acc4{0.f, 0.f, 0.f, 0.f};
@@ -120,8 +121,8 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                                 sv += corner_weight<DIM, float>(aw, kk) * x;
                             }
                         }
+                        sv *= mk;
                     }
-                    sv *= rec_mask<DIM>(r);
                     float *row = dst + (tl * BC + 4 * sq) * SS + sj;
 #pragma unroll
                     for (int v = 0; v < 4; ++v) row[v * SS] = sv[v];

@@ -349,7 +349,7 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
         void *xcl = at(workspace, L.xcl), *wf = at(workspace, L.wf);
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
         if (pl.fw.ok) {
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.fw.Mg_pad, pl.fw.Cg_pad, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
                          launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, bias, output, s));
         } else {
@@ -447,7 +447,7 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
         } else {
             void *wf = at(workspace, L.wf);
             if (pl.fw.ok) {
-                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.fw.Mg_pad, pl.fw.Cg_pad, s));
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
                 TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
                              launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, nullptr, grad_input, s));
             } else {

@@ -31,6 +31,7 @@ constexpr int NW = 8;               // waves per workgroup
 constexpr int NT = 64 * NW;
 constexpr int PB = 2;               // 16-pixel blocks per wave
 constexpr int TM = WIN_TMAX;
+constexpr int PF = 3;               // X window prefetch distance, steps
 // MB = 16-row blocks per wave (rows per workgroup 16 * MB); XQ = X window quads
 // prefetched per thread (cells * 4 <= XQ * NT): the 64-row variant spends the
 // registers its smaller accumulator frees on a larger window
@@ -108,7 +109,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
             const float mk = rec_mask<DIM>(r);
             acc4 sv;
             if (fc >= 0) {
-                sv = window_sample<DIM>(wt, xwin, fc, 4 * qd, r);
+                sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * qd, r, mk);
             } else {
                 Point<DIM, float> pt;
 #pragma unroll
@@ -136,18 +137,22 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                         sv += corner_weight<DIM, float>(aw, kk) * x;
                     }
                 }
+                sv *= mk;
             }
-            bv[pb] = mk * sv;
+            bv[pb] = sv;
         }
     };
 
-    // A operand: W[m][c] fragments, rows m = mt * 128 + mb * 16 + lane % 16, 4 channels of
-    // the slice at 4 * (lane / 16); layout Wf[grp][t][m][c] with padded rows / channels
-    const float *wrow = wf + ((size_t)grp * g.Kn * fw.Mg_pad + mt * BMR + (lane & 15)) * fw.Cg_pad + 4 * q;
-    auto load_w = [&](int cs, int t, acc4 (&wr)[MB]) {
-        const float *p = wrow + (size_t)t * fw.Mg_pad * fw.Cg_pad + cs * BC;
+    // A operand: W[m][c] fragments, rows m = mt * BMR + mb * 16 + lane % 16, channels
+    // 4 * (lane / 16) .. + 3 of the slice. Layout Wp[grp][slice][t][Mg_pad / 16][16 m][16 c]
+    // (fwd_win_weight_kernel): the row blocks of one (slice, tap) are 1 KB apart and each
+    // is one contiguous 1 KB wave load; consecutive taps of a slice are adjacent.
+    const size_t step_elems = (size_t)fw.Mg_pad * BC;
+    const float *wlane = wf + (size_t)grp * slices * g.Kn * step_elems + (size_t)mt * MB * 256 + (lane & 15) * BC + 4 * q;
+    auto wptr = [&](int cs, int t) { return wlane + ((size_t)cs * g.Kn + t) * step_elems; };
+    auto load_w = [&](const float *p, acc4 (&wr)[MB]) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) wr[mb] = *reinterpret_cast<const acc4 *>(p + (size_t)mb * 16 * fw.Cg_pad);
+        for (int mb = 0; mb < MB; ++mb) wr[mb] = *reinterpret_cast<const acc4 *>(p + mb * 256);
     };
 
     acc4 acc[MB][PB];
@@ -157,16 +162,16 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
         for (int pb = 0; pb < PB; ++pb) acc[mb][pb] = acc4{0.f, 0.f, 0.f, 0.f};
 
     // MFMAs of one step with B fragments bv and A fragments wr; each row block's fragment
-    // is reloaded for step (csn, tn) right after its last use (issue order pinned)
-    auto mfma_step = [&](const acc4 (&bv)[PB], acc4 (&wr)[MB], bool more, int csn, int tn) {
-        const float *pn = wrow + (size_t)tn * fw.Mg_pad * fw.Cg_pad + csn * BC;
+    // is reloaded from pn (the next step's, or this step's own at the end of a pass) right
+    // after its last use (issue order pinned)
+    auto mfma_step = [&](const acc4 (&bv)[PB], acc4 (&wr)[MB], const float *pn) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
                 for (int pb = 0; pb < PB; ++pb) acc[mb][pb] = mfma16x16x4(wr[mb][kk], bv[pb][kk], acc[mb][pb]);
-            if (more) wr[mb] = *reinterpret_cast<const acc4 *>(pn + (size_t)mb * 16 * fw.Cg_pad);
+            wr[mb] = *reinterpret_cast<const acc4 *>(pn + mb * 256);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -181,7 +186,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
         if (og_s != geo_og || mg_s != geo_mg) {
             tile.ogu = og_s;
             tile.mgu = mg_s;
-            fill_geo<DIM, T>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
+            fill_geo<DIM, T, 3>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
             geo_og = og_s;
             geo_mg = mg_s;
         }
@@ -196,20 +201,22 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
         // B fragments are in bcur, its weight fragments in wa.
         acc4 wa[MB], bcur[PB], bnxt[PB];
         prefetch_x(0);
-        load_w(0, t0, wa);
+        load_w(wptr(0, t0), wa);
         __syncthreads();   // previous pass done with the tables
         open_slice(0, t0, ntaps);
         __syncthreads();
         build_b(0, 0, bcur);
+        // the next slice's X window is requested PF steps before it is needed (memory
+        // latency exceeds one step's MFMAs), or at the slice's first step when shorter
+        const int pf_tl = max(ntaps - PF, 0);
         for (int k = 0; k < nsteps; ++k) {
             const bool more = k + 1 < nsteps;
             const int kn = k + 1, csn = kn / ntaps, tln = kn - csn * ntaps;
+            const int cs = k / ntaps;
             const bool new_slice = more && tln == 0;
-            if (new_slice)
-                prefetch_x(csn);   // in flight during this step's MFMAs
-            else if (more)
-                build_b(csn, tln, bnxt);
-            mfma_step(bcur, wa, more, csn, t0 + tln);
+            if (k - cs * ntaps == pf_tl && cs + 1 < slices) prefetch_x(cs + 1);
+            if (more && !new_slice) build_b(csn, tln, bnxt);
+            mfma_step(bcur, wa, more ? wptr(csn, t0 + tln) : wptr(cs, t0 + k - cs * ntaps));
             if (new_slice) {
                 __syncthreads();   // every wave done reading the current window
                 open_slice(csn, t0, ntaps);
@@ -238,6 +245,27 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                     y[((size_t)tile.b * g.M + mg_glob) * g.Pn + p] = from_acc<T, float>(r);
                 }
             }
+    }
+}
+
+// weight (M, Cg, Kn) -> Wp[G][slices][Kn][Mg_pad / 16][16 m][16 c], zero padded
+template <typename T>
+__global__ void fwd_win_weight_kernel(const T *__restrict__ w, float *__restrict__ wp, int G, int Mg, int Cg, int Kn,
+                                      int slices, int Mg_pad) {
+    const size_t total = (size_t)G * slices * Kn * Mg_pad * BC;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int ci = (int)(i % BC);
+        size_t r = i / BC;
+        const int m = (int)(r % Mg_pad);   // row blocks of 16 are consecutive: m = block * 16 + row
+        r /= Mg_pad;
+        const int t = (int)(r % Kn);
+        r /= Kn;
+        const int cs = (int)(r % slices);
+        const int grp = (int)(r / slices);
+        const int c = cs * BC + ci;
+        float v = 0.f;
+        if (m < Mg && c < Cg) v = to_acc<float>(w[(((size_t)grp * Mg + m) * Cg + c) * Kn + t]);
+        wp[i] = v;
     }
 }
 
@@ -302,6 +330,25 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     f.Cg_pad = (g.Cg + BC - 1) / BC * BC;
     f.ok = true;
     return f;
+}
+
+hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *wp, hipStream_t s) {
+    const int slices = fw.Cg_pad / BC;
+    const size_t n = (size_t)g.G * slices * g.Kn * fw.Mg_pad * BC;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+#define TVDCN_FWL(T)                                                                                             \
+    hipLaunchKernelGGL((fwd_win_weight_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, s, static_cast<const T *>(w), \
+                       static_cast<float *>(wp), g.G, g.Mg, g.Cg, g.Kn, slices, fw.Mg_pad);                      \
+    return hipGetLastError();
+    switch (dtype) {
+        case kF32: { TVDCN_FWL(float) }
+        case kF16: { TVDCN_FWL(__half) }
+        case kBF16: { TVDCN_FWL(__hip_bfloat16) }
+    }
+#undef TVDCN_FWL
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,

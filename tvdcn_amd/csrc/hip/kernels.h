@@ -98,6 +98,8 @@ hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int
 hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTiles &t, const void *xcl,
                                   const void *wf, const void *offset, const void *mask, const void *bias, void *y,
                                   hipStream_t s);
+// weight -> the windowed forward's fragment-major layout (fwd_win.hip)
+hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *wp, hipStream_t s);
 hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,
                           const void *wf, const void *offset, const void *mask, const void *bias, void *y,
                           hipStream_t s);

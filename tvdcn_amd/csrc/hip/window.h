@@ -98,8 +98,10 @@ struct Tile {
 // outside the grid need no test there: the X window holds zeros at those cells
 // (which reproduces the zero padding and the sample range rule, whose excluded
 // points have every corner outside the grid), and scatter into them is dropped
-// when the window is flushed. Pixels outside the grid get position -4 on every axis
-// (no corner inside the grid), mask 0 and no fast cell.
+// when the window is flushed. A record with a fast cell holds the fractional part
+// of each position (the high-corner weight) in place of the position. Pixels outside
+// the grid get position -4 on every axis (no corner inside the grid), mask 0 and no
+// fast cell.
 template <int DIM> __device__ __forceinline__ float rec_mask(const acc4 &r) { return DIM == 3 ? r[3] : r[DIM]; }
 template <int DIM> __device__ __forceinline__ int rec_fast_cell(const acc4 &r) {
     return DIM == 3 ? -1 : __float_as_int(r[3]);
@@ -114,65 +116,112 @@ __device__ __forceinline__ int fast_cell(const acc4 &r) {
     return -1;
 }
 
-// Sampled value of one channel quad (offset xq within the cell) at a record whose fast
-// cell is fc (DIM <= 2): every corner cell lies in the window (zeros outside the
-// grid), so the plain bilinear formulas apply.
+// mask * sampled value of one channel quad (offset xq within the cell) at a fast
+// record (DIM <= 2): every corner cell lies in the window (zeros outside the grid), so
+// the plain bilinear formulas apply, with the mask folded into the corner weights.
 template <int DIM>
-__device__ __forceinline__ acc4 window_sample(const WinTiles &wt, const float *xwin, int fc, int xq, const acc4 &r) {
+__device__ __forceinline__ acc4 window_sample_masked(const WinTiles &wt, const float *xwin, int fc, int xq,
+                                                     const acc4 &r, float mk) {
     const float *xc = xwin + fc * XS + xq;
-    const float fx = r[DIM - 1] - floorf(r[DIM - 1]);
-    auto row = [&](int off) {
-        const acc4 x0 = *reinterpret_cast<const acc4 *>(xc + off * XS);
-        const acc4 x1 = *reinterpret_cast<const acc4 *>(xc + (off + 1) * XS);
-        return (1.f - fx) * x0 + fx * x1;
-    };
+    const float fx = r[DIM - 1];
+    const acc4 x00 = *reinterpret_cast<const acc4 *>(xc);
+    const acc4 x01 = *reinterpret_cast<const acc4 *>(xc + XS);
     if constexpr (DIM == 1) {
-        return row(0);
+        const float w1 = mk * fx, w0 = mk - w1;
+        return w0 * x00 + w1 * x01;
     } else {
-        const float fy = r[0] - floorf(r[0]);
-        return (1.f - fy) * row(0) + fy * row(wt.WE[2]);
+        const acc4 x10 = *reinterpret_cast<const acc4 *>(xc + wt.WE[2] * XS);
+        const acc4 x11 = *reinterpret_cast<const acc4 *>(xc + (wt.WE[2] + 1) * XS);
+        const float a1 = mk * r[0], a0 = mk - a1;
+        const float w01 = a0 * fx, w00 = a0 - w01, w11 = a1 * fx, w10 = a1 - w11;
+        return w00 * x00 + w01 * x01 + w10 * x10 + w11 * x11;
     }
 }
 
-template <int DIM, typename T>
+// RPT = records per thread per batch (WIN_TMAX * BPX / 512 = 4.5: one batch at 5); a
+// caller short of registers passes fewer.
+template <int DIM, typename T, int RPT = 5>
 __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const Tile &tile, const T *__restrict__ offset,
                                          const T *__restrict__ mask, int t0, int ntaps, acc4 *geo, int tid, int nthreads) {
+    // records e = tid, tid + nthreads, ...: every global load of a batch is issued
+    // before any is consumed (one memory latency per batch, not one per record)
     const bool deformable = offset != nullptr;
-    for (int e = tid; e < ntaps * BPX; e += nthreads) {
-        const int tl = e / BPX, i = e % BPX;
-        const int p = tile.pixel(g, wt, i);
-        acc4 r;
-        float mk = 0.f;
-        int cell = -1;
+    const int n = ntaps * BPX;
+    for (int e0 = 0; e0 < n; e0 += RPT * nthreads) {
+        int pv[RPT];
+        float ov[RPT][DIM], mv[RPT];
 #pragma unroll
-        for (int a = 0; a < DIM; ++a) r[a] = -4.f;
-        if (p >= 0) {
-            const Point<DIM, float> pt = sample_point<DIM, float, T>(g, offset, tile.b, p, t0 + tl, tile.ogu);
+        for (int j = 0; j < RPT; ++j) {
+            const int e = e0 + tid + j * nthreads;
+            const int tl = e / BPX, i = e % BPX;
+            const int p = e < n ? tile.pixel(g, wt, i) : -1;
+            pv[j] = p;
+            mv[j] = 0.f;
 #pragma unroll
-            for (int a = 0; a < DIM; ++a) r[a] = pt.pos[a];
-            mk = mask_at<float, T>(g, mask, tile.b, tile.mgu, t0 + tl, p);
-            if (DIM < 3 && wt.cells > 0) {
-                const AxisW<DIM, float> aw = axis_weights<DIM, float>(g, pt, deformable);
-                bool fast = true;
-                int lin = 0;
+            for (int a = 0; a < DIM; ++a) ov[j][a] = 0.f;
+            if (p >= 0) {
+                const int t = t0 + tl;
+                if (deformable) {
+                    const T *o = offset + ((size_t)(tile.b * g.og + tile.ogu) * g.Kn + t) * DIM * (size_t)g.Pn + p;
+#pragma unroll
+                    for (int a = 0; a < DIM; ++a) ov[j][a] = to_acc<float>(o[(size_t)a * g.Pn]);
+                }
+                mv[j] = mask_at<float, T>(g, mask, tile.b, tile.mgu, t, p);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+            const int e = e0 + tid + j * nthreads;
+            if (e >= n) continue;
+            const int tl = e / BPX, i = e % BPX;
+            const int p = pv[j];
+            acc4 r;
+            float mk = 0.f;
+            int cell = -1;
+#pragma unroll
+            for (int a = 0; a < DIM; ++a) r[a] = -4.f;
+            if (p >= 0) {
+                int kk[DIM], pp[DIM];
+                decompose_tap<DIM>(g, t0 + tl, kk);
+                decompose_pix<DIM>(g, p, pp);
+                Point<DIM, float> pt;
 #pragma unroll
                 for (int a = 0; a < DIM; ++a) {
                     const int ee = 3 - DIM + a;
-                    const int l = aw.lo[a] - tile.org[ee];
-                    fast = fast && l >= 0 && l + 1 < wt.WE[ee];
-                    lin = lin * wt.WE[ee] + l;
+                    pt.base[a] = pp[a] * g.st[ee] - g.pad[ee] + kk[a] * g.dil[ee];
+                    pt.pos[a] = (float)pt.base[a] + ov[j][a];
+                    r[a] = pt.pos[a];
                 }
-                cell = fast ? lin : -1;
+                mk = mv[j];
+                if (DIM < 3 && wt.cells > 0) {
+                    const AxisW<DIM, float> aw = axis_weights<DIM, float>(g, pt, deformable);
+                    bool fast = true;
+                    int lin = 0;
+#pragma unroll
+                    for (int a = 0; a < DIM; ++a) {
+                        const int ee = 3 - DIM + a;
+                        const int l = aw.lo[a] - tile.org[ee];
+                        fast = fast && l >= 0 && l + 1 < wt.WE[ee];
+                        lin = lin * wt.WE[ee] + l;
+                    }
+                    cell = fast ? lin : -1;
+                    // fast records keep only the fractional part of each position
+                    // (the high-corner weight): the fast paths need nothing else
+                    if (fast) {
+#pragma unroll
+                        for (int a = 0; a < DIM; ++a) r[a] = aw.fh[a];
+                    }
+                }
             }
+            if constexpr (DIM == 3) {
+                r[3] = mk;
+            } else {
+                if (DIM == 1) r[2] = 0.f;
+                r[DIM] = mk;
+                r[3] = __int_as_float(cell);
+            }
+            geo[tl * BPX + i] = r;
         }
-        if constexpr (DIM == 3) {
-            r[3] = mk;
-        } else {
-            if (DIM == 1) r[2] = 0.f;
-            r[DIM] = mk;
-            r[3] = __int_as_float(cell);
-        }
-        geo[tl * BPX + i] = r;
     }
 }
 
@@ -204,20 +253,71 @@ __device__ __forceinline__ void for_cells(const Geo &g, const WinTiles &wt, cons
 }
 
 // X window: xwin[cell * XS + 4 * quad .. + 3] = channels c0 + 4 * quad .. of the cell
-// (threads take (cell, quad) pairs: nthreads must be a multiple of 4)
+// (threads take (cell, quad) pairs: nthreads must be a multiple of 4). Loads go out in
+// batches of XB per thread before any is stored.
 __device__ __forceinline__ void fill_xwin(const Geo &g, const WinTiles &wt, const Tile &tile, const float *__restrict__ xb,
                                           float *xwin, int tid, int nthreads) {
+    constexpr int XB = 8;
     const int qd = tid & 3;
     const bool q_ok = tile.c0 + 4 * qd < g.Cg;
-    for_cells(g, wt, tile, tid >> 2, nthreads >> 2, [&](int cell, int si) {
-        acc4 v = acc4{0.f, 0.f, 0.f, 0.f};
-        if (si >= 0 && q_ok) v = *reinterpret_cast<const acc4 *>(xb + (size_t)si * g.C + 4 * qd);
-        *reinterpret_cast<acc4 *>(xwin + cell * XS + 4 * qd) = v;
-    });
+    const int step = nthreads >> 2;
+    const int first = tid >> 2;
+    // cell walker (no divisions per cell): (lz, ly, lx) of `cell`
+    int lx = first % wt.WE[2];
+    int rr = first / wt.WE[2];
+    int ly = rr % wt.WE[1];
+    int lz = rr / wt.WE[1];
+    const int sx_step = step % wt.WE[2], sy_step = (step / wt.WE[2]) % wt.WE[1], sz_step = step / (wt.WE[2] * wt.WE[1]);
+    for (int c0 = first; c0 < wt.cells; c0 += XB * step) {
+        acc4 v[XB];
+#pragma unroll
+        for (int j = 0; j < XB; ++j) {
+            const int cell = c0 + j * step;
+            const int sz = tile.org[0] + lz, sy = tile.org[1] + ly, sx = tile.org[2] + lx;
+            const bool in = cell < wt.cells && q_ok && sz >= 0 && sz < g.S[0] && sy >= 0 && sy < g.S[1] && sx >= 0 &&
+                            sx < g.S[2];
+            v[j] = acc4{0.f, 0.f, 0.f, 0.f};
+            if (in) v[j] = *reinterpret_cast<const acc4 *>(xb + (size_t)((sz * g.S[1] + sy) * g.S[2] + sx) * g.C + 4 * qd);
+            lx += sx_step;
+            ly += sy_step;
+            lz += sz_step;
+            if (lx >= wt.WE[2]) {
+                lx -= wt.WE[2];
+                ++ly;
+            }
+            if (ly >= wt.WE[1]) {
+                ly -= wt.WE[1];
+                ++lz;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < XB; ++j) {
+            const int cell = c0 + j * step;
+            if (cell < wt.cells) *reinterpret_cast<acc4 *>(xwin + cell * XS + 4 * qd) = v[j];
+        }
+    }
 }
 
-// The sampling geometry of a geo record: the point (integer base for offset-free
-// sampling, where the stored position is an exact integer) and its axis weights.
+// Absolute sampling positions of a record: a fast record holds fractional parts, whose
+// integer parts follow from its cell (lo = window origin + cell coordinates).
+template <int DIM>
+__device__ __forceinline__ acc4 record_position(const WinTiles &wt, const Tile &tile, acc4 r) {
+    const int fc = rec_fast_cell<DIM>(r);
+    if (DIM < 3 && fc >= 0) {
+        const int lx = fc % wt.WE[2];
+        if constexpr (DIM == 1) {
+            r[0] += (float)(tile.org[2] + lx);
+        } else {
+            r[0] += (float)(tile.org[1] + fc / wt.WE[2]);
+            r[1] += (float)(tile.org[2] + lx);
+        }
+    }
+    return r;
+}
+
+// The sampling geometry of a record holding absolute positions (see record_position):
+// the point (integer base for offset-free sampling, where the stored position is an
+// exact integer) and its axis weights.
 template <int DIM>
 __device__ __forceinline__ AxisW<DIM, float> record_weights(const Geo &g, const acc4 &r, bool deformable) {
     Point<DIM, float> pt;
