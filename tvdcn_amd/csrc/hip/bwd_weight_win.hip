@@ -38,7 +38,8 @@ constexpr int TM = WIN_TMAX;
 constexpr int GEO_WORDS = TM * BPX * 4;
 constexpr int SBUF_WORDS = 2 * TM * BC * SS;
 
-template <int DIM, typename T>
+// FULL: every pass uses all TM tap slots (no per-tap guards)
+template <int DIM, typename T, bool FULL>
 __global__ void __launch_bounds__(NT)
 bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const T *__restrict__ z,
                       const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
@@ -130,62 +131,84 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
             };
 
             // A operand: Z[m][4 consecutive chunk pixels], m = mrow + mb * 16 + lane % 16
-            int zp4[4];   // pixel of the lane's 4 chunk positions for the current chunk
+            const T *zrow[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int m = min(mrow + mb * 16 + (lane & 15), g.Mg - 1);
+                zrow[mb] = z + ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
+            }
+            // quad path: a chunk lies within one row of the box (box_x >= KP) and P_x % 4 == 0,
+            // so the lane's 4 pixels are consecutive and all inside or all outside the grid;
+            // in a tile wholly inside the grid every quad is inside
+            const bool quad = ww.z_vec && wt.box[2] >= KP;
+            const bool full = quad && tile.p0[0] + wt.box[0] <= g.P[0] && tile.p0[1] + wt.box[1] <= g.P[1] &&
+                              tile.p0[2] + wt.box[2] <= g.P[2];
+            // Z of chunk k; pixels outside the grid stay 0 (never loaded, so that a non-finite
+            // value there cannot leak into the sums)
             auto load_a = [&](int k, acc4 (&za)[MB]) {
                 const int i0 = k * KP + 4 * q;
-                int p[4];
+                if (quad) {
+                    const int iz = i0 >> wt.lbxy, iy = (i0 >> wt.lbx) & (wt.box[1] - 1), ix = i0 & (wt.box[2] - 1);
+                    const int pz = tile.p0[0] + iz, py = tile.p0[1] + iy, px = tile.p0[2] + ix;
+                    const int p = (pz * g.P[1] + py) * g.P[2] + px;
+                    if (full) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) p[u] = tile.pixel(g, wt, i0 + u);
-                const bool contig = ww.z_vec && p[0] >= 0 && p[3] == p[0] + 3;
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    const int m = min(mrow + mb * 16 + (lane & 15), g.Mg - 1);
-                    const T *zr = z + ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
-                    if (contig) {
-                        const Vec4<float> v = load4_t<float, T>(zr + p[0]);
-                        za[mb] = acc4{v.x, v.y, v.z, v.w};
+                        for (int mb = 0; mb < MB; ++mb) {
+                            const Vec4<float> v = load4_t<float, T>(zrow[mb] + p);
+                            za[mb] = acc4{v.x, v.y, v.z, v.w};
+                        }
                     } else {
+                        const bool ok = pz < g.P[0] && py < g.P[1] && px < g.P[2];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) za[mb][u] = p[u] >= 0 ? to_acc<float>(zr[p[u]]) : 0.f;
+                        for (int mb = 0; mb < MB; ++mb) {
+                            za[mb] = acc4{0.f, 0.f, 0.f, 0.f};
+                            if (ok) {
+                                const Vec4<float> v = load4_t<float, T>(zrow[mb] + p);
+                                za[mb] = acc4{v.x, v.y, v.z, v.w};
+                            }
+                        }
                     }
-                }
+                } else {
+                    int pu[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) zp4[u] = p[u];
+                    for (int u = 0; u < 4; ++u) pu[u] = tile.pixel(g, wt, i0 + u);
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            za[mb][u] = 0.f;
+                            if (pu[u] >= 0) za[mb][u] = to_acc<float>(zrow[mb][pu[u]]);
+                        }
+                }
             };
 
-            acc4 za[MB], zn[MB];
-            load_a(0, za);
-            build_s(0, 0);
-            __syncthreads();
-            for (int k = 0; k < NCH; ++k) {
-                const int bf = k & 1;
-                const bool more = k + 1 < NCH;
-                // pixels outside the grid contribute nothing (their S is 0; Z is zeroed
-                // so that a non-finite value there cannot leak)
-                acc4 zc[MB];
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) zc[mb][u] = zp4[u] >= 0 ? za[mb][u] : 0.f;
-                }
-                if (more) load_a(k + 1, zn);
-                const float *sb = sbuf + bf * (TM * BC * SS) + (lane & 15) * SS + 4 * q;
-#pragma unroll
-                for (int tp = 0; tp < TM; ++tp) {
-                    if (tp < ntaps) {
-                        const acc4 bv = *reinterpret_cast<const acc4 *>(sb + tp * BC * SS);
-#pragma unroll
-                        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-                            for (int mb = 0; mb < MB; ++mb) acc[mb][tp] = mfma16x16x4(zc[mb][kk], bv[kk], acc[mb][tp]);
-                    }
-                }
-                if (more) {
-                    build_s(k + 1, bf ^ 1);
-#pragma unroll
-                    for (int mb = 0; mb < MB; ++mb) za[mb] = zn[mb];
-                }
+            {
+                acc4 za[MB], zn[MB];
+                load_a(0, za);
+                build_s(0, 0);
                 __syncthreads();
+                for (int k = 0; k < NCH; ++k) {
+                    const int bf = k & 1;
+                    const bool more = k + 1 < NCH;
+                    if (more) load_a(k + 1, zn);
+                    const float *sb = sbuf + bf * (TM * BC * SS) + (lane & 15) * SS + 4 * q;
+#pragma unroll
+                    for (int tp = 0; tp < TM; ++tp) {
+                        if (FULL || tp < ntaps) {
+                            const acc4 bv = *reinterpret_cast<const acc4 *>(sb + tp * BC * SS);
+#pragma unroll
+                            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                                for (int mb = 0; mb < MB; ++mb) acc[mb][tp] = mfma16x16x4(za[mb][kk], bv[kk], acc[mb][tp]);
+                        }
+                    }
+                    if (more) {
+                        build_s(k + 1, bf ^ 1);
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb) za[mb] = zn[mb];
+                    }
+                    __syncthreads();
+                }
             }
         }
 
@@ -207,10 +230,10 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     }
 }
 
-template <int DIM, typename T>
+template <int DIM, typename T, bool FULL>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, hipStream_t s) {
-    auto kern = bwd_weight_win_kernel<DIM, T>;
+    auto kern = bwd_weight_win_kernel<DIM, T, FULL>;
     const size_t lds = ((size_t)GEO_WORDS + SBUF_WORDS + (size_t)wt.cells * XS) * sizeof(float);
     static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
     if (!attr_set) {
@@ -229,10 +252,14 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, hipStream_t s) {
+    const bool full = wt.tpp == TM && g.Kn % TM == 0;
     switch (dim) {
-        case 1: return launch_k<1, T>(g, wt, ww, z, xcl, offset, mask, part, s);
-        case 2: return launch_k<2, T>(g, wt, ww, z, xcl, offset, mask, part, s);
-        case 3: return launch_k<3, T>(g, wt, ww, z, xcl, offset, mask, part, s);
+        case 1: return full ? launch_k<1, T, true>(g, wt, ww, z, xcl, offset, mask, part, s)
+                            : launch_k<1, T, false>(g, wt, ww, z, xcl, offset, mask, part, s);
+        case 2: return full ? launch_k<2, T, true>(g, wt, ww, z, xcl, offset, mask, part, s)
+                            : launch_k<2, T, false>(g, wt, ww, z, xcl, offset, mask, part, s);
+        case 3: return full ? launch_k<3, T, true>(g, wt, ww, z, xcl, offset, mask, part, s)
+                            : launch_k<3, T, false>(g, wt, ww, z, xcl, offset, mask, part, s);
     }
     return hipErrorInvalidValue;
 }
