@@ -55,6 +55,23 @@ static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
 constexpr int GEO_WORDS = WIN_TMAX * BPX * 4;
 constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + BC + 4;
 
+// Nearest integer, halves rounded up (v_cvt_rpi_i32_f32 = floor(x + 0.5)): one instruction
+// where round-to-nearest-even takes two; |x| < 2^29 here
+__device__ __forceinline__ int fixed_round(float x) {
+    int r;
+    asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
+// Sum over the four 16-lane rows of the wave (lanes l, l ^ 16, l ^ 32, l ^ 48), every lane
+// receiving the total: two row swaps (gfx950 v_permlane16/32_swap) instead of LDS shuffles
+__device__ __forceinline__ float row_sum4(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 template <int DIM, typename T, bool SCATTER, bool COORD>
 __global__ void __launch_bounds__(NT)
 bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, const float *__restrict__ wchunks,
@@ -275,48 +292,56 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                     const float fy = DIM == 2 ? r[0] : 0.f;
                     constexpr int NF = DIM == 2 ? 4 : 2;
                     int cell[NF];
-                    float w[NF];
                     cell[0] = fc;
                     cell[1] = fc + 1;
                     if constexpr (DIM == 2) {
                         cell[2] = fc + wt.WE[2];
                         cell[3] = fc + wt.WE[2] + 1;
-                        w[0] = (1.f - fy) * (1.f - fx);
-                        w[1] = (1.f - fy) * fx;
-                        w[2] = fy * (1.f - fx);
-                        w[3] = fy * fx;
-                    } else {
-                        w[0] = 1.f - fx;
-                        w[1] = fx;
                     }
                     if constexpr (COORD) {
-                        acc4 x[NF];
+                        // every quantity is linear in X: contract the lane's 4 channels with G
+                        // per corner first (gk), then apply the bilinear / coordinate weights
+                        float gk[NF];
 #pragma unroll
-                        for (int k = 0; k < NF; ++k) x[k] = *reinterpret_cast<const acc4 *>(xwin + cell[k] * XS + mq);
-                        acc4 sv = w[0] * x[0];
-#pragma unroll
-                        for (int k = 1; k < NF; ++k) sv += w[k] * x[k];
-                        acc4 d[DIM];
-                        if constexpr (DIM == 2) {
-                            d[0] = (1.f - fx) * (x[2] - x[0]) + fx * (x[3] - x[1]);   // d/dy
-                            d[1] = (1.f - fy) * (x[1] - x[0]) + fy * (x[3] - x[2]);   // d/dx
-                        } else {
-                            d[0] = x[1] - x[0];
+                        for (int k = 0; k < NF; ++k) {
+                            const acc4 x = *reinterpret_cast<const acc4 *>(xwin + cell[k] * XS + mq);
+                            gk[k] = gv[0] * x[0] + gv[1] * x[1] + gv[2] * x[2] + gv[3] * x[3];
                         }
-#pragma unroll
-                        for (int a = 0; a < DIM; ++a)
-                            qv[a] = mk * (gv[0] * d[a][0] + gv[1] * d[a][1] + gv[2] * d[a][2] + gv[3] * d[a][3]);
-                        qv[DIM] = gv[0] * sv[0] + gv[1] * sv[1] + gv[2] * sv[2] + gv[3] * sv[3];
+                        if constexpr (DIM == 2) {
+                            const float ex0 = gk[1] - gk[0], ex1 = gk[3] - gk[2];   // along x, rows y0 / y1
+                            const float ey0 = gk[2] - gk[0], ey1 = gk[3] - gk[1];   // along y, columns x0 / x1
+                            const float t0 = gk[0] + fx * ex0, t1 = gk[2] + fx * ex1;
+                            qv[0] = mk * (ey0 + fx * (ey1 - ey0));   // d/dy
+                            qv[1] = mk * (ex0 + fy * (ex1 - ex0));   // d/dx
+                            qv[2] = t0 + fy * (t1 - t0);             // sampled value
+                        } else {
+                            const float ex = gk[1] - gk[0];
+                            qv[0] = mk * ex;
+                            qv[1] = gk[0] + fx * ex;
+                        }
                     }
                     if constexpr (SCATTER) {
                         if (cq_ok) {
+                            // mask-weighted corner weights; G pre-scaled to fixed point per channel
+                            float wm[NF];
+                            if constexpr (DIM == 2) {
+                                const float a1 = mk * fy, a0 = mk - a1;
+                                wm[1] = a0 * fx;
+                                wm[0] = a0 - wm[1];
+                                wm[3] = a1 * fx;
+                                wm[2] = a1 - wm[3];
+                            } else {
+                                wm[1] = mk * fx;
+                                wm[0] = mk - wm[1];
+                            }
+                            float gs[4];
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) gs[v] = ldexpf(gv[v], sexp[v]);
 #pragma unroll
                             for (int k = 0; k < NF; ++k) {
-                                const float s = mk * w[k];
                                 unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + cell[k] * CS + mq);
 #pragma unroll
-                                for (int v = 0; v < 4; ++v)
-                                    atomicAdd(dst + v, (unsigned int)__float2int_rn(ldexpf(s * gv[v], sexp[v])));
+                                for (int v = 0; v < 4; ++v) atomicAdd(dst + v, (unsigned int)fixed_round(wm[k] * gs[v]));
                             }
                         }
                     }
@@ -372,7 +397,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                                     unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + loc[k] * CS + mq);
 #pragma unroll
                                     for (int v = 0; v < 4; ++v)
-                                        atomicAdd(dst + v, (unsigned int)__float2int_rn(ldexpf(s * gv[v], sexp[v])));
+                                        atomicAdd(dst + v, (unsigned int)fixed_round(ldexpf(s * gv[v], sexp[v])));
                                 } else {
                                     float *dst = gdst + (size_t)gidx[k] * g.C;
 #pragma unroll
@@ -386,8 +411,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                 if constexpr (COORD) {
 #pragma unroll
                     for (int a = 0; a <= DIM; ++a) {
-                        qv[a] += __shfl_xor(qv[a], 16);
-                        qv[a] += __shfl_xor(qv[a], 32);
+                        qv[a] = row_sum4(qv[a]);
                     }
                     const int p = zp[pb];
                     if (q == 0 && p >= 0) {
