@@ -235,17 +235,23 @@ def run_suite_case(n, dtype, steps, warmup):
     gout = torch.randn(out_shape, generator=torch.Generator().manual_seed(4000 + n)).to(dev, dtype)
     fwd_ms, step_ms, kern = time_path(params, fwd, gout, steps, warmup)
     F = suite_flops(c)
+    # backward contractions: conv grad-columns + grad-weight; transposed also recomputes Wᵀ·X for the
+    # offset / mask gradients (3 contractions)
+    nb = 3 if c["tr"] else 2
     es = torch.finfo(dtype).bits // 8
     mask_bytes = es * (logits.numel() if logits is not None else 0)
     roof = family_rooflines(kern, F, es * gout.numel(), mask_bytes)
     return {
         "case": c["name"], "dtype": str(dtype).replace("torch.", ""), "compute": "f32 (fp32 MFMA, fp32 accumulate)",
         "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(step_ms - fwd_ms, 4), "fwd_bwd_ms": round(step_ms, 4),
-        "gflop_fwd": round(F / 1e9, 3), "gflop_fwd_bwd": round(3 * F / 1e9, 3),
+        "gflop_fwd": round(F / 1e9, 3), "gflop_bwd": round(nb * F / 1e9, 3),
+        "gflop_fwd_bwd": round((1 + nb) * F / 1e9, 3),
         "fwd_tflops": round(F / (fwd_ms * 1e-3) / 1e12, 2),
         "fwd_frac_mfma_fp32": round(F / (fwd_ms * 1e-3) / PEAK_FP32_MFMA, 4),
-        "fwd_bwd_tflops": round(3 * F / (step_ms * 1e-3) / 1e12, 2),
-        "fwd_bwd_frac_mfma_fp32": round(3 * F / (step_ms * 1e-3) / PEAK_FP32_MFMA, 4),
+        "bwd_tflops": round(nb * F / ((step_ms - fwd_ms) * 1e-3) / 1e12, 2),
+        "bwd_frac_mfma_fp32": round(nb * F / ((step_ms - fwd_ms) * 1e-3) / PEAK_FP32_MFMA, 4),
+        "fwd_bwd_tflops": round((1 + nb) * F / (step_ms * 1e-3) / 1e12, 2),
+        "fwd_bwd_frac_mfma_fp32": round((1 + nb) * F / (step_ms * 1e-3) / PEAK_FP32_MFMA, 4),
         "kernels": roof,
     }
 
@@ -300,10 +306,17 @@ def cpu_baseline(inp, batch):
         times.append(time.perf_counter() - t0)
     ms = statistics.median(times) * 1e3 * (8 / batch)
     cores = len(os.sched_getaffinity(0))
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
     return dict(value=round(ms, 1), unit="ms", cores=cores, kind="reference",
                 sample=f"reference CPU path (oracle/_ref: tvdcn 1.1.0 cpu/ kernels + ATen addmm_), forward+backward "
                        f"of {batch} of the 8 images, median of {reps} after 1 warm-up, scaled x{8 // batch} to the "
-                       f"full batch; torch threads {torch.get_num_threads()}, reference OpenMP loops 32 threads")
+                       f"full batch; {model}; torch threads {torch.get_num_threads()}, reference OpenMP loops "
+                       f"32 threads")
 
 
 def main():

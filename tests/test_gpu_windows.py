@@ -48,3 +48,28 @@ def test_nonfinite_grad_out_fp32():
         if fin.any():
             e = rel_err(gr[fin], r[fin])
             assert e < TOL[torch.float32][1], f"grad_{name} rel err {e}"
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_offset_free_nonfinite_input_fp32(dim):
+    """Integer sampling (offset None) touches only the sampled pixel: an inf in the input must
+    reach exactly the outputs / gradients the reference's integer sampling reaches."""
+    in_size = {2: [20, 18], 3: [6, 10, 9]}[dim]
+    case = make_case(dim, False, batch=2, cin=32, cout=32, kernel=[3] * dim, stride=[1] * dim, padding=[1] * dim,
+                     dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim, seed=530 + dim, deformable=False)
+    case["input"] = case["input"].clone()
+    case["input"][1, 3][(2,) * dim] = float("inf")
+    g = torch.Generator().manual_seed(531)
+    gout = torch.rand(case["out_shape"], generator=g, dtype=torch.float64)
+    out, grads, _ = run_gpu(case, torch.float32, grad_out=gout)
+    ref_out, ref_grads = run_oracle(case, gout, torch.float32)
+    for name, gr, r in zip(("output", "input", "weight", "offset", "mask", "bias"), [out] + list(grads), [ref_out] + list(ref_grads)):
+        if r is None:
+            continue
+        gr = gr.detach().double().cpu()
+        assert torch.equal(torch.isnan(gr), torch.isnan(r)), f"{name}: nan pattern differs"
+        assert torch.equal(torch.isinf(gr), torch.isinf(r)), f"{name}: inf pattern differs"
+        fin = torch.isfinite(r)
+        if fin.any():
+            e = rel_err(gr[fin], r[fin])
+            assert e < TOL[torch.float32][1], f"{name} rel err {e}"

@@ -285,7 +285,62 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                 const acc4 gv = gt[pb];
                 const int fc = rec_fast_cell<DIM>(r);
                 float qv[DIM + 1];
-                if (DIM < 3 && fc >= 0 && (!SCATTER || use_window)) {
+                bool done = false;
+                if constexpr (DIM == 3) {
+                    if (!SCATTER || use_window) {
+                        // 3D: one branch-light path for every lane (window margins of about one
+                        // cell: most waves hold a lane with a corner outside the window)
+                        done = true;
+                        const Corners3 cr(g, wt, tile, r, deformable);
+                        if constexpr (COORD) {
+                            // G contracted with X per corner, then the trilinear / coordinate weights
+                            float gs = 0.f, gz = 0.f, gy = 0.f, gxx = 0.f;
+#pragma unroll
+                            for (int k = 0; k < 8; ++k) {
+                                if (k > 0 && !deformable) break;
+                                const acc4 x = corner_x3(g, wt, cr, k, xwin, mq, xb + mq, cq_ok);
+                                const float gk = gv[0] * x[0] + gv[1] * x[1] + gv[2] * x[2] + gv[3] * x[3];
+                                const int bz = k >> 2, by = (k >> 1) & 1, bx = k & 1;
+                                const float wz = bz ? cr.fh[0] : 1.f - cr.fh[0];
+                                const float wy = by ? cr.fh[1] : 1.f - cr.fh[1];
+                                const float wx = bx ? cr.fh[2] : 1.f - cr.fh[2];
+                                gs += wz * wy * wx * gk;
+                                gz += (bz ? gk : -gk) * (wy * wx);
+                                gy += (by ? gk : -gk) * (wz * wx);
+                                gxx += (bx ? gk : -gk) * (wz * wy);
+                            }
+                            qv[0] = mk * gz;
+                            qv[1] = mk * gy;
+                            qv[2] = mk * gxx;
+                            qv[3] = cr.inside ? gs : 0.f;
+                        }
+                        if constexpr (SCATTER) {
+                            if (cq_ok) {
+                                float gsc[4];
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) gsc[v] = ldexpf(gv[v], sexp[v]);
+                                float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+#pragma unroll
+                                for (int k = 0; k < 8; ++k) {
+                                    if (k > 0 && !deformable) break;
+                                    if (!cr.in_grid(k)) continue;
+                                    const float sw = mk * cr.weight(k);
+                                    if (cr.in_win(k)) {
+                                        unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + cr.cell(wt, k) * CS + mq);
+#pragma unroll
+                                        for (int v = 0; v < 4; ++v)
+                                            atomicAdd(dst + v, (unsigned int)fixed_round(sw * gsc[v]));
+                                    } else {
+                                        float *dst = gdst + (size_t)cr.idx(g, k) * g.C;
+#pragma unroll
+                                        for (int v = 0; v < 4; ++v) atomic_add(dst + v, sw * gv[v]);
+                                    }
+                                }
+                            }
+                        }
+                    }
+                } else if (fc >= 0 && (!SCATTER || use_window)) {
+                    done = true;
                     // fast path: every corner cell is in the window (zeros / dropped
                     // outside the grid), plain bilinear formulas
                     const float fx = r[DIM - 1];   // fast records hold the fractional parts
@@ -345,7 +400,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
                             }
                         }
                     }
-                } else {
+                }
+                if (!done) {
                     // general path: per-corner validity, window membership and global fallback
                     // (also taken by fast records when the pass scatters to global memory)
                     const AxisW<DIM, float> aw = record_weights<DIM>(g, record_position<DIM>(wt, tile, r), deformable);

@@ -98,7 +98,9 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                     const int fc = fast_cell<DIM>(r);
                     const float mk = rec_mask<DIM>(r);
                     acc4 sv;
-                    if (fc >= 0) {
+                    if constexpr (DIM == 3) {
+                        sv = sample3_masked(g, wt, tile, xwin, 4 * sq, xb + 4 * sq, cq_ok, r, deformable);
+                    } else if (fc >= 0) {
                         // every corner cell is in the window (zeros outside the grid)
                         sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * sq, r, mk);
                     } else {

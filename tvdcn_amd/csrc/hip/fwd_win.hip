@@ -108,7 +108,9 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
             const int fc = fast_cell<DIM>(r);
             const float mk = rec_mask<DIM>(r);
             acc4 sv;
-            if (fc >= 0) {
+            if constexpr (DIM == 3) {
+                sv = sample3_masked(g, wt, tile, xwin, 4 * qd, xg + cs * BC + 4 * qd, q_ok, r, deformable);
+            } else if (fc >= 0) {
                 sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * qd, r, mk);
             } else {
                 Point<DIM, float> pt;
@@ -291,7 +293,10 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const vo
 template <int DIM, typename T>
 hipError_t launch_m(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
                     const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
-    if (fw.mb == 8) return launch_k<DIM, T, 8>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+    // 3D: 64-row tiles only (the trilinear sampler needs the registers)
+    if constexpr (DIM < 3) {
+        if (fw.mb == 8) return launch_k<DIM, T, 8>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+    }
     if (fw.mb == 4) return launch_k<DIM, T, 4>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
     return hipErrorInvalidValue;
 }
@@ -319,7 +324,7 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     // 128-row tiles unless the GEMM side is small or the grid would leave CUs idle
     // (one workgroup per CU at a time: the window takes most of the LDS)
     const long long spatial = (long long)g.G * g.B * base.ntile[0] * base.ntile[1] * base.ntile[2];
-    f.mb = (g.Mg <= 64 || spatial * ((g.Mg + 127) / 128) < 256) ? 4 : 8;
+    f.mb = (dim == 3 || g.Mg <= 64 || spatial * ((g.Mg + 127) / 128) < 256) ? 4 : 8;
     const int rows = 16 * f.mb;
     const long long max_cells = (long long)xq_of(f.mb) * NT / 4;
     wt = win_resize(base, g, dim, (size_t)GEO_WORDS * sizeof(float), XS * sizeof(float), max_cells);

@@ -99,7 +99,8 @@ struct Tile {
 // (which reproduces the zero padding and the sample range rule, whose excluded
 // points have every corner outside the grid), and scatter into them is dropped
 // when the window is flushed. A record with a fast cell holds the fractional part
-// of each position (the high-corner weight) in place of the position. Pixels outside
+// of each position (the high-corner weight) in place of the position; offset-free
+// records never get one. Pixels outside
 // the grid get position -4 on every axis (no corner inside the grid), mask 0 and no
 // fast cell.
 template <int DIM> __device__ __forceinline__ float rec_mask(const acc4 &r) { return DIM == 3 ? r[3] : r[DIM]; }
@@ -136,6 +137,90 @@ __device__ __forceinline__ acc4 window_sample_masked(const WinTiles &wt, const f
         const float w01 = a0 * fx, w00 = a0 - w01, w11 = a1 * fx, w10 = a1 - w11;
         return w00 * x00 + w01 * x01 + w10 * x10 + w11 * x11;
     }
+}
+
+// Corner geometry of a 3D record (absolute positions) against the tile's window and the
+// sampled grid: per axis the low corner, the high-corner weight and whether each of the two
+// corner coordinates lies in the window / in the grid. Corner k = (z bit, y bit, x bit) sits at
+// window cell cell0 + bz * WE_y * WE_x + by * WE_x + bx and grid index idx0 + bz * S_y * S_x +
+// by * S_x + bx. Offset-free sampling (integer positions) has only the low corner.
+struct Corners3 {
+    float fh[3];
+    bool win[3][2], grid[3][2];
+    int cell0, idx0;
+    bool inside;   // sample range rule: -1 < pos < S on every axis
+    __device__ __forceinline__ Corners3(const Geo &g, const WinTiles &wt, const Tile &tile, const acc4 &r,
+                                        bool deformable) {
+        int lo[3], wl[3];
+        inside = true;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const float f = floorf(r[a]);
+            lo[a] = (int)f;
+            fh[a] = deformable ? r[a] - f : 0.f;
+            inside = inside && r[a] > -1.f && r[a] < (float)g.S[a];
+            wl[a] = lo[a] - tile.org[a];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                win[a][b] = (unsigned)(wl[a] + b) < (unsigned)wt.WE[a];
+                grid[a][b] = (unsigned)(lo[a] + b) < (unsigned)g.S[a];
+            }
+        }
+        cell0 = (wl[0] * wt.WE[1] + wl[1]) * wt.WE[2] + wl[2];
+        idx0 = (lo[0] * g.S[1] + lo[1]) * g.S[2] + lo[2];
+    }
+    __device__ __forceinline__ bool in_win(int k) const { return win[0][k >> 2] && win[1][(k >> 1) & 1] && win[2][k & 1]; }
+    __device__ __forceinline__ bool in_grid(int k) const {
+        return grid[0][k >> 2] && grid[1][(k >> 1) & 1] && grid[2][k & 1];
+    }
+    __device__ __forceinline__ int cell(const WinTiles &wt, int k) const {
+        return cell0 + (k >> 2) * (wt.WE[1] * wt.WE[2]) + ((k >> 1) & 1) * wt.WE[2] + (k & 1);
+    }
+    __device__ __forceinline__ int idx(const Geo &g, int k) const {
+        return idx0 + (k >> 2) * (g.S[1] * g.S[2]) + ((k >> 1) & 1) * g.S[2] + (k & 1);
+    }
+    // trilinear weight of corner k (product in the reference's axis order)
+    __device__ __forceinline__ float weight(int k) const {
+        const float wz = (k >> 2) ? fh[0] : 1.f - fh[0];
+        const float wy = ((k >> 1) & 1) ? fh[1] : 1.f - fh[1];
+        const float wx = (k & 1) ? fh[2] : 1.f - fh[2];
+        return wz * wy * wx;
+    }
+};
+
+// X of one channel quad at corner k: from the window when the corner lies in it (window
+// cells outside the grid hold zeros), else from global memory (xgq: the channels-last X of
+// the tile's image at the quad's first channel), zero outside the grid. The LDS read is
+// unconditional (clamped) and the global read sits in its own branch: the two address
+// spaces are never merged into one pointer.
+__device__ __forceinline__ acc4 corner_x3(const Geo &g, const WinTiles &wt, const Corners3 &cr, int k, const float *xwin,
+                                          int xq, const float *__restrict__ xgq, bool q_ok) {
+    const bool iw = cr.in_win(k);
+    acc4 x = *reinterpret_cast<const acc4 *>(xwin + (iw ? cr.cell(wt, k) : 0) * XS + xq);
+    if (!iw) {
+        x = acc4{0.f, 0.f, 0.f, 0.f};
+        if (q_ok && cr.in_grid(k)) x = *reinterpret_cast<const acc4 *>(xgq + (size_t)cr.idx(g, k) * g.C);
+    }
+    return x;
+}
+
+// mask * sample of one channel quad at a 3D record: one branch-light path for every lane
+// (the 3D windows that fit in LDS have margins of about one cell, so most waves hold some
+// lane with a corner outside the window; a separate in-window fast path would run beside
+// this one rather than instead of it).
+__device__ __forceinline__ acc4 sample3_masked(const Geo &g, const WinTiles &wt, const Tile &tile, const float *xwin,
+                                               int xq, const float *__restrict__ xgq, bool q_ok, const acc4 &r,
+                                               bool deformable) {
+    const Corners3 cr(g, wt, tile, r, deformable);
+    acc4 sv = acc4{0.f, 0.f, 0.f, 0.f};
+    if (!cr.inside) return sv;
+    const float mk = r[3];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        if (k > 0 && !deformable) break;
+        sv += (mk * cr.weight(k)) * corner_x3(g, wt, cr, k, xwin, xq, xgq, q_ok);
+    }
+    return sv;
 }
 
 // RPT = records per thread per batch (WIN_TMAX * BPX / 512 = 4.5: one batch at 5); a
@@ -204,6 +289,10 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
                         fast = fast && l >= 0 && l + 1 < wt.WE[ee];
                         lin = lin * wt.WE[ee] + l;
                     }
+                    // offset-free sampling never takes the fast paths: its integer sampling reads
+                    // the low corner only (a high corner, even at weight 0, must not be touched,
+                    // so that a non-finite value there cannot leak in)
+                    fast = fast && deformable;
                     cell = fast ? lin : -1;
                     // fast records keep only the fractional part of each position
                     // (the high-corner weight): the fast paths need nothing else
