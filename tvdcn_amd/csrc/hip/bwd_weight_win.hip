@@ -28,8 +28,11 @@ using namespace win;
 
 constexpr int NW = 8;               // waves per workgroup
 constexpr int NT = 64 * NW;
-constexpr int MB = 2;               // 16-row blocks per wave
-constexpr int BMW = NW * MB * 16;   // rows per workgroup (256)
+// Row layouts: MB 16-row blocks per wave and TG tap groups. The waves split into TG groups
+// of NW / TG; group g takes the taps t = g (mod TG) of every pass for the rows of its waves,
+// so that a GEMM side of 64 rows still keeps all eight waves on MFMAs:
+//   MB = 2, TG = 1: 256 rows per workgroup;  MB = 1, TG = 2: 64 rows, taps split by parity.
+template <int MB, int TG> constexpr int rows_of() { return (NW / TG) * MB * 16; }
 constexpr int KP = 16;              // pixels per chunk
 constexpr int NCH = BPX / KP;       // chunks per tile
 constexpr int SS = KP + 4;          // S tile row stride (rows = (tap, channel))
@@ -39,12 +42,13 @@ constexpr int GEO_WORDS = TM * BPX * 4;
 constexpr int SBUF_WORDS = 2 * TM * BC * SS;
 
 // FULL: every pass uses all TM tap slots (no per-tap guards)
-template <int DIM, typename T, bool FULL>
+template <int DIM, typename T, bool FULL, int MB, int TG>
 __global__ void __launch_bounds__(NT)
 bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const T *__restrict__ z,
                       const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
                       float *__restrict__ part) {
     constexpr int NC = 1 << DIM;
+    constexpr int BMW = rows_of<MB, TG>();
     extern __shared__ float smem[];
     acc4 *geo = reinterpret_cast<acc4 *>(smem);         // [TM][BPX]
     float *sbuf = smem + GEO_WORDS;                     // [2][TM * BC][SS]
@@ -65,7 +69,8 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     const int s_beg = split * ww.tiles_per_split;
     const int s_end = min(ww.n_spatial, s_beg + ww.tiles_per_split);
     const bool deformable = offset != nullptr;
-    const int mrow = mt * BMW + wave * (MB * 16);    // first row of this wave
+    const int tg = wave / (NW / TG);                     // this wave's tap group
+    const int mrow = mt * BMW + (wave % (NW / TG)) * (MB * 16);   // first row of this wave
 
     // S-builder item of this thread: chunk pixel j, channel quad sq, taps st, st + 8, ...
     const int sj = tid & 15, sq = (tid >> 4) & 3, st0 = tid >> 6;
@@ -196,7 +201,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                     const float *sb = sbuf + bf * (TM * BC * SS) + (lane & 15) * SS + 4 * q;
 #pragma unroll
                     for (int tp = 0; tp < TM; ++tp) {
-                        if (FULL || tp < ntaps) {
+                        if ((FULL || tp < ntaps) && (TG == 1 || tp % TG == tg)) {
                             const acc4 bv = *reinterpret_cast<const acc4 *>(sb + tp * BC * SS);
 #pragma unroll
                             for (int kk = 0; kk < 4; ++kk)
@@ -217,7 +222,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
         // this split's block: part[split][grp][t][m][c]
 #pragma unroll
         for (int tp = 0; tp < TM; ++tp) {
-            if (tp >= ntaps) continue;
+            if (tp >= ntaps || (TG > 1 && tp % TG != tg)) continue;
             float *dst = part + (((size_t)split * g.G + grp) * g.Kn + t0 + tp) * g.Mg * (size_t)g.Cg;
             const int c = ct * BC + (lane & 15);
             if (c >= g.Cg) continue;
@@ -232,10 +237,10 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     }
 }
 
-template <int DIM, typename T, bool FULL>
+template <int DIM, typename T, bool FULL, int MB, int TG>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, hipStream_t s) {
-    auto kern = bwd_weight_win_kernel<DIM, T, FULL>;
+    auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG>;
     const size_t lds = ((size_t)GEO_WORDS + SBUF_WORDS + (size_t)wt.cells * XS) * sizeof(float);
     static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
     if (!attr_set) {
@@ -255,13 +260,17 @@ template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, hipStream_t s) {
     const bool full = wt.tpp == TM && g.Kn % TM == 0;
+    auto pick = [&](auto dim_tag) -> hipError_t {
+        constexpr int D = decltype(dim_tag)::value;
+        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2>(g, wt, ww, z, xcl, offset, mask, part, s)
+                                    : launch_k<D, T, false, 1, 2>(g, wt, ww, z, xcl, offset, mask, part, s);
+        return full ? launch_k<D, T, true, 2, 1>(g, wt, ww, z, xcl, offset, mask, part, s)
+                    : launch_k<D, T, false, 2, 1>(g, wt, ww, z, xcl, offset, mask, part, s);
+    };
     switch (dim) {
-        case 1: return full ? launch_k<1, T, true>(g, wt, ww, z, xcl, offset, mask, part, s)
-                            : launch_k<1, T, false>(g, wt, ww, z, xcl, offset, mask, part, s);
-        case 2: return full ? launch_k<2, T, true>(g, wt, ww, z, xcl, offset, mask, part, s)
-                            : launch_k<2, T, false>(g, wt, ww, z, xcl, offset, mask, part, s);
-        case 3: return full ? launch_k<3, T, true>(g, wt, ww, z, xcl, offset, mask, part, s)
-                            : launch_k<3, T, false>(g, wt, ww, z, xcl, offset, mask, part, s);
+        case 1: return pick(std::integral_constant<int, 1>());
+        case 2: return pick(std::integral_constant<int, 2>());
+        case 3: return pick(std::integral_constant<int, 3>());
     }
     return hipErrorInvalidValue;
 }
@@ -273,10 +282,13 @@ size_t weight_win_fixed_bytes() { return (size_t)(GEO_WORDS + SBUF_WORDS) * size
 WeightWin plan_weight_win(const Geo &g, const WinTiles &wt) {
     WeightWin w{};
     w.ok = false;
-    // needs the windowed tiling and enough rows to keep the eight waves busy
-    if (!wt.ok || g.Mg < 128 || (size_t)GEO_WORDS * 4 + SBUF_WORDS * 4 + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
+    // needs the windowed tiling; GEMM sides up to 128 rows take 64-row tiles with the taps
+    // split between two wave groups, larger ones 256-row tiles
+    if (!wt.ok || g.Mg < 16 || (size_t)GEO_WORDS * 4 + SBUF_WORDS * 4 + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
         return w;
-    w.m_tiles = (g.Mg + BMW - 1) / BMW;
+    w.tg = g.Mg <= 128 ? 2 : 1;
+    const int rows = w.tg == 2 ? rows_of<1, 2>() : rows_of<2, 1>();
+    w.m_tiles = (g.Mg + rows - 1) / rows;
     w.n_spatial = g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2];
     const long long per_split_groups = (long long)g.G * w.m_tiles * wt.c_tiles;
     // one workgroup per CU, about one wave of workgroups

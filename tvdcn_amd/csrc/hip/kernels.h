@@ -51,7 +51,8 @@ struct WinTiles {
 // 16-channel slice, 256 rows) and a run of spatial tiles of the WinTiles tiling.
 struct WeightWin {
     bool ok;
-    int m_tiles;         // 256-row blocks of the GEMM side
+    int tg;              // tap groups: 1 (256-row tiles) or 2 (64-row tiles, taps split by parity)
+    int m_tiles;         // row tiles of the GEMM side
     int n_spatial;       // spatial tiles (B x ntile0 x ntile1 x ntile2)
     int tiles_per_split, n_split;
     bool z_vec;          // 4 consecutive tile pixels are contiguous and 16-byte aligned
