@@ -74,7 +74,7 @@ __device__ __forceinline__ float row_sum4(float v) {
 
 template <int DIM, typename T, bool SCATTER, bool COORD>
 __global__ void __launch_bounds__(NT)
-bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, const float *__restrict__ wchunks,
+bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wchunks,
                     const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
                     float *__restrict__ gx_cl, float *__restrict__ goff, float *__restrict__ gmask) {
     constexpr int NC = 1 << DIM;
@@ -195,12 +195,13 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *__restrict__ z, con
             for (int ms = 0; ms < wt.m_steps; ms += 2) {
                 const bool has1 = ms + 1 < wt.m_steps;
                 load_z(min(ms + 1, wt.m_steps - 1), zbb);
-                // keep the prefetch ahead of this step's MFMAs (the scheduler would sink it)
-                __builtin_amdgcn_sched_barrier(0);
+                // keep the prefetch ahead of this step's MFMAs: without the fence the loads are
+                // sunk next to their first use (a full memory latency exposed every step)
+                issue_fence();
                 step(ms, za);
                 if (has1) {
                     load_z(min(ms + 2, wt.m_steps - 1), za);
-                    __builtin_amdgcn_sched_barrier(0);
+                    issue_fence();
                     step(ms + 1, zbb);
                 }
             }

@@ -24,6 +24,15 @@ constexpr int XS = BC + 4; // X window cell stride (floats; 16-byte quads)
 
 typedef f32x4 acc4;
 
+// Holds the memory operations issued above it in place: IR-level passes may not move loads
+// or stores across it (the empty asm clobbers memory) and neither may the machine scheduler
+// (sched_barrier); it waits for nothing. Used after prefetches, which would otherwise be
+// sunk next to their first use.
+__device__ __forceinline__ void issue_fence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // Per-workgroup tile context.
 struct Tile {
     int b;              // image
