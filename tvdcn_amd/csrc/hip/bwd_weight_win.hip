@@ -11,10 +11,11 @@
 // tiles); eight waves, wave w owning 32 rows. The dW block [rows][16 c][taps of the
 // pass] stays in accumulators (72 registers per lane) across the whole run of tiles.
 // Per tile (a box of 256 column pixels of one image, see window.h) the sampling
-// table and the X window are filled once; then the tile is walked in 16-pixel
-// chunks: the sampled columns S[tap][c][px] of the next chunk are formed from the
-// window (LDS reads only, global loads for the rare corners outside it) into a
-// double-buffered LDS tile while the MFMAs of the current chunk run:
+// table and the X window are filled once; then the tile is walked in 32-pixel
+// chunks (one barrier each): the sampled columns S[tap][c][px] of the next chunk are
+// formed from the window (LDS reads only, global loads for the rare corners outside it)
+// into a double-buffered LDS tile while the MFMAs of the current chunk run, per 16-pixel
+// half of the chunk:
 //   A = Z[m][px] (4 consecutive pixels per lane, one 16-byte load when contiguous),
 //   B = S[px][c] of one tap, D = dW[m][c] of that tap.
 // At the end of the run the block is stored to a split slot of the workspace and
@@ -33,7 +34,7 @@ constexpr int NT = 64 * NW;
 // so that a GEMM side of 64 rows still keeps all eight waves on MFMAs:
 //   MB = 2, TG = 1: 256 rows per workgroup;  MB = 1, TG = 2: 64 rows, taps split by parity.
 template <int MB, int TG> constexpr int rows_of() { return (NW / TG) * MB * 16; }
-constexpr int KP = 16;              // pixels per chunk
+constexpr int KP = 32;              // pixels per chunk (two 16-pixel halves per MFMA K block)
 constexpr int NCH = BPX / KP;       // chunks per tile
 constexpr int SS = KP + 4;          // S tile row stride (rows = (tap, channel))
 constexpr int TM = WIN_TMAX;
@@ -72,8 +73,9 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     const int tg = wave / (NW / TG);                     // this wave's tap group
     const int mrow = mt * BMW + (wave % (NW / TG)) * (MB * 16);   // first row of this wave
 
-    // S-builder item of this thread: chunk pixel j, channel quad sq, taps st, st + 8, ...
-    const int sj = tid & 15, sq = (tid >> 4) & 3, st0 = tid >> 6;
+    // S-builder item of this thread: chunk pixel j, channel quad sq, taps st, st + 4, ...
+    const int sj = tid & 31, sq = (tid >> 5) & 3, st0 = tid >> 7;
+    constexpr int SSTEP = NT / (KP * 4);   // tap stride of the items
 
     for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
         const int ntaps = min(wt.tpp, g.Kn - t0);
@@ -98,7 +100,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
             auto build_s = [&](int k, int bf) {
                 float *dst = sbuf + bf * (TM * BC * SS);
                 const int i = k * KP + sj;
-                for (int tl = st0; tl < ntaps; tl += NW) {
+                for (int tl = st0; tl < ntaps; tl += SSTEP) {
                     const acc4 r = geo[tl * BPX + i];
                     const int fc = fast_cell<DIM>(r);
                     const float mk = rec_mask<DIM>(r);
@@ -144,16 +146,17 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                 const int m = min(mrow + mb * 16 + (lane & 15), g.Mg - 1);
                 zrow[mb] = z + ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
             }
-            // quad path: a chunk lies within one row of the box (box_x >= KP) and P_x % 4 == 0,
-            // so the lane's 4 pixels are consecutive and all inside or all outside the grid;
-            // in a tile wholly inside the grid every quad is inside
-            const bool quad = ww.z_vec && wt.box[2] >= KP;
+            // quad path: a 16-pixel half chunk lies within one row of the box (box_x >= 16) and
+            // P_x % 4 == 0, so the lane's 4 pixels are consecutive and all inside or all outside
+            // the grid; in a tile wholly inside the grid every quad is inside
+            const bool quad = ww.z_vec && wt.box[2] >= 16;
             const bool full = quad && tile.p0[0] + wt.box[0] <= g.P[0] && tile.p0[1] + wt.box[1] <= g.P[1] &&
                               tile.p0[2] + wt.box[2] <= g.P[2];
-            // Z of chunk k; pixels outside the grid stay 0 (never loaded, so that a non-finite
-            // value there cannot leak into the sums)
-            auto load_a = [&](int k, acc4 (&za)[MB]) {
-                const int i0 = k * KP + 4 * q;
+            // Z of half h of chunk k (pixels k * KP + 16 h + 4 * (lane / 16) .. + 3); pixels
+            // outside the grid stay 0 (never loaded, so that a non-finite value there cannot
+            // leak into the sums)
+            auto load_a = [&](int k, int h, acc4 (&za)[MB]) {
+                const int i0 = k * KP + 16 * h + 4 * q;
                 if (quad) {
                     const int iz = i0 >> wt.lbxy, iy = (i0 >> wt.lbx) & (wt.box[1] - 1), ix = i0 & (wt.box[2] - 1);
                     const int pz = tile.p0[0] + iz, py = tile.p0[1] + iy, px = tile.p0[2] + ix;
@@ -190,29 +193,38 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
             };
 
             {
-                acc4 za[MB], zn[MB];
-                load_a(0, za);
+                acc4 za[2][MB], zn[2][MB];
+                load_a(0, 0, za[0]);
+                load_a(0, 1, za[1]);
                 build_s(0, 0);
                 __syncthreads();
                 for (int k = 0; k < NCH; ++k) {
                     const int bf = k & 1;
                     const bool more = k + 1 < NCH;
-                    if (more) load_a(k + 1, zn);
+                    if (more) {
+                        load_a(k + 1, 0, zn[0]);
+                        load_a(k + 1, 1, zn[1]);
+                    }
                     const float *sb = sbuf + bf * (TM * BC * SS) + (lane & 15) * SS + 4 * q;
 #pragma unroll
-                    for (int tp = 0; tp < TM; ++tp) {
-                        if ((FULL || tp < ntaps) && (TG == 1 || tp % TG == tg)) {
-                            const acc4 bv = *reinterpret_cast<const acc4 *>(sb + tp * BC * SS);
+                    for (int h = 0; h < 2; ++h)
 #pragma unroll
-                            for (int kk = 0; kk < 4; ++kk)
+                        for (int tp = 0; tp < TM; ++tp) {
+                            if ((FULL || tp < ntaps) && (TG == 1 || tp % TG == tg)) {
+                                const acc4 bv = *reinterpret_cast<const acc4 *>(sb + tp * BC * SS + 16 * h);
 #pragma unroll
-                                for (int mb = 0; mb < MB; ++mb) acc[mb][tp] = mfma16x16x4(za[mb][kk], bv[kk], acc[mb][tp]);
+                                for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                                    for (int mb = 0; mb < MB; ++mb)
+                                        acc[mb][tp] = mfma16x16x4(za[h][mb][kk], bv[kk], acc[mb][tp]);
+                            }
                         }
-                    }
                     if (more) {
                         build_s(k + 1, bf ^ 1);
 #pragma unroll
-                        for (int mb = 0; mb < MB; ++mb) za[mb] = zn[mb];
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int mb = 0; mb < MB; ++mb) za[h][mb] = zn[h][mb];
                     }
                     __syncthreads();
                 }
