@@ -262,7 +262,7 @@ SUITE = [(2, torch.float32), (3, torch.float32), (4, torch.float32), (5, torch.f
 
 TRAFFIC_KERNELS = {"gather_gemm": "fwd_win_kernel<2, float, 8>",
                    "data_grad": "bwd_data_win_kernel<2, float, true, true>",
-                   "weight_grad": "bwd_weight_win_kernel<2, float, true>"}
+                   "weight_grad": "bwd_weight_win_kernel<2, float, true, 2, 1>"}
 
 
 def load_traffic(family):
