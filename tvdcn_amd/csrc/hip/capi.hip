@@ -168,7 +168,7 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
 
 // Workspace sub-buffers (byte offsets into the caller's workspace).
 struct Layout {
-    size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, wpart = 0, goff_acc = 0, gmask_acc = 0;
+    size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, wpart = 0, goff_acc = 0, gmask_acc = 0, yacc = 0;
     size_t total = 0;
 };
 
@@ -190,11 +190,15 @@ Layout layout(const Plan &pl, bool backward) {
         return o;
     };
     const size_t SENTINEL = (size_t)-1;
-    L.xcl = L.wf = L.wd = L.cl_acc = L.wpart = L.goff_acc = L.gmask_acc = SENTINEL;
+    L.xcl = L.wf = L.wd = L.cl_acc = L.wpart = L.goff_acc = L.gmask_acc = L.yacc = SENTINEL;
+    // fp32 output of a slice-split windowed forward when the output dtype is not fp32
+    const bool split_acc = pl.fw.ok && pl.fw.ksplit > 1 && pl.dtype != kF32;
+    const size_t yacc_bytes = align_up((size_t)g.B * g.M * g.Pn * sizeof(float));
     if (!backward) {
         if (!pl.transposed) {
             L.xcl = take(cl_bytes);
             L.wf = take(wf_bytes);
+            if (split_acc) L.yacc = take(yacc_bytes);
         } else {
             L.wd = take(wd_bytes);
             L.cl_acc = take(cl_bytes);
@@ -202,9 +206,10 @@ Layout layout(const Plan &pl, bool backward) {
     } else {
         L.xcl = take(cl_bytes);
         L.wd = take(wd_bytes);
-        if (pl.transposed)
+        if (pl.transposed) {
             L.wf = take(wf_bytes);
-        else
+            if (split_acc) L.yacc = take(yacc_bytes);
+        } else
             L.cl_acc = take(cl_bytes);
         L.wpart = take(align_up(pl.ww.ok ? pl.ww.part_elems * sizeof(float) : pl.wt.part_elems * a));
         if (!acc_is_storage(pl.dtype)) {
@@ -350,8 +355,15 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
         if (pl.fw.ok) {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
+            void *y32 = nullptr;
+            if (pl.fw.ksplit > 1) {
+                y32 = dt == kF32 ? output : at(workspace, L.yacc);
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, y32, (size_t)g.B * g.M * g.Pn, s));
+            }
             TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
-                         launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, bias, output, s));
+                         launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, bias, output, y32, s));
+            if (pl.fw.ksplit > 1 && dt != kF32)
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, y32, output, (size_t)g.B * g.M * g.Pn, s));
         } else {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
@@ -448,8 +460,16 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
             void *wf = at(workspace, L.wf);
             if (pl.fw.ok) {
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
+                void *y32 = nullptr;
+                if (pl.fw.ksplit > 1) {
+                    y32 = dt == kF32 ? grad_input : at(workspace, L.yacc);
+                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, y32, (size_t)g.B * g.M * g.Pn, s));
+                }
                 TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
-                             launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, nullptr, grad_input, s));
+                             launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, nullptr, grad_input, y32, s));
+                if (pl.fw.ksplit > 1 && dt != kF32)
+                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                                 launch_acc_to_storage(dt, y32, grad_input, (size_t)g.B * g.M * g.Pn, s));
             } else {
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_fwd_layout(dt, g, weight, wf, pl.ft.Mg_pad, pl.ft.Cg_pad, s));
                 TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,

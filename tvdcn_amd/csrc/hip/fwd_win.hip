@@ -44,7 +44,7 @@ template <int DIM, typename T, int MB>
 __global__ void __launch_bounds__(NT)
 fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__restrict__ xcl,
                const float *__restrict__ wf, const T *__restrict__ offset, const T *__restrict__ mask,
-               const T *__restrict__ bias, T *__restrict__ y) {
+               const T *__restrict__ bias, T *__restrict__ y, float *__restrict__ y32) {
     constexpr int NC = 1 << DIM;
     constexpr int BMR = MB * 16;
     constexpr int XQ = xq_of(MB);
@@ -60,11 +60,14 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     int L = xcd_remap(blockIdx.x, gridDim.x);
     const int mt = L % fw.m_tiles;
     L /= fw.m_tiles;
+    const int ks = L % fw.ksplit;   // share of the channel slices (fw.ksplit == 2: fp32 partials in y32)
+    L /= fw.ksplit;
     const int n_sp = g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2];
     const int sp = L % n_sp;
     const int grp = L / n_sp;
     const bool deformable = offset != nullptr;
     const int slices = (g.Cg + BC - 1) / BC;
+    const int cs_lo = ks * fw.slices_per, cs_hi = min(slices, cs_lo + fw.slices_per);
 
     Tile tile;
     tile.init(g, wt, sp, 0, grp);
@@ -196,29 +199,30 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
 
     for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
         const int ntaps = min(wt.tpp, g.Kn - t0);
-        const int nsteps = slices * ntaps;
+        const int nsteps = (cs_hi - cs_lo) * ntaps;
         geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
 
-        // step k = (slice k / ntaps, tap k % ntaps). Invariant at the top of step k: its
-        // B fragments are in bcur, its weight fragments in wa.
+        // step k = (slice cs_lo + k / ntaps, tap k % ntaps). Invariant at the top of step k:
+        // its B fragments are in bcur, its weight fragments in wa.
         acc4 wa[MB], bcur[PB], bnxt[PB];
-        prefetch_x(0);
-        load_w(wptr(0, t0), wa);
+        prefetch_x(cs_lo);
+        load_w(wptr(cs_lo, t0), wa);
         __syncthreads();   // previous pass done with the tables
-        open_slice(0, t0, ntaps);
+        open_slice(cs_lo, t0, ntaps);
         __syncthreads();
-        build_b(0, 0, bcur);
+        build_b(cs_lo, 0, bcur);
         // the next slice's X window is requested PF steps before it is needed (memory
         // latency exceeds one step's MFMAs), or at the slice's first step when shorter
         const int pf_tl = max(ntaps - PF, 0);
         for (int k = 0; k < nsteps; ++k) {
             const bool more = k + 1 < nsteps;
-            const int kn = k + 1, csn = kn / ntaps, tln = kn - csn * ntaps;
-            const int cs = k / ntaps;
+            const int kn = k + 1, csn_r = kn / ntaps, tln = kn - csn_r * ntaps;
+            const int cs_r = k / ntaps;
+            const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
             const bool new_slice = more && tln == 0;
-            if (k - cs * ntaps == pf_tl && cs + 1 < slices) prefetch_x(cs + 1);
+            if (k - cs_r * ntaps == pf_tl && cs + 1 < cs_hi) prefetch_x(cs + 1);
             if (more && !new_slice) build_b(csn, tln, bnxt);
-            mfma_step(bcur, wa, more ? wptr(csn, t0 + tln) : wptr(cs, t0 + k - cs * ntaps));
+            mfma_step(bcur, wa, more ? wptr(csn, t0 + tln) : wptr(cs, t0 + k - cs_r * ntaps));
             if (new_slice) {
                 __syncthreads();   // every wave done reading the current window
                 open_slice(csn, t0, ntaps);
@@ -230,7 +234,9 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
         }
     }
 
-    // ---- epilogue: + bias, store NC<spatial> ---------------------------------------
+    // ---- epilogue: + bias, store NC<spatial>. With two slice shares, each adds its fp32
+    //      partial to y32 (zeroed by the caller; bias with the first share): a sum of two
+    //      terms onto zero is the same in either order, so the result is deterministic.
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
         const int p = tile.pixel(g, wt, wave * (PB * 16) + pb * 16 + (lane & 15));
@@ -243,8 +249,12 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 if (m < g.Mg) {
                     const int mg_glob = grp * g.Mg + m;
                     float r = acc[mb][pb][v];
-                    if (bias != nullptr) r += to_acc<float>(bias[mg_glob]);
-                    y[((size_t)tile.b * g.M + mg_glob) * g.Pn + p] = from_acc<T, float>(r);
+                    if (bias != nullptr && ks == 0) r += to_acc<float>(bias[mg_glob]);
+                    const size_t o = ((size_t)tile.b * g.M + mg_glob) * g.Pn + p;
+                    if (fw.ksplit == 1)
+                        y[o] = from_acc<T, float>(r);
+                    else
+                        atomic_add(y32 + o, r);
                 }
             }
     }
@@ -273,7 +283,7 @@ __global__ void fwd_win_weight_kernel(const T *__restrict__ w, float *__restrict
 
 template <int DIM, typename T, int MB>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
-                    const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
+                    const void *offset, const void *mask, const void *bias, void *y, void *y32, hipStream_t s) {
     auto kern = fwd_win_kernel<DIM, T, MB>;
     const size_t lds = ((size_t)GEO_WORDS + (size_t)wt.cells * XS) * sizeof(float);
     static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
@@ -283,31 +293,31 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const vo
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const long long blocks = (long long)g.G * g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2] * fw.m_tiles;
+    const long long blocks = (long long)g.G * g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2] * fw.m_tiles * fw.ksplit;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, wt, fw, static_cast<const float *>(xcl),
                        static_cast<const float *>(wf), static_cast<const T *>(offset), static_cast<const T *>(mask),
-                       static_cast<const T *>(bias), static_cast<T *>(y));
+                       static_cast<const T *>(bias), static_cast<T *>(y), static_cast<float *>(y32));
     return hipGetLastError();
 }
 
 template <int DIM, typename T>
 hipError_t launch_m(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
-                    const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
+                    const void *offset, const void *mask, const void *bias, void *y, void *y32, hipStream_t s) {
     // 3D: 64-row tiles only (the trilinear sampler needs the registers)
     if constexpr (DIM < 3) {
-        if (fw.mb == 8) return launch_k<DIM, T, 8>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        if (fw.mb == 8) return launch_k<DIM, T, 8>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
     }
-    if (fw.mb == 4) return launch_k<DIM, T, 4>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+    if (fw.mb == 4) return launch_k<DIM, T, 4>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
     return hipErrorInvalidValue;
 }
 
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
-                    const void *offset, const void *mask, const void *bias, void *y, hipStream_t s) {
+                    const void *offset, const void *mask, const void *bias, void *y, void *y32, hipStream_t s) {
     switch (dim) {
-        case 1: return launch_m<1, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
-        case 2: return launch_m<2, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
-        case 3: return launch_m<3, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case 1: return launch_m<1, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
+        case 2: return launch_m<2, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
+        case 3: return launch_m<3, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
     }
     return hipErrorInvalidValue;
 }
@@ -333,6 +343,11 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     f.m_tiles = (g.Mg + rows - 1) / rows;
     f.Mg_pad = f.m_tiles * rows;
     f.Cg_pad = (g.Cg + BC - 1) / BC * BC;
+    // a grid that cannot give every CU a workgroup splits the channel slices in two (fp32
+    // partials added onto a zeroed output: deterministic for two shares)
+    const int slices = f.Cg_pad / BC;
+    f.ksplit = (spatial * f.m_tiles < 256 && slices >= 2) ? 2 : 1;
+    f.slices_per = (slices + f.ksplit - 1) / f.ksplit;
     f.ok = true;
     return f;
 }
@@ -357,12 +372,13 @@ hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, cons
 }
 
 hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,
-                          const void *wf, const void *offset, const void *mask, const void *bias, void *y,
+                          const void *wf, const void *offset, const void *mask, const void *bias, void *y, void *y32,
                           hipStream_t s) {
+    if (fw.ksplit != 1 && y32 == nullptr) return hipErrorInvalidValue;
     switch (dtype) {
-        case kF32: return launch_d<float>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, s);
-        case kF16: return launch_d<__half>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, s);
-        case kBF16: return launch_d<__hip_bfloat16>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, s);
+        case kF32: return launch_d<float>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
+        case kF16: return launch_d<__half>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
+        case kBF16: return launch_d<__hip_bfloat16>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
     }
     return hipErrorInvalidValue;
 }

@@ -65,6 +65,9 @@ struct FwdWin {
     bool ok;
     int mb;              // 16-row blocks per workgroup (8 or 4)
     int m_tiles;         // (16 * mb)-row blocks of the GEMM side
+    int ksplit;          // 1, or 2: the channel slices split between two workgroups whose fp32
+                         // partials are added onto a zeroed fp32 output (y32)
+    int slices_per;      // 16-channel slices per share
     int Mg_pad, Cg_pad;  // padded weight layout Wf[G][Kn][Mg_pad][Cg_pad]
 };
 
@@ -102,7 +105,7 @@ hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTil
 // weight -> the windowed forward's fragment-major layout (fwd_win.hip)
 hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *wp, hipStream_t s);
 hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,
-                          const void *wf, const void *offset, const void *mask, const void *bias, void *y,
+                          const void *wf, const void *offset, const void *mask, const void *bias, void *y, void *y32,
                           hipStream_t s);
 hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t, bool scatter, bool coord,
                            const void *z, const void *wd, const void *xcl, const void *offset, const void *mask,
