@@ -145,8 +145,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
         const float *p = wbase + ((size_t)ms * g.Kn + t0) * (BC * BM);
 #pragma unroll
         for (int tp = 0; tp < TMAX; ++tp) {
-            // taps past the pass re-read its last tap (in bounds); their products are never used
-            wr[tp] = *reinterpret_cast<const acc4 *>(p + min(tp, ntaps - 1) * (BC * BM));
+            // slots past the pass hold zeros; their products are never used
+            wr[tp] = acc4{0.f, 0.f, 0.f, 0.f};
+            if (tp < ntaps) wr[tp] = *reinterpret_cast<const acc4 *>(p + tp * (BC * BM));
         }
     };
 
@@ -184,8 +185,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                 acc[tp][pb] = mfma16x16x4(wr[tp][kk], zv, acc[tp][pb]);
                             }
                     }
-                    const int tq = FULL ? tp : min(tp, ntaps - 1);
-                    wr[tp] = *reinterpret_cast<const acc4 *>(wbase + ((size_t)msn * g.Kn + t0 + tq) * (BC * BM));
+                    // (slots past the pass are never loaded nor used)
+                    if (FULL || tp < ntaps)
+                        wr[tp] = *reinterpret_cast<const acc4 *>(wbase + ((size_t)msn * g.Kn + t0 + tp) * (BC * BM));
                     // issue order: this tap's MFMAs, then its reload (a full step ahead of use)
                     __builtin_amdgcn_sched_barrier(0);
                 }
