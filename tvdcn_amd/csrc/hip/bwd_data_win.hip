@@ -46,7 +46,13 @@ constexpr int NW = 8;             // waves per workgroup (two per SIMD)
 constexpr int NT = 64 * NW;       // threads per workgroup
 constexpr int PB = 2;             // 16-pixel blocks per wave (NW * PB * 16 = BPX)
 constexpr int BM = 16;            // GEMM-side channels per K step
-constexpr int CS = BC + 1;        // fixed-point window cell stride (odd: spreads the LDS banks)
+// Fixed-point window: channel-major [16 c][cst], cst = window cells rounded so that
+// cst = 4 (mod 16). A scatter instruction's lanes are 16 pixels x 4 channel quads; the
+// pixels of a 16-pixel block hit neighbouring cells, and the four channels c, c + 4, c + 8,
+// c + 12 of one instruction sit 4 * cst = 16 (mod 64) words apart, so the lanes spread
+// over distinct LDS banks (a cell-major [cell][17] layout put lanes of different pixels
+// on the same banks).
+__host__ __device__ constexpr int fix_stride(int cells) { return ((cells + 11) & ~15) + 4; }
 constexpr int FIX_BITS = 29;      // fixed-point headroom: |cell sum| * 2^s_c < 2^29
 static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
 
@@ -85,7 +91,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     float *bsum = smem + GEO_WORDS;                            // [NW][BC] partial bounds
     int *scl = reinterpret_cast<int *>(bsum + NW * BC);        // [BC] scale exponents, [BC] = non-finite flag
     float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X window (COORD)
-    int *iwin = reinterpret_cast<int *>(xwin + (COORD ? wt.cells * XS : 0));   // [cells][CS] fixed point
+    int *iwin = reinterpret_cast<int *>(xwin + (COORD ? wt.cells * XS : 0));   // [BC][cst] fixed point
+    const int cst = fix_stride(wt.cells);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -109,7 +116,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     //      fixed-point window (scatter)
     if constexpr (COORD) fill_xwin(g, wt, tile, xb, xwin, tid, NT);
     if constexpr (SCATTER) {
-        for (int i = tid; i < wt.cells * CS; i += NT) iwin[i] = 0;
+        for (int i = tid; i < BC * cst; i += NT) iwin[i] = 0;
     }
 
     // ---- K-loop operands, straight to registers ---------------------------------
@@ -329,10 +336,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                     if (!cr.in_grid(k)) continue;
                                     const float sw = mk * cr.weight(k);
                                     if (cr.in_win(k)) {
-                                        unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + cr.cell(wt, k) * CS + mq);
+                                        unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + cr.cell(wt, k));
 #pragma unroll
                                         for (int v = 0; v < 4; ++v)
-                                            atomicAdd(dst + v, (unsigned int)fixed_round(sw * gsc[v]));
+                                            atomicAdd(dst + v * cst, (unsigned int)fixed_round(sw * gsc[v]));
                                     } else {
                                         float *dst = gdst + (size_t)cr.idx(g, k) * g.C;
 #pragma unroll
@@ -397,9 +404,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                             for (int v = 0; v < 4; ++v) gs[v] = ldexpf(gv[v], sexp[v]);
 #pragma unroll
                             for (int k = 0; k < NF; ++k) {
-                                unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + cell[k] * CS + mq);
+                                unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + cell[k]);
 #pragma unroll
-                                for (int v = 0; v < 4; ++v) atomicAdd(dst + v, (unsigned int)fixed_round(wm[k] * gs[v]));
+                                for (int v = 0; v < 4; ++v) atomicAdd(dst + v * cst, (unsigned int)fixed_round(wm[k] * gs[v]));
                             }
                         }
                     }
@@ -453,10 +460,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                 if (gidx[k] < 0) continue;
                                 const float s = mk * w[k];
                                 if (use_window && loc[k] >= 0) {
-                                    unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + loc[k] * CS + mq);
+                                    unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + loc[k]);
 #pragma unroll
                                     for (int v = 0; v < 4; ++v)
-                                        atomicAdd(dst + v, (unsigned int)fixed_round(ldexpf(s * gv[v], sexp[v])));
+                                        atomicAdd(dst + v * cst, (unsigned int)fixed_round(ldexpf(s * gv[v], sexp[v])));
                                 } else {
                                     float *dst = gdst + (size_t)gidx[k] * g.C;
 #pragma unroll
@@ -494,9 +501,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
             const bool c_ok = c0 + c < g.Cg;
             float *gbase = gx_cl + (size_t)b * g.Sn * g.C + cg0 + c;
             for_cells(g, wt, tile, tid >> 4, NT / 16, [&](int cell, int si) {
-                const int iv = iwin[cell * CS + c];
+                const int iv = iwin[c * cst + cell];
                 if (iv == 0) return;
-                iwin[cell * CS + c] = 0;   // ready for the next pass
+                iwin[c * cst + cell] = 0;   // ready for the next pass
                 // window cells outside the grid hold only contributions of corners outside it
                 if (si >= 0 && c_ok) atomic_add(gbase + (size_t)si * g.C, ldexpf((float)iv, -se));
             });
@@ -528,7 +535,8 @@ __global__ void weight_win_kernel(const T *__restrict__ w, float *__restrict__ o
 }
 
 template <bool SCATTER, bool COORD> size_t lds_bytes(const WinTiles &t) {
-    return ((size_t)FIXED_WORDS + (size_t)t.cells * ((SCATTER ? CS : 0) + (COORD ? XS : 0))) * sizeof(float);
+    return ((size_t)FIXED_WORDS + (SCATTER ? (size_t)BC * fix_stride(t.cells) : 0) + (COORD ? (size_t)t.cells * XS : 0)) *
+           sizeof(float);
 }
 
 template <int DIM, typename T, bool SCATTER, bool COORD>
@@ -656,7 +664,9 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
     t.m_steps = (g.Mg + BM - 1) / BM;
     // per window cell: the fixed-point accumulators (scatter) and / or the X values
     // (offset/mask gradients), as the launches this plan serves need them
-    t = win_resize(t, g, dim, FIXED_WORDS * sizeof(float), ((scatter ? CS : 0) + (coord ? XS : 0)) * sizeof(float));
+    // (+ BC * 16 words: the fixed-point window's stride rounding)
+    t = win_resize(t, g, dim, (FIXED_WORDS + (scatter ? BC * 16 : 0)) * sizeof(float),
+                   ((scatter ? BC : 0) + (coord ? XS : 0)) * sizeof(float));
     const int npass = (g.Kn + WIN_TMAX - 1) / WIN_TMAX;
     t.tpp = (g.Kn + npass - 1) / npass;
     t.chunk_elems = (size_t)g.G * t.c_tiles * t.m_steps * g.Kn * BC * BM;
