@@ -36,6 +36,7 @@ constexpr int NT = 64 * NW;
 template <int MB, int TG> constexpr int rows_of() { return (NW / TG) * MB * 16; }
 constexpr int KP = 32;              // pixels per chunk (two 16-pixel halves per MFMA K block)
 constexpr int NCH = BPX / KP;       // chunks per tile
+constexpr int NH = KP / 16;         // 16-pixel MFMA K blocks per chunk
 constexpr int SS = KP + 4;          // S tile row stride (rows = (tap, channel))
 constexpr int TM = WIN_TMAX;
 
@@ -193,21 +194,21 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
             };
 
             {
-                acc4 za[2][MB], zn[2][MB];
-                load_a(0, 0, za[0]);
-                load_a(0, 1, za[1]);
+                acc4 za[NH][MB], zn[NH][MB];
+#pragma unroll
+                for (int h = 0; h < NH; ++h) load_a(0, h, za[h]);
                 build_s(0, 0);
                 __syncthreads();
                 for (int k = 0; k < NCH; ++k) {
                     const int bf = k & 1;
                     const bool more = k + 1 < NCH;
                     if (more) {
-                        load_a(k + 1, 0, zn[0]);
-                        load_a(k + 1, 1, zn[1]);
+#pragma unroll
+                        for (int h = 0; h < NH; ++h) load_a(k + 1, h, zn[h]);
                     }
                     const float *sb = sbuf + bf * (TM * BC * SS) + (lane & 15) * SS + 4 * q;
 #pragma unroll
-                    for (int h = 0; h < 2; ++h)
+                    for (int h = 0; h < NH; ++h)
 #pragma unroll
                         for (int tp = 0; tp < TM; ++tp) {
                             if ((FULL || tp < ntaps) && (TG == 1 || tp % TG == tg)) {
@@ -222,7 +223,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                     if (more) {
                         build_s(k + 1, bf ^ 1);
 #pragma unroll
-                        for (int h = 0; h < 2; ++h)
+                        for (int h = 0; h < NH; ++h)
 #pragma unroll
                             for (int mb = 0; mb < MB; ++mb) za[h][mb] = zn[h][mb];
                     }
