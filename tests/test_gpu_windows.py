@@ -73,3 +73,32 @@ def test_offset_free_nonfinite_input_fp32(dim):
         if fin.any():
             e = rel_err(gr[fin], r[fin])
             assert e < TOL[torch.float32][1], f"{name} rel err {e}"
+
+
+def test_nonfinite_bound_in_a_later_pass_fp32():
+    """25 taps = three passes of the data gradient's window: an inf weight at tap 12 makes only
+    the second pass's bound non-finite, so the window flushes what the first pass accumulated
+    and the second pass scatters through global atomics."""
+    case = make_case(2, False, batch=2, cin=32, cout=32, kernel=[5, 5], stride=[1, 1], padding=[2, 2],
+                     dilation=[1, 1], in_size=[20, 18], out_pad=[0, 0], seed=540)
+    case["weight"] = case["weight"].clone()
+    case["weight"][3, 5, 2, 2] = float("inf")   # tap 12 = (2, 2)
+    g = torch.Generator().manual_seed(541)
+    gout = torch.rand(case["out_shape"], generator=g, dtype=torch.float64)
+    _, grads, _ = run_gpu(case, torch.float32, grad_out=gout)
+    _, ref_grads = run_oracle(case, gout, torch.float32)
+    for name, gr, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
+        gr = gr.detach().double().cpu()
+        assert torch.equal(torch.isnan(gr), torch.isnan(r)), f"grad_{name}: nan pattern differs"
+        assert torch.equal(torch.isinf(gr), torch.isinf(r)), f"grad_{name}: inf pattern differs"
+        fin = torch.isfinite(r)
+        if fin.any():
+            e = rel_err(gr[fin], r[fin])
+            assert e < TOL[torch.float32][1], f"grad_{name} rel err {e}"
+
+
+def test_many_taps_multi_pass_fp32():
+    """25 taps: the window accumulates three passes and is rescaled as the bound grows."""
+    case = make_case(2, False, batch=2, cin=32, cout=64, kernel=[5, 5], stride=[1, 1], padding=[2, 2],
+                     dilation=[1, 1], in_size=[24, 22], out_pad=[0, 0], seed=545, offset_scale=3.0)
+    check(case, torch.float32)

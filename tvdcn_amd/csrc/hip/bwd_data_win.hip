@@ -24,17 +24,20 @@
 //     pixel and quantity).
 //   * The scatter accumulates in the LDS window in 32-bit fixed point with
 //     integer LDS atomics (ds_add_u32 measured at ~5 cycles per wave instruction
-//     on gfx950, ds_add_f32 at ~190). Channel c of a pass uses the scale
-//     2^s_c, s_c = 29 - ceil(log2 B_c), B_c = sum over the pass's (pixel, tap) of
-//     |G * mask|: a bilinear corner weight is at most 1 and each (pixel, tap)
-//     reaches a cell through at most one corner, so every cell sum stays below
-//     2^29 (no overflow) and is rounded at B_c * 2^-29 per term (~1e-9 B_c).
-//     Integer sums are also order independent. A non-finite B_c sends the pass
-//     to global float atomics so that inf/nan propagate as in the reference.
-//     Corners outside the window go to global float atomics.
+//     on gfx950, ds_add_f32 at ~190). Channel c uses the scale 2^s_c,
+//     s_c = 29 - ceil(log2 B_c), B_c = sum of |G * mask| over every (pixel, tap)
+//     accumulated so far: a bilinear corner weight is at most 1 and each (pixel,
+//     tap) reaches a cell through at most one corner, so every cell sum stays
+//     below 2^29 (no overflow) and is rounded at B_c * 2^-29 per term (~1e-9 B_c).
+//     Integer sums are also order independent. When a pass of taps grows B_c,
+//     the values already held are shifted down to the new scale. A non-finite
+//     bound sends the pass to global float atomics (after flushing what the
+//     window holds) so that inf/nan propagate as in the reference. Corners
+//     outside the window go to global float atomics.
 //   * The window (sampled-grid box around the tile's undeformed footprint plus a
-//     margin R per axis) is flushed after each pass: one float atomic per
-//     non-zero (cell, channel), 16 consecutive channels per cell.
+//     margin R per axis) accumulates over all passes of the tile and is flushed
+//     once: one float atomic per non-zero (cell, channel), 16 consecutive channels
+//     per cell.
 #include "window.h"
 
 namespace tvdcn_hip {
@@ -55,11 +58,12 @@ constexpr int BM = 16;            // GEMM-side channels per K step
 __host__ __device__ constexpr int fix_stride(int cells) { return ((cells + 11) & ~15) + 4; }
 constexpr int FIX_BITS = 29;      // fixed-point headroom: |cell sum| * 2^s_c < 2^29
 static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
+static_assert(NT == BC * 32, "window rescale: 32 threads per channel");
 
 // LDS words ahead of the windows: geometry table [WIN_TMAX][BPX] x (position, mask),
 // per-wave channel bounds, scale exponents
 constexpr int GEO_WORDS = WIN_TMAX * BPX * 4;
-constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + BC + 4;
+constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + 3 * BC + 4;
 
 // Nearest integer, halves rounded up (v_cvt_rpi_i32_f32 = floor(x + 0.5)): one instruction
 // where round-to-nearest-even takes two; |x| < 2^29 here
@@ -90,6 +94,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     acc4 *geo = reinterpret_cast<acc4 *>(smem);                // [TMAX][BPX] sampling table (window.h)
     float *bsum = smem + GEO_WORDS;                            // [NW][BC] partial bounds
     int *scl = reinterpret_cast<int *>(bsum + NW * BC);        // [BC] scale exponents, [BC] = non-finite flag
+    float *btot = bsum + NW * BC + BC + 4;                     // [BC] bound of what the window holds
+    int *shift = reinterpret_cast<int *>(btot + BC);           // [BC] rescale of the window for a pass
     float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X window (COORD)
     int *iwin = reinterpret_cast<int *>(xwin + (COORD ? wt.cells * XS : 0));   // [BC][cst] fixed point
     const int cst = fix_stride(wt.cells);
@@ -158,6 +164,25 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
         }
     };
 
+    // ---- the fixed-point window accumulates over every pass of the tile and is flushed
+    //      once, at the end (or before a pass whose bound is not finite): one float atomic
+    //      per non-zero (cell, channel), 16 consecutive channels per cell
+    bool win_data = false;   // the window holds accumulated values (uniform)
+    auto flush_window = [&]() {
+        const int c = tid & 15;
+        const int se = scl[c];
+        const bool c_ok = c0 + c < g.Cg;
+        float *gbase = gx_cl + (size_t)b * g.Sn * g.C + cg0 + c;
+        for_cells(g, wt, tile, tid >> 4, NT / 16, [&](int cell, int si) {
+            const int iv = iwin[c * cst + cell];
+            if (iv == 0) return;
+            iwin[c * cst + cell] = 0;   // cleared for what follows
+            // window cells outside the grid hold only contributions of corners outside it
+            if (si >= 0 && c_ok) atomic_add(gbase + (size_t)si * g.C, ldexpf((float)iv, -se));
+        });
+        __syncthreads();
+    };
+
     for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
         const int ntaps = min(wt.tpp, g.Kn - t0);
 
@@ -224,7 +249,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
             kloop(std::false_type(), std::true_type());
         __syncthreads();   // geometry table (and X window) written
 
-        // ---- fixed-point scale per channel of this pass -------------------------------
+        // ---- fixed-point scale per channel: the bound covers this pass plus everything
+        //      the window already holds; when it grows, the held values are shifted down
+        //      to the new (smaller or equal) scale
         int sexp[4] = {0, 0, 0, 0};   // scale exponents of this lane's channels c0 + mq + v
         bool use_window = false;
         if constexpr (SCATTER) {
@@ -255,17 +282,38 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 float bc = 0.f;
 #pragma unroll
                 for (int w = 0; w < NW; ++w) bc += bsum[w * BC + tid];
-                int e = 0;
-                if (bc > 0.f && isfinite(bc)) frexpf(bc, &e);   // bc < 2^e
-                scl[tid] = FIX_BITS - e;
+                const float tot = (win_data ? btot[tid] : 0.f) + bc;
                 // the pass uses the window only if every bound is finite (ballot over 16 lanes)
-                const unsigned long long bad = __ballot(!isfinite(bc));
+                const unsigned long long bad = __ballot(!isfinite(tot));
+                int e = 0;
+                if (tot > 0.f && isfinite(tot)) frexpf(tot, &e);   // tot < 2^e
+                shift[tid] = 0;
+                if (bad == 0ull) {
+                    if (win_data) shift[tid] = scl[tid] - (FIX_BITS - e);   // >= 0: the bound only grows
+                    scl[tid] = FIX_BITS - e;
+                    btot[tid] = tot;
+                }
                 if (tid == 0) scl[BC] = bad != 0ull;
             }
             __syncthreads();
+            if (scl[BC] != 0) {
+                // not finite: what the window holds goes out at its scale, the pass goes to
+                // global float atomics (inf / nan propagate as in the reference)
+                if (win_data) flush_window();
+                win_data = false;
+            } else {
+                if (win_data) {
+                    // arithmetic shifts (rounding down by under one unit of the new scale)
+                    const int c = tid >> 5, sh = shift[c];
+                    if (sh > 0)
+                        for (int cell = tid & 31; cell < cst; cell += 32) iwin[c * cst + cell] >>= sh;
+                    __syncthreads();
+                }
+                use_window = wt.cells > 0;
+                win_data = use_window;
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) sexp[v] = scl[mq + v];
-            use_window = wt.cells > 0 && scl[BC] == 0;
         }
 
         // ---- epilogue: every wave walks its own pixels tap by tap, no barriers -------
@@ -494,20 +542,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
         }
         __syncthreads();   // all waves done with the geometry table and the window
 
-        // ---- flush the window: one float atomic per non-zero (cell, channel) ----------
-        if (SCATTER && use_window) {
-            const int c = tid & 15;
-            const int se = scl[c];
-            const bool c_ok = c0 + c < g.Cg;
-            float *gbase = gx_cl + (size_t)b * g.Sn * g.C + cg0 + c;
-            for_cells(g, wt, tile, tid >> 4, NT / 16, [&](int cell, int si) {
-                const int iv = iwin[c * cst + cell];
-                if (iv == 0) return;
-                iwin[c * cst + cell] = 0;   // ready for the next pass
-                // window cells outside the grid hold only contributions of corners outside it
-                if (si >= 0 && c_ok) atomic_add(gbase + (size_t)si * g.C, ldexpf((float)iv, -se));
-            });
-            __syncthreads();   // window cleared before the next pass scatters into it
+        // ---- after the last pass, the window goes out
+        if (SCATTER && win_data && t0 + wt.tpp >= g.Kn) {
+            flush_window();
+            win_data = false;
         }
     }
 }
