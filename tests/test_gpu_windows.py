@@ -75,6 +75,34 @@ def test_offset_free_nonfinite_input_fp32(dim):
             assert e < TOL[torch.float32][1], f"{name} rel err {e}"
 
 
+@pytest.mark.parametrize("dim", [1, 2, 3])
+def test_deformable_nonfinite_input_fp32(dim):
+    """An inf in the input under fractional sampling: the offset gradients of the taps whose
+    corners hold it are +-inf in the reference's corner sums (nan only where a corner weight
+    is zero), and the mask gradient is +-inf; forms that take differences of corners first
+    would give inf - inf = nan there."""
+    in_size = {1: [40], 2: [20, 18], 3: [6, 10, 9]}[dim]
+    case = make_case(dim, False, batch=2, cin=32, cout=32, kernel=[3] * dim, stride=[1] * dim, padding=[1] * dim,
+                     dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim, seed=550 + dim)
+    case["input"] = case["input"].clone()
+    case["input"][1, 3][(2,) * dim] = float("inf")
+    g = torch.Generator().manual_seed(551)
+    gout = torch.rand(case["out_shape"], generator=g, dtype=torch.float64)
+    out, grads, _ = run_gpu(case, torch.float32, grad_out=gout)
+    ref_out, ref_grads = run_oracle(case, gout, torch.float32)
+    assert torch.isinf(ref_grads[2]).any(), "the inf must reach some offset gradient"
+    for name, gr, r in zip(("output", "input", "weight", "offset", "mask", "bias"), [out] + list(grads), [ref_out] + list(ref_grads)):
+        if r is None:
+            continue
+        gr = gr.detach().double().cpu()
+        assert torch.equal(torch.isnan(gr), torch.isnan(r)), f"{name}: nan pattern differs"
+        assert torch.equal(torch.isinf(gr), torch.isinf(r)), f"{name}: inf pattern differs"
+        fin = torch.isfinite(r)
+        if fin.any():
+            e = rel_err(gr[fin], r[fin])
+            assert e < TOL[torch.float32][1], f"{name} rel err {e}"
+
+
 def test_nonfinite_bound_in_a_later_pass_fp32():
     """25 taps = three passes of the data gradient's window: an inf weight at tap 12 makes only
     the second pass's bound non-finite, so the window flushes what the first pass accumulated

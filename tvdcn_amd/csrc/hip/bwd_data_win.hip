@@ -65,6 +65,23 @@ static_assert(NT == BC * 32, "window rescale: 32 threads per channel");
 constexpr int GEO_WORDS = WIN_TMAX * BPX * 4;
 constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + 3 * BC + 4;
 
+// Offset / mask gradient terms of one (pixel, tap) as the reference's corner sums, from
+// gk[k] = G contracted with X at corner k (k = 2 * y bit + x bit in 2D, x bit in 1D):
+// q[a] = mk * d(sample)/d(pos_a), q[DIM] = sample
+template <int DIM>
+__device__ __forceinline__ void coord_direct(const float *gk, float fy, float fx, float mk, float *q) {
+    if constexpr (DIM == 2) {
+        const float gy = -(1.f - fx) * gk[0] - fx * gk[1] + (1.f - fx) * gk[2] + fx * gk[3];
+        const float gx = -(1.f - fy) * gk[0] + (1.f - fy) * gk[1] - fy * gk[2] + fy * gk[3];
+        q[0] = mk * gy;
+        q[1] = mk * gx;
+        q[2] = (1.f - fy) * (1.f - fx) * gk[0] + (1.f - fy) * fx * gk[1] + fy * (1.f - fx) * gk[2] + fy * fx * gk[3];
+    } else {
+        q[0] = mk * (-gk[0] + gk[1]);
+        q[1] = (1.f - fx) * gk[0] + fx * gk[1];
+    }
+}
+
 // Nearest integer, halves rounded up (v_cvt_rpi_i32_f32 = floor(x + 0.5)): one instruction
 // where round-to-nearest-even takes two; |x| < 2^29 here
 __device__ __forceinline__ int fixed_round(float x) {
@@ -432,6 +449,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                             qv[0] = mk * ex;
                             qv[1] = gk[0] + fx * ex;
                         }
+                        // a non-finite gk makes the factored sample non-finite; the reference's
+                        // corner sums then keep the +-inf that the factored differences turn
+                        // into inf - inf
+                        if (!isfinite(qv[DIM])) coord_direct<DIM>(gk, fy, fx, mk, qv);
                     }
                     if constexpr (SCATTER) {
                         if (cq_ok) {
