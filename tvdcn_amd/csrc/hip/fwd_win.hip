@@ -71,17 +71,24 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
 
     Tile tile;
     tile.init(g, wt, sp, 0, grp);
+    if constexpr (DIM == 3) {
+        if (tid < XS) xwin[wt.cells * XS + tid] = 0.f;   // zero cell of the 3D corner reads
+    }
     const float *xg = xcl + (size_t)tile.b * g.Sn * g.C + (size_t)grp * g.Cg;   // group's channel 0
 
 
     // X window prefetch: quad e = tid + j * NT of the window (cell e / 4, quad e % 4). The
     // cells (and their grid indices) are the same for every slice: resolved once.
+    // (3D resolves them at each fill: its registers are taken by the B fragments of a tap group)
     int xsi[XQ];   // flat sampled-grid index of the thread's cells (-1: outside the grid / window)
+    auto resolve_cells = [&]() {
 #pragma unroll
-    for (int j = 0; j < XQ; ++j) {
-        const int e = tid + j * NT;
-        xsi[j] = e < wt.cells * 4 ? tile.cell_index(g, wt, e >> 2) : -1;
-    }
+        for (int j = 0; j < XQ; ++j) {
+            const int e = tid + j * NT;
+            xsi[j] = e < wt.cells * 4 ? tile.cell_index(g, wt, e >> 2) : -1;
+        }
+    };
+    if constexpr (DIM != 3) resolve_cells();
     acc4 xpre[XQ];
     auto prefetch_x = [&](int cs) {
         const float *xb = xg + cs * BC + 4 * (tid & 3);
@@ -111,9 +118,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
             const int fc = fast_cell<DIM>(r);
             const float mk = rec_mask<DIM>(r);
             acc4 sv;
-            if constexpr (DIM == 3) {
-                sv = sample3_masked(g, wt, tile, xwin, 4 * qd, xg + cs * BC + 4 * qd, q_ok, r, deformable);
-            } else if (fc >= 0) {
+            if (fc >= 0) {
                 sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * qd, r, mk);
             } else {
                 Point<DIM, float> pt;
@@ -185,6 +190,10 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     // table rebuilt when the slice's offset / mask group differs from the last one
     int geo_og = -1, geo_mg = -1;
     auto open_slice = [&](int cs, int t0, int ntaps) {
+        if constexpr (DIM == 3) {
+            resolve_cells();
+            prefetch_x(cs);
+        }
         store_x();
         const int c_first = grp * g.Cg + cs * BC;
         const int og_s = g.og ? c_first / g.cpo : 0, mg_s = g.mg ? c_first / g.cpm : 0;
@@ -197,40 +206,108 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
         }
     };
 
-    for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
-        const int ntaps = min(wt.tpp, g.Kn - t0);
-        const int nsteps = (cs_hi - cs_lo) * ntaps;
-        geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
-
-        // step k = (slice cs_lo + k / ntaps, tap k % ntaps). Invariant at the top of step k:
-        // its B fragments are in bcur, its weight fragments in wa.
-        acc4 wa[MB], bcur[PB], bnxt[PB];
-        prefetch_x(cs_lo);
-        load_w(wptr(cs_lo, t0), wa);
-        __syncthreads();   // previous pass done with the tables
-        open_slice(cs_lo, t0, ntaps);
-        __syncthreads();
-        build_b(cs_lo, 0, bcur);
-        // the next slice's X window is requested PF steps before it is needed (memory
-        // latency exceeds one step's MFMAs), or at the slice's first step when shorter
-        const int pf_tl = max(ntaps - PF, 0);
-        for (int k = 0; k < nsteps; ++k) {
-            const bool more = k + 1 < nsteps;
-            const int kn = k + 1, csn_r = kn / ntaps, tln = kn - csn_r * ntaps;
-            const int cs_r = k / ntaps;
-            const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
-            const bool new_slice = more && tln == 0;
-            if (k - cs_r * ntaps == pf_tl && cs + 1 < cs_hi) prefetch_x(cs + 1);
-            if (more && !new_slice) build_b(csn, tln, bnxt);
-            mfma_step(bcur, wa, more ? wptr(csn, t0 + tln) : wptr(cs, t0 + k - cs_r * ntaps));
-            if (new_slice) {
-                __syncthreads();   // every wave done reading the current window
-                open_slice(csn, t0, ntaps);
-                __syncthreads();
-                build_b(csn, 0, bnxt);
-            }
+    if constexpr (DIM == 3) {
+        // 3D: taps in groups of four, lane row q sampling tap 4 * group + q at its pixel for
+        // all 16 channels of the slice (the corner geometry formed once per (pixel, tap)
+        // rather than once per channel quad); a row transpose then gives every lane its
+        // channel quad of the group's four taps, the B fragments of four steps.
+        auto build_group = [&](int cs, int tg, int ntaps, acc4 (&bq)[4][PB]) {
+            const int tl = tg * 4 + q;
+            const int nq = min(4, (g.Cg - cs * BC) >> 2);   // channel quads of the slice in the group
 #pragma unroll
-            for (int pb = 0; pb < PB; ++pb) bcur[pb] = bnxt[pb];
+            for (int pb = 0; pb < PB; ++pb) {
+                acc4 sv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sv[j] = acc4{0.f, 0.f, 0.f, 0.f};
+                if (tl < ntaps) {
+                    const acc4 r = geo[tl * BPX + wave * (PB * 16) + pb * 16 + (lane & 15)];
+                    if (nq == 4)
+                        sample3_all<true>(g, wt, tile, xwin, xg + cs * BC, 4, r, deformable, sv);
+                    else
+                        sample3_all<false>(g, wt, tile, xwin, xg + cs * BC, nq, r, deformable, sv);
+                }
+                transpose_rows4(sv);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bq[j][pb] = sv[j];
+            }
+        };
+        for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
+            const int ntaps = min(wt.tpp, g.Kn - t0);
+            const int ngr = (ntaps + 3) >> 2;   // tap groups per slice
+            const int ngroups = (cs_hi - cs_lo) * ngr;
+            geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
+
+            // group k = (slice cs_lo + k / ngr, taps 4 * (k % ngr) ..): its B fragments are
+            // built at its start (the sampling's LDS latency is covered by the other wave of
+            // the SIMD), then its steps run; wa holds the weight fragments of the next step.
+            // The X window of a slice is loaded at the slice switch (the registers a prefetch
+            // would hold across the steps are taken by the group's B fragments).
+            acc4 wa[MB];
+            load_w(wptr(cs_lo, t0), wa);
+            __syncthreads();   // previous pass done with the tables
+            open_slice(cs_lo, t0, ntaps);
+            __syncthreads();
+            for (int k = 0; k < ngroups; ++k) {
+                const bool more = k + 1 < ngroups;
+                const int cs_r = k / ngr, tg = k - cs_r * ngr;
+                const int csn_r = (k + 1) / ngr, tgn = k + 1 - csn_r * ngr;
+                const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
+                acc4 bq[4][PB];
+                build_group(cs, tg, ntaps, bq);
+                const int nt = min(4, ntaps - tg * 4);
+                const int tb = t0 + tg * 4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (j < nt) {
+                        // weight fragments of the step after this one (this step's own at the end)
+                        const float *pn = j + 1 < nt ? wptr(cs, tb + j + 1)
+                                                     : (more ? wptr(csn, t0 + tgn * 4) : wptr(cs, tb + j));
+                        mfma_step(bq[j], wa, pn);
+                    }
+                }
+                if (more && tgn == 0) {
+                    __syncthreads();   // every wave done reading the current window
+                    open_slice(csn, t0, ntaps);
+                    __syncthreads();
+                }
+            }
+        }
+    } else {
+        for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
+            const int ntaps = min(wt.tpp, g.Kn - t0);
+            const int nsteps = (cs_hi - cs_lo) * ntaps;
+            geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
+
+            // step k = (slice cs_lo + k / ntaps, tap k % ntaps). Invariant at the top of step k:
+            // its B fragments are in bcur, its weight fragments in wa.
+            acc4 wa[MB], bcur[PB], bnxt[PB];
+            prefetch_x(cs_lo);
+            load_w(wptr(cs_lo, t0), wa);
+            __syncthreads();   // previous pass done with the tables
+            open_slice(cs_lo, t0, ntaps);
+            __syncthreads();
+            build_b(cs_lo, 0, bcur);
+            // the next slice's X window is requested PF steps before it is needed (memory
+            // latency exceeds one step's MFMAs), or at the slice's first step when shorter
+            const int pf_tl = max(ntaps - PF, 0);
+            for (int k = 0; k < nsteps; ++k) {
+                const bool more = k + 1 < nsteps;
+                const int kn = k + 1, csn_r = kn / ntaps, tln = kn - csn_r * ntaps;
+                const int cs_r = k / ntaps;
+                const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
+                const bool new_slice = more && tln == 0;
+                if (k - cs_r * ntaps == pf_tl && cs + 1 < cs_hi) prefetch_x(cs + 1);
+                if (more && !new_slice) build_b(csn, tln, bnxt);
+                mfma_step(bcur, wa, more ? wptr(csn, t0 + tln) : wptr(cs, t0 + k - cs_r * ntaps));
+                if (new_slice) {
+                    __syncthreads();   // every wave done reading the current window
+                    open_slice(csn, t0, ntaps);
+                    __syncthreads();
+                    build_b(csn, 0, bnxt);
+                }
+    #pragma unroll
+                for (int pb = 0; pb < PB; ++pb) bcur[pb] = bnxt[pb];
+            }
         }
     }
 
@@ -285,7 +362,7 @@ template <int DIM, typename T, int MB>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
                     const void *offset, const void *mask, const void *bias, void *y, void *y32, hipStream_t s) {
     auto kern = fwd_win_kernel<DIM, T, MB>;
-    const size_t lds = ((size_t)GEO_WORDS + (size_t)wt.cells * XS) * sizeof(float);
+    const size_t lds = ((size_t)GEO_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
     static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -337,8 +414,10 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     f.mb = (dim == 3 || g.Mg <= 64 || spatial * ((g.Mg + 127) / 128) < 256) ? 4 : 8;
     const int rows = 16 * f.mb;
     const long long max_cells = (long long)xq_of(f.mb) * NT / 4;
-    wt = win_resize(base, g, dim, (size_t)GEO_WORDS * sizeof(float), XS * sizeof(float), max_cells);
-    const size_t lds = ((size_t)GEO_WORDS + (size_t)wt.cells * XS) * sizeof(float);
+    // (3D: one more cell, the zero cell)
+    const int zc = dim == 3 ? 1 : 0;
+    wt = win_resize(base, g, dim, (size_t)(GEO_WORDS + zc * XS) * sizeof(float), XS * sizeof(float), max_cells - zc);
+    const size_t lds = ((size_t)GEO_WORDS + (size_t)(wt.cells + zc) * XS) * sizeof(float);
     if (lds > WIN_LDS_TARGET || wt.cells > max_cells) return f;
     f.m_tiles = (g.Mg + rows - 1) / rows;
     f.Mg_pad = f.m_tiles * rows;
@@ -348,6 +427,9 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     const int slices = f.Cg_pad / BC;
     f.ksplit = (spatial * f.m_tiles < 256 && slices >= 2) ? 2 : 1;
     f.slices_per = (slices + f.ksplit - 1) / f.ksplit;
+    // 3D samples taps in groups of four: passes of eight taps fill their groups (27 taps:
+    // 8, 8, 8, 3 = seven groups, where passes of nine would take nine)
+    if (dim == 3 && g.Kn > WIN_TMAX) wt.tpp = 8;
     f.ok = true;
     return f;
 }

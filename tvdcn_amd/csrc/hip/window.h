@@ -232,6 +232,76 @@ __device__ __forceinline__ acc4 sample3_masked(const Geo &g, const WinTiles &wt,
     return sv;
 }
 
+// mask * sample of all 16 channels of the tile's slice at a 3D record: s[j] = channels
+// 4j .. 4j + 3 (xgs: the channels-last X of the tile's image at the slice's first channel;
+// nq: channel quads of the slice inside the group, 4 when FULLQ). The corner geometry and
+// the eight mask-folded weights are formed once for the 16 channels. Window cell wt.cells
+// must hold zeros (the zero cell): a corner outside the window reads it, and a corner
+// outside the window but inside the grid then overwrites it with the global values.
+template <bool FULLQ>
+__device__ __forceinline__ void sample3_all(const Geo &g, const WinTiles &wt, const Tile &tile, const float *xwin,
+                                            const float *__restrict__ xgs, int nq, const acc4 &r, bool deformable,
+                                            acc4 (&s)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = acc4{0.f, 0.f, 0.f, 0.f};
+    const Corners3 cr(g, wt, tile, r, deformable);
+    if (!cr.inside) return;
+    auto corner = [&](int k, float w) {
+        const bool iw = cr.in_win(k);
+        const float *xc = xwin + (iw ? cr.cell(wt, k) : wt.cells) * XS;
+        acc4 x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const acc4 *>(xc + 4 * j);
+        if (!iw && cr.in_grid(k)) {
+            const float *xp = xgs + (size_t)cr.idx(g, k) * g.C;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (FULLQ || j < nq) x[j] = *reinterpret_cast<const acc4 *>(xp + 4 * j);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] += w * x[j];
+    };
+    const float mk = r[3];
+    if (deformable) {
+        // mask-folded trilinear weights: (z, y) pairs first, then x
+        const float z1 = mk * cr.fh[0], z0 = mk - z1;
+        const float zy[4] = {z0 - z0 * cr.fh[1], z0 * cr.fh[1], z1 - z1 * cr.fh[1], z1 * cr.fh[1]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float w1 = zy[j] * cr.fh[2];
+            corner(2 * j, zy[j] - w1);
+            corner(2 * j + 1, w1);
+        }
+    } else {
+        corner(0, mk);   // offset-free sampling: the low corner only
+    }
+}
+
+// 4 x 4 transpose of 16-byte blocks across the four 16-lane rows of the wave: on return,
+// row r's block c holds what row c held in block r. Two stages of row swaps (gfx950
+// v_permlane32_swap: rows 2, 3 of the first operand <-> rows 0, 1 of the second;
+// v_permlane16_swap: odd rows of the first <-> even rows of the second).
+__device__ __forceinline__ void transpose_rows4(acc4 (&b)[4]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(b[c][v]), __float_as_uint(b[c + 2][v]),
+                                                            false, false);
+            b[c][v] = __uint_as_float(p[0]);
+            b[c + 2][v] = __uint_as_float(p[1]);
+        }
+#pragma unroll
+    for (int c = 0; c < 4; c += 2)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(b[c][v]), __float_as_uint(b[c + 1][v]),
+                                                            false, false);
+            b[c][v] = __uint_as_float(p[0]);
+            b[c + 1][v] = __uint_as_float(p[1]);
+        }
+}
+
 // RPT = records per thread per batch (WIN_TMAX * BPX / 512 = 4.5: one batch at 5); a
 // caller short of registers passes fewer.
 template <int DIM, typename T, int RPT = 5>
