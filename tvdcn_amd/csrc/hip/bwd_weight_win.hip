@@ -74,7 +74,12 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     const int tg = wave / (NW / TG);                     // this wave's tap group
     const int mrow = mt * BMW + (wave % (NW / TG)) * (MB * 16);   // first row of this wave
 
+    if constexpr (DIM == 3) {
+        if (tid < XS) xwin[wt.cells * XS + tid] = 0.f;   // zero cell of the 3D corner reads
+    }
+
     // S-builder item of this thread: chunk pixel j, channel quad sq, taps st, st + 4, ...
+    // (3D: chunk pixel j, taps tid / 32, + 16, ..., all 16 channels)
     const int sj = tid & 31, sq = (tid >> 5) & 3, st0 = tid >> 7;
     constexpr int SSTEP = NT / (KP * 4);   // tap stride of the items
 
@@ -101,14 +106,31 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
             auto build_s = [&](int k, int bf) {
                 float *dst = sbuf + bf * (TM * BC * SS);
                 const int i = k * KP + sj;
+                if constexpr (DIM == 3) {
+                    // 3D: one item per (chunk pixel, tap) for all 16 channels (the corner geometry
+                    // formed once per sample rather than once per channel quad)
+                    const int nq = min(4, (g.Cg - tile.c0) >> 2);
+                    for (int tl = tid >> 5; tl < ntaps; tl += NT / KP) {
+                        const acc4 r = geo[tl * BPX + i];
+                        acc4 sv[4];
+                        if (nq == 4)
+                            sample3_all<true, true>(g, wt, tile, xwin, xb, 4, r, deformable, sv);
+                        else
+                            sample3_all<false, true>(g, wt, tile, xwin, xb, nq, r, deformable, sv);
+                        float *row = dst + tl * BC * SS + sj;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) row[(4 * j + v) * SS] = sv[j][v];
+                    }
+                    return;
+                }
                 for (int tl = st0; tl < ntaps; tl += SSTEP) {
                     const acc4 r = geo[tl * BPX + i];
                     const int fc = fast_cell<DIM>(r);
                     const float mk = rec_mask<DIM>(r);
                     acc4 sv;
-                    if constexpr (DIM == 3) {
-                        sv = sample3_masked(g, wt, tile, xwin, 4 * sq, xb + 4 * sq, cq_ok, r, deformable);
-                    } else if (fc >= 0) {
+                    if (fc >= 0) {
                         // every corner cell is in the window (zeros outside the grid)
                         sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * sq, r, mk);
                     } else {
@@ -254,7 +276,7 @@ template <int DIM, typename T, bool FULL, int MB, int TG>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, hipStream_t s) {
     auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG>;
-    const size_t lds = ((size_t)GEO_WORDS + SBUF_WORDS + (size_t)wt.cells * XS) * sizeof(float);
+    const size_t lds = ((size_t)GEO_WORDS + SBUF_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
     static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -290,14 +312,14 @@ hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &
 
 }  // namespace
 
-size_t weight_win_fixed_bytes() { return (size_t)(GEO_WORDS + SBUF_WORDS) * sizeof(float); }
+size_t weight_win_fixed_bytes(int dim) { return (size_t)(GEO_WORDS + SBUF_WORDS + (dim == 3 ? XS : 0)) * sizeof(float); }
 
-WeightWin plan_weight_win(const Geo &g, const WinTiles &wt) {
+WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     WeightWin w{};
     w.ok = false;
     // needs the windowed tiling; GEMM sides up to 128 rows take 64-row tiles with the taps
     // split between two wave groups, larger ones 256-row tiles
-    if (!wt.ok || g.Mg < 16 || (size_t)GEO_WORDS * 4 + SBUF_WORDS * 4 + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
+    if (!wt.ok || g.Mg < 16 || weight_win_fixed_bytes(dim) + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
         return w;
     w.tg = g.Mg <= 128 ? 2 : 1;
     const int rows = w.tg == 2 ? rows_of<1, 2>() : rows_of<2, 1>();

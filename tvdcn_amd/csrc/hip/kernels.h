@@ -75,13 +75,13 @@ FwdTiles plan_fwd(const Geo &g, int dtype);
 // windowed forward plan over the base tiling; wt receives the tiling with the forward's
 // own window margin
 FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt);
-WeightWin plan_weight_win(const Geo &g, const WinTiles &wt);
+WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim);
 WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coord);
 // the same tiling with the window margin re-sized for another kernel's LDS budget
 // (cell_cap > 0: at most that many window cells)
 WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_bytes, size_t cell_bytes,
                     long long cell_cap = 0);
-size_t weight_win_fixed_bytes();   // LDS of the windowed weight gradient besides its X window
+size_t weight_win_fixed_bytes(int dim);   // LDS of the windowed weight gradient besides its X window
 size_t x_window_cell_bytes();
 DataTiles plan_data(const Geo &g, int dtype);
 WeightTiles plan_weight(const Geo &g, int dtype);

@@ -238,7 +238,7 @@ __device__ __forceinline__ acc4 sample3_masked(const Geo &g, const WinTiles &wt,
 // the eight mask-folded weights are formed once for the 16 channels. Window cell wt.cells
 // must hold zeros (the zero cell): a corner outside the window reads it, and a corner
 // outside the window but inside the grid then overwrites it with the global values.
-template <bool FULLQ>
+template <bool FULLQ, bool PAIRWISE = false>
 __device__ __forceinline__ void sample3_all(const Geo &g, const WinTiles &wt, const Tile &tile, const float *xwin,
                                             const float *__restrict__ xgs, int nq, const acc4 &r, bool deformable,
                                             acc4 (&s)[4]) {
@@ -271,6 +271,7 @@ __device__ __forceinline__ void sample3_all(const Geo &g, const WinTiles &wt, co
             const float w1 = zy[j] * cr.fh[2];
             corner(2 * j, zy[j] - w1);
             corner(2 * j + 1, w1);
+            if constexpr (PAIRWISE) __builtin_amdgcn_sched_barrier(0);   // two corners in flight at a time
         }
     } else {
         corner(0, mk);   // offset-free sampling: the low corner only
