@@ -347,3 +347,41 @@ def test_fastdiv_constants_are_exact():
                  [rng.randrange(0, 1 << 31) for _ in range(200)]:
             if 0 <= n < (1 << 31):
                 assert fastdiv(n, d) == n // d, (n, d)
+
+
+@pytest.mark.parametrize("dim,transposed", [(1, False), (2, False), (3, False), (1, True), (2, True), (3, True)])
+def test_torch_compile_fullgraph_on_meta(dim, transposed):
+    """torch.compile traces the ops without graph breaks (fullgraph=True): the Meta kernels serve
+    as the fake-tensor implementations, forward and backward."""
+    from torch._dynamo.testing import CompileCounterWithBackend
+    torch._dynamo.reset()
+    k = 3
+    S = [6] * dim
+    if transposed:
+        fn = getattr(tvdcn_amd, f"deform_conv_transpose{dim}d")
+        x = meta(2, 4, *S)
+        w = meta(4, 3, *[k] * dim)                    # (Cin, Cout, k...)
+        out_sz = [s + k - 1 for s in S]
+        o = meta(2, dim * k ** dim, *S)                # offsets on the input grid
+        m = meta(2, k ** dim, *S)
+    else:
+        fn = getattr(tvdcn_amd, f"deform_conv{dim}d")
+        x = meta(2, 4, *S)
+        w = meta(5, 4, *[k] * dim)
+        out_sz = [s - k + 1 for s in S]
+        o = meta(2, dim * k ** dim, *out_sz)
+        m = meta(2, k ** dim, *out_sz)
+    b = meta(w.shape[1] if transposed else w.shape[0])
+    leaves = [t.requires_grad_(True) for t in (x, w, o, m, b)]
+
+    def f(x, w, o, m, b):
+        return torch.relu(fn(x, w, o, m, b)).sum()
+
+    cnt = CompileCounterWithBackend("aot_eager")
+    out = torch.compile(f, backend=cnt, fullgraph=True)(*leaves)
+    out.backward()
+    assert cnt.frame_count == 1
+    for t in leaves:
+        assert t.grad is not None and t.grad.shape == t.shape
+    if transposed:
+        assert list(fn(x, w, o, m, b).shape[2:]) == out_sz
