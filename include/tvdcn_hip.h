@@ -61,12 +61,18 @@ typedef enum {
  *              output (batch, out_channels, *out_size)
  * offset_groups = 0 means offset is None; mask_groups = 0 means mask is None.
  * output_padding is used only when transposed = 1.
+ * flags: TVDCN_FLAG_CHANNELS_LAST (conv only) = input, and in the backward grad_input, are in
+ * channels-last order (batch, *in_size, in_channels); every other tensor keeps the layout
+ * above. No counterpart in the reference, which makes every input NC<spatial>-contiguous
+ * (cuda/deform_conv2d_kernel.cpp:114-118); it spares the layout copies for callers whose
+ * activations are channels-last.
  */
+#define TVDCN_FLAG_CHANNELS_LAST 1
 typedef struct {
     int32_t dim;
     int32_t transposed;
     int32_t dtype;            /* tvdcn_dtype */
-    int32_t reserved;
+    int32_t flags;            /* TVDCN_FLAG_*; 0 = the layouts above */
     int64_t batch;
     int64_t in_channels;
     int64_t out_channels;

@@ -51,7 +51,7 @@ def test_c_abi_exports_every_declared_function(lib):
 
 class Desc(ctypes.Structure):
     _fields_ = [("dim", ctypes.c_int32), ("transposed", ctypes.c_int32), ("dtype", ctypes.c_int32),
-                ("reserved", ctypes.c_int32), ("batch", ctypes.c_int64), ("in_channels", ctypes.c_int64),
+                ("flags", ctypes.c_int32), ("batch", ctypes.c_int64), ("in_channels", ctypes.c_int64),
                 ("out_channels", ctypes.c_int64), ("groups", ctypes.c_int64), ("offset_groups", ctypes.c_int64),
                 ("mask_groups", ctypes.c_int64), ("in_size", ctypes.c_int64 * 3), ("kernel", ctypes.c_int64 * 3),
                 ("stride", ctypes.c_int64 * 3), ("padding", ctypes.c_int64 * 3), ("dilation", ctypes.c_int64 * 3),
@@ -118,6 +118,13 @@ def test_c_abi_argument_errors(lib):
     st = lib.tvdcn_deform_conv_forward(ctypes.byref(d), None, None, ctypes.c_void_p(16), ctypes.c_void_p(16), None,
                                        None, None, ctypes.c_size_t(0), None)
     assert st == 1 and b"offset_groups" in lib.tvdcn_last_error()
+    # descriptor flags: unknown bits, and channels-last input on the transposed op
+    for d, msg in ((cfg2_desc(flags=2), b"unknown flags"),
+                   (cfg2_desc(flags=1, transposed=1, out_channels=128, offset_groups=2, mask_groups=2),
+                    b"channels-last")):
+        st = lib.tvdcn_deform_conv_forward(ctypes.byref(d), None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                           None, None, None, ctypes.c_size_t(0), None)
+        assert st == 1 and msg in lib.tvdcn_last_error()
 
 
 REF_SCHEMAS = {

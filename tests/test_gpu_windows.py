@@ -11,6 +11,7 @@
 import pytest
 import torch
 
+import tvdcn_amd
 from helpers import make_case, rel_err
 from test_gpu_parity import TOL, check, run_gpu, run_oracle
 
@@ -130,3 +131,29 @@ def test_many_taps_multi_pass_fp32():
     case = make_case(2, False, batch=2, cin=32, cout=64, kernel=[5, 5], stride=[1, 1], padding=[2, 2],
                      dilation=[1, 1], in_size=[24, 22], out_pad=[0, 0], seed=545, offset_scale=3.0)
     check(case, torch.float32)
+
+
+@pytest.mark.parametrize("dim,dtype", [(2, torch.float32), (2, torch.bfloat16), (3, torch.float32)])
+def test_channels_last_input(dim, dtype):
+    """A channels-last conv input is sampled in place (fp32) or widened in place (half types), and
+    its gradient comes back channels-last; the numbers are those of the NC<spatial> path."""
+    in_size = {2: [20, 18], 3: [6, 10, 9]}[dim]
+    case = make_case(dim, False, batch=2, cin=32, cout=48, kernel=[3] * dim, stride=[1] * dim, padding=[1] * dim,
+                     dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim, seed=560 + dim)
+    out, grads, gout = run_gpu(case, dtype)
+    fmt = torch.channels_last if dim == 2 else torch.channels_last_3d
+    names = ("input", "weight", "offset", "mask", "bias")
+    ts = [case[n].to("cuda:0", dtype) for n in names]
+    ts[0] = ts[0].contiguous(memory_format=fmt)
+    assert not ts[0].is_contiguous()
+    ts = [t.requires_grad_(True) for t in ts]
+    fn = getattr(tvdcn_amd, f"deform_conv{dim}d")
+    y = fn(*ts, stride=case["stride"], padding=case["padding"], dilation=case["dilation"], groups=case["groups"])
+    y.backward(gout.to("cuda:0", dtype))
+    torch.cuda.synchronize()
+    assert ts[0].grad.is_contiguous(memory_format=fmt)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert rel_err(y, out) < tol
+    for n, t, r in zip(names, ts, grads):
+        e = rel_err(t.grad, r)
+        assert e < tol, f"grad_{n} rel err {e}"

@@ -84,6 +84,9 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     if (d->batch < 0 || d->in_channels <= 0 || d->out_channels <= 0)
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "batch must be >= 0 and channels positive");
     if (d->groups <= 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "groups must be positive");
+    if (d->flags & ~TVDCN_FLAG_CHANNELS_LAST) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "unknown flags");
+    if ((d->flags & TVDCN_FLAG_CHANNELS_LAST) && d->transposed)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "channels-last input is supported for the non-transposed ops");
     if (d->in_channels % d->groups || d->out_channels % d->groups)
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "in_channels and out_channels must be divisible by groups");
     if (d->offset_groups < 0 || d->mask_groups < 0)
@@ -352,7 +355,12 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
     g_last_error.clear();
     if (!pl.transposed) {
         void *xcl = at(workspace, L.xcl), *wf = at(workspace, L.wf);
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
+        if (!(desc->flags & TVDCN_FLAG_CHANNELS_LAST))
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
+        else if (acc_is_storage(dt))
+            xcl = const_cast<void *>(input);   // already the kernels' layout and type
+        else
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, input, xcl, (size_t)g.B * g.Sn * g.C, s));
         if (pl.fw.ok) {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
             void *y32 = nullptr;
@@ -434,14 +442,21 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     const void *X = pl.transposed ? grad_out : input;
     {
         void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
+        const bool cl_in = (desc->flags & TVDCN_FLAG_CHANNELS_LAST) != 0;   // conv only
+        if (!cl_in)
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
+        else if (direct)
+            xcl = const_cast<void *>(X);   // already the kernels' layout and type
+        else
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, X, xcl, (size_t)g.B * g.Sn * g.C, s));
         const bool coord = offset != nullptr || mask != nullptr;
         if (pl.wn_s.ok)
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
         if (!pl.transposed) {
-            void *gx_cl = at(workspace, L.cl_acc);
+            // channels-last grad_input of the accumulation type is accumulated in place
+            void *gx_cl = cl_in && direct ? grad_input : at(workspace, L.cl_acc);
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
             if (pl.wn_s.ok && coord && pl.data_split) {
                 // two launches, each with the larger window its LDS share allows
@@ -455,7 +470,12 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
             else
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask,
                                                                         gx_cl, goff, gmask, s));
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_from_channels_last(dt, gx_cl, grad_input, nullptr, g.B, g.C, g.Sn, s));
+            if (!cl_in)
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                             launch_from_channels_last(dt, gx_cl, grad_input, nullptr, g.B, g.C, g.Sn, s));
+            else if (!direct)
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                             launch_acc_to_storage(dt, gx_cl, grad_input, (size_t)g.B * g.Sn * g.C, s));
         } else {
             void *wf = at(workspace, L.wf);
             if (pl.fw.ok) {

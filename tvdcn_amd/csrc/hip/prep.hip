@@ -102,6 +102,12 @@ __global__ void acc_to_storage_kernel(const A *__restrict__ a, T *__restrict__ o
         o[i] = from_acc<T, A>(a[i]);
 }
 
+template <typename T, typename A>
+__global__ void storage_to_acc_kernel(const T *__restrict__ x, A *__restrict__ a, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        a[i] = to_acc<A>(x[i]);
+}
+
 // grad_bias[c] = sum_{b, s} gout[b][c][s]; one 1024-thread workgroup per channel,
 // four consecutive positions per load when rows are 4-aligned; per-thread partial sums
 // in a fixed order, then a fixed reduction tree (deterministic)
@@ -223,6 +229,17 @@ hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n
         using A = decltype(av);
         hipLaunchKernelGGL((acc_to_storage_kernel<T, A>), dim3(grid_for(n)), dim3(256), 0, s,
                            static_cast<const A *>(acc), static_cast<T *>(out), n);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_storage_to_acc(int dtype, const void *x, void *acc, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        hipLaunchKernelGGL((storage_to_acc_kernel<T, A>), dim3(grid_for(n)), dim3(256), 0, s,
+                           static_cast<const T *>(x), static_cast<A *>(acc), n);
         return hipGetLastError();
     });
 }

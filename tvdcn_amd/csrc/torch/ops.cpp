@@ -68,9 +68,11 @@ struct Problem {
     int dim;
     bool transposed;
     bool unbatched;
+    bool channels_last;   // conv input kept in channels-last order (TVDCN_FLAG_CHANNELS_LAST)
     tvdcn_conv_desc desc;
     std::vector<int64_t> out_size;
-    Tensor input, weight, offset, mask, bias;   // batched, contiguous (offset/mask/bias may be undefined)
+    // batched, contiguous (input: channels-last when channels_last); offset/mask/bias may be undefined
+    Tensor input, weight, offset, mask, bias;
 };
 
 // Shape checks of the reference forward drivers, in the same order and with the
@@ -108,7 +110,12 @@ Problem make_problem(int dim, bool transposed, const Tensor &input, const Tensor
     TORCH_CHECK(!modulated || mask->dim() == input.dim(), "Expected ", dim + 1, "D (unbatched) or ", dim + 2,
                 "D (batched) mask, but got mask of size: ", modulated ? mask->sizes() : at::IntArrayRef());
 
-    pr.input = input.contiguous();
+    // a batched conv input that is channels-last (and not also plain contiguous) is handed over
+    // as it is: the kernels sample channels-last data, so no layout copy is needed
+    const auto cl_format = dim == 2 ? at::MemoryFormat::ChannelsLast : at::MemoryFormat::ChannelsLast3d;
+    pr.channels_last = !transposed && !pr.unbatched && (dim == 2 || dim == 3) && input.is_contiguous(cl_format) &&
+                       !input.is_contiguous();
+    pr.input = pr.channels_last ? input : input.contiguous();
     pr.weight = weight.contiguous();
     pr.offset = deformable ? offset->contiguous() : Tensor();
     pr.mask = modulated ? mask->contiguous() : Tensor();
@@ -216,6 +223,7 @@ Problem make_problem(int dim, bool transposed, const Tensor &input, const Tensor
     std::memset(&d, 0, sizeof(d));
     d.dim = dim;
     d.transposed = transposed;
+    d.flags = pr.channels_last ? TVDCN_FLAG_CHANNELS_LAST : 0;
     d.dtype = -1;
     d.batch = B;
     d.in_channels = Cin;
@@ -257,7 +265,7 @@ void *mut_ptr_or_null(const Tensor &t) { return t.defined() ? t.data_ptr() : nul
 Tensor aligned(const Tensor &t) {
     if (!t.defined()) return t;
     if ((reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) == 0) return t;
-    return t.clone(at::MemoryFormat::Contiguous);
+    return t.clone(at::MemoryFormat::Preserve);   // keeps a channels-last input channels-last
 }
 
 hipStream_t current_stream(const Tensor &t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
