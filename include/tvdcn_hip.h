@@ -66,8 +66,14 @@ typedef enum {
  * above. No counterpart in the reference, which makes every input NC<spatial>-contiguous
  * (cuda/deform_conv2d_kernel.cpp:114-118); it spares the layout copies for callers whose
  * activations are channels-last.
+ * TVDCN_FLAG_MASK_SIGMOID = the mask tensor holds logits: the kernels use
+ * mask_scale * sigmoid(logit) as the mask (tvdcn's MaskSigmoid, ops/activations/mask_sigmoid.py:11-21,
+ * folded into the mask load), and the backward's grad_mask is the gradient with respect to the
+ * logits. Needs a mask and mask_scale > 0. No counterpart in the reference, whose packed modules
+ * run the activation as a separate pass.
  */
 #define TVDCN_FLAG_CHANNELS_LAST 1
+#define TVDCN_FLAG_MASK_SIGMOID 2
 typedef struct {
     int32_t dim;
     int32_t transposed;
@@ -85,6 +91,7 @@ typedef struct {
     int64_t padding[3];
     int64_t dilation[3];
     int64_t output_padding[3];
+    double mask_scale;        /* TVDCN_FLAG_MASK_SIGMOID only */
 } tvdcn_conv_desc;
 
 /* Output spatial size (out_size[0..dim)); returns TVDCN_STATUS_SUCCESS or an error

@@ -55,7 +55,7 @@ class Desc(ctypes.Structure):
                 ("out_channels", ctypes.c_int64), ("groups", ctypes.c_int64), ("offset_groups", ctypes.c_int64),
                 ("mask_groups", ctypes.c_int64), ("in_size", ctypes.c_int64 * 3), ("kernel", ctypes.c_int64 * 3),
                 ("stride", ctypes.c_int64 * 3), ("padding", ctypes.c_int64 * 3), ("dilation", ctypes.c_int64 * 3),
-                ("output_padding", ctypes.c_int64 * 3)]
+                ("output_padding", ctypes.c_int64 * 3), ("mask_scale", ctypes.c_double)]
 
 
 def cfg2_desc(**over):
@@ -119,9 +119,11 @@ def test_c_abi_argument_errors(lib):
                                        None, None, ctypes.c_size_t(0), None)
     assert st == 1 and b"offset_groups" in lib.tvdcn_last_error()
     # descriptor flags: unknown bits, and channels-last input on the transposed op
-    for d, msg in ((cfg2_desc(flags=2), b"unknown flags"),
+    for d, msg in ((cfg2_desc(flags=4), b"unknown flags"),
                    (cfg2_desc(flags=1, transposed=1, out_channels=128, offset_groups=2, mask_groups=2),
-                    b"channels-last")):
+                    b"channels-last"),
+                   (cfg2_desc(flags=2, mask_scale=0.0), b"sigmoid mask"),
+                   (cfg2_desc(flags=2, mask_scale=2.0, mask_groups=0), b"sigmoid mask")):
         st = lib.tvdcn_deform_conv_forward(ctypes.byref(d), None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
                                            None, None, None, ctypes.c_size_t(0), None)
         assert st == 1 and msg in lib.tvdcn_last_error()
@@ -392,3 +394,26 @@ def test_torch_compile_fullgraph_on_meta(dim, transposed):
         assert t.grad is not None and t.grad.shape == t.shape
     if transposed:
         assert list(fn(x, w, o, m, b).shape[2:]) == out_sz
+
+
+def test_sigmoid_mask_op_on_meta():
+    """The fused sigmoid-mask op: shapes, gradients to the logits, double-backward refusal, and a
+    packed module with the default mask activation taking it."""
+    x = meta(2, 4, 8, 8).requires_grad_(True)
+    w = meta(5, 4, 3, 3).requires_grad_(True)
+    o = meta(2, 18, 6, 6).requires_grad_(True)
+    lg = meta(2, 9, 6, 6).requires_grad_(True)
+    y = torch.ops.tvdcn_amd.deform_conv_sigmoid_mask(x, w, o, lg, None, [1, 1], [0, 0], [0, 0], [1, 1], 1, False,
+                                                     2.0)
+    assert y.shape == (2, 5, 6, 6)
+    gx, gw, go, gl = torch.autograd.grad(y.sum(), (x, w, o, lg), create_graph=True)
+    assert gl.shape == lg.shape and go.shape == o.shape
+    with pytest.raises(RuntimeError, match="double backwards on deform_conv_sigmoid_mask not supported"):
+        gl.sum().backward()
+    with pytest.raises(RuntimeError, match="mask_scale"):
+        torch.ops.tvdcn_amd.deform_conv_sigmoid_mask(x, w, o, lg, None, [1, 1], [0, 0], [0, 0], [1, 1], 1, False, 0.0)
+    m = tvdcn_amd.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True, device="meta")
+    offset, logits, scale = m._generate(meta(2, 4, 8, 8))
+    assert scale == 2.0 and logits.shape == (2, 9, 8, 8)
+    s = tvdcn_amd.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True, mask_activation="softmax", device="meta")
+    assert s._generate(meta(2, 4, 8, 8))[2] is None

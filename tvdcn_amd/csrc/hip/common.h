@@ -54,6 +54,7 @@ struct Geo {
     int Sn, Pn, Kn;
     int NP;                // B * Pn
     FastDiv dPn, dP2, dP12, dK2, dK12;   // divisors Pn, P[2], P[1]*P[2], K[2], K[1]*K[2]
+    double mask_scale = 0.0;   // > 0: the mask tensor holds logits; the kernels use mask_scale * sigmoid(logit)
 };
 
 // ---------------------------------------------------------------------------
@@ -338,10 +339,32 @@ __device__ __forceinline__ GatherCorners<DIM, A> gather_corners(const Geo &g, co
     return gc;
 }
 
+// Mask value of (b, mask group, tap, column pixel): the tensor's value, or mask_scale *
+// sigmoid(value) when the mask holds logits (tvdcn/ops/activations/mask_sigmoid.py:11-21
+// applied in the load instead of as a separate pass)
+// (mask_raw: the stored value, 1 without a mask; mask_activate: the sigmoid when the mask holds
+// logits — split so that batched loads are all issued before any value is used)
 template <typename A, typename T>
-__device__ __forceinline__ A mask_at(const Geo &g, const T *__restrict__ mask, int b, int mgi, int t, int p) {
+__device__ __forceinline__ A mask_raw(const Geo &g, const T *__restrict__ mask, int b, int mgi, int t, int p) {
     if (mask == nullptr) return A(1);
     return to_acc<A>(mask[((size_t)(b * g.mg + mgi) * g.Kn + t) * (size_t)g.Pn + p]);
 }
+template <typename A>
+__device__ __forceinline__ A mask_activate(const Geo &g, A v) {
+    if (g.mask_scale > 0.0) {   // uniform
+        // fp32: hardware exp2 and reciprocal (a few instructions, ~2 ulp), so that the rarely
+        // taken branch adds little code to the kernels' hot loops
+        if constexpr (std::is_same_v<A, float>)
+            return (float)g.mask_scale * __builtin_amdgcn_rcpf(1.f + __expf(-v));
+        else
+            return (A)g.mask_scale / (A(1) + exp(-v));
+    }
+    return v;
+}
+template <typename A, typename T>
+__device__ __forceinline__ A mask_at(const Geo &g, const T *__restrict__ mask, int b, int mgi, int t, int p) {
+    return mask_activate<A>(g, mask_raw<A, T>(g, mask, b, mgi, t, p));
+}
+
 
 }  // namespace tvdcn_hip

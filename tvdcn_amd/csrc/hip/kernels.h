@@ -97,6 +97,9 @@ hipError_t launch_weight_data_layout(int dtype, const Geo &g, const void *w, voi
 hipError_t launch_fill_zero(int elem_bytes, void *p, size_t n, hipStream_t s);   // elem_bytes 2, 4 or 8
 hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n, hipStream_t s);
 hipError_t launch_storage_to_acc(int dtype, const void *x, void *acc, size_t n, hipStream_t s);   // elementwise widening
+// gmask_acc (accumulation type) *= d(scale * sigmoid(logit)) / d(logit), elementwise
+hipError_t launch_mask_sigmoid_grad(int dtype, const void *logits, void *gmask_acc, double scale, size_t n,
+                                    hipStream_t s);
 hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s);
 
 // the three GEMM families

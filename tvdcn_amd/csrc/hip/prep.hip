@@ -102,6 +102,23 @@ __global__ void acc_to_storage_kernel(const A *__restrict__ a, T *__restrict__ o
         o[i] = from_acc<T, A>(a[i]);
 }
 
+// Mask gradient of logits: the kernels accumulate d(loss)/d(mask value) per (b, group, tap,
+// pixel); with mask value m = scale * sigmoid(logit), d(m)/d(logit) = m * (1 - m / scale)
+// depends on that element only, so it scales the accumulated sum once.
+template <typename T, typename A>
+__global__ void mask_sigmoid_grad_kernel(const T *__restrict__ logits, A *__restrict__ gmask, double scale, size_t n) {
+    const A sc = (A)scale;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const A v = to_acc<A>(logits[i]);
+        A m;
+        if constexpr (std::is_same_v<A, float>)
+            m = sc / (1.f + expf(-v));
+        else
+            m = sc / (A(1) + exp(-v));
+        gmask[i] *= m - m * m / sc;
+    }
+}
+
 template <typename T, typename A>
 __global__ void storage_to_acc_kernel(const T *__restrict__ x, A *__restrict__ a, size_t n) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -229,6 +246,18 @@ hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n
         using A = decltype(av);
         hipLaunchKernelGGL((acc_to_storage_kernel<T, A>), dim3(grid_for(n)), dim3(256), 0, s,
                            static_cast<const A *>(acc), static_cast<T *>(out), n);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_mask_sigmoid_grad(int dtype, const void *logits, void *gmask_acc, double scale, size_t n,
+                                    hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        hipLaunchKernelGGL((mask_sigmoid_grad_kernel<T, A>), dim3(grid_for(n)), dim3(256), 0, s,
+                           static_cast<const T *>(logits), static_cast<A *>(gmask_acc), scale, n);
         return hipGetLastError();
     });
 }

@@ -331,7 +331,7 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
 #pragma unroll
                     for (int a = 0; a < DIM; ++a) ov[j][a] = to_acc<float>(o[(size_t)a * g.Pn]);
                 }
-                mv[j] = mask_at<float, T>(g, mask, tile.b, tile.mgu, t, p);
+                mv[j] = mask_raw<float, T>(g, mask, tile.b, tile.mgu, t, p);
             }
         }
 #pragma unroll
@@ -390,6 +390,15 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
                 r[3] = __int_as_float(cell);
             }
             geo[tl * BPX + i] = r;
+        }
+    }
+    // mask logits (mask_scale > 0): the thread activates the masks of its own records in a
+    // separate pass, so that the loops above keep their code when masks are plain values
+    if (mask != nullptr && g.mask_scale > 0.0) {
+        for (int e = tid; e < n; e += nthreads) {
+            if (tile.pixel(g, wt, e % BPX) < 0) continue;   // outside the grid: mask 0
+            float *m = reinterpret_cast<float *>(geo + e) + (DIM == 3 ? 3 : DIM);
+            *m = mask_activate<float>(g, *m);
         }
     }
 }

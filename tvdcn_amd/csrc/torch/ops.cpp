@@ -21,6 +21,7 @@
 #include <torch/autograd.h>
 #include <torch/library.h>
 
+#include <cmath>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -268,6 +269,15 @@ Tensor aligned(const Tensor &t) {
     return t.clone(at::MemoryFormat::Preserve);   // keeps a channels-last input channels-last
 }
 
+// mask_scale > 0: the mask holds logits, activated as mask_scale * sigmoid in the kernels
+void set_mask_sigmoid(Problem &pr, double mask_scale) {
+    if (mask_scale == 0.0) return;
+    TORCH_CHECK(mask_scale > 0.0 && std::isfinite(mask_scale), "mask_scale must be a positive finite number");
+    TORCH_CHECK(pr.mask.defined(), "a sigmoid mask needs a mask tensor");
+    pr.desc.flags |= TVDCN_FLAG_MASK_SIGMOID;
+    pr.desc.mask_scale = mask_scale;
+}
+
 hipStream_t current_stream(const Tensor &t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
 
 // ---------------------------------------------------------------------------
@@ -276,12 +286,13 @@ hipStream_t current_stream(const Tensor &t) { return c10::hip::getCurrentHIPStre
 Tensor forward_hip(int dim, bool transposed, const Tensor &input, const Tensor &weight,
                    const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
                    at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding,
-                   at::IntArrayRef dilation, int64_t groups, const char *name) {
+                   at::IntArrayRef dilation, int64_t groups, const char *name, double mask_scale = 0.0) {
     TORCH_CHECK(input.is_cuda(), name, ": expected a GPU (HIP) tensor");
     c10::DeviceGuard guard(input.device());
     Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
                               dilation, groups, name);
     pr.desc.dtype = dtype_code(pr.input.scalar_type());
+    set_mask_sigmoid(pr, mask_scale);
     Tensor output = at::empty(out_shape(pr), pr.input.options());
     if (output.numel() > 0) {
         const size_t ws_bytes = tvdcn_deform_conv_forward_workspace_size(&pr.desc);
@@ -304,12 +315,13 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_hip(
     int dim, bool transposed, const Tensor &grad, const Tensor &input, const Tensor &weight,
     const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
     at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding, at::IntArrayRef dilation,
-    int64_t groups, const char *name) {
+    int64_t groups, const char *name, double mask_scale = 0.0) {
     TORCH_CHECK(input.is_cuda(), name, ": expected a GPU (HIP) tensor");
     c10::DeviceGuard guard(input.device());
     Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
                               dilation, groups, name);
     pr.desc.dtype = dtype_code(pr.input.scalar_type());
+    set_mask_sigmoid(pr, mask_scale);
     Tensor g = grad.contiguous();
     if (pr.unbatched) g = g.unsqueeze(0);
     TORCH_CHECK(g.sizes() == at::IntArrayRef(out_shape(pr)), name, ": grad has shape ", g.sizes(), ", expected ",
@@ -704,6 +716,164 @@ class MaskSoftmaxFunction : public torch::autograd::Function<MaskSoftmaxFunction
 
 Tensor mask_softmax_autograd(const Tensor &x, int64_t K) { return MaskSoftmaxFunction::apply(x, K); }
 
+// ---------------------------------------------------------------------------
+// deform_conv_sigmoid_mask: conv / transposed conv (rank from len(stride)) whose mask
+// tensor holds logits, activated as mask_scale * sigmoid in the kernels' mask load; the
+// backward's mask gradient is with respect to the logits. Used by the packed modules for
+// their default mask activation (MaskSigmoid); no counterpart op in the reference.
+// ---------------------------------------------------------------------------
+int sig_dim(at::IntArrayRef stride) {
+    TORCH_CHECK(stride.size() >= 1 && stride.size() <= 3, "deform_conv_sigmoid_mask: stride must have 1 to 3 ",
+                "elements (one per spatial axis)");
+    return (int)stride.size();
+}
+
+Tensor sig_fwd_hip(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+                   const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                   at::IntArrayRef d, int64_t g, bool tr, double scale) {
+    TORCH_CHECK(scale > 0.0, "mask_scale must be a positive finite number");
+    return forward_hip(sig_dim(s), tr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, "deform_conv_sigmoid_mask",
+                       scale);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> sig_bwd_hip(const Tensor &gr, const Tensor &i, const Tensor &w,
+                                                               const optional<Tensor> &o, const Tensor &m,
+                                                               const optional<Tensor> &b, at::IntArrayRef s,
+                                                               at::IntArrayRef p, at::IntArrayRef op,
+                                                               at::IntArrayRef d, int64_t g, bool tr, double scale) {
+    TORCH_CHECK(scale > 0.0, "mask_scale must be a positive finite number");
+    return backward_hip(sig_dim(s), tr, gr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g,
+                        "deform_conv_sigmoid_mask", scale);
+}
+
+Tensor sig_fwd_meta(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+                    const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                    at::IntArrayRef d, int64_t g, bool tr, double scale) {
+    TORCH_CHECK(scale > 0.0, "mask_scale must be a positive finite number");
+    return forward_meta(sig_dim(s), tr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, "deform_conv_sigmoid_mask");
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> sig_bwd_meta(const Tensor &gr, const Tensor &i, const Tensor &w,
+                                                                const optional<Tensor> &o, const Tensor &m,
+                                                                const optional<Tensor> &b, at::IntArrayRef s,
+                                                                at::IntArrayRef p, at::IntArrayRef op,
+                                                                at::IntArrayRef d, int64_t g, bool tr, double scale) {
+    TORCH_CHECK(scale > 0.0, "mask_scale must be a positive finite number");
+    return backward_meta(sig_dim(s), tr, gr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g,
+                         "deform_conv_sigmoid_mask");
+}
+
+using SigFwdSig = Tensor(const Tensor &, const Tensor &, const optional<Tensor> &, const Tensor &,
+                         const optional<Tensor> &, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef,
+                         int64_t, bool, double);
+using SigBwdSig = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor>(
+    const Tensor &, const Tensor &, const Tensor &, const optional<Tensor> &, const Tensor &, const optional<Tensor> &,
+    at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t, bool, double);
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> sig_call_backward(
+    const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+    const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op, at::IntArrayRef d, int64_t g,
+    bool tr, double scale) {
+    static auto bop = c10::Dispatcher::singleton()
+                          .findSchemaOrThrow("tvdcn_amd::_deform_conv_sigmoid_mask_backward", "")
+                          .typed<SigBwdSig>();
+    return bop.call(gr, i, w, o, m, b, s, p, op, d, g, tr, scale);
+}
+
+class SigmoidMaskFunction : public torch::autograd::Function<SigmoidMaskFunction> {
+   public:
+    static torch::autograd::Variable forward(torch::autograd::AutogradContext *ctx, const Tensor &input,
+                                             const Tensor &weight, const optional<Tensor> &offset,
+                                             const Tensor &mask, const optional<Tensor> &bias, at::IntArrayRef stride,
+                                             at::IntArrayRef padding, at::IntArrayRef out_pad,
+                                             at::IntArrayRef dilation, int64_t groups, bool transposed,
+                                             double scale) {
+        at::AutoDispatchBelowADInplaceOrView guard;
+        static auto fop = c10::Dispatcher::singleton()
+                              .findSchemaOrThrow("tvdcn_amd::deform_conv_sigmoid_mask", "")
+                              .typed<SigFwdSig>();
+        Tensor output =
+            fop.call(input, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups, transposed, scale);
+        ctx->save_for_backward({input, weight, offset.value_or(Tensor()), mask, bias.value_or(Tensor())});
+        ctx->saved_data["stride"] = stride.vec();
+        ctx->saved_data["padding"] = padding.vec();
+        ctx->saved_data["output_padding"] = out_pad.vec();
+        ctx->saved_data["dilation"] = dilation.vec();
+        ctx->saved_data["groups"] = groups;
+        ctx->saved_data["transposed"] = transposed;
+        ctx->saved_data["scale"] = scale;
+        return output;
+    }
+
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext *ctx,
+                                                   const torch::autograd::variable_list &grad_output) {
+        auto saved = ctx->get_saved_variables();
+        auto grads = sig_call_backward(
+            grad_output[0], saved[0], saved[1], opt(saved[2]), saved[3], opt(saved[4]),
+            ctx->saved_data["stride"].toIntVector(), ctx->saved_data["padding"].toIntVector(),
+            ctx->saved_data["output_padding"].toIntVector(), ctx->saved_data["dilation"].toIntVector(),
+            ctx->saved_data["groups"].toInt(), ctx->saved_data["transposed"].toBool(),
+            ctx->saved_data["scale"].toDouble());
+        return {std::get<0>(grads), std::get<1>(grads), std::get<2>(grads), std::get<3>(grads), std::get<4>(grads),
+                Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+class SigmoidMaskBackwardFunction : public torch::autograd::Function<SigmoidMaskBackwardFunction> {
+   public:
+    static torch::autograd::variable_list forward(torch::autograd::AutogradContext *, const Tensor &grad,
+                                                  const Tensor &input, const Tensor &weight,
+                                                  const optional<Tensor> &offset, const Tensor &mask,
+                                                  const optional<Tensor> &bias, at::IntArrayRef stride,
+                                                  at::IntArrayRef padding, at::IntArrayRef out_pad,
+                                                  at::IntArrayRef dilation, int64_t groups, bool transposed,
+                                                  double scale) {
+        at::AutoDispatchBelowADInplaceOrView guard;
+        auto r = sig_call_backward(grad, input, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups,
+                                   transposed, scale);
+        auto ph = [&](const Tensor &t) { return t.defined() ? t : at::empty({0}, input.options()); };
+        return {std::get<0>(r), std::get<1>(r), ph(std::get<2>(r)), std::get<3>(r), ph(std::get<4>(r))};
+    }
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext *,
+                                                   const torch::autograd::variable_list &) {
+        TORCH_CHECK(false, "double backwards on deform_conv_sigmoid_mask not supported");
+        return {};
+    }
+};
+
+Tensor sig_fwd_autograd(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+                        const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                        at::IntArrayRef d, int64_t g, bool tr, double scale) {
+    return SigmoidMaskFunction::apply(i, w, o, m, b, s, p, op, d, g, tr, scale);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> sig_bwd_autograd(const Tensor &gr, const Tensor &i,
+                                                                    const Tensor &w, const optional<Tensor> &o,
+                                                                    const Tensor &m, const optional<Tensor> &b,
+                                                                    at::IntArrayRef s, at::IntArrayRef p,
+                                                                    at::IntArrayRef op, at::IntArrayRef d, int64_t g,
+                                                                    bool tr, double scale) {
+    auto r = SigmoidMaskBackwardFunction::apply(gr, i, w, o, m, b, s, p, op, d, g, tr, scale);
+    const bool has_off = o.has_value() && o->defined();
+    const bool has_bias = b.has_value() && b->defined();
+    return {r[0], r[1], has_off ? r[2] : Tensor(), r[3], has_bias ? r[4] : Tensor()};
+}
+
+Tensor sig_fwd_autocast(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+                        const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                        at::IntArrayRef d, int64_t g, bool tr, double scale) {
+    c10::impl::ExcludeDispatchKeyGuard no_autocast(c10::DispatchKey::Autocast);
+    auto f32 = [](const Tensor &t) { return at::autocast::cached_cast(at::kFloat, t, c10::DeviceType::CUDA); };
+    auto f32o = [&](const optional<Tensor> &t) -> optional<Tensor> {
+        if (!t.has_value() || !t->defined()) return t;
+        return f32(*t);
+    };
+    static auto fop = c10::Dispatcher::singleton()
+                          .findSchemaOrThrow("tvdcn_amd::deform_conv_sigmoid_mask", "")
+                          .typed<SigFwdSig>();
+    return fop.call(f32(i), f32(w), f32o(o), f32(m), f32o(b), s, p, op, d, g, tr, scale).to(i.scalar_type());
+}
+
 int64_t hip_version() { return tvdcn_hip_version(); }
 std::string arch_flags() { return tvdcn_arch_flags(); }
 
@@ -742,6 +912,13 @@ TORCH_LIBRARY(tvdcn_amd, m) {
     m.def(TVDCN_TR_BWD_SCHEMA(2));
     m.def(TVDCN_TR_SCHEMA(3));
     m.def(TVDCN_TR_BWD_SCHEMA(3));
+    m.def("deform_conv_sigmoid_mask(Tensor input, Tensor weight, Tensor? offset, Tensor mask, Tensor? bias, "
+          "SymInt[] stride, SymInt[] padding, SymInt[] output_padding, SymInt[] dilation, SymInt groups, "
+          "bool transposed, float mask_scale) -> Tensor");
+    m.def("_deform_conv_sigmoid_mask_backward(Tensor grad, Tensor input, Tensor weight, Tensor? offset, "
+          "Tensor mask, Tensor? bias, SymInt[] stride, SymInt[] padding, SymInt[] output_padding, "
+          "SymInt[] dilation, SymInt groups, bool transposed, float mask_scale) "
+          "-> (Tensor, Tensor, Tensor, Tensor, Tensor)");
     m.def("mask_softmax(Tensor mask, int kernel_numel) -> Tensor");
     m.def("_mask_softmax_backward(Tensor grad, Tensor output, int kernel_numel) -> Tensor");
     m.def("_cuda_version", &tvdcn_amd::hip_version);
@@ -767,6 +944,8 @@ TORCH_LIBRARY_IMPL(tvdcn_amd, CUDA, m) {
     TVDCN_IMPL_CONV(1, fwd_hip, bwd_hip)
     TVDCN_IMPL_CONV(2, fwd_hip, bwd_hip)
     TVDCN_IMPL_CONV(3, fwd_hip, bwd_hip)
+    m.impl("deform_conv_sigmoid_mask", TORCH_FN(tvdcn_amd::sig_fwd_hip));
+    m.impl("_deform_conv_sigmoid_mask_backward", TORCH_FN(tvdcn_amd::sig_bwd_hip));
     m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_hip));
     m.impl("_mask_softmax_backward", TORCH_FN(tvdcn_amd::mask_softmax_backward_hip));
 }
@@ -775,6 +954,8 @@ TORCH_LIBRARY_IMPL(tvdcn_amd, Meta, m) {
     TVDCN_IMPL_CONV(1, fwd_meta, bwd_meta)
     TVDCN_IMPL_CONV(2, fwd_meta, bwd_meta)
     TVDCN_IMPL_CONV(3, fwd_meta, bwd_meta)
+    m.impl("deform_conv_sigmoid_mask", TORCH_FN(tvdcn_amd::sig_fwd_meta));
+    m.impl("_deform_conv_sigmoid_mask_backward", TORCH_FN(tvdcn_amd::sig_bwd_meta));
     m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_meta));
     m.impl("_mask_softmax_backward", TORCH_FN(tvdcn_amd::mask_softmax_backward_meta));
 }
@@ -783,6 +964,8 @@ TORCH_LIBRARY_IMPL(tvdcn_amd, Autograd, m) {
     TVDCN_IMPL_CONV(1, fwd_ag, bwd_ag)
     TVDCN_IMPL_CONV(2, fwd_ag, bwd_ag)
     TVDCN_IMPL_CONV(3, fwd_ag, bwd_ag)
+    m.impl("deform_conv_sigmoid_mask", TORCH_FN(tvdcn_amd::sig_fwd_autograd));
+    m.impl("_deform_conv_sigmoid_mask_backward", TORCH_FN(tvdcn_amd::sig_bwd_autograd));
     m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_autograd));
 }
 
@@ -793,4 +976,5 @@ TORCH_LIBRARY_IMPL(tvdcn_amd, Autocast, m) {
     m.impl("deform_conv_transpose1d", TORCH_FN(tvdcn_amd::Tr1::fwd_ac_t));
     m.impl("deform_conv_transpose2d", TORCH_FN(tvdcn_amd::Tr2::fwd_ac_t));
     m.impl("deform_conv_transpose3d", TORCH_FN(tvdcn_amd::Tr3::fwd_ac_t));
+    m.impl("deform_conv_sigmoid_mask", TORCH_FN(tvdcn_amd::sig_fwd_autocast));
 }

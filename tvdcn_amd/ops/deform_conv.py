@@ -77,6 +77,19 @@ def deform_conv3d(input: Tensor, weight: Tensor, offset: Optional[Tensor] = None
 _FUNCTIONAL = {1: deform_conv1d, 2: deform_conv2d, 3: deform_conv3d}
 
 
+def _deform_conv_sigmoid_mask(dim: int, input: Tensor, weight: Tensor, offset: Optional[Tensor], mask_logits: Tensor,
+                              bias: Optional[Tensor], stride, padding, output_padding, dilation, groups: int,
+                              transposed: bool, mask_scale: float) -> Tensor:
+    """Deformable (transposed) convolution whose mask is ``mask_scale * sigmoid(mask_logits)``, the
+    activation applied in the kernels' mask load (the packed modules' default ``MaskSigmoid``,
+    tvdcn/ops/deform_conv.py:502-505, without its separate passes). Gradients flow to the logits."""
+    _assert_has_ops()
+    nt = _NTUPLE[dim]
+    return torch.ops.tvdcn_amd.deform_conv_sigmoid_mask(input, weight, offset, mask_logits, bias, nt(stride),
+                                                        nt(padding), nt(output_padding), nt(dilation), groups,
+                                                        transposed, float(mask_scale))
+
+
 class _DeformConvNd(_ConvNd):
     """Base of the deformable convolution modules (tvdcn/ops/deform_conv.py:206-265)."""
 
@@ -131,7 +144,15 @@ class _DeformConvDim(_DeformConvNd):
                          groups, bias, padding_mode, device=device, dtype=dtype)
 
     def _conv_forward(self, input: Tensor, weight: Tensor, offset: Optional[Tensor], mask: Optional[Tensor],
-                      bias: Optional[Tensor]) -> Tensor:
+                      bias: Optional[Tensor], mask_sigmoid_scale: Optional[float] = None) -> Tensor:
+        if mask_sigmoid_scale is not None:
+            # mask holds logits: the sigmoid runs inside the kernels
+            padding = self.padding
+            if self.padding_mode != "zeros":
+                input = F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode)
+                padding = (0,) * self._dim
+            return _deform_conv_sigmoid_mask(self._dim, input, weight, offset, mask, bias, self.stride, padding,
+                                             (0,) * self._dim, self.dilation, self.groups, False, mask_sigmoid_scale)
         fn = _FUNCTIONAL[self._dim]
         if self.padding_mode != "zeros":
             # non-zero padding modes: pad explicitly, then convolve without padding
@@ -232,16 +253,21 @@ class _PackedMixin:
                     init.zeros_(gen.bias)
 
     def _generate(self, input: Tensor):
-        offset = mask = None
+        """offset, mask and the mask's sigmoid scale: a ``MaskSigmoid`` activation (the default) is
+        left to the kernels, which apply it in their mask load — the mask is then returned as
+        logits with the scale; any other activation is applied here (scale None)."""
+        offset = mask = scale = None
         if self.deformable and self.offset_generator is not None:
             offset = self.offset_generator(input)
             if self.offset_activation is not None:
                 offset = self.offset_activation(offset)
         if self.modulated and self.mask_generator is not None:
             mask = self.mask_generator(input)
-            if self.mask_activation is not None:
+            if type(self.mask_activation) is MaskSigmoid:
+                scale = self.mask_activation.scale
+            elif self.mask_activation is not None:
                 mask = self.mask_activation(mask)
-        return offset, mask
+        return offset, mask, scale
 
 
 def _make_packed(base, dim: int, doc: str):
@@ -269,8 +295,8 @@ def _make_packed(base, dim: int, doc: str):
             self._reset_generators()
 
         def forward(self, input: Tensor) -> Tensor:
-            offset, mask = self._generate(input)
-            return self._conv_forward(input, self.weight, offset, mask, self.bias)
+            offset, mask, scale = self._generate(input)
+            return self._conv_forward(input, self.weight, offset, mask, self.bias, mask_sigmoid_scale=scale)
 
     return _Packed
 

@@ -14,7 +14,7 @@ from torch import Tensor
 from torch.nn.common_types import _size_1_t, _size_2_t, _size_3_t, _size_any_t
 from torch.nn.modules.utils import _pair, _single, _triple
 
-from .deform_conv import _DeformConvNd, _PackedMixin
+from .deform_conv import _DeformConvNd, _PackedMixin, _deform_conv_sigmoid_mask
 from ..extension import _assert_has_ops
 from ..utils import _log_api_usage_once
 
@@ -129,11 +129,17 @@ class _DeformConvTransposeDim(_DeformConvTransposeNd):
 
     def _conv_transpose_forward(self, input: Tensor, weight: Tensor, offset: Optional[Tensor],
                                 mask: Optional[Tensor], bias: Optional[Tensor],
-                                output_size: Optional[List[int]] = None) -> Tensor:
+                                output_size: Optional[List[int]] = None,
+                                mask_sigmoid_scale: Optional[float] = None) -> Tensor:
         if self.padding_mode != "zeros":
             raise ValueError(f"Only `zeros` padding mode is supported for {type(self).__name__}.")
         output_padding = self._output_padding(input, output_size, list(self.stride), list(self.padding),
                                               list(self.kernel_size), self._dim, list(self.dilation))
+        if mask_sigmoid_scale is not None:
+            # mask holds logits: the sigmoid runs inside the kernels
+            return _deform_conv_sigmoid_mask(self._dim, input, weight, offset, mask, bias, self.stride, self.padding,
+                                             tuple(output_padding), self.dilation, self.groups, True,
+                                             mask_sigmoid_scale)
         return _FUNCTIONAL[self._dim](input, weight, offset, mask, bias, self.stride, self.padding,
                                       tuple(output_padding), self.dilation, self.groups)
 
@@ -194,8 +200,9 @@ def _make_packed(base, dim: int, doc: str):
             self._reset_generators()
 
         def forward(self, input: Tensor, output_size: Optional[List[int]] = None) -> Tensor:
-            offset, mask = self._generate(input)
-            return self._conv_transpose_forward(input, self.weight, offset, mask, self.bias, output_size)
+            offset, mask, scale = self._generate(input)
+            return self._conv_transpose_forward(input, self.weight, offset, mask, self.bias, output_size,
+                                                mask_sigmoid_scale=scale)
 
     return _Packed
 
