@@ -157,3 +157,15 @@ def test_channels_last_input(dim, dtype):
     for n, t, r in zip(names, ts, grads):
         e = rel_err(t.grad, r)
         assert e < tol, f"grad_{n} rel err {e}"
+
+
+@pytest.mark.parametrize("dim,transposed,cin,cout,k,size", [
+    (1, False, 32, 256, 5, [300]), (2, False, 32, 160, 2, [20, 18]), (1, True, 256, 32, 3, [150]),
+    (2, False, 48, 144, 2, [9, 33])])
+def test_weight_gradient_short_passes_fp32(dim, transposed, cin, cout, k, size):
+    """Passes of at most 5 taps on GEMM sides above 128 rows take the weight gradient's
+    (5 tap slots, 64-pixel chunk) shape; ragged tiles and GEMM sides that are not multiples of
+    256 rows included."""
+    case = make_case(dim, transposed, batch=2, cin=cin, cout=cout, kernel=[k] * dim, stride=[1] * dim,
+                     padding=[1] * dim, dilation=[1] * dim, in_size=size, out_pad=[0] * dim, seed=570 + dim)
+    check(case, torch.float32)

@@ -34,21 +34,37 @@ constexpr int NT = 64 * NW;
 // so that a GEMM side of 64 rows still keeps all eight waves on MFMAs:
 //   MB = 2, TG = 1: 256 rows per workgroup;  MB = 1, TG = 2: 64 rows, taps split by parity.
 template <int MB, int TG> constexpr int rows_of() { return (NW / TG) * MB * 16; }
-constexpr int KP = 32;              // pixels per chunk (two 16-pixel halves per MFMA K block)
-constexpr int NCH = BPX / KP;       // chunks per tile
-constexpr int NH = KP / 16;         // 16-pixel MFMA K blocks per chunk
-constexpr int SS = KP + 4;          // S tile row stride (rows = (tap, channel))
-constexpr int TM = WIN_TMAX;
-
-constexpr int GEO_WORDS = TM * BPX * 4;
-constexpr int SBUF_WORDS = 2 * TM * BC * SS;
+// Tap slots and chunk size: TM tap slots per pass held in accumulators, KP pixels per chunk.
+// Passes of up to 9 taps take (9, 32); passes of up to 5 taps (1D k <= 5, 2D k = 2) take
+// (5, 64): the registers the unused tap slots would hold carry a chunk twice as long, so each
+// barrier and operand load serves twice the MFMAs.
+template <int TMV, int KPV> struct WShape {
+    static constexpr int TM = TMV;
+    static constexpr int KP = KPV;          // pixels per chunk (16-pixel MFMA K blocks)
+    static constexpr int NCH = BPX / KP;    // chunks per tile
+    static constexpr int NH = KP / 16;      // 16-pixel MFMA K blocks per chunk
+    static constexpr int SS = KP + 4;       // S tile row stride (rows = (tap, channel))
+    static constexpr int GEO_WORDS = TM * BPX * 4;
+    static constexpr int SBUF_WORDS = 2 * TM * BC * SS;
+};
+constexpr int SMALL_TM = 5;
+// the (5, 64) shape serves 256-row tiles (GEMM sides above 128 rows); 64-row tiles split the
+// taps between two wave groups and keep (9, 32)
+bool small_shape(const Geo &g, int tpp) { return tpp <= SMALL_TM && g.Mg > 128; }
+size_t fixed_words(const Geo &g, int tpp) {
+    return small_shape(g, tpp) ? WShape<SMALL_TM, 64>::GEO_WORDS + WShape<SMALL_TM, 64>::SBUF_WORDS
+                               : WShape<WIN_TMAX, 32>::GEO_WORDS + WShape<WIN_TMAX, 32>::SBUF_WORDS;
+}
 
 // FULL: every pass uses all TM tap slots (no per-tap guards)
-template <int DIM, typename T, bool FULL, int MB, int TG>
+template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
 __global__ void __launch_bounds__(NT)
 bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const T *__restrict__ z,
                       const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
                       float *__restrict__ part) {
+    using SH = WShape<TMV, KPV>;
+    constexpr int TM = SH::TM, KP = SH::KP, NCH = SH::NCH, NH = SH::NH, SS = SH::SS;
+    constexpr int GEO_WORDS = SH::GEO_WORDS, SBUF_WORDS = SH::SBUF_WORDS;
     constexpr int NC = 1 << DIM;
     constexpr int BMW = rows_of<MB, TG>();
     extern __shared__ float smem[];
@@ -78,9 +94,9 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
         if (tid < XS) xwin[wt.cells * XS + tid] = 0.f;   // zero cell of the 3D corner reads
     }
 
-    // S-builder item of this thread: chunk pixel j, channel quad sq, taps st, st + 4, ...
-    // (3D: chunk pixel j, taps tid / 32, + 16, ..., all 16 channels)
-    const int sj = tid & 31, sq = (tid >> 5) & 3, st0 = tid >> 7;
+    // S-builder item of this thread: chunk pixel j, channel quad sq, taps st, st + SSTEP, ...
+    // (3D: chunk pixel j, taps tid / KP, + NT / KP, ..., all 16 channels)
+    const int sj = tid % KP, sq = (tid / KP) & 3, st0 = tid / (KP * 4);
     constexpr int SSTEP = NT / (KP * 4);   // tap stride of the items
 
     for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
@@ -110,7 +126,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                     // 3D: one item per (chunk pixel, tap) for all 16 channels (the corner geometry
                     // formed once per sample rather than once per channel quad)
                     const int nq = min(4, (g.Cg - tile.c0) >> 2);
-                    for (int tl = tid >> 5; tl < ntaps; tl += NT / KP) {
+                    for (int tl = tid / KP; tl < ntaps; tl += NT / KP) {
                         const acc4 r = geo[tl * BPX + i];
                         acc4 sv[4];
                         if (nq == 4)
@@ -272,11 +288,14 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     }
 }
 
-template <int DIM, typename T, bool FULL, int MB, int TG>
+template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, hipStream_t s) {
-    auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG>;
-    const size_t lds = ((size_t)GEO_WORDS + SBUF_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
+    using SH = WShape<TMV, KPV>;
+    if (wt.tpp > TMV) return hipErrorInvalidValue;   // a pass must fit the tap slots
+    auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG, TMV, KPV>;
+    const size_t lds =
+        ((size_t)SH::GEO_WORDS + SH::SBUF_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
     static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -294,13 +313,18 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, hipStream_t s) {
-    const bool full = wt.tpp == TM && g.Kn % TM == 0;
+    const bool small = small_shape(g, wt.tpp);
+    const int tm = small ? SMALL_TM : WIN_TMAX;
+    const bool full = wt.tpp == tm && g.Kn % tm == 0;
     auto pick = [&](auto dim_tag) -> hipError_t {
         constexpr int D = decltype(dim_tag)::value;
-        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2>(g, wt, ww, z, xcl, offset, mask, part, s)
-                                    : launch_k<D, T, false, 1, 2>(g, wt, ww, z, xcl, offset, mask, part, s);
-        return full ? launch_k<D, T, true, 2, 1>(g, wt, ww, z, xcl, offset, mask, part, s)
-                    : launch_k<D, T, false, 2, 1>(g, wt, ww, z, xcl, offset, mask, part, s);
+        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, s)
+                                    : launch_k<D, T, false, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, s);
+        if (small)
+            return full ? launch_k<D, T, true, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, s)
+                        : launch_k<D, T, false, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, s);
+        return full ? launch_k<D, T, true, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, s)
+                    : launch_k<D, T, false, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, s);
     };
     switch (dim) {
         case 1: return pick(std::integral_constant<int, 1>());
@@ -312,14 +336,16 @@ hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &
 
 }  // namespace
 
-size_t weight_win_fixed_bytes(int dim) { return (size_t)(GEO_WORDS + SBUF_WORDS + (dim == 3 ? XS : 0)) * sizeof(float); }
+size_t weight_win_fixed_bytes(const Geo &g, int dim, int tpp) {
+    return (fixed_words(g, tpp) + (dim == 3 ? XS : 0)) * sizeof(float);
+}
 
 WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     WeightWin w{};
     w.ok = false;
     // needs the windowed tiling; GEMM sides up to 128 rows take 64-row tiles with the taps
     // split between two wave groups, larger ones 256-row tiles
-    if (!wt.ok || g.Mg < 16 || weight_win_fixed_bytes(dim) + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
+    if (!wt.ok || g.Mg < 16 || weight_win_fixed_bytes(g, dim, wt.tpp) + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
         return w;
     w.tg = g.Mg <= 128 ? 2 : 1;
     const int rows = w.tg == 2 ? rows_of<1, 2>() : rows_of<2, 1>();

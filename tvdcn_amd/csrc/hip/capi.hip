@@ -168,7 +168,7 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     // grad-columns contraction but each gets about twice the window
     pl.data_split = pl.wn_s.ok && pl.wn_s.R[2] < 2 && pl.wn_x.R[2] > pl.wn_s.R[2] && pl.wn_c.R[2] > pl.wn_s.R[2];
     pl.wt = plan_weight(g, pl.dtype);
-    pl.wn_w = win_resize(pl.wn_s, g, pl.dim, weight_win_fixed_bytes(pl.dim), x_window_cell_bytes());
+    pl.wn_w = win_resize(pl.wn_s, g, pl.dim, weight_win_fixed_bytes(g, pl.dim, pl.wn_s.tpp), x_window_cell_bytes());
     pl.ww = plan_weight_win(g, pl.wn_w, pl.dim);
     pl.fw = plan_fwd_win(g, pl.wn_s, pl.dim, pl.wn_f);
     return TVDCN_STATUS_SUCCESS;

@@ -81,7 +81,8 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
 // (cell_cap > 0: at most that many window cells)
 WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_bytes, size_t cell_bytes,
                     long long cell_cap = 0);
-size_t weight_win_fixed_bytes(int dim);   // LDS of the windowed weight gradient besides its X window
+// LDS of the windowed weight gradient besides its X window (its shape follows the pass length)
+size_t weight_win_fixed_bytes(const Geo &g, int dim, int tpp);
 size_t x_window_cell_bytes();
 DataTiles plan_data(const Geo &g, int dtype);
 WeightTiles plan_weight(const Geo &g, int dtype);
