@@ -185,19 +185,54 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     //      once, at the end (or before a pass whose bound is not finite): one float atomic
     //      per non-zero (cell, channel), 16 consecutive channels per cell
     bool win_data = false;   // the window holds accumulated values (uniform)
-    auto flush_window = [&]() {
+    // thread = (channel tid % 16, cells tid / 16, + 32, ...); FB cells' values are read before
+    // any is used (one LDS latency per batch). keep: the window is used again (cleared as
+    // read, barrier at the end); at the end of the workgroup neither is needed.
+    auto flush_window = [&](bool keep) {
+        constexpr int FB = 8;
+        constexpr int STEP = NT / 16;
         const int c = tid & 15;
         const int se = scl[c];
         const bool c_ok = c0 + c < g.Cg;
         float *gbase = gx_cl + (size_t)b * g.Sn * g.C + cg0 + c;
-        for_cells(g, wt, tile, tid >> 4, NT / 16, [&](int cell, int si) {
-            const int iv = iwin[c * cst + cell];
-            if (iv == 0) return;
-            iwin[c * cst + cell] = 0;   // cleared for what follows
-            // window cells outside the grid hold only contributions of corners outside it
-            if (si >= 0 && c_ok) atomic_add(gbase + (size_t)si * g.C, ldexpf((float)iv, -se));
-        });
-        __syncthreads();
+        const int first = tid >> 4;
+        // cell walker (no divisions per cell), as in for_cells
+        int lx = first % wt.WE[2];
+        int rr = first / wt.WE[2];
+        int ly = rr % wt.WE[1];
+        int lz = rr / wt.WE[1];
+        const int sx_step = STEP % wt.WE[2], sy_step = (STEP / wt.WE[2]) % wt.WE[1],
+                  sz_step = STEP / (wt.WE[2] * wt.WE[1]);
+        for (int cell0 = first; cell0 < wt.cells; cell0 += FB * STEP) {
+            int iv[FB], si[FB];
+#pragma unroll
+            for (int j = 0; j < FB; ++j) {
+                const int cell = cell0 + j * STEP;
+                iv[j] = cell < wt.cells ? iwin[c * cst + cell] : 0;
+                const int sz = tile.org[0] + lz, sy = tile.org[1] + ly, sx = tile.org[2] + lx;
+                // window cells outside the grid hold only contributions of corners outside it
+                const bool in = sz >= 0 && sz < g.S[0] && sy >= 0 && sy < g.S[1] && sx >= 0 && sx < g.S[2];
+                si[j] = in && c_ok ? (sz * g.S[1] + sy) * g.S[2] + sx : -1;
+                lx += sx_step;
+                ly += sy_step;
+                lz += sz_step;
+                if (lx >= wt.WE[2]) {
+                    lx -= wt.WE[2];
+                    ++ly;
+                }
+                if (ly >= wt.WE[1]) {
+                    ly -= wt.WE[1];
+                    ++lz;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < FB; ++j) {
+                if (iv[j] == 0) continue;
+                if (keep) iwin[c * cst + cell0 + j * STEP] = 0;   // cleared for what follows
+                if (si[j] >= 0) atomic_add(gbase + (size_t)si[j] * g.C, ldexpf((float)iv[j], -se));
+            }
+        }
+        if (keep) __syncthreads();
     };
 
     for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
@@ -316,7 +351,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
             if (scl[BC] != 0) {
                 // not finite: what the window holds goes out at its scale, the pass goes to
                 // global float atomics (inf / nan propagate as in the reference)
-                if (win_data) flush_window();
+                if (win_data) flush_window(true);
                 win_data = false;
             } else {
                 if (win_data) {
@@ -565,7 +600,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 
         // ---- after the last pass, the window goes out
         if (SCATTER && win_data && t0 + wt.tpp >= g.Kn) {
-            flush_window();
+            flush_window(false);   // the workgroup's last use of the window
             win_data = false;
         }
     }
