@@ -417,3 +417,18 @@ def test_sigmoid_mask_op_on_meta():
     assert scale == 2.0 and logits.shape == (2, 9, 8, 8)
     s = tvdcn_amd.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True, mask_activation="softmax", device="meta")
     assert s._generate(meta(2, 4, 8, 8))[2] is None
+
+
+@pytest.mark.parametrize("dim,transposed", [(1, 0), (2, 0), (3, 0), (2, 1)])
+def test_c_abi_empty_batch_queries(lib, dim, transposed):
+    """Workspace queries of an empty batch (host planning only): GEMM sides of 16 rows and more
+    once divided by a zero split count."""
+    lib.tvdcn_deform_conv_forward_workspace_size.restype = ctypes.c_size_t
+    lib.tvdcn_deform_conv_backward_workspace_size.restype = ctypes.c_size_t
+    for ch in (4, 32, 256):
+        d = Desc(dim=dim, transposed=transposed, dtype=0, batch=0, in_channels=ch, out_channels=ch, groups=1,
+                 offset_groups=1, mask_groups=1)
+        for i in range(3):
+            d.in_size[i], d.kernel[i], d.stride[i], d.padding[i], d.dilation[i] = 7, 3, 1, 1, 1
+        assert lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(d)) > 0
+        assert lib.tvdcn_deform_conv_backward_workspace_size(ctypes.byref(d)) > 0

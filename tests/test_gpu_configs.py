@@ -199,6 +199,19 @@ def test_empty_batch(transposed):
     assert w.grad.abs().sum().item() == 0.0 and x.grad.shape == x.shape
 
 
+def test_empty_batch_wide_gemm_side():
+    """An empty batch whose GEMM side takes the windowed weight gradient (>= 16 rows): its split
+    count once divided by zero on the host."""
+    x = torch.zeros(0, 32, 6, 6, device=DEV, requires_grad=True)
+    w = torch.rand(32, 32, 3, 3, device=DEV, requires_grad=True)
+    o = torch.zeros(0, 18, 4, 4, device=DEV, requires_grad=True)
+    m = torch.zeros(0, 9, 4, 4, device=DEV, requires_grad=True)
+    out = tvdcn_amd.deform_conv2d(x, w, o, m)
+    out.sum().backward()
+    torch.cuda.synchronize()
+    assert out.shape == (0, 32, 4, 4) and w.grad.abs().sum().item() == 0.0
+
+
 def test_mask_softmax_cfg3_shape_and_half():
     g = torch.Generator().manual_seed(3)
     logits = torch.randn(16, 20, 4096, generator=g)

@@ -101,3 +101,32 @@ def test_packed_module_default_sigmoid_is_fused(transposed):
     for (name, p), a in zip(m.named_parameters(), fused):
         e = rel_err(a, p.grad)
         assert e < 1e-4, f"{name} grad rel err {e}"
+
+
+def test_fused_sigmoid_mask_without_offsets_and_empty_batch():
+    """Offset-free sampling with a logit mask, and an empty batch (zero gradients)."""
+    case = make_case(2, False, batch=2, cin=32, cout=32, kernel=[3, 3], stride=[1, 1], padding=[1, 1],
+                     dilation=[1, 1], in_size=[14, 12], out_pad=[0, 0], seed=640, deformable=False)
+    g = torch.Generator().manual_seed(641)
+    logits = torch.randn(case["mask"].shape, generator=g, dtype=torch.float64)
+    vals = [case["input"], case["weight"], None, logits, case["bias"]]
+    ref = [None if v is None else v.to(DEV, torch.float32).requires_grad_(True) for v in vals]
+    fus = [None if v is None else v.to(DEV, torch.float32).requires_grad_(True) for v in vals]
+    y_ref = tvdcn_amd.deform_conv2d(ref[0], ref[1], None, 2.0 * torch.sigmoid(ref[3]), ref[4], padding=1)
+    gout = torch.randn(y_ref.shape, generator=g, dtype=torch.float64).to(DEV, torch.float32)
+    y_ref.backward(gout)
+    y = _deform_conv_sigmoid_mask(2, fus[0], fus[1], None, fus[3], fus[4], 1, 1, 0, 1, 1, False, 2.0)
+    y.backward(gout)
+    torch.cuda.synchronize()
+    assert rel_err(y, y_ref) < 1e-5
+    for a, r in zip(fus, ref):
+        if a is not None:
+            assert rel_err(a.grad, r.grad) < 1e-4
+    # empty batch
+    x = torch.zeros(0, 32, 14, 12, device=DEV, requires_grad=True)
+    w = fus[1].detach().clone().requires_grad_(True)
+    lg = torch.zeros(0, 9, 14, 12, device=DEV, requires_grad=True)
+    y0 = _deform_conv_sigmoid_mask(2, x, w, None, lg, None, 1, 1, 0, 1, 1, False, 2.0)
+    assert y0.shape == (0, 32, 14, 12)
+    y0.sum().backward()
+    assert w.grad is not None and float(w.grad.abs().sum()) == 0.0 and lg.grad.shape == lg.shape

@@ -356,7 +356,8 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     long long splits = (256 + per_split_groups - 1) / per_split_groups;
     if (splits > w.n_spatial) splits = w.n_spatial;
     if (splits < 1) splits = 1;
-    w.tiles_per_split = (int)((w.n_spatial + splits - 1) / splits);
+    // (at least one tile per split: an empty batch has no spatial tiles)
+    w.tiles_per_split = (int)std::max<long long>(1, (w.n_spatial + splits - 1) / splits);
     w.n_split = (w.n_spatial + w.tiles_per_split - 1) / w.tiles_per_split;
     w.z_vec = g.P[2] % 4 == 0 && wt.box[2] >= 4;
     w.part_elems = (size_t)w.n_split * g.G * g.Kn * g.Mg * g.Cg;
