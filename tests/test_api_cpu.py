@@ -432,3 +432,47 @@ def test_c_abi_empty_batch_queries(lib, dim, transposed):
             d.in_size[i], d.kernel[i], d.stride[i], d.padding[i], d.dilation[i] = 7, 3, 1, 1, 1
         assert lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(d)) > 0
         assert lib.tvdcn_deform_conv_backward_workspace_size(ctypes.byref(d)) > 0
+
+
+def test_c_abi_planning_fuzz(lib):
+    """Host planning over random valid descriptors (ranks, conv / transposed, strides, paddings,
+    dilations, groups, offset / mask groups, dtypes, flags, empty batches): every workspace
+    query returns without crashing, and a positive size exactly when the output size query
+    accepts the descriptor."""
+    import random
+    rnd = random.Random(2024)
+    lib.tvdcn_conv_output_size.restype = ctypes.c_int
+    lib.tvdcn_deform_conv_forward_workspace_size.restype = ctypes.c_size_t
+    lib.tvdcn_deform_conv_backward_workspace_size.restype = ctypes.c_size_t
+    out = (ctypes.c_int64 * 3)()
+    for _ in range(400):
+        dim = rnd.choice((1, 2, 3))
+        tr = rnd.random() < 0.4
+        groups = rnd.choice((1, 1, 2, 4))
+        cin = groups * rnd.choice((1, 2, 3, 4, 8, 12, 16, 20, 32, 48))
+        cout = groups * rnd.choice((1, 2, 3, 4, 8, 16, 24, 40, 64))
+        cols = cout if tr else cin
+        og = rnd.choice([g for g in (0, 1, 2, 4) if g == 0 or (cin % g == 0 and cols % g == 0)])
+        mg = rnd.choice([g for g in (0, 1, 2, 4) if g == 0 or (cin % g == 0 and cols % g == 0)])
+        flags = 0
+        if not tr and dim > 1 and rnd.random() < 0.2:
+            flags |= 1
+        if mg and rnd.random() < 0.2:
+            flags |= 2
+        d = Desc(dim=dim, transposed=int(tr), dtype=rnd.choice((0, 1, 2, 3)), flags=flags,
+                 batch=rnd.choice((0, 1, 2, 3)), in_channels=cin, out_channels=cout, groups=groups,
+                 offset_groups=og, mask_groups=mg, mask_scale=2.0)
+        for i in range(3):
+            d.in_size[i] = rnd.choice((1, 2, 5, 9, 17, 33)) if i < dim else 1
+            d.kernel[i] = rnd.choice((1, 2, 3, 4)) if i < dim else 1
+            d.stride[i] = rnd.choice((1, 1, 2, 3)) if i < dim else 1
+            d.padding[i] = rnd.choice((0, 1, 2)) if i < dim else 0
+            d.dilation[i] = rnd.choice((1, 1, 2)) if i < dim else 1
+            d.output_padding[i] = rnd.choice((0, 1)) if (tr and i < dim and d.stride[i] > 1) else 0
+        ok = lib.tvdcn_conv_output_size(ctypes.byref(d), out) == 0
+        fw = lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(d))
+        bw = lib.tvdcn_deform_conv_backward_workspace_size(ctypes.byref(d))
+        if not ok:
+            assert fw == 0 and bw == 0
+        else:
+            assert bw > 0
