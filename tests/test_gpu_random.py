@@ -1,0 +1,48 @@
+"""Seeded random problems against the float64 oracle (fp32 on the GPU): ranks 1-3, conv and
+transposed, groups, offset / mask groups, kernel sizes, strides, paddings, dilations, output
+paddings, channel counts on and off the 4- and 16-channel granularity of the windowed kernels,
+offset scales from sub-pixel to far beyond the LDS windows. Each case prints its parameters."""
+import random
+
+import pytest
+import torch
+
+from helpers import make_case
+from test_gpu_parity import check
+
+pytestmark = pytest.mark.gpu
+
+
+def random_case(seed):
+    rnd = random.Random(seed)
+    dim = rnd.choice((1, 2, 2, 3))
+    transposed = rnd.random() < 0.35
+    groups = rnd.choice((1, 1, 1, 2))
+    cin = groups * rnd.choice((2, 4, 8, 16, 20, 32))
+    cout = groups * rnd.choice((3, 4, 16, 24, 32, 48))
+    cols = cout if transposed else cin
+    divs = [g for g in (1, 2, 4) if cin % g == 0 and cols % g == 0]
+    og, mg = rnd.choice(divs), rnd.choice(divs)
+    kernel = [rnd.choice((1, 2, 3, 4)) for _ in range(dim)]
+    stride = [rnd.choice((1, 1, 2, 3)) for _ in range(dim)]
+    padding = [rnd.choice((0, 1, 2)) for _ in range(dim)]
+    dilation = [rnd.choice((1, 1, 2)) for _ in range(dim)]
+    out_pad = [rnd.randrange(0, max(s, d)) if transposed else 0 for s, d in zip(stride, dilation)]
+    hi = {1: 40, 2: 14, 3: 7}[dim]
+    in_size = []
+    for a in range(dim):
+        lo = 1 if transposed else max(1, dilation[a] * (kernel[a] - 1) + 1 - 2 * padding[a])
+        in_size.append(rnd.randint(lo, max(lo, hi)))
+    params = dict(batch=rnd.choice((1, 2)), cin=cin, cout=cout, groups=groups, og=og, mg=mg,
+                  deformable=rnd.random() < 0.85, modulated=rnd.random() < 0.7, bias=rnd.random() < 0.7,
+                  kernel=kernel, stride=stride, padding=padding, dilation=dilation, out_pad=out_pad,
+                  in_size=in_size, seed=seed, offset_scale=rnd.choice((0.5, 2.0, 6.0)))
+    return dim, transposed, params
+
+
+@pytest.mark.parametrize("seed", range(700, 764))
+def test_random_problem_fp32(seed):
+    dim, transposed, params = random_case(seed)
+    print(f"seed {seed}: dim {dim} transposed {transposed} {params}", flush=True)
+    case = make_case(dim, transposed, **params)
+    check(case, torch.float32)
