@@ -31,7 +31,11 @@ def random_case(seed):
     hi = {1: 40, 2: 14, 3: 7}[dim]
     in_size = []
     for a in range(dim):
-        lo = 1 if transposed else max(1, dilation[a] * (kernel[a] - 1) + 1 - 2 * padding[a])
+        span = dilation[a] * (kernel[a] - 1)
+        if transposed:   # (in - 1) * stride - 2 * padding + span + out_pad + 1 >= 1
+            lo = 1 + max(0, -(-(2 * padding[a] - span - out_pad[a]) // stride[a]))
+        else:            # in + 2 * padding >= span + 1
+            lo = max(1, span + 1 - 2 * padding[a])
         in_size.append(rnd.randint(lo, max(lo, hi)))
     params = dict(batch=rnd.choice((1, 2)), cin=cin, cout=cout, groups=groups, og=og, mg=mg,
                   deformable=rnd.random() < 0.85, modulated=rnd.random() < 0.7, bias=rnd.random() < 0.7,
@@ -46,3 +50,12 @@ def test_random_problem_fp32(seed):
     print(f"seed {seed}: dim {dim} transposed {transposed} {params}", flush=True)
     case = make_case(dim, transposed, **params)
     check(case, torch.float32)
+
+
+@pytest.mark.parametrize("seed", range(800, 816))
+def test_random_problem_half_and_double(seed):
+    dim, transposed, params = random_case(seed)
+    dtype = (torch.float16, torch.bfloat16, torch.float64)[seed % 3]
+    print(f"seed {seed}: {dtype} dim {dim} transposed {transposed} {params}", flush=True)
+    case = make_case(dim, transposed, **params)
+    check(case, dtype)
