@@ -7,8 +7,8 @@ import random
 import pytest
 import torch
 
-from helpers import make_case
-from test_gpu_parity import check
+from helpers import make_case, rel_err
+from test_gpu_parity import check, run_gpu, run_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -59,3 +59,38 @@ def test_random_problem_half_and_double(seed):
     print(f"seed {seed}: {dtype} dim {dim} transposed {transposed} {params}", flush=True)
     case = make_case(dim, transposed, **params)
     check(case, dtype)
+
+
+@pytest.mark.parametrize("seed", range(900, 912))
+def test_random_medium_problem_fp32(seed):
+    """Larger channel counts and grids (several channel slices and spatial tiles, multi-pass tap
+    sets, split forward grids) on the windowed kernels."""
+    rnd = random.Random(seed)
+    dim = rnd.choice((1, 2, 2, 3))
+    transposed = rnd.random() < 0.3
+    cin = rnd.choice((64, 96, 128))
+    cout = rnd.choice((64, 128, 144))
+    cols = cout if transposed else cin
+    og = rnd.choice([g for g in (1, 2, 4) if cin % g == 0 and cols % g == 0 and (cols // g) % 16 == 0])
+    mg = rnd.choice([g for g in (1, 2, 4) if cin % g == 0 and cols % g == 0 and (cols // g) % 16 == 0])
+    k = rnd.choice((2, 3, 4)) if dim < 3 else rnd.choice((2, 3))
+    stride = rnd.choice((1, 1, 2)) if not transposed else 2
+    size = {1: [rnd.randint(200, 600)], 2: [rnd.randint(16, 40), rnd.randint(16, 40)],
+            3: [rnd.randint(4, 9), rnd.randint(8, 16), rnd.randint(8, 16)]}[dim]
+    params = dict(batch=2, cin=cin, cout=cout, groups=1, og=og, mg=mg, kernel=[k] * dim, stride=[stride] * dim,
+                  padding=[k // 2] * dim, dilation=[1] * dim, out_pad=[1 if transposed else 0] * dim,
+                  in_size=size, seed=seed, offset_scale=rnd.choice((1.0, 3.0)))
+    print(f"seed {seed}: dim {dim} transposed {transposed} {params}", flush=True)
+    case = make_case(dim, transposed, **params)
+    # Sampling positions of up to ~700 (1D grids): a float32 position (integer base + offset,
+    # rounded once, as the reference's fp32 kernels compute it) is off by up to half an ulp,
+    # 3e-5 at 512..1024, which moves bilinear weights by that much against the float64 oracle.
+    # Structural mistakes show as errors of 1e-3 and more; the bound below leaves room for the
+    # rounding only.
+    out, grads, gout = run_gpu(case, torch.float32)
+    ref_out, ref_grads = run_oracle(case, gout, torch.float32)
+    assert rel_err(out, ref_out) < 1e-4, "forward"
+    for name, gr, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
+        if r is not None:
+            e = rel_err(gr, r)
+            assert e < 1e-3 if name == "offset" else e < 2e-4, f"grad_{name} rel err {e}"
