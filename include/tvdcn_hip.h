@@ -134,6 +134,22 @@ tvdcn_status tvdcn_mask_softmax_backward(int32_t dtype, int64_t batch, int64_t g
                                          int64_t spatial_numel, const void *y, const void *grad_y, void *grad_x,
                                          void *stream);
 
+/*
+ * Copies a float32 NC<spatial> tensor (batch x channels x spatial_numel, contiguous) into
+ * channels-last order N<spatial>C, the order the convolution kernels sample. Passed as the
+ * input of tvdcn_deform_conv_forward / _backward with TVDCN_FLAG_CHANNELS_LAST, the copy
+ * stands in for the layout copy each of those calls makes otherwise, so one copy can serve a
+ * forward and its backward. No counterpart in the reference (its kernels gather from
+ * NC<spatial> directly, tvdcn/csrc/ops/cuda/deform_conv2d_common_kernels.cu:170-200); for
+ * training loops that keep the input of a forward for its backward.
+ */
+tvdcn_status tvdcn_to_channels_last(int32_t dtype, int64_t batch, int64_t channels, int64_t spatial_numel,
+                                    const void *input, void *output, void *stream);
+/* The inverse copy, N<spatial>C -> NC<spatial> (float32): brings a gradient that a
+ * channels-last backward call wrote back to the order of the caller's tensor. */
+tvdcn_status tvdcn_from_channels_last(int32_t dtype, int64_t batch, int64_t channels, int64_t spatial_numel,
+                                      const void *input, void *output, void *stream);
+
 /* Thread-local text of the last error (empty string when none). */
 const char *tvdcn_last_error(void);
 

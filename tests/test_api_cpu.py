@@ -476,3 +476,23 @@ def test_c_abi_planning_fuzz(lib):
             assert fw == 0 and bw == 0
         else:
             assert bw > 0
+
+
+def test_c_abi_layout_copy_argument_checks(lib):
+    """tvdcn_to_channels_last / tvdcn_from_channels_last: float32 only, sizes checked on the host,
+    empty tensors succeed without touching the device."""
+    lib.tvdcn_last_error.restype = ctypes.c_char_p
+    for fn in (lib.tvdcn_to_channels_last, lib.tvdcn_from_channels_last):
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                       ctypes.c_void_p, ctypes.c_void_p]
+        assert fn(1, 2, 3, 4, None, None, None) != 0                          # float64
+        assert b"float32 only" in lib.tvdcn_last_error()
+        assert fn(0, -1, 3, 4, None, None, None) != 0
+        assert b"negative size" in lib.tvdcn_last_error()
+        assert fn(0, 1 << 20, 1 << 10, 1 << 10, None, None, None) != 0       # 2^40 elements
+        assert b"32-bit indexing" in lib.tvdcn_last_error()
+        assert fn(0, 0, 3, 4, None, None, None) == 0                          # empty batch
+        assert lib.tvdcn_last_error() == b""
+        assert fn(0, 2, 3, 4, None, None, None) != 0                          # null pointers
+        assert b"null pointer" in lib.tvdcn_last_error()

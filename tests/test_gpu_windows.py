@@ -169,3 +169,54 @@ def test_weight_gradient_short_passes_fp32(dim, transposed, cin, cout, k, size):
     case = make_case(dim, transposed, batch=2, cin=cin, cout=cout, kernel=[k] * dim, stride=[1] * dim,
                      padding=[1] * dim, dilation=[1] * dim, in_size=size, out_pad=[0] * dim, seed=570 + dim)
     check(case, torch.float32)
+
+
+def test_layout_copies_through_c_abi():
+    """tvdcn_to_channels_last / tvdcn_from_channels_last on the GPU: bit-exact permutations
+    (ragged sizes, off the 32 x 32 tile of the copy kernels), and their round trip."""
+    import ctypes
+    from tvdcn_amd import extension
+    lib = ctypes.CDLL(extension.HIP_LIB_PATH)
+    for fn in (lib.tvdcn_to_channels_last, lib.tvdcn_from_channels_last):
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                       ctypes.c_void_p, ctypes.c_void_p]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for B, C, S in ((3, 37, 1000), (1, 256, 4096), (2, 5, 33)):
+        print(f"layout copy B={B} C={C} S={S}", flush=True)
+        x = torch.randn(B, C, S, device="cuda:0")
+        cl = torch.empty(B, S, C, device="cuda:0")
+        back = torch.empty_like(x)
+        assert lib.tvdcn_to_channels_last(0, B, C, S, x.data_ptr(), cl.data_ptr(), stream) == 0
+        assert lib.tvdcn_from_channels_last(0, B, C, S, cl.data_ptr(), back.data_ptr(), stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(cl, x.permute(0, 2, 1))
+        assert torch.equal(back, x)
+
+
+@pytest.mark.parametrize("dim", [2, 3])
+def test_forward_copy_kept_for_backward(dim):
+    """float32 NC<spatial> inputs: the forward's channels-last copy serves the backward, and
+    grad_input comes back in the input's own (NC<spatial>) order with the numbers of the
+    backward op called on the original input."""
+    in_size = {2: [20, 18], 3: [6, 10, 9]}[dim]
+    case = make_case(dim, False, batch=2, cin=32, cout=48, kernel=[3] * dim, stride=[1] * dim, padding=[1] * dim,
+                     dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim, seed=570 + dim)
+    names = ("input", "weight", "offset", "mask", "bias")
+    ts = [case[n].to("cuda:0", torch.float32) for n in names]
+    params = ([1] * dim, [1] * dim, [1] * dim, 1)
+    fwd = getattr(torch.ops.tvdcn_amd, f"deform_conv{dim}d")
+    bwd = getattr(torch.ops.tvdcn_amd, f"_deform_conv{dim}d_backward")
+    with torch.no_grad():
+        y_ref = fwd(*ts, *params)
+    gy = torch.randn(y_ref.shape, device="cuda:0")
+    ref = bwd(gy, *ts, *params)
+    leaves = [t.clone().requires_grad_(True) for t in ts]
+    y = fwd(*leaves, *params)
+    y.backward(gy)
+    torch.cuda.synchronize()
+    assert leaves[0].grad.is_contiguous()
+    assert rel_err(y, y_ref) < 1e-6
+    for n, t, r in zip(names, leaves, ref):
+        e = rel_err(t.grad, r)
+        assert e < 1e-6, f"grad_{n} rel err {e}"

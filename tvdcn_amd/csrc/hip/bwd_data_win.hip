@@ -638,13 +638,9 @@ hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void 
                     const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
     auto kern = bwd_data_win_kernel<DIM, T, SCATTER, COORD>;
     const size_t lds = lds_bytes<SCATTER, COORD>(tl);
-    static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)WIN_LDS_TARGET);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
+    if (const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kern), lds_raised); e != hipSuccess)
+        return e;
     const long long blocks = (long long)g.G * g.B * tl.ntile[0] * tl.ntile[1] * tl.ntile[2] * tl.c_tiles;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, tl, static_cast<const T *>(z),
                        static_cast<const float *>(wchunks), static_cast<const float *>(xcl),

@@ -296,13 +296,9 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const
     auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG, TMV, KPV>;
     const size_t lds =
         ((size_t)SH::GEO_WORDS + SH::SBUF_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
-    static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)WIN_LDS_TARGET);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
+    if (const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kern), lds_raised); e != hipSuccess)
+        return e;
     const long long blocks = (long long)g.G * ww.n_split * ww.m_tiles * wt.c_tiles;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, wt, ww, static_cast<const T *>(z),
                        static_cast<const float *>(xcl), static_cast<const T *>(offset), static_cast<const T *>(mask),

@@ -314,6 +314,27 @@ struct TimedScope {
         TVDCN_CHECK_HIP(expr);              \
     } while (0)
 
+tvdcn_status layout_copy(bool to_cl, int32_t dtype, int64_t batch, int64_t channels, int64_t spatial_numel,
+                         const void *input, void *output, void *stream) {
+    const char *what = to_cl ? "to_channels_last" : "from_channels_last";
+    if (dtype != TVDCN_DTYPE_FLOAT32) return fail(TVDCN_STATUS_NOT_SUPPORTED, std::string(what) + ": float32 only");
+    if (batch < 0 || channels < 0 || spatial_numel < 0)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, std::string(what) + ": negative size");
+    if (!fits_int(batch) || !fits_int(channels) || !fits_int(spatial_numel) ||
+        (double)batch * (double)channels * (double)spatial_numel > (double)INT_MAX)
+        return fail(TVDCN_STATUS_NOT_SUPPORTED, std::string(what) + ": tensor too large for 32-bit indexing");
+    g_last_error.clear();
+    if (batch == 0 || channels == 0 || spatial_numel == 0) return TVDCN_STATUS_SUCCESS;
+    if (input == nullptr || output == nullptr)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, std::string(what) + ": null pointer");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int B = (int)batch, C = (int)channels, Sn = (int)spatial_numel;
+    if (to_cl)
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(kF32, input, output, B, C, Sn, s));
+    else
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_from_channels_last(kF32, input, output, nullptr, B, C, Sn, s));
+    return TVDCN_STATUS_SUCCESS;
+}
 }  // namespace
 
 extern "C" {
@@ -529,6 +550,16 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
         TVDCN_LAUNCH(TVDCN_KERNEL_BIAS_GRAD, s, launch_bias_grad(dt, grad_out, grad_bias, g.B, Cout, So, s));
     }
     return TVDCN_STATUS_SUCCESS;
+}
+
+tvdcn_status tvdcn_to_channels_last(int32_t dtype, int64_t batch, int64_t channels, int64_t spatial_numel,
+                                    const void *input, void *output, void *stream) {
+    return layout_copy(true, dtype, batch, channels, spatial_numel, input, output, stream);
+}
+
+tvdcn_status tvdcn_from_channels_last(int32_t dtype, int64_t batch, int64_t channels, int64_t spatial_numel,
+                                      const void *input, void *output, void *stream) {
+    return layout_copy(false, dtype, batch, channels, spatial_numel, input, output, stream);
 }
 
 tvdcn_status tvdcn_mask_softmax_forward(int32_t dtype, int64_t batch, int64_t groups, int64_t kernel_numel,

@@ -363,13 +363,9 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const vo
                     const void *offset, const void *mask, const void *bias, void *y, void *y32, hipStream_t s) {
     auto kern = fwd_win_kernel<DIM, T, MB>;
     const size_t lds = ((size_t)GEO_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
-    static bool attr_set = false;   // benign race: setting the same attribute twice is harmless
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)WIN_LDS_TARGET);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
+    if (const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kern), lds_raised); e != hipSuccess)
+        return e;
     const long long blocks = (long long)g.G * g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2] * fw.m_tiles * fw.ksplit;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, wt, fw, static_cast<const float *>(xcl),
                        static_cast<const float *>(wf), static_cast<const T *>(offset), static_cast<const T *>(mask),

@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include "common.h"
 
 namespace tvdcn_hip {
@@ -34,6 +35,20 @@ struct WeightTiles {
 // up to WIN_TMAX taps per pass, bilinear scatter pre-accumulated in LDS.
 constexpr int WIN_TMAX = 9;                   // taps held in accumulators per pass
 constexpr size_t WIN_LDS_TARGET = 156 * 1024; // bytes of LDS per workgroup (gfx950: 160 KB per CU)
+
+// Raise a kernel's dynamic-LDS limit to WIN_LDS_TARGET on the current device, once per
+// device (devices 0..63 tracked as bits of `done`; others set it on every call). Safe to
+// call from several host threads: setting the attribute twice is harmless.
+inline hipError_t raise_lds_limit(const void *kern, std::atomic<unsigned long long> &done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const unsigned long long bit = dev >= 0 && dev < 64 ? 1ull << dev : 0ull;
+    if (bit != 0ull && (done.load(std::memory_order_acquire) & bit) != 0ull) return hipSuccess;
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)WIN_LDS_TARGET);
+    if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+    return e;
+}
 struct WinTiles {
     bool ok;             // eligible: fp32/fp16/bf16, C % 4 == 0, 16-channel tiles group-uniform
     int box[3];          // tile box (embedded axes), product 256, powers of two

@@ -15,8 +15,10 @@
 //   autocast       ops/autocast/deform_conv2d_kernel.cpp:9-38 and twins
 //   library info   tvdcn.cpp:24-53 (_cuda_version, _cuda_arch_flags)
 #include <ATen/ATen.h>
+#include <ATen/FunctionalTensorWrapper.h>
 #include <ATen/autocast_mode.h>
 #include <c10/core/DeviceGuard.h>
+#include <c10/core/impl/TorchDispatchModeTLS.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/autograd.h>
 #include <torch/library.h>
@@ -453,6 +455,34 @@ Tensor call_forward(const Tensor &input, const Tensor &weight, const optional<Te
 
 optional<Tensor> opt(const Tensor &t) { return t.defined() ? optional<Tensor>(t) : optional<Tensor>(); }
 
+// float32 2D / 3D conv inputs in NC<spatial> order: the forward makes the channels-last copy
+// that the kernels sample (tvdcn_to_channels_last) and keeps it for the backward, which would
+// otherwise make the same copy again; the backward writes grad_input channels-last and brings
+// it back to NC<spatial> (tvdcn_from_channels_last). Every other input passes through as it is.
+bool keeps_cl_copy(const Tensor &x, int dim, bool transposed) {
+    if (transposed || (dim != 2 && dim != 3) || !x.is_cuda() || x.scalar_type() != at::kFloat ||
+        x.dim() != dim + 2 || !x.is_contiguous() || x.numel() == 0)
+        return false;
+    // traced calls (fake / functional tensors, dispatch modes) hold no device memory to copy
+    // and record dispatcher ops only: they keep the plain path
+    if (c10::impl::dispatch_mode_enabled() || x.key_set().has(c10::DispatchKey::Python) ||
+        at::functionalization::impl::isFunctionalTensor(x))
+        return false;
+    return x.size(1) > 1 && x.numel() > x.size(0) * x.size(1);   // else both orders coincide
+}
+
+Tensor cl_copy(const Tensor &x, int dim, bool to_cl) {
+    const auto cl_fmt = dim == 2 ? at::MemoryFormat::ChannelsLast : at::MemoryFormat::ChannelsLast3d;
+    TORCH_CHECK(to_cl ? x.is_contiguous() : x.is_contiguous(cl_fmt), "cl_copy: unexpected memory layout");
+    c10::DeviceGuard guard(x.device());
+    const int64_t B = x.size(0), C = x.size(1), S = x.numel() / (B * C);
+    Tensor y = at::empty_like(x, to_cl ? cl_fmt : at::MemoryFormat::Contiguous);
+    const auto fn = to_cl ? tvdcn_to_channels_last : tvdcn_from_channels_last;
+    check_status(fn(TVDCN_DTYPE_FLOAT32, B, C, S, x.data_ptr(), y.data_ptr(), current_stream(y)),
+                 to_cl ? "to_channels_last" : "from_channels_last");
+    return y;
+}
+
 template <int DIM, bool TR>
 class DeformFunction : public torch::autograd::Function<DeformFunction<DIM, TR>> {
    public:
@@ -462,10 +492,12 @@ class DeformFunction : public torch::autograd::Function<DeformFunction<DIM, TR>>
                                              at::IntArrayRef stride, at::IntArrayRef padding,
                                              at::IntArrayRef out_pad, at::IntArrayRef dilation, int64_t groups) {
         at::AutoDispatchBelowADInplaceOrView guard;
-        Tensor output = call_forward<DIM, TR>(input, weight, offset, mask, bias, stride, padding, out_pad, dilation,
-                                              groups);
-        ctx->save_for_backward({input, weight, offset.value_or(Tensor()), mask.value_or(Tensor()),
+        const bool cl = keeps_cl_copy(input, DIM, TR);
+        const Tensor x = cl ? cl_copy(input, DIM, true) : input;
+        Tensor output = call_forward<DIM, TR>(x, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups);
+        ctx->save_for_backward({x, weight, offset.value_or(Tensor()), mask.value_or(Tensor()),
                                 bias.value_or(Tensor())});
+        ctx->saved_data["cl_copy"] = cl;
         ctx->saved_data["stride"] = stride.vec();
         ctx->saved_data["padding"] = padding.vec();
         ctx->saved_data["output_padding"] = out_pad.vec();
@@ -484,6 +516,8 @@ class DeformFunction : public torch::autograd::Function<DeformFunction<DIM, TR>>
         const int64_t groups = ctx->saved_data["groups"].toInt();
         auto grads = call_backward<DIM, TR>(grad_output[0], saved[0], saved[1], opt(saved[2]), opt(saved[3]),
                                             opt(saved[4]), stride, padding, out_pad, dilation, groups);
+        if (ctx->saved_data["cl_copy"].toBool() && std::get<0>(grads).defined())
+            std::get<0>(grads) = cl_copy(std::get<0>(grads), DIM, false);
         return {std::get<0>(grads), std::get<1>(grads), std::get<2>(grads), std::get<3>(grads), std::get<4>(grads),
                 Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
     }
