@@ -826,9 +826,13 @@ class SigmoidMaskFunction : public torch::autograd::Function<SigmoidMaskFunction
         static auto fop = c10::Dispatcher::singleton()
                               .findSchemaOrThrow("tvdcn_amd::deform_conv_sigmoid_mask", "")
                               .typed<SigFwdSig>();
+        const int dim = (int)stride.size();
+        const bool cl = keeps_cl_copy(input, dim, transposed);
+        const Tensor x = cl ? cl_copy(input, dim, true) : input;
         Tensor output =
-            fop.call(input, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups, transposed, scale);
-        ctx->save_for_backward({input, weight, offset.value_or(Tensor()), mask, bias.value_or(Tensor())});
+            fop.call(x, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups, transposed, scale);
+        ctx->save_for_backward({x, weight, offset.value_or(Tensor()), mask, bias.value_or(Tensor())});
+        ctx->saved_data["cl_copy"] = cl;
         ctx->saved_data["stride"] = stride.vec();
         ctx->saved_data["padding"] = padding.vec();
         ctx->saved_data["output_padding"] = out_pad.vec();
@@ -848,6 +852,8 @@ class SigmoidMaskFunction : public torch::autograd::Function<SigmoidMaskFunction
             ctx->saved_data["output_padding"].toIntVector(), ctx->saved_data["dilation"].toIntVector(),
             ctx->saved_data["groups"].toInt(), ctx->saved_data["transposed"].toBool(),
             ctx->saved_data["scale"].toDouble());
+        if (ctx->saved_data["cl_copy"].toBool() && std::get<0>(grads).defined())
+            std::get<0>(grads) = cl_copy(std::get<0>(grads), (int)saved[0].dim() - 2, false);
         return {std::get<0>(grads), std::get<1>(grads), std::get<2>(grads), std::get<3>(grads), std::get<4>(grads),
                 Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
     }
