@@ -282,28 +282,38 @@ bwd_weight_kernel(const Geo g, const T *__restrict__ z, const A *__restrict__ xc
 }
 
 // dW[grp*Mg + m][c][t] = sum over splits of part[ks][grp][t][m][c] (fixed order: deterministic)
+// units_per_split > 0: split ks covers units [ks * ups, (ks + 1) * ups) of (pass, spatial tile),
+// pass-major; tap t (pass t / tpp) sums the splits that meet units [pass * n_sp, (pass + 1) * n_sp)
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) weight_reduce_kernel(const A *__restrict__ part, T *__restrict__ gw, int k_splits,
-                                                            int G, int Kn, int Mg, int Cg) {
+                                                            int G, int Kn, int Mg, int Cg, int ups, int n_sp, int tpp) {
     const size_t per_split = (size_t)G * Kn * Mg * Cg;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < per_split;
          i += (size_t)gridDim.x * blockDim.x) {
-        A sum = A(0);
-        for (int ks = 0; ks < k_splits; ++ks) sum += part[ks * per_split + i];
         const int c = (int)(i % Cg);
         const int m = (int)((i / Cg) % Mg);
         const int t = (int)((i / ((size_t)Cg * Mg)) % Kn);
         const int grp = (int)(i / ((size_t)Cg * Mg * Kn));
+        int ks0 = 0, ks1 = k_splits;
+        if (ups > 0) {
+            const long long pass = t / tpp;
+            ks0 = (int)(pass * n_sp / ups);
+            ks1 = min(k_splits, (int)(((pass + 1) * n_sp - 1) / ups) + 1);
+        }
+        A sum = A(0);
+        for (int ks = ks0; ks < ks1; ++ks) sum += part[ks * per_split + i];
         gw[(((size_t)grp * Mg + m) * Cg + c) * Kn + t] = from_acc<T, A>(sum);
     }
 }
 
 template <typename T, typename A>
-hipError_t launch_reduce(const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s) {
+hipError_t launch_reduce(const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s, int ups, int n_sp,
+                         int tpp) {
+    if (ups > 0 && (n_sp <= 0 || tpp <= 0)) return hipErrorInvalidValue;
     const size_t n = (size_t)g.G * g.Kn * g.Mg * g.Cg;
     const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL((weight_reduce_kernel<T, A>), dim3(blocks), dim3(256), 0, s, static_cast<const A *>(part),
-                       static_cast<T *>(gw), k_splits, g.G, g.Kn, g.Mg, g.Cg);
+                       static_cast<T *>(gw), k_splits, g.G, g.Kn, g.Mg, g.Cg, ups, n_sp, tpp);
     return hipGetLastError();
 }
 
@@ -349,7 +359,7 @@ hipError_t launch_d(int dim, const Geo &g, const WeightTiles &tl, const void *z,
         case 3: e = launch_w<3, T, A>(g, tl, z, xcl, offset, mask, part, s); break;
     }
     if (e != hipSuccess) return e;
-    return launch_reduce<T, A>(g, tl.k_splits, part, gw, s);
+    return launch_reduce<T, A>(g, tl.k_splits, part, gw, s, 0, 0, 0);
 }
 
 }  // namespace
@@ -377,12 +387,13 @@ WeightTiles plan_weight(const Geo &g, int dtype) {
     return t;
 }
 
-hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s) {
+hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s,
+                                int ups, int n_sp, int tpp) {
     switch (dtype) {
-        case kF32: return launch_reduce<float, float>(g, k_splits, part, gw, s);
-        case kF64: return launch_reduce<double, double>(g, k_splits, part, gw, s);
-        case kF16: return launch_reduce<__half, float>(g, k_splits, part, gw, s);
-        case kBF16: return launch_reduce<__hip_bfloat16, float>(g, k_splits, part, gw, s);
+        case kF32: return launch_reduce<float, float>(g, k_splits, part, gw, s, ups, n_sp, tpp);
+        case kF64: return launch_reduce<double, double>(g, k_splits, part, gw, s, ups, n_sp, tpp);
+        case kF16: return launch_reduce<__half, float>(g, k_splits, part, gw, s, ups, n_sp, tpp);
+        case kBF16: return launch_reduce<__hip_bfloat16, float>(g, k_splits, part, gw, s, ups, n_sp, tpp);
     }
     return hipErrorInvalidValue;
 }

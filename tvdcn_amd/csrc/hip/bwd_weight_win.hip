@@ -84,8 +84,10 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     L /= ww.m_tiles;
     const int split = L % ww.n_split;
     const int grp = L / ww.n_split;
-    const int s_beg = split * ww.tiles_per_split;
-    const int s_end = min(ww.n_spatial, s_beg + ww.tiles_per_split);
+    // this split's units u = pass * n_spatial + spatial tile, u in [u_beg, u_end)
+    const long long n_sp = ww.n_spatial;
+    const long long u_beg = (long long)split * ww.units_per_split;
+    const long long u_end = min((long long)((g.Kn + wt.tpp - 1) / wt.tpp) * n_sp, u_beg + ww.units_per_split);
     const bool deformable = offset != nullptr;
     const int tg = wave / (NW / TG);                     // this wave's tap group
     const int mrow = mt * BMW + (wave % (NW / TG)) * (MB * 16);   // first row of this wave
@@ -99,8 +101,11 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     const int sj = tid % KP, sq = (tid / KP) & 3, st0 = tid / (KP * 4);
     constexpr int SSTEP = NT / (KP * 4);   // tap stride of the items
 
-    for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
+    for (int pass = (int)(u_beg / n_sp); (long long)pass * n_sp < u_end; ++pass) {
+        const int t0 = pass * wt.tpp;
         const int ntaps = min(wt.tpp, g.Kn - t0);
+        const int s_beg = (int)(max(u_beg, pass * n_sp) - pass * n_sp);
+        const int s_end = (int)(min(u_end, (pass + 1) * n_sp) - pass * n_sp);
 
         acc4 acc[MB][TM];
 #pragma unroll
@@ -348,13 +353,14 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     w.m_tiles = (g.Mg + rows - 1) / rows;
     w.n_spatial = g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2];
     const long long per_split_groups = (long long)g.G * w.m_tiles * wt.c_tiles;
-    // one workgroup per CU, about one wave of workgroups
+    // one workgroup per CU, about one wave of workgroups, over units of (pass, spatial tile)
+    const long long units = (long long)((g.Kn + wt.tpp - 1) / wt.tpp) * w.n_spatial;
     long long splits = (256 + per_split_groups - 1) / per_split_groups;
-    if (splits > w.n_spatial) splits = w.n_spatial;
+    if (splits > units) splits = units;
     if (splits < 1) splits = 1;
-    // (at least one tile per split: an empty batch has no spatial tiles)
-    w.tiles_per_split = (int)std::max<long long>(1, (w.n_spatial + splits - 1) / splits);
-    w.n_split = (w.n_spatial + w.tiles_per_split - 1) / w.tiles_per_split;
+    // (at least one unit per split: an empty batch has no spatial tiles)
+    w.units_per_split = (int)std::max<long long>(1, (units + splits - 1) / splits);
+    w.n_split = (int)std::max<long long>(1, (units + w.units_per_split - 1) / w.units_per_split);
     w.z_vec = g.P[2] % 4 == 0 && wt.box[2] >= 4;
     w.part_elems = (size_t)w.n_split * g.G * g.Kn * g.Mg * g.Cg;
     w.ok = g.B > 0;
@@ -371,7 +377,7 @@ hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTile
         case kBF16: e = launch_d<__hip_bfloat16>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
     }
     if (e != hipSuccess) return e;
-    return launch_weight_reduce(dtype, g, ww.n_split, part, gw, s);
+    return launch_weight_reduce(dtype, g, ww.n_split, part, gw, s, ww.units_per_split, ww.n_spatial, wt.tpp);
 }
 
 }  // namespace tvdcn_hip

@@ -69,7 +69,10 @@ struct WeightWin {
     int tg;              // tap groups: 1 (256-row tiles) or 2 (64-row tiles, taps split by parity)
     int m_tiles;         // row tiles of the GEMM side
     int n_spatial;       // spatial tiles (B x ntile0 x ntile1 x ntile2)
-    int tiles_per_split, n_split;
+    // split = a run of units_per_split (pass, spatial tile) units, pass-major: a split may
+    // cover the end of one pass and the start of the next, so the work divides evenly
+    // whatever the number of passes
+    int units_per_split, n_split;
     bool z_vec;          // 4 consecutive tile pixels are contiguous and 16-byte aligned
     size_t part_elems;   // workspace floats for the split partials
 };
@@ -139,7 +142,10 @@ hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTile
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
                                  void *gw, hipStream_t s);
 // gw (storage type, layout (M, Cg, Kn)) = sum over k_splits of part[ks][G][Kn][Mg][Cg]
-hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s);
+// dW = sum over splits of the partials; with units_per_split > 0 (windowed kernel) tap t sums only
+// the splits whose unit range meets its pass (t / tpp) over n_spatial tiles
+hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s,
+                                int units_per_split = 0, int n_spatial = 0, int tpp = 0);
 // writes split partials to `part` (WeightTiles::part_elems accumulator elements),
 // then reduces them into gw (storage type, layout (M, Cg, Kn))
 hipError_t launch_bwd_weight(int dtype, int dim, const Geo &g, const WeightTiles &t, const void *z, const void *xcl,
