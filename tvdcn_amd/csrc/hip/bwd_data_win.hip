@@ -606,26 +606,37 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     }
 }
 
-// weight (M, Cg, Kn) -> chunks [G][c_tiles][m_steps][Kn][16 c][16 m], zero padded
+// weight (M, Cg, Kn) -> chunks [G][c_tiles][m_steps][Kn][16 c][16 m], zero padded.
+// Block = (group, channel slice, row step, run of up to WL_TK taps): reads 16 rows of
+// 16 channels x the run's taps (contiguous runs of taps per channel), transposes through
+// LDS, writes its 256 * taps contiguous output floats.
+constexpr int WL_TK = 16;
 template <typename T>
-__global__ void weight_win_kernel(const T *__restrict__ w, float *__restrict__ out, int G, int Mg, int Cg, int Kn,
-                                  int c_tiles, int m_steps) {
-    const size_t total = (size_t)G * c_tiles * m_steps * Kn * BC * BM;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-        const int mi = (int)(i % BM);
-        const int ci = (int)((i / BM) % BC);
-        size_t r = i / (BM * BC);
-        const int t = (int)(r % Kn);
-        r /= Kn;
-        const int ms = (int)(r % m_steps);
-        r /= m_steps;
-        const int ct = (int)(r % c_tiles);
-        const int grp = (int)(r / c_tiles);
+__global__ void __launch_bounds__(256)
+weight_win_kernel(const T *__restrict__ w, float *__restrict__ out, int G, int Mg, int Cg, int Kn, int c_tiles,
+                  int m_steps) {
+    __shared__ float tile[WL_TK][BC][BM + 1];   // [tap][c][m]
+    const int tchunks = (Kn + WL_TK - 1) / WL_TK;
+    int L = blockIdx.x;
+    const int tc = L % tchunks;
+    L /= tchunks;
+    const int ms = L % m_steps;
+    L /= m_steps;
+    const int ct = L % c_tiles;
+    const int grp = L / c_tiles;
+    const int t0 = tc * WL_TK, nt = min(WL_TK, Kn - t0);
+    const int n = BM * BC * nt;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        const int tt = e % nt, r = e / nt;   // (m, c, tap), taps fastest
+        const int ci = r % BC, mi = r / BC;
         const int m = ms * BM + mi, c = ct * BC + ci;
         float v = 0.f;
-        if (m < Mg && c < Cg) v = to_acc<float>(w[(((size_t)grp * Mg + m) * Cg + c) * Kn + t]);
-        out[i] = v;
+        if (m < Mg && c < Cg) v = to_acc<float>(w[(((size_t)grp * Mg + m) * Cg + c) * Kn + t0 + tt]);
+        tile[tt][ci][mi] = v;
     }
+    __syncthreads();
+    float *dst = out + ((((size_t)grp * c_tiles + ct) * m_steps + ms) * Kn + t0) * (BC * BM);
+    for (int e = threadIdx.x; e < n; e += blockDim.x) dst[e] = tile[e / (BM * BC)][(e / BM) % BC][e % BM];
 }
 
 template <bool SCATTER, bool COORD> size_t lds_bytes(const WinTiles &t) {
@@ -766,10 +777,9 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
 
 hipError_t launch_weight_win_layout(int dtype, const Geo &g, const WinTiles &t, const void *w, void *chunks,
                                     hipStream_t s) {
-    const size_t n = t.chunk_elems;
-    size_t blocks = (n + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    if (blocks < 1) blocks = 1;
+    const long long blocks = (long long)g.G * t.c_tiles * t.m_steps * ((g.Kn + WL_TK - 1) / WL_TK);
+    if (blocks <= 0) return hipSuccess;
+    if (blocks > INT_MAX) return hipErrorInvalidValue;
 #define TVDCN_WW(T)                                                                                             \
     hipLaunchKernelGGL((weight_win_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, s, static_cast<const T *>(w), \
                        static_cast<float *>(chunks), g.G, g.Mg, g.Cg, g.Kn, t.c_tiles, t.m_steps);               \

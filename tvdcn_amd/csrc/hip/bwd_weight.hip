@@ -283,25 +283,26 @@ bwd_weight_kernel(const Geo g, const T *__restrict__ z, const A *__restrict__ xc
 
 // dW[grp*Mg + m][c][t] = sum over splits of part[ks][grp][t][m][c] (fixed order: deterministic)
 // units_per_split > 0: split ks covers units [ks * ups, (ks + 1) * ups) of (pass, spatial tile),
-// pass-major; tap t (pass t / tpp) sums the splits that meet units [pass * n_sp, (pass + 1) * n_sp)
+// pass-major; tap t (pass t / tpp) sums the splits that meet units [pass * n_sp, (pass + 1) * n_sp).
+// 32-bit index arithmetic: the weight's element count and the unit count fit in int.
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) weight_reduce_kernel(const A *__restrict__ part, T *__restrict__ gw, int k_splits,
                                                             int G, int Kn, int Mg, int Cg, int ups, int n_sp, int tpp) {
-    const size_t per_split = (size_t)G * Kn * Mg * Cg;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < per_split;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const int c = (int)(i % Cg);
-        const int m = (int)((i / Cg) % Mg);
-        const int t = (int)((i / ((size_t)Cg * Mg)) % Kn);
-        const int grp = (int)(i / ((size_t)Cg * Mg * Kn));
+    const int per_split = G * Kn * Mg * Cg;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < per_split; i += gridDim.x * blockDim.x) {
+        const int c = i % Cg;
+        const int r = i / Cg;
+        const int m = r % Mg;
+        const int t = (r / Mg) % Kn;
+        const int grp = r / (Mg * Kn);
         int ks0 = 0, ks1 = k_splits;
         if (ups > 0) {
-            const long long pass = t / tpp;
-            ks0 = (int)(pass * n_sp / ups);
-            ks1 = min(k_splits, (int)(((pass + 1) * n_sp - 1) / ups) + 1);
+            const unsigned pass = (unsigned)(t / tpp);
+            ks0 = (int)(pass * (unsigned)n_sp / (unsigned)ups);
+            ks1 = min(k_splits, (int)(((pass + 1u) * (unsigned)n_sp - 1u) / (unsigned)ups) + 1);
         }
         A sum = A(0);
-        for (int ks = ks0; ks < ks1; ++ks) sum += part[ks * per_split + i];
+        for (int ks = ks0; ks < ks1; ++ks) sum += part[(size_t)ks * per_split + i];
         gw[(((size_t)grp * Mg + m) * Cg + c) * Kn + t] = from_acc<T, A>(sum);
     }
 }
@@ -311,6 +312,7 @@ hipError_t launch_reduce(const Geo &g, int k_splits, const void *part, void *gw,
                          int tpp) {
     if (ups > 0 && (n_sp <= 0 || tpp <= 0)) return hipErrorInvalidValue;
     const size_t n = (size_t)g.G * g.Kn * g.Mg * g.Cg;
+    if (n > (size_t)INT_MAX) return hipErrorInvalidValue;
     const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL((weight_reduce_kernel<T, A>), dim3(blocks), dim3(256), 0, s, static_cast<const A *>(part),
                        static_cast<T *>(gw), k_splits, g.G, g.Kn, g.Mg, g.Cg, ups, n_sp, tpp);

@@ -355,6 +355,7 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     const long long per_split_groups = (long long)g.G * w.m_tiles * wt.c_tiles;
     // one workgroup per CU, about one wave of workgroups, over units of (pass, spatial tile)
     const long long units = (long long)((g.Kn + wt.tpp - 1) / wt.tpp) * w.n_spatial;
+    if (units > INT_MAX) return w;   // the reduction indexes units in 32 bits
     long long splits = (256 + per_split_groups - 1) / per_split_groups;
     if (splits > units) splits = units;
     if (splits < 1) splits = 1;

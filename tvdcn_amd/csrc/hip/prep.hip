@@ -93,7 +93,7 @@ __global__ void weight_d_kernel(const T *__restrict__ w, A *__restrict__ wd, int
 template <typename A>
 __global__ void fill_zero_kernel(A *__restrict__ p, size_t n) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = A(0);
+        p[i] = A{};
 }
 
 template <typename T, typename A>
@@ -227,6 +227,22 @@ hipError_t launch_weight_data_layout(int dtype, const Geo &g, const void *w, voi
 
 hipError_t launch_fill_zero(int elem_bytes, void *p, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
+    if (elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return hipErrorInvalidValue;
+    // 16-byte aligned buffers: the whole 16-byte words with vector stores, the few
+    // elements past the last one with the element kernel
+    if (reinterpret_cast<uintptr_t>(p) % 16 == 0) {
+        const size_t words = n * elem_bytes / 16;
+        if (words > 0) {
+            hipLaunchKernelGGL((fill_zero_kernel<uint4>), dim3(grid_for(words)), dim3(256), 0, s, static_cast<uint4 *>(p),
+                               words);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        const size_t done = words * 16 / elem_bytes;
+        if (done == n) return hipSuccess;
+        p = static_cast<char *>(p) + done * elem_bytes;
+        n -= done;
+    }
     if (elem_bytes == 8)
         hipLaunchKernelGGL((fill_zero_kernel<double>), dim3(grid_for(n)), dim3(256), 0, s, static_cast<double *>(p), n);
     else if (elem_bytes == 4)
