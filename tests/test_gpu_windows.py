@@ -220,3 +220,55 @@ def test_forward_copy_kept_for_backward(dim):
     for n, t, r in zip(names, leaves, ref):
         e = rel_err(t.grad, r)
         assert e < 1e-6, f"grad_{n} rel err {e}"
+
+
+def _samples_on_cell_boundaries(case, tol=2e-5):
+    """Mask over grad_offset's elements: True where the sample's exact (float64) position lies
+    within tol of an integer on some axis. There the bilinear / trilinear coordinate derivative
+    jumps, and a float32 position (integer base + offset, rounded once, as the reference's fp32
+    kernels form it: cuda/deform_conv2d_common_kernels.cu:170-178) may fall on the other side
+    (half an ulp: 4e-6 at |position| < 64), so the float32 offset gradient there is the other
+    one-sided derivative. Conv (not transposed) geometry."""
+    dim = case["dim"]
+    k = list(case["weight"].shape[2:])
+    st, pad, dil = case["stride"], case["padding"], case["dilation"]
+    off = case["offset"].to(torch.float32).double()
+    B, out = off.shape[0], list(off.shape[2:])
+    K = 1
+    for v in k:
+        K *= v
+    og = off.shape[1] // (K * dim)
+    off = off.reshape(B, og, *k, dim, *out)
+    near = torch.zeros(B, og, *k, *out, dtype=torch.bool)
+    for a in range(dim):
+        o = torch.arange(out[a], dtype=torch.float64) * st[a] - pad[a]
+        kk = torch.arange(k[a], dtype=torch.float64) * dil[a]
+        kshape = [1] * (2 + dim) + [1] * dim
+        kshape[2 + a] = k[a]
+        oshape = [1] * (2 + dim) + [1] * dim
+        oshape[2 + dim + a] = out[a]
+        pos = kk.reshape(kshape) + o.reshape(oshape) + off.select(2 + dim, a)
+        near |= (pos - pos.round()).abs() < tol
+    return near.unsqueeze(2 + dim).expand(B, og, *k, dim, *out).reshape(case["offset"].shape)
+
+
+def test_weight_splits_across_pass_boundaries_fp32():
+    """3D, 27 taps (three passes) over 135 spatial tiles: the windowed weight gradient's splits
+    run over (pass, tile) units two at a time, so split 67 holds the last tile of pass 0 and
+    the first of pass 1, and the reduction sums per tap only the splits that meet its pass.
+    Every other quantity at the usual bounds; the offset gradient away from the (about 1e-4 of
+    all) samples that sit on a cell boundary, where its value is one-sided."""
+    case = make_case(3, False, batch=3, cin=16, cout=32, kernel=[3, 3, 3], stride=[1, 1, 1], padding=[1, 1, 1],
+                     dilation=[1, 1, 1], in_size=[12, 24, 40], out_pad=[0, 0, 0], seed=590)
+    out, grads, gout = run_gpu(case, torch.float32)
+    ref_out, ref_grads = run_oracle(case, gout, torch.float32)
+    assert rel_err(out, ref_out) < 1e-5
+    near = _samples_on_cell_boundaries(case)
+    print(f"offset-gradient elements on cell boundaries: {int(near.sum())} of {near.numel()}", flush=True)
+    assert float(near.double().mean()) < 1e-3
+    for name, g, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
+        g = g.double().cpu()
+        if name == "offset":
+            g = torch.where(near, r, g)
+        e = rel_err(g, r)
+        assert e < 1e-4, f"grad_{name} rel err {e}"
