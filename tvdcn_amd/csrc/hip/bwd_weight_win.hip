@@ -7,9 +7,10 @@
 // (tvdcn/csrc/ops/cuda/deform_conv2d_kernel.cpp:600-626; transposed
 // deform_conv_transpose2d_kernel.cpp:586-613; 1D/3D twins).
 //
-// Workgroup = (group, 16-channel slice, up to 256 GEMM-side rows, a run of spatial
-// tiles); eight waves, wave w owning 32 rows. The dW block [rows][16 c][taps of the
-// pass] stays in accumulators (72 registers per lane) across the whole run of tiles.
+// Workgroup = (group, 16-channel slice, up to 256 GEMM-side rows, a run of (pass,
+// spatial tile) units, pass-major, so that the runs are equal whatever the number of
+// passes); eight waves, wave w owning 32 rows. The dW block [rows][16 c][taps of the
+// pass] stays in accumulators (72 registers per lane) across the run's tiles of a pass.
 // Per tile (a box of 256 column pixels of one image, see window.h) the sampling
 // table and the X window are filled once; then the tile is walked in 32-pixel
 // chunks (one barrier each): the sampled columns S[tap][c][px] of the next chunk are
@@ -18,8 +19,9 @@
 // half of the chunk:
 //   A = Z[m][px] (4 consecutive pixels per lane, one 16-byte load when contiguous),
 //   B = S[px][c] of one tap, D = dW[m][c] of that tap.
-// At the end of the run the block is stored to a split slot of the workspace and
-// the splits are summed in a fixed order (deterministic).
+// At the end of each pass of the run the block is stored to the split's slot of the
+// workspace; per tap, the splits whose runs meet its pass are summed in a fixed order
+// (deterministic).
 #include "window.h"
 
 namespace tvdcn_hip {

@@ -63,7 +63,7 @@ struct WinTiles {
 };
 
 // Windowed weight-gradient kernel (bwd_weight_win.hip): workgroups own (group,
-// 16-channel slice, 256 rows) and a run of spatial tiles of the WinTiles tiling.
+// 16-channel slice, 256 rows) and a run of (pass, spatial tile) units of the WinTiles tiling.
 struct WeightWin {
     bool ok;
     int tg;              // tap groups: 1 (256-row tiles) or 2 (64-row tiles, taps split by parity)
