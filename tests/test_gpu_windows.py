@@ -194,12 +194,12 @@ def test_layout_copies_through_c_abi():
         assert torch.equal(back, x)
 
 
-@pytest.mark.parametrize("dim", [2, 3])
+@pytest.mark.parametrize("dim", [1, 2, 3])
 def test_forward_copy_kept_for_backward(dim):
     """float32 NC<spatial> inputs: the forward's channels-last copy serves the backward, and
     grad_input comes back in the input's own (NC<spatial>) order with the numbers of the
     backward op called on the original input."""
-    in_size = {2: [20, 18], 3: [6, 10, 9]}[dim]
+    in_size = {1: [70], 2: [20, 18], 3: [6, 10, 9]}[dim]
     case = make_case(dim, False, batch=2, cin=32, cout=48, kernel=[3] * dim, stride=[1] * dim, padding=[1] * dim,
                      dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim, seed=570 + dim)
     names = ("input", "weight", "offset", "mask", "bias")
@@ -272,3 +272,25 @@ def test_weight_splits_across_pass_boundaries_fp32():
             g = torch.where(near, r, g)
         e = rel_err(g, r)
         assert e < 1e-4, f"grad_{name} rel err {e}"
+
+
+def test_channels_last_1d_input():
+    """A 1D conv input in (batch, length, channels) order, seen as (B, C, L) with strides
+    (L * C, 1, C) (a permuted tensor; torch has no 1D channels-last format), is sampled in
+    place; its gradient comes back in the same order, with the numbers of the NC<spatial> path."""
+    case = make_case(1, False, batch=2, cin=32, cout=48, kernel=[3], stride=[1], padding=[1], dilation=[1],
+                     in_size=[70], out_pad=[0], seed=580)
+    out, grads, gout = run_gpu(case, torch.float32)
+    names = ("input", "weight", "offset", "mask", "bias")
+    ts = [case[n].to("cuda:0", torch.float32) for n in names]
+    ts[0] = ts[0].permute(0, 2, 1).contiguous().permute(0, 2, 1)
+    assert ts[0].stride() == (70 * 32, 1, 32)
+    ts = [t.requires_grad_(True) for t in ts]
+    y = tvdcn_amd.deform_conv1d(*ts, stride=1, padding=1, dilation=1)
+    y.backward(gout.to("cuda:0", torch.float32))
+    torch.cuda.synchronize()
+    assert ts[0].grad.stride() == (70 * 32, 1, 32)
+    assert rel_err(y, out) < 1e-5
+    for n, t, r in zip(names, ts, grads):
+        e = rel_err(t.grad, r)
+        assert e < 1e-5, f"grad_{n} rel err {e}"

@@ -78,6 +78,17 @@ struct Problem {
     Tensor input, weight, offset, mask, bias;
 };
 
+// Dense channels-last order (batch, *spatial, channels) of a batched conv input: torch's
+// channels_last / channels_last_3d formats in 2D / 3D; in 1D (no torch format) a (B, C, L)
+// tensor with strides (L * C, 1, C), as a permuted (B, L, C) tensor has.
+bool is_channels_last(const Tensor &x, int dim) {
+    if (x.dim() != dim + 2) return false;
+    if (dim == 2) return x.is_contiguous(at::MemoryFormat::ChannelsLast);
+    if (dim == 3) return x.is_contiguous(at::MemoryFormat::ChannelsLast3d);
+    const int64_t C = x.size(1), L = x.size(2);
+    return (C == 1 || x.stride(1) == 1) && (L == 1 || x.stride(2) == C) && (x.size(0) == 1 || x.stride(0) == C * L);
+}
+
 // Shape checks of the reference forward drivers, in the same order and with the
 // same wording (rank-generic).
 Problem make_problem(int dim, bool transposed, const Tensor &input, const Tensor &weight,
@@ -115,9 +126,7 @@ Problem make_problem(int dim, bool transposed, const Tensor &input, const Tensor
 
     // a batched conv input that is channels-last (and not also plain contiguous) is handed over
     // as it is: the kernels sample channels-last data, so no layout copy is needed
-    const auto cl_format = dim == 2 ? at::MemoryFormat::ChannelsLast : at::MemoryFormat::ChannelsLast3d;
-    pr.channels_last = !transposed && !pr.unbatched && (dim == 2 || dim == 3) && input.is_contiguous(cl_format) &&
-                       !input.is_contiguous();
+    pr.channels_last = !transposed && !pr.unbatched && is_channels_last(input, dim) && !input.is_contiguous();
     pr.input = pr.channels_last ? input : input.contiguous();
     pr.weight = weight.contiguous();
     pr.offset = deformable ? offset->contiguous() : Tensor();
@@ -460,7 +469,7 @@ optional<Tensor> opt(const Tensor &t) { return t.defined() ? optional<Tensor>(t)
 // otherwise make the same copy again; the backward writes grad_input channels-last and brings
 // it back to NC<spatial> (tvdcn_from_channels_last). Every other input passes through as it is.
 bool keeps_cl_copy(const Tensor &x, int dim, bool transposed) {
-    if (transposed || (dim != 2 && dim != 3) || !x.is_cuda() || x.scalar_type() != at::kFloat ||
+    if (transposed || dim < 1 || dim > 3 || !x.is_cuda() || x.scalar_type() != at::kFloat ||
         x.dim() != dim + 2 || !x.is_contiguous() || x.numel() == 0)
         return false;
     // traced calls (fake / functional tensors, dispatch modes) hold no device memory to copy
@@ -472,11 +481,16 @@ bool keeps_cl_copy(const Tensor &x, int dim, bool transposed) {
 }
 
 Tensor cl_copy(const Tensor &x, int dim, bool to_cl) {
-    const auto cl_fmt = dim == 2 ? at::MemoryFormat::ChannelsLast : at::MemoryFormat::ChannelsLast3d;
-    TORCH_CHECK(to_cl ? x.is_contiguous() : x.is_contiguous(cl_fmt), "cl_copy: unexpected memory layout");
+    TORCH_CHECK(to_cl ? x.is_contiguous() : is_channels_last(x, dim), "cl_copy: unexpected memory layout");
     c10::DeviceGuard guard(x.device());
     const int64_t B = x.size(0), C = x.size(1), S = x.numel() / (B * C);
-    Tensor y = at::empty_like(x, to_cl ? cl_fmt : at::MemoryFormat::Contiguous);
+    Tensor y;
+    if (!to_cl)
+        y = at::empty_like(x, at::MemoryFormat::Contiguous);
+    else if (dim == 1)
+        y = at::empty({B, x.size(2), C}, x.options()).permute({0, 2, 1});   // (B, C, L), strides (L * C, 1, C)
+    else
+        y = at::empty_like(x, dim == 2 ? at::MemoryFormat::ChannelsLast : at::MemoryFormat::ChannelsLast3d);
     const auto fn = to_cl ? tvdcn_to_channels_last : tvdcn_from_channels_last;
     check_status(fn(TVDCN_DTYPE_FLOAT32, B, C, S, x.data_ptr(), y.data_ptr(), current_stream(y)),
                  to_cl ? "to_channels_last" : "from_channels_last");
