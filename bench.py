@@ -13,7 +13,8 @@ Printed JSON line (rank 0): the driver contract plus
                    duration measured with HIP events recorded on the launch stream
                    (tvdcn_kernel_timer_* in the C ABI), against MI355X peak;
   cpu_baseline  -- the reference's own CPU path (oracle/_ref, compiled from the
-                   reference sources) timed on this host on a bounded sample;
+                   reference sources) timed on this host on the full workload, in a
+                   child process (oracle/ref_child.py);
   kernels       -- every kernel family's average launch time and roofline fraction.
 """
 import argparse
@@ -58,8 +59,8 @@ def flops_fwd(batch=8):
 
 
 def _kernel_lib():
-    import tvdcn_amd
-    lib = ctypes.CDLL(tvdcn_amd.extension.HIP_LIB_PATH)
+    import tvdcn
+    lib = ctypes.CDLL(tvdcn.extension.HIP_LIB_PATH)
     lib.tvdcn_kernel_timer_enable.argtypes = [ctypes.c_int32]
     lib.tvdcn_kernel_timer_read.argtypes = [ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(ctypes.c_int64)]
@@ -116,13 +117,13 @@ def time_path(params, fwd, gout, steps, warmup):
 
 
 def gpu_bench(inp, steps, warmup):
-    import tvdcn_amd
+    import tvdcn
     dev = torch.device("cuda:0")
     params = [inp[k].to(dev).requires_grad_(True) for k in ("input", "weight", "offset", "mask", "bias")]
     gout = inp["grad_out"].to(dev)
 
     def fwd():
-        return tvdcn_amd.deform_conv2d(*params, stride=1, padding=1, dilation=1, groups=1)
+        return tvdcn.deform_conv2d(*params, stride=1, padding=1, dilation=1, groups=1)
 
     return time_path(params, fwd, gout, steps, warmup)
 
@@ -215,20 +216,28 @@ def suite_flops(c):
     return 2.0 * B * out_px * w.shape[0] * (x.shape[1] // groups) * kn
 
 
-def run_suite_case(n, dtype, steps, warmup):
-    import tvdcn_amd
+def run_suite_case(n, dtype, steps, warmup, cpu=False):
+    """One config of the suite. Configs 3 and 5 take their softmax mask the way
+    PackedDeformConv*(mask_activation="softmax") does: the softmax of the logits applied in the kernels'
+    mask load (tvdcn::deform_conv_mask_activation), its gradient flowing to the logits."""
+    import tvdcn
+    from tvdcn.ops.deform_conv import _deform_conv_mask_activation
     c = suite_case(n)
     dev = torch.device("cuda:0")
     mk = lambda t: None if t is None else t.to(dev, dtype).requires_grad_(True)
     x, w, o, m, b, logits = (mk(c[k]) for k in ("x", "w", "o", "m", "b", "logits"))
     params = [t for t in (x, w, o, m, b, logits) if t is not None]
-    op = getattr(tvdcn_amd, c["op"])
+    op = getattr(tvdcn, c["op"])
     dim = x.dim() - 2
-    softmax = getattr(tvdcn_amd, f"mask_softmax{dim}d")
+    kw = c["kw"]
+    lst = lambda v: [v] * dim
 
     def fwd():
-        mask = softmax(logits, c["ks"]) if logits is not None else m
-        return op(x, w, o, mask, b, **c["kw"])
+        if logits is not None:
+            return _deform_conv_mask_activation(x, w, o, logits, b, lst(kw["stride"]), lst(kw["padding"]),
+                                                lst(kw.get("output_padding", 0)), lst(kw["dilation"]),
+                                                kw["groups"], c["tr"], 2, 0.0)
+        return op(x, w, o, m, b, **kw)
 
     with torch.no_grad():
         out_shape = fwd().shape
@@ -241,8 +250,9 @@ def run_suite_case(n, dtype, steps, warmup):
     es = torch.finfo(dtype).bits // 8
     mask_bytes = es * (logits.numel() if logits is not None else 0)
     roof = family_rooflines(kern, F, es * gout.numel(), mask_bytes)
-    return {
+    row = {
         "case": c["name"], "dtype": str(dtype).replace("torch.", ""), "compute": "f32 (fp32 MFMA, fp32 accumulate)",
+        "mask": "softmax of logits in the mask load" if logits is not None else "given",
         "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(step_ms - fwd_ms, 4), "fwd_bwd_ms": round(step_ms, 4),
         "gflop_fwd": round(F / 1e9, 3), "gflop_bwd": round(nb * F / 1e9, 3),
         "gflop_fwd_bwd": round((1 + nb) * F / 1e9, 3),
@@ -254,6 +264,9 @@ def run_suite_case(n, dtype, steps, warmup):
         "fwd_bwd_frac_mfma_fp32": round((1 + nb) * F / (step_ms * 1e-3) / PEAK_FP32_MFMA, 4),
         "kernels": roof,
     }
+    if cpu and dtype == torch.float32:
+        row["cpu_baseline"] = cpu_baseline_case(c, gout.cpu(), reps=1)
+    return row
 
 
 SUITE = [(2, torch.float32), (3, torch.float32), (4, torch.float32), (5, torch.float32), (5, torch.float16),
@@ -281,42 +294,66 @@ def load_traffic(family):
     return None
 
 
-def cpu_baseline(inp, batch):
-    """The reference's CPU implementation (oracle/_ref) on `batch` images of the same tensors."""
-    from oracle import oracle
-    if not oracle.load_reference():
-        return None
-    x, o, m, g = (inp[k][:batch] for k in ("input", "offset", "mask", "grad_out"))
-    w, b = inp["weight"], inp["bias"]
-    ops = torch.ops.tvdcn
-
-    def run():
-        with torch.inference_mode():
-            ops.deform_conv2d(x, w, o, m, b, [1, 1], [1, 1], [1, 1], 1)
-            ops._deform_conv2d_backward(g, x, w, o, m, b, [1, 1], [1, 1], [1, 1], 1)
-
-    t0 = time.perf_counter()
-    run()   # warm-up
-    first = time.perf_counter() - t0
-    reps = 3 if first < 8.0 else 1
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    ms = statistics.median(times) * 1e3 * (8 / batch)
-    cores = len(os.sched_getaffinity(0))
-    model = "unknown CPU"
+def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
-            model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+            return next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
     except (OSError, StopIteration):
-        pass
-    return dict(value=round(ms, 1), unit="ms", cores=cores, kind="reference",
-                sample=f"reference CPU path (oracle/_ref: tvdcn 1.1.0 cpu/ kernels + ATen addmm_), forward+backward "
-                       f"of {batch} of the 8 images, median of {reps} after 1 warm-up, scaled x{8 // batch} to the "
-                       f"full batch; {model}; torch threads {torch.get_num_threads()}, reference OpenMP loops "
+        return "unknown CPU"
+
+
+def _reference_times(name, args, bwd_args, reps):
+    """(forward seconds, backward seconds) per call of the reference's CPU ops, median of `reps` calls
+    after one warm-up call each, in a child process (oracle/ref_child.py: the reference build registers
+    the torch.ops.tvdcn namespace, as this build's library does)."""
+    from oracle import oracle
+    res = oracle.run_reference([{"threads": None},
+                                {"op": name, "args": args, "repeat": reps + 1},
+                                {"op": f"_{name}_backward", "args": bwd_args, "repeat": reps + 1}])
+    fwd = statistics.median(res[1]["times"][1:])
+    bwd = statistics.median(res[2]["times"][1:])
+    return fwd, bwd, res[0]
+
+
+def cpu_baseline(inp, reps=3):
+    """The reference's CPU implementation (oracle/_ref) on the full workload: forward + backward of all
+    8 images, the same tensors the GPU run uses."""
+    from oracle import oracle
+    if not oracle.have_reference():
+        return None
+    args = [inp[k] for k in ("input", "weight", "offset", "mask", "bias")] + [[1, 1], [1, 1], [1, 1], 1]
+    fwd, bwd, threads = _reference_times("deform_conv2d", args, [inp["grad_out"]] + args, reps)
+    return dict(value=round((fwd + bwd) * 1e3, 1), unit="ms", cores=len(os.sched_getaffinity(0)),
+                kind="reference", fwd_ms=round(fwd * 1e3, 1), bwd_ms=round(bwd * 1e3, 1),
+                sample=f"reference CPU path (oracle/_ref: tvdcn 1.1.0 cpu/ kernels + ATen addmm_), forward and "
+                       f"backward of the full workload (8 of 8 images), each the median of {reps} calls after 1 "
+                       f"warm-up call; {_cpu_model()}; torch threads {threads['torch']}, reference OpenMP loops "
                        f"32 threads")
+
+
+def cpu_baseline_case(c, gout, reps=1):
+    """The reference's CPU path on a suite config's full tensors (mask given as its softmax / sigmoid
+    values; the reference runs the activation in torch, not timed here)."""
+    from oracle import oracle
+    if not oracle.have_reference():
+        return None
+    dim = c["x"].dim() - 2
+    m = c["m"]
+    if c["logits"] is not None:
+        B, ch = c["logits"].shape[:2]
+        kn = 1
+        for k in c["ks"]:
+            kn *= k
+        m = torch.softmax(c["logits"].view(B, ch // kn, kn, -1), 2).view(c["logits"].shape)
+    kw = c["kw"]
+    lst = lambda v: [v] * dim
+    params = [lst(kw["stride"]), lst(kw["padding"])] + ([lst(kw["output_padding"])] if c["tr"] else []) + \
+        [lst(kw["dilation"]), kw["groups"]]
+    args = [c["x"], c["w"], c["o"], m, c["b"]] + params
+    fwd, bwd, threads = _reference_times(c["op"], args, [gout] + args, reps)
+    return dict(fwd_ms=round(fwd * 1e3, 1), fwd_bwd_ms=round((fwd + bwd) * 1e3, 1),
+                cores=len(os.sched_getaffinity(0)), kind="reference", torch_threads=threads["torch"],
+                sample=f"full workload, {reps} call(s) each after 1 warm-up call")
 
 
 def main():
@@ -324,7 +361,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-batch", type=int, default=2, help="images of the workload timed on the CPU (divides 8)")
+    ap.add_argument("--cpu-reps", type=int, default=3, help="timed reference CPU calls (after one warm-up call)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--configs", action="store_true",
                     help="instead of the metric line, print one JSON line per BASELINE config 2-5 (cfg5 also in "
@@ -353,7 +390,8 @@ def main():
     if args.configs:
         for n, dt in SUITE:
             print(f"[bench] suite cfg{n} {dt}", file=sys.stderr, flush=True)
-            print(json.dumps(run_suite_case(n, dt, args.steps, args.warmup)), flush=True)
+            print(json.dumps(run_suite_case(n, dt, args.steps, args.warmup, cpu=not args.no_cpu_baseline)),
+                  flush=True)
             torch.cuda.empty_cache()
         return
 
@@ -371,7 +409,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(inp, args.cpu_batch)
+        cpu = cpu_baseline(inp, args.cpu_reps)
         if cpu:
             print(f"[bench] cpu baseline {cpu['value']} ms ({cpu['cores']} cores)", file=sys.stderr, flush=True)
 

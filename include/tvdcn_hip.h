@@ -71,9 +71,15 @@ typedef enum {
  * folded into the mask load), and the backward's grad_mask is the gradient with respect to the
  * logits. Needs a mask and mask_scale > 0. No counterpart in the reference, whose packed modules
  * run the activation as a separate pass.
+ * TVDCN_FLAG_MASK_SOFTMAX = the mask tensor holds logits: the kernels use their softmax over the
+ * prod(kernel) taps of each (batch, mask group, column pixel) as the mask (tvdcn's
+ * mask_softmax{1,2,3}d, ops/activations/mask_softmax.py:19-126, folded into the mask load), and
+ * the backward's grad_mask is the gradient with respect to the logits. Needs a mask; excludes
+ * TVDCN_FLAG_MASK_SIGMOID. Same counterpart as above.
  */
 #define TVDCN_FLAG_CHANNELS_LAST 1
 #define TVDCN_FLAG_MASK_SIGMOID 2
+#define TVDCN_FLAG_MASK_SOFTMAX 4
 typedef struct {
     int32_t dim;
     int32_t transposed;

@@ -6,8 +6,9 @@ Two checkers live under oracle/:
   (``deform_oracle.c``); wrapped by :func:`forward`, :func:`backward`,
   :func:`mask_softmax_forward`, :func:`mask_softmax_backward`.
 * ``_ref/libtvdcn_ref.so`` -- the reference's own CPU path compiled from its
-  sources by ``oracle/Makefile``; :func:`load_reference` registers it as
-  ``torch.ops.tvdcn``.
+  sources by ``oracle/Makefile``. It registers the ``torch.ops.tvdcn`` namespace,
+  as the product library does, so :func:`run_reference` runs it in a child
+  process (``oracle/ref_child.py``).
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg import
 this module. Product code (tvdcn_amd/) never does.
@@ -15,6 +16,8 @@ this module. Product code (tvdcn_amd/) never does.
 import ctypes
 import os
 import subprocess
+import sys
+import tempfile
 
 import torch
 
@@ -23,7 +26,6 @@ ORACLE_LIB = os.path.join(_HERE, "_build", "liboracle.so")
 REF_LIB = os.path.join(_HERE, "_ref", "libtvdcn_ref.so")
 
 _lib = None
-_ref_loaded = False
 
 
 class _Desc(ctypes.Structure):
@@ -74,16 +76,25 @@ def _load():
     return _lib
 
 
-def load_reference():
-    """Register the reference's own CPU ops as torch.ops.tvdcn (idempotent). Returns bool."""
-    global _ref_loaded
-    if _ref_loaded:
-        return True
-    if not os.path.exists(REF_LIB):
-        return False
-    torch.ops.load_library(REF_LIB)
-    _ref_loaded = True
-    return True
+def have_reference():
+    """True when the reference's CPU build (oracle/_ref) exists."""
+    return os.path.exists(REF_LIB)
+
+
+def run_reference(requests, env=None):
+    """Runs requests (see oracle/ref_child.py) against the reference build in a child process;
+    returns the list of results. CPU tensors only."""
+    if not have_reference():
+        raise RuntimeError(f"{REF_LIB} is not built")
+    root = os.path.dirname(_HERE)
+    with tempfile.TemporaryDirectory() as tmp:
+        src, dst = os.path.join(tmp, "req.pt"), os.path.join(tmp, "res.pt")
+        torch.save(list(requests), src)
+        proc = subprocess.run([sys.executable, "-m", "oracle.ref_child", src, dst], cwd=root, env=env,
+                              stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"reference child process failed ({proc.returncode}):\n{proc.stdout}")
+        return torch.load(dst, weights_only=True)
 
 
 def _ptr(t):

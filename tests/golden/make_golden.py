@@ -102,8 +102,11 @@ def run_reference(c, ts):
 
 def main():
     from oracle import oracle
-    if not oracle.load_reference():
+    if not oracle.have_reference():
         raise SystemExit("oracle/_ref/libtvdcn_ref.so is missing: run `make -C oracle ref` first")
+    # this script loads the reference build only (never the product library, which registers
+    # the same torch.ops.tvdcn namespace)
+    torch.ops.load_library(oracle.REF_LIB)
     gen = torch.Generator().manual_seed(12)
     n = 0
     for c in cases():

@@ -52,3 +52,39 @@ def make_case(dim, transposed=False, batch=2, cin=4, cout=6, groups=1, og=1, mg=
     return dict(dim=dim, transposed=transposed, input=cast(x), weight=cast(w), offset=cast(off), mask=cast(msk),
                 bias=cast(b), stride=stride, padding=padding, dilation=dilation, output_padding=out_pad,
                 groups=groups, out_shape=[batch, cout] + o)
+
+
+class OracleDeformConv(torch.autograd.Function):
+    """The float64 oracle as an autograd function on CPU tensors: a reference for compositions
+    (generator convolutions, mask activations) whose other parts torch differentiates in float64."""
+
+    @staticmethod
+    def forward(ctx, x, w, o, m, b, dim, params):
+        from oracle import oracle
+        ctx.save_for_backward(x, w, o, m, b)
+        ctx.dim, ctx.params = dim, params
+        return oracle.forward(dim, x, w, o, m, b, **params)
+
+    @staticmethod
+    def backward(ctx, g):
+        from oracle import oracle
+        x, w, o, m, b = ctx.saved_tensors
+        grads = oracle.backward(ctx.dim, g.contiguous(), x, w, o, m, b, **ctx.params)
+        return tuple(grads) + (None, None)
+
+
+def oracle_conv(dim, x, w, o, m, b, stride, padding, dilation, groups, transposed=False, output_padding=0):
+    """deform_conv{dim}d / deform_conv_transpose{dim}d through the float64 oracle, differentiable"""
+    params = dict(stride=stride, padding=padding, dilation=dilation, groups=groups, transposed=transposed,
+                  output_padding=output_padding)
+    return OracleDeformConv.apply(x, w, o, m, b, dim, params)
+
+
+def mask_activation_f64(logits, activation, kernel_numel, scale=2.0):
+    """the packed modules' mask activations in float64 torch ops: 1 = scale * sigmoid, 2 = softmax over the
+    kernel taps of each mask group (tvdcn/ops/activations/mask_sigmoid.py:11-21, mask_softmax.py:19-126)"""
+    if activation == 1:
+        return scale * torch.sigmoid(logits)
+    B, ch = logits.shape[:2]
+    v = logits.reshape(B, ch // kernel_numel, kernel_numel, -1)
+    return torch.softmax(v, dim=2).reshape(logits.shape)

@@ -16,8 +16,8 @@ import re
 import pytest
 import torch
 
-import tvdcn_amd
-from tvdcn_amd import extension
+import tvdcn
+from tvdcn import extension
 from oracle import oracle
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -36,10 +36,10 @@ def lib():
 
 
 def test_native_library_loaded():
-    assert tvdcn_amd.has_ops()
-    assert tvdcn_amd.with_cuda()
-    assert tvdcn_amd.cuda_arch_list() == ["gfx950"]
-    assert tvdcn_amd.cuda_version() > 60000000
+    assert tvdcn.has_ops()
+    assert tvdcn.with_cuda()
+    assert tvdcn.cuda_arch_list() == ["gfx950"]
+    assert tvdcn.cuda_version() > 60000000
 
 
 def test_c_abi_exports_every_declared_function(lib):
@@ -119,7 +119,9 @@ def test_c_abi_argument_errors(lib):
                                        None, None, ctypes.c_size_t(0), None)
     assert st == 1 and b"offset_groups" in lib.tvdcn_last_error()
     # descriptor flags: unknown bits, and channels-last input on the transposed op
-    for d, msg in ((cfg2_desc(flags=4), b"unknown flags"),
+    for d, msg in ((cfg2_desc(flags=8), b"unknown flags"),
+                   (cfg2_desc(flags=6, mask_scale=2.0), b"exclude each other"),
+                   (cfg2_desc(flags=4, mask_groups=0), b"softmax mask"),
                    (cfg2_desc(flags=1, transposed=1, out_channels=128, offset_groups=2, mask_groups=2),
                     b"channels-last"),
                    (cfg2_desc(flags=2, mask_scale=0.0), b"sigmoid mask"),
@@ -141,24 +143,30 @@ REF_SCHEMAS = {
 }
 
 
+TWELVE = [n for dim in (1, 2, 3) for base in (f"deform_conv{dim}d", f"deform_conv_transpose{dim}d")
+          for n in (base, f"_{base}_backward")]
+
+
+@pytest.fixture(scope="module")
+def reference_schemas():
+    """schema strings of the reference build (run in a child process: it registers torch.ops.tvdcn too)"""
+    if not oracle.have_reference():
+        return None
+    return dict(zip(TWELVE, oracle.run_reference([{"schema": n} for n in TWELVE])))
+
+
 @pytest.mark.parametrize("name", sorted(REF_SCHEMAS))
 def test_schemas_match_reference(name):
-    schema = str(getattr(torch.ops.tvdcn_amd, name).default._schema)
-    assert schema == f"tvdcn_amd::{name}{REF_SCHEMAS[name]}"
+    schema = str(getattr(torch.ops.tvdcn, name).default._schema)
+    assert schema == f"tvdcn::{name}{REF_SCHEMAS[name]}"
 
 
-def test_all_twelve_ops_and_backward_schemas_exist():
-    for dim in (1, 2, 3):
-        for base in (f"deform_conv{dim}d", f"deform_conv_transpose{dim}d"):
-            fwd = str(getattr(torch.ops.tvdcn_amd, base).default._schema)
-            bwd = str(getattr(torch.ops.tvdcn_amd, f"_{base}_backward").default._schema)
-            assert "-> Tensor" in fwd
-            assert bwd.endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
-            if oracle.load_reference():
-                ref_f = str(getattr(torch.ops.tvdcn, base).default._schema).split("::", 1)[1]
-                ref_b = str(getattr(torch.ops.tvdcn, f"_{base}_backward").default._schema).split("::", 1)[1]
-                assert fwd.split("::", 1)[1] == ref_f
-                assert bwd.split("::", 1)[1] == ref_b
+def test_all_twelve_ops_and_backward_schemas_exist(reference_schemas):
+    for name in TWELVE:
+        schema = str(getattr(torch.ops.tvdcn, name).default._schema)
+        assert schema.endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor)" if name.startswith("_") else "-> Tensor")
+        if reference_schemas is not None:
+            assert schema == reference_schemas[name]
 
 
 def meta(*shape):
@@ -173,29 +181,16 @@ def test_meta_shapes(dim):
     for kk in k:
         kn *= kk
     out = [s - kk + 1 for s, kk in zip(sz, k)]
-    y = getattr(tvdcn_amd, f"deform_conv{dim}d")(meta(2, 4, *sz), meta(6, 2, *k), meta(2, 2 * dim * kn, *out),
+    y = getattr(tvdcn, f"deform_conv{dim}d")(meta(2, 4, *sz), meta(6, 2, *k), meta(2, 2 * dim * kn, *out),
                                                  meta(2, 3 * kn, *out)[:, :kn], meta(6), groups=2)
     assert list(y.shape) == [2, 6] + out
-    yt = getattr(tvdcn_amd, f"deform_conv_transpose{dim}d")(meta(2, 4, *sz), meta(4, 3, *k), meta(2, dim * kn, *sz),
+    yt = getattr(tvdcn, f"deform_conv_transpose{dim}d")(meta(2, 4, *sz), meta(4, 3, *k), meta(2, dim * kn, *sz),
                                                             None, meta(6), stride=2, padding=1, output_padding=1,
                                                             groups=2)
     assert list(yt.shape) == [2, 6] + [(s - 1) * 2 - 2 + kk + 1 for s, kk in zip(sz, k)]
     # unbatched
-    y1 = getattr(tvdcn_amd, f"deform_conv{dim}d")(meta(4, *sz), meta(6, 4, *k), meta(dim * kn, *out))
+    y1 = getattr(tvdcn, f"deform_conv{dim}d")(meta(4, *sz), meta(6, 4, *k), meta(dim * kn, *out))
     assert list(y1.shape) == [6] + out
-
-
-def reference_error(fn_name, *args):
-    """message raised by the reference build for the same (CPU) arguments, or None"""
-    if not oracle.load_reference():
-        return None
-    cpu = [torch.zeros(a.shape) if isinstance(a, torch.Tensor) else a for a in args]
-    try:
-        with torch.inference_mode():
-            getattr(torch.ops.tvdcn, fn_name)(*cpu)
-    except RuntimeError as e:
-        return str(e)
-    return ""
 
 
 INVALID = [
@@ -216,14 +211,25 @@ INVALID = [
 ]
 
 
+@pytest.fixture(scope="module")
+def reference_errors():
+    """message the reference build raises for each INVALID case on CPU zeros of the same shapes"""
+    if not oracle.have_reference():
+        return None
+    reqs = [{"error": "deform_conv2d",
+             "args": [torch.zeros(a.shape) if isinstance(a, torch.Tensor) else a for a in args] +
+                     [[1, 1], [0, 0], [1, 1], 1]} for _, args, _ in INVALID]
+    return dict(zip((c[0] for c in INVALID), oracle.run_reference(reqs)))
+
+
 @pytest.mark.parametrize("label,args,msg", INVALID, ids=[c[0] for c in INVALID])
-def test_validation_errors_match_reference(label, args, msg):
+def test_validation_errors_match_reference(label, args, msg, reference_errors):
     with pytest.raises(RuntimeError) as ei:
-        torch.ops.tvdcn_amd.deform_conv2d(*args, [1, 1], [0, 0], [1, 1], 1)
+        torch.ops.tvdcn.deform_conv2d(*args, [1, 1], [0, 0], [1, 1], 1)
     assert msg in str(ei.value)
-    ref = reference_error("deform_conv2d", *args, [1, 1], [0, 0], [1, 1], 1)
-    if ref is not None:
-        assert msg in ref, ref
+    if reference_errors is not None:
+        ref = reference_errors[label]
+        assert ref is not None and msg in ref, ref
 
 
 @pytest.mark.parametrize("what", ["stride", "pad", "dilation"])
@@ -231,26 +237,26 @@ def test_parameter_errors(what):
     s, p, d = [1, 1], [0, 0], [1, 1]
     {"stride": s, "pad": p, "dilation": d}[what][0] = -1 if what == "pad" else 0
     with pytest.raises(RuntimeError, match=what + "_h"):
-        torch.ops.tvdcn_amd.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, None, None, s, p, d, 1)
+        torch.ops.tvdcn.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, None, None, s, p, d, 1)
 
 
 def test_groups_error():
     with pytest.raises(RuntimeError, match="groups"):
-        torch.ops.tvdcn_amd.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, None, None, [1, 1], [0, 0],
+        torch.ops.tvdcn.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3), None, None, None, [1, 1], [0, 0],
                                           [1, 1], 2)
 
 
 def test_dtype_mismatch_error():
     with pytest.raises(RuntimeError):
-        torch.ops.tvdcn_amd.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3).double(), None, None, None, [1, 1],
+        torch.ops.tvdcn.deform_conv2d(meta(2, 4, 8, 8), meta(5, 4, 3, 3).double(), None, None, None, [1, 1],
                                           [0, 0], [1, 1], 1)
 
 
 def test_cpu_tensors_are_refused():
     with pytest.raises(NotImplementedError, match="CPU"):
-        tvdcn_amd.deform_conv2d(torch.rand(1, 2, 5, 5), torch.rand(2, 2, 3, 3), torch.rand(1, 18, 3, 3))
+        tvdcn.deform_conv2d(torch.rand(1, 2, 5, 5), torch.rand(2, 2, 3, 3), torch.rand(1, 18, 3, 3))
     with pytest.raises(NotImplementedError, match="CPU"):
-        tvdcn_amd.mask_softmax2d(torch.rand(1, 9, 3, 3), (3, 3))
+        tvdcn.mask_softmax2d(torch.rand(1, 9, 3, 3), (3, 3))
 
 
 def test_meta_autograd_and_double_backward():
@@ -259,7 +265,7 @@ def test_meta_autograd_and_double_backward():
     o = meta(2, 18, 6, 6).requires_grad_(True)
     m = meta(2, 9, 6, 6).requires_grad_(True)
     b = meta(5).requires_grad_(True)
-    y = tvdcn_amd.deform_conv2d(x, w, o, m, b)
+    y = tvdcn.deform_conv2d(x, w, o, m, b)
     gx, gw, go, gm, gb = torch.autograd.grad(y.sum(), (x, w, o, m, b), create_graph=True)
     assert gx.shape == x.shape and gw.shape == w.shape and go.shape == o.shape and gm.shape == m.shape
     assert gb.shape == b.shape
@@ -270,56 +276,56 @@ def test_meta_autograd_and_double_backward():
 def test_meta_autograd_without_offset_mask_bias():
     x = meta(2, 4, 8, 8).requires_grad_(True)
     w = meta(5, 4, 3, 3).requires_grad_(True)
-    y = tvdcn_amd.deform_conv2d(x, w)
+    y = tvdcn.deform_conv2d(x, w)
     y.sum().backward()
     assert x.grad.shape == x.shape and w.grad.shape == w.shape
-    gs = torch.ops.tvdcn_amd._deform_conv2d_backward(meta(2, 5, 6, 6), meta(2, 4, 8, 8), meta(5, 4, 3, 3), None,
+    gs = torch.ops.tvdcn._deform_conv2d_backward(meta(2, 5, 6, 6), meta(2, 4, 8, 8), meta(5, 4, 3, 3), None,
                                                      None, None, [1, 1], [0, 0], [1, 1], 1)
     assert gs[2] is None and gs[3] is None and gs[4] is None
 
 
 def test_modules_api():
-    m = tvdcn_amd.DeformConv2d(4, 6, 3, padding=1, groups=2, bias=False)
+    m = tvdcn.DeformConv2d(4, 6, 3, padding=1, groups=2, bias=False)
     assert m.weight.shape == (6, 2, 3, 3) and m.bias is None
     assert "bias=False" in repr(m) and "groups=2" in repr(m)
-    p = tvdcn_amd.PackedDeformConv2d(4, 8, 3, padding=1, offset_groups=2, mask_groups=4, modulated=True,
+    p = tvdcn.PackedDeformConv2d(4, 8, 3, padding=1, offset_groups=2, mask_groups=4, modulated=True,
                                      mask_activation="softmax")
     assert p.offset_generator.weight.shape == (2 * 9 * 2, 2, 3, 3)
     assert p.mask_generator.weight.shape == (9 * 4, 1, 3, 3)
     assert float(p.offset_generator.weight.detach().abs().sum()) == 0.0
-    assert isinstance(p.mask_activation, tvdcn_amd.MaskSoftmax2d)
-    t = tvdcn_amd.PackedDeformConvTranspose2d(4, 6, 4, stride=2, padding=1, modulated=True)
+    assert isinstance(p.mask_activation, tvdcn.MaskSoftmax2d)
+    t = tvdcn.PackedDeformConvTranspose2d(4, 6, 4, stride=2, padding=1, modulated=True)
     assert t.offset_generator.kernel_size == (1, 1) and t.mask_generator.out_channels == 16
-    assert isinstance(t.mask_activation, tvdcn_amd.MaskSigmoid) and t.mask_activation.scale == 2.0
-    for cls in (tvdcn_amd.PackedDeformConv1d, tvdcn_amd.PackedDeformConv3d, tvdcn_amd.PackedDeformConvTranspose1d,
-                tvdcn_amd.PackedDeformConvTranspose3d):
+    assert isinstance(t.mask_activation, tvdcn.MaskSigmoid) and t.mask_activation.scale == 2.0
+    for cls in (tvdcn.PackedDeformConv1d, tvdcn.PackedDeformConv3d, tvdcn.PackedDeformConvTranspose1d,
+                tvdcn.PackedDeformConvTranspose3d):
         assert cls(4, 4, 3).deformable
     with pytest.raises(ValueError, match="in_channels must be divisible by offset_groups"):
-        tvdcn_amd.PackedDeformConv2d(4, 8, 3, offset_groups=3)
+        tvdcn.PackedDeformConv2d(4, 8, 3, offset_groups=3)
     with pytest.raises(ValueError, match="out_channels must be divisible by mask_groups"):
-        tvdcn_amd.PackedDeformConv2d(4, 6, 3, mask_groups=4)
+        tvdcn.PackedDeformConv2d(4, 6, 3, mask_groups=4)
     with pytest.raises(ValueError, match="no activation is supported for offset"):
-        tvdcn_amd.PackedDeformConv2d(4, 8, 3, offset_activation="tanh")
+        tvdcn.PackedDeformConv2d(4, 8, 3, offset_activation="tanh")
     with pytest.raises(ValueError, match="only"):
-        tvdcn_amd.PackedDeformConv2d(4, 8, 3, mask_activation="relu")
+        tvdcn.PackedDeformConv2d(4, 8, 3, mask_activation="relu")
 
 
 def test_module_forward_on_meta():
-    m = tvdcn_amd.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True, device="meta")
+    m = tvdcn.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True, device="meta")
     assert m(meta(2, 4, 8, 8)).shape == (2, 6, 8, 8)
-    r = tvdcn_amd.DeformConv2d(4, 6, 3, padding=1, padding_mode="reflect", device="meta")
+    r = tvdcn.DeformConv2d(4, 6, 3, padding=1, padding_mode="reflect", device="meta")
     assert r(meta(2, 4, 8, 8), meta(2, 18, 8, 8)).shape == (2, 6, 8, 8)
-    t = tvdcn_amd.DeformConvTranspose2d(4, 6, 3, stride=2, padding=1, device="meta")
+    t = tvdcn.DeformConvTranspose2d(4, 6, 3, stride=2, padding=1, device="meta")
     assert t(meta(2, 4, 5, 5), None, output_size=[10, 10]).shape == (2, 6, 10, 10)
     with pytest.raises(ValueError, match="requested an output size"):
         t(meta(2, 4, 5, 5), None, output_size=[20, 20])
-    bad = tvdcn_amd.DeformConvTranspose2d(4, 6, 3, padding_mode="reflect", device="meta")
+    bad = tvdcn.DeformConvTranspose2d(4, 6, 3, padding_mode="reflect", device="meta")
     with pytest.raises(ValueError, match="zeros"):
         bad(meta(2, 4, 5, 5), None)
 
 
 def test_output_padding_matches_torch_rule():
-    ours = tvdcn_amd.DeformConvTranspose2d(4, 6, 3, stride=3, padding=1, dilation=2)
+    ours = tvdcn.DeformConvTranspose2d(4, 6, 3, stride=3, padding=1, dilation=2)
     ref = torch.nn.ConvTranspose2d(4, 6, 3, stride=3, padding=1, dilation=2)
     x = torch.empty(1, 4, 7, 5)
     for size in ([21, 15], [22, 16], [23, 17]):
@@ -329,13 +335,13 @@ def test_output_padding_matches_torch_rule():
 
 def test_mask_activation_errors():
     with pytest.raises(ValueError, match="scale must be positive"):
-        tvdcn_amd.mask_sigmoid(torch.zeros(2), scale=0.0)
-    assert torch.allclose(tvdcn_amd.mask_sigmoid(torch.zeros(3)), torch.ones(3))
+        tvdcn.mask_sigmoid(torch.zeros(2), scale=0.0)
+    assert torch.allclose(tvdcn.mask_sigmoid(torch.zeros(3)), torch.ones(3))
     with pytest.raises(RuntimeError, match="mask tensor at dimension 1 is not valid"):
-        tvdcn_amd.mask_softmax2d(meta(2, 5, 3, 3), (3, 3))
-    y = tvdcn_amd.mask_softmax3d(meta(2, 54, 2, 3, 4), 3)
+        tvdcn.mask_softmax2d(meta(2, 5, 3, 3), (3, 3))
+    y = tvdcn.mask_softmax3d(meta(2, 54, 2, 3, 4), 3)
     assert y.shape == (2, 54, 2, 3, 4)
-    assert tvdcn_amd.MaskSoftmax1d(5)(meta(2, 10, 7)).shape == (2, 10, 7)
+    assert tvdcn.MaskSoftmax1d(5)(meta(2, 10, 7)).shape == (2, 10, 7)
 
 
 def fastdiv(n, d):
@@ -367,14 +373,14 @@ def test_torch_compile_fullgraph_on_meta(dim, transposed):
     k = 3
     S = [6] * dim
     if transposed:
-        fn = getattr(tvdcn_amd, f"deform_conv_transpose{dim}d")
+        fn = getattr(tvdcn, f"deform_conv_transpose{dim}d")
         x = meta(2, 4, *S)
         w = meta(4, 3, *[k] * dim)                    # (Cin, Cout, k...)
         out_sz = [s + k - 1 for s in S]
         o = meta(2, dim * k ** dim, *S)                # offsets on the input grid
         m = meta(2, k ** dim, *S)
     else:
-        fn = getattr(tvdcn_amd, f"deform_conv{dim}d")
+        fn = getattr(tvdcn, f"deform_conv{dim}d")
         x = meta(2, 4, *S)
         w = meta(5, 4, *[k] * dim)
         out_sz = [s - k + 1 for s in S]
@@ -396,27 +402,122 @@ def test_torch_compile_fullgraph_on_meta(dim, transposed):
         assert list(fn(x, w, o, m, b).shape[2:]) == out_sz
 
 
-def test_sigmoid_mask_op_on_meta():
-    """The fused sigmoid-mask op: shapes, gradients to the logits, double-backward refusal, and a
-    packed module with the default mask activation taking it."""
+@pytest.mark.parametrize("activation", [1, 2])
+def test_mask_activation_op_on_meta(activation):
+    """The fused mask-activation op: shapes, gradients to the logits, double-backward refusal, argument
+    errors, and the packed modules' choice of the fused path."""
     x = meta(2, 4, 8, 8).requires_grad_(True)
     w = meta(5, 4, 3, 3).requires_grad_(True)
     o = meta(2, 18, 6, 6).requires_grad_(True)
     lg = meta(2, 9, 6, 6).requires_grad_(True)
-    y = torch.ops.tvdcn_amd.deform_conv_sigmoid_mask(x, w, o, lg, None, [1, 1], [0, 0], [0, 0], [1, 1], 1, False,
-                                                     2.0)
+    op = torch.ops.tvdcn.deform_conv_mask_activation
+    y = op(x, w, o, lg, None, [1, 1], [0, 0], [0, 0], [1, 1], 1, False, activation, 2.0)
     assert y.shape == (2, 5, 6, 6)
     gx, gw, go, gl = torch.autograd.grad(y.sum(), (x, w, o, lg), create_graph=True)
     assert gl.shape == lg.shape and go.shape == o.shape
-    with pytest.raises(RuntimeError, match="double backwards on deform_conv_sigmoid_mask not supported"):
+    with pytest.raises(RuntimeError, match="double backwards on deform_conv_mask_activation not supported"):
         gl.sum().backward()
-    with pytest.raises(RuntimeError, match="mask_scale"):
-        torch.ops.tvdcn_amd.deform_conv_sigmoid_mask(x, w, o, lg, None, [1, 1], [0, 0], [0, 0], [1, 1], 1, False, 0.0)
-    m = tvdcn_amd.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True, device="meta")
-    offset, logits, scale = m._generate(meta(2, 4, 8, 8))
-    assert scale == 2.0 and logits.shape == (2, 9, 8, 8)
-    s = tvdcn_amd.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True, mask_activation="softmax", device="meta")
-    assert s._generate(meta(2, 4, 8, 8))[2] is None
+    with pytest.raises(RuntimeError, match="activation must be"):
+        op(x, w, o, lg, None, [1, 1], [0, 0], [0, 0], [1, 1], 1, False, 3, 2.0)
+    if activation == 1:
+        with pytest.raises(RuntimeError, match="mask_scale"):
+            op(x, w, o, lg, None, [1, 1], [0, 0], [0, 0], [1, 1], 1, False, 1, 0.0)
+
+
+def test_packed_modules_choose_the_fused_mask_activation():
+    name = "sigmoid"
+    for cls, ks in ((tvdcn.PackedDeformConv2d, (3, 3)), (tvdcn.PackedDeformConvTranspose1d, (3,))):
+        for name, code in (("sigmoid", 1), ("softmax", 2)):
+            m = cls(4, 6, 3, modulated=True, mask_activation=name, device="meta")
+            assert m._mask_fusion()[0] == code
+            offset, logits, fused, scale = m._generate(meta(2, 4, *([8] * len(ks))))
+            assert fused == code and logits.shape[1] == len(ks) and (scale == 2.0 or code == 2) or \
+                logits.shape[1] == 3 ** len(ks)
+    m = tvdcn.PackedDeformConv2d(4, 6, 3, modulated=True, device="meta")
+    m.mask_activation = torch.nn.Sigmoid()            # any other activation runs as a module
+    assert m._mask_fusion() == (0, 0.0)
+    m.mask_activation = tvdcn.MaskSoftmax2d((3, 1))   # a softmax over other taps is not fused
+    assert m._mask_fusion() == (0, 0.0)
+    m.mask_activation = tvdcn.MaskSigmoid(0.5)
+    assert m._mask_fusion() == (1, 0.5)
+    m.mask_activation = tvdcn.MaskSigmoid(-1.0)       # left to MaskSigmoid, which raises ValueError
+    assert m._mask_fusion() == (0, 0.0)
+    with pytest.raises(ValueError, match="scale must be positive"):
+        m(meta(2, 4, 8, 8))
+
+
+MODULES = [
+    ("DeformConv1d", (4, 6, 3), (2, 4, 9)), ("DeformConv2d", (4, 6, 3), (2, 4, 9, 8)),
+    ("DeformConv3d", (4, 6, 3), (2, 4, 5, 6, 7)),
+    ("DeformConvTranspose1d", (4, 6, 3), (2, 4, 9)), ("DeformConvTranspose2d", (4, 6, 3), (2, 4, 9, 8)),
+    ("DeformConvTranspose3d", (4, 6, 3), (2, 4, 5, 6, 7)),
+    ("PackedDeformConv1d", (4, 6, 3), (2, 4, 9)), ("PackedDeformConv2d", (4, 6, 3), (2, 4, 9, 8)),
+    ("PackedDeformConv3d", (4, 6, 3), (2, 4, 5, 6, 7)),
+    ("PackedDeformConvTranspose1d", (4, 6, 3), (2, 4, 9)),
+    ("PackedDeformConvTranspose2d", (4, 6, 3), (2, 4, 9, 8)),
+    ("PackedDeformConvTranspose3d", (4, 6, 3), (2, 4, 5, 6, 7)),
+    ("MaskSoftmax1d", (3,), (2, 6, 9)), ("MaskSoftmax2d", (3,), (2, 18, 9, 8)),
+    ("MaskSoftmax3d", (3,), (2, 54, 5, 6, 7)), ("MaskSigmoid", (), (2, 9, 8)),
+]
+
+
+@pytest.mark.parametrize("packed_kw", [{}, {"modulated": True}, {"modulated": True, "mask_activation": "softmax"},
+                                       {"deformable": False, "modulated": True}, {"padding_mode": "reflect"}])
+@pytest.mark.parametrize("name,args,shape", MODULES, ids=[m[0] for m in MODULES])
+def test_torchscript_modules(name, args, shape, packed_kw):
+    """Every module class compiles with torch.jit.script, as tvdcn's examples do
+    (examples/deform_conv_modules_example.py:8,23), and the scripted module computes the eager
+    module's shapes (meta tensors: the Meta kernels run the same validation)."""
+    cls = getattr(tvdcn, name)
+    kw = {}
+    if name.startswith("Packed"):
+        kw = dict(packed_kw)
+        if "Transpose" in name and kw.get("padding_mode", "zeros") != "zeros":
+            kw.pop("padding_mode")
+    elif packed_kw:
+        pytest.skip("packed-module options")
+    if name.startswith("Deform") and "Transpose" not in name:
+        kw["padding"] = 1
+    m = cls(*args, **kw, device="meta") if not name.startswith("Mask") else cls(*args)
+    sm = torch.jit.script(m)
+    x = meta(*shape)
+    if name.startswith("Packed") or name.startswith("Mask"):
+        ins = (x,)
+    else:
+        dim = len(shape) - 2
+        k = 3 ** dim
+        grid = shape[2:]
+        ins = (x, meta(shape[0], dim * k, *grid), meta(shape[0], k, *grid))
+    assert sm(*ins).shape == m(*ins).shape
+
+
+def test_torchscript_functional_defaults():
+    """The functional ops script with their int defaults (int-or-tuple parameters)"""
+    f = torch.jit.script(tvdcn.deform_conv2d)
+    y = f(meta(2, 4, 9, 8), meta(6, 4, 3, 3))
+    assert y.shape == (2, 6, 7, 6)
+    y = f(meta(2, 4, 9, 8), meta(6, 4, 3, 3), padding=1, stride=(2, 1))
+    assert y.shape == (2, 6, 5, 8)
+    ft = torch.jit.script(tvdcn.deform_conv_transpose1d)
+    assert ft(meta(2, 4, 9), meta(4, 6, 3), stride=2, output_padding=1).shape == (2, 6, 20)
+
+
+def test_drop_in_package_layout():
+    """import tvdcn gives the reference's package layout (tvdcn/__init__.py, tvdcn/ops/__init__.py,
+    tvdcn/ops/activations/__init__.py) on the MI355X implementation"""
+    import importlib
+    import tvdcn_amd
+    for mod in ("tvdcn.ops", "tvdcn.ops.activations", "tvdcn.ops.activations.mask_softmax",
+                "tvdcn.ops.activations.mask_sigmoid", "tvdcn.ops.deform_conv", "tvdcn.ops.deform_conv_transpose",
+                "tvdcn.extension", "tvdcn.utils"):
+        assert importlib.import_module(mod) is importlib.import_module(mod.replace("tvdcn", "tvdcn_amd", 1))
+    from tvdcn.ops import deform_conv2d, PackedDeformConvTranspose3d  # noqa: F401
+    from tvdcn.ops.activations import MaskSigmoid, mask_softmax2d  # noqa: F401
+    public = [n for n in dir(tvdcn_amd) if not n.startswith("_")]
+    for n in public:
+        assert getattr(tvdcn, n) is getattr(tvdcn_amd, n)
+    assert tvdcn.deform_conv2d is tvdcn.ops.deform_conv2d
+    assert torch.ops.tvdcn.deform_conv2d.default._schema.name == "tvdcn::deform_conv2d"
 
 
 @pytest.mark.parametrize("dim,transposed", [(1, 0), (2, 0), (3, 0), (2, 1)])

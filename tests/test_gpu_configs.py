@@ -17,13 +17,13 @@ import numpy as np
 import pytest
 import torch
 
-import tvdcn_amd
+import tvdcn
 from oracle import oracle
 from helpers import rel_err
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-HAVE_REF = os.path.exists(oracle.REF_LIB)
+HAVE_REF = oracle.have_reference()
 
 
 def kaiming(shape, fan_in, g):
@@ -66,18 +66,13 @@ def config(n):
 
 
 def reference(c, gout):
-    assert oracle.load_reference()
-    ops = torch.ops.tvdcn
+    """forward and the five gradients from the reference's CPU build (child process)"""
     dim = c["dim"]
-    args = (c["x"], c["w"], c["o"], c["m"], c["b"])
-    with torch.inference_mode():
-        if c["tr"]:
-            out = getattr(ops, f"deform_conv_transpose{dim}d")(*args, c["s"], c["p"], c["op"], c["d"], c["G"])
-            grads = getattr(ops, f"_deform_conv_transpose{dim}d_backward")(gout, *args, c["s"], c["p"], c["op"],
-                                                                            c["d"], c["G"])
-        else:
-            out = getattr(ops, f"deform_conv{dim}d")(*args, c["s"], c["p"], c["d"], c["G"])
-            grads = getattr(ops, f"_deform_conv{dim}d_backward")(gout, *args, c["s"], c["p"], c["d"], c["G"])
+    args = [c["x"], c["w"], c["o"], c["m"], c["b"]]
+    name = f"deform_conv_transpose{dim}d" if c["tr"] else f"deform_conv{dim}d"
+    params = [c["s"], c["p"], c["op"], c["d"], c["G"]] if c["tr"] else [c["s"], c["p"], c["d"], c["G"]]
+    out, grads = oracle.run_reference([{"op": name, "args": args + params},
+                                       {"op": f"_{name}_backward", "args": [gout] + args + params}])
     return out, grads
 
 
@@ -86,9 +81,9 @@ def ours(c, gout, dtype):
           for t in (c["x"], c["w"], c["o"], c["m"], c["b"])]
     dim = c["dim"]
     if c["tr"]:
-        out = getattr(tvdcn_amd, f"deform_conv_transpose{dim}d")(*ts, c["s"], c["p"], c["op"], c["d"], c["G"])
+        out = getattr(tvdcn, f"deform_conv_transpose{dim}d")(*ts, c["s"], c["p"], c["op"], c["d"], c["G"])
     else:
-        out = getattr(tvdcn_amd, f"deform_conv{dim}d")(*ts, c["s"], c["p"], c["d"], c["G"])
+        out = getattr(tvdcn, f"deform_conv{dim}d")(*ts, c["s"], c["p"], c["d"], c["G"])
     out.backward(gout.to(DEV, dtype))
     torch.cuda.synchronize()
     return out, [t.grad if t is not None else None for t in ts]
@@ -144,7 +139,7 @@ def test_cfg2_zero_offset_is_miopen_conv():
     """size-independent closed form at full size: zero offsets, unit mask == torch's own conv2d"""
     c = config(2)
     x, w = c["x"].to(DEV), c["w"].to(DEV)
-    out = tvdcn_amd.deform_conv2d(x, w, torch.zeros_like(c["o"]).to(DEV), torch.ones_like(c["m"]).to(DEV),
+    out = tvdcn.deform_conv2d(x, w, torch.zeros_like(c["o"]).to(DEV), torch.ones_like(c["m"]).to(DEV),
                                   None, 1, 1, 1)
     ref = torch.nn.functional.conv2d(x.double(), w.double(), padding=1)
     assert rel_err(out, ref) < 1e-5
@@ -163,9 +158,9 @@ def test_golden_fixture_on_gpu(path):
     names = ("input", "weight", "offset", "mask", "bias")
     ts = [t[n].to(DEV).requires_grad_(True) if n in t else None for n in names]
     if tr:
-        out = getattr(tvdcn_amd, f"deform_conv_transpose{dim}d")(*ts, s, p, op, d, G)
+        out = getattr(tvdcn, f"deform_conv_transpose{dim}d")(*ts, s, p, op, d, G)
     else:
-        out = getattr(tvdcn_amd, f"deform_conv{dim}d")(*ts, s, p, d, G)
+        out = getattr(tvdcn, f"deform_conv{dim}d")(*ts, s, p, d, G)
     out.backward(t["grad_out"].to(DEV))
     torch.cuda.synchronize()
     tf, tb = {torch.float64: (1e-9, 1e-9), torch.float32: (1e-5, 1e-4), torch.float16: (1e-2, 1e-2)}[dtype]
@@ -188,11 +183,11 @@ def test_empty_batch(transposed):
     if transposed:
         w = torch.rand(4, 3, 3, 3, device=DEV, requires_grad=True)
         o = torch.zeros(0, 18, 6, 6, device=DEV, requires_grad=True)
-        out = tvdcn_amd.deform_conv_transpose2d(x, w, o, None, torch.rand(3, device=DEV))
+        out = tvdcn.deform_conv_transpose2d(x, w, o, None, torch.rand(3, device=DEV))
     else:
         w = torch.rand(5, 4, 3, 3, device=DEV, requires_grad=True)
         o = torch.zeros(0, 18, 4, 4, device=DEV, requires_grad=True)
-        out = tvdcn_amd.deform_conv2d(x, w, o, None, torch.rand(5, device=DEV))
+        out = tvdcn.deform_conv2d(x, w, o, None, torch.rand(5, device=DEV))
     assert out.shape[0] == 0
     out.sum().backward()
     torch.cuda.synchronize()
@@ -206,7 +201,7 @@ def test_empty_batch_wide_gemm_side():
     w = torch.rand(32, 32, 3, 3, device=DEV, requires_grad=True)
     o = torch.zeros(0, 18, 4, 4, device=DEV, requires_grad=True)
     m = torch.zeros(0, 9, 4, 4, device=DEV, requires_grad=True)
-    out = tvdcn_amd.deform_conv2d(x, w, o, m)
+    out = tvdcn.deform_conv2d(x, w, o, m)
     out.sum().backward()
     torch.cuda.synchronize()
     assert out.shape == (0, 32, 4, 4) and w.grad.abs().sum().item() == 0.0
@@ -217,7 +212,7 @@ def test_mask_softmax_cfg3_shape_and_half():
     logits = torch.randn(16, 20, 4096, generator=g)
     for dtype, tol in [(torch.float32, 1e-6), (torch.float16, 1e-2), (torch.bfloat16, 1e-2)]:
         x = logits.to(DEV, dtype).requires_grad_(True)
-        y = tvdcn_amd.mask_softmax1d(x, 5)
+        y = tvdcn.mask_softmax1d(x, 5)
         ref = torch.softmax(logits.to(dtype).double().view(16, 4, 5, 4096), 2).view(16, 20, 4096)
         assert rel_err(y, ref) < tol
         gy = torch.randn(16, 20, 4096, generator=g)

@@ -9,7 +9,7 @@ against the eager ops on the same inputs.
 import pytest
 import torch
 
-import tvdcn_amd
+import tvdcn
 from helpers import make_case, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -19,10 +19,10 @@ DEV = "cuda:0"
 
 def _ops(dim, transposed):
     if transposed:
-        return (getattr(torch.ops.tvdcn_amd, f"deform_conv_transpose{dim}d"),
-                getattr(torch.ops.tvdcn_amd, f"_deform_conv_transpose{dim}d_backward"))
-    return (getattr(torch.ops.tvdcn_amd, f"deform_conv{dim}d"),
-            getattr(torch.ops.tvdcn_amd, f"_deform_conv{dim}d_backward"))
+        return (getattr(torch.ops.tvdcn, f"deform_conv_transpose{dim}d"),
+                getattr(torch.ops.tvdcn, f"_deform_conv_transpose{dim}d_backward"))
+    return (getattr(torch.ops.tvdcn, f"deform_conv{dim}d"),
+            getattr(torch.ops.tvdcn, f"_deform_conv{dim}d_backward"))
 
 
 @pytest.mark.parametrize("dim,transposed", [(2, False), (2, True), (3, False)])
@@ -82,7 +82,7 @@ def test_torch_compile_on_gpu_fp32():
     names = ("input", "weight", "offset", "mask", "bias")
 
     def f(x, w, o, m, b):
-        return (tvdcn_amd.deform_conv2d(x, w, o, m, b, padding=1) ** 2).sum()
+        return (tvdcn.deform_conv2d(x, w, o, m, b, padding=1) ** 2).sum()
 
     def leaves():
         return [case[n].to(DEV, torch.float32).requires_grad_(True) for n in names]

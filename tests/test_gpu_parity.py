@@ -1,4 +1,4 @@
-"""GPU parity: tvdcn_amd's HIP kernels against the float64 oracle (a C restatement of
+"""GPU parity: tvdcn's HIP kernels against the float64 oracle (a C restatement of
 tvdcn's CPU algorithm, itself pinned to the reference build and the golden fixtures).
 
 Tolerances (norm-wise, see helpers.rel_err): float64 1e-9; float32 forward 1e-5 and
@@ -10,7 +10,7 @@ import itertools
 import pytest
 import torch
 
-import tvdcn_amd
+import tvdcn
 from oracle import oracle
 from helpers import make_case, rel_err
 
@@ -26,11 +26,11 @@ def run_gpu(case, dtype, grad_out=None):
     names = ("input", "weight", "offset", "mask", "bias")
     ts = [case[n].to(DEV, dtype).requires_grad_(True) if case[n] is not None else None for n in names]
     if case["transposed"]:
-        fn = getattr(tvdcn_amd, f"deform_conv_transpose{case['dim']}d")
+        fn = getattr(tvdcn, f"deform_conv_transpose{case['dim']}d")
         out = fn(*ts, stride=case["stride"], padding=case["padding"], output_padding=case["output_padding"],
                  dilation=case["dilation"], groups=case["groups"])
     else:
-        fn = getattr(tvdcn_amd, f"deform_conv{case['dim']}d")
+        fn = getattr(tvdcn, f"deform_conv{case['dim']}d")
         out = fn(*ts, stride=case["stride"], padding=case["padding"], dilation=case["dilation"],
                  groups=case["groups"])
     if grad_out is None:
@@ -112,7 +112,7 @@ def test_unbatched_and_no_bias():
     w = case["weight"].to(DEV)
     o = case["offset"][0].to(DEV)
     m = case["mask"][0].to(DEV)
-    out = tvdcn_amd.deform_conv2d(x, w, o, m, None, case["stride"], case["padding"], case["dilation"])
+    out = tvdcn.deform_conv2d(x, w, o, m, None, case["stride"], case["padding"], case["dilation"])
     ref = oracle.forward(2, case["input"], case["weight"], case["offset"], case["mask"], None,
                          case["stride"], case["padding"], case["dilation"])
     assert out.shape == ref.shape[1:]
@@ -127,7 +127,7 @@ def test_zero_offset_unit_mask_is_conv2d():
     b = torch.randn(32, generator=g, dtype=torch.float64).to(DEV)
     off = torch.zeros(2, 2 * 9, 7, 7, dtype=torch.float64, device=DEV)
     msk = torch.ones(2, 9, 7, 7, dtype=torch.float64, device=DEV)
-    out = tvdcn_amd.deform_conv2d(x, w, off, msk, b, stride=2, padding=1, dilation=1, groups=2)
+    out = tvdcn.deform_conv2d(x, w, off, msk, b, stride=2, padding=1, dilation=1, groups=2)
     ref = torch.nn.functional.conv2d(x, w, b, stride=2, padding=1, groups=2)
     assert rel_err(out, ref) < 1e-10
 
@@ -137,7 +137,7 @@ def test_mask_softmax_matches_torch_softmax():
     for dim, ks, shape in [(1, (5,), (3, 20, 33)), (2, (4, 4), (2, 32, 6, 7)), (3, (3, 3, 3), (2, 27, 3, 4, 5)),
                            (2, (7, 7), (1, 98, 5, 5))]:
         x = torch.randn(*shape, generator=g, dtype=torch.float64).to(DEV).requires_grad_(True)
-        y = getattr(tvdcn_amd, f"mask_softmax{dim}d")(x, ks)
+        y = getattr(tvdcn, f"mask_softmax{dim}d")(x, ks)
         kn = 1
         for k in ks:
             kn *= k

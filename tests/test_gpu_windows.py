@@ -11,7 +11,7 @@
 import pytest
 import torch
 
-import tvdcn_amd
+import tvdcn
 from helpers import make_case, rel_err
 from test_gpu_parity import TOL, check, run_gpu, run_oracle
 
@@ -147,7 +147,7 @@ def test_channels_last_input(dim, dtype):
     ts[0] = ts[0].contiguous(memory_format=fmt)
     assert not ts[0].is_contiguous()
     ts = [t.requires_grad_(True) for t in ts]
-    fn = getattr(tvdcn_amd, f"deform_conv{dim}d")
+    fn = getattr(tvdcn, f"deform_conv{dim}d")
     y = fn(*ts, stride=case["stride"], padding=case["padding"], dilation=case["dilation"], groups=case["groups"])
     y.backward(gout.to("cuda:0", dtype))
     torch.cuda.synchronize()
@@ -175,7 +175,7 @@ def test_layout_copies_through_c_abi():
     """tvdcn_to_channels_last / tvdcn_from_channels_last on the GPU: bit-exact permutations
     (ragged sizes, off the 32 x 32 tile of the copy kernels), and their round trip."""
     import ctypes
-    from tvdcn_amd import extension
+    from tvdcn import extension
     lib = ctypes.CDLL(extension.HIP_LIB_PATH)
     for fn in (lib.tvdcn_to_channels_last, lib.tvdcn_from_channels_last):
         fn.restype = ctypes.c_int
@@ -205,8 +205,8 @@ def test_forward_copy_kept_for_backward(dim):
     names = ("input", "weight", "offset", "mask", "bias")
     ts = [case[n].to("cuda:0", torch.float32) for n in names]
     params = ([1] * dim, [1] * dim, [1] * dim, 1)
-    fwd = getattr(torch.ops.tvdcn_amd, f"deform_conv{dim}d")
-    bwd = getattr(torch.ops.tvdcn_amd, f"_deform_conv{dim}d_backward")
+    fwd = getattr(torch.ops.tvdcn, f"deform_conv{dim}d")
+    bwd = getattr(torch.ops.tvdcn, f"_deform_conv{dim}d_backward")
     with torch.no_grad():
         y_ref = fwd(*ts, *params)
     gy = torch.randn(y_ref.shape, device="cuda:0")
@@ -286,7 +286,7 @@ def test_channels_last_1d_input():
     ts[0] = ts[0].permute(0, 2, 1).contiguous().permute(0, 2, 1)
     assert ts[0].stride() == (70 * 32, 1, 32)
     ts = [t.requires_grad_(True) for t in ts]
-    y = tvdcn_amd.deform_conv1d(*ts, stride=1, padding=1, dilation=1)
+    y = tvdcn.deform_conv1d(*ts, stride=1, padding=1, dilation=1)
     y.backward(gout.to("cuda:0", torch.float32))
     torch.cuda.synchronize()
     assert ts[0].grad.stride() == (70 * 32, 1, 32)

@@ -83,20 +83,15 @@ def test_fixture_count():
 @pytest.mark.parametrize("dim,transposed", [(1, False), (2, False), (3, False), (1, True), (2, True), (3, True)])
 def test_oracle_matches_reference_build_random(dim, transposed):
     """fresh random cases (larger channel counts, og != mg) straight through the reference build"""
-    assert oracle.load_reference()
     case = make_case(dim, transposed, batch=3, cin=8, cout=12, groups=2, og=4, mg=2, seed=77 + dim,
                      in_size={1: [9], 2: [6, 7], 3: [4, 5, 4]}[dim])
     x, w, o, m, b = (case[n] for n in NAMES)
     s, p, d, op, G = case["stride"], case["padding"], case["dilation"], case["output_padding"], case["groups"]
     gout = torch.rand(case["out_shape"], dtype=torch.float64, generator=torch.Generator().manual_seed(3))
-    ops = torch.ops.tvdcn
-    with torch.inference_mode():
-        if transposed:
-            ref = getattr(ops, f"deform_conv_transpose{dim}d")(x, w, o, m, b, s, p, op, d, G)
-            rg = getattr(ops, f"_deform_conv_transpose{dim}d_backward")(gout, x, w, o, m, b, s, p, op, d, G)
-        else:
-            ref = getattr(ops, f"deform_conv{dim}d")(x, w, o, m, b, s, p, d, G)
-            rg = getattr(ops, f"_deform_conv{dim}d_backward")(gout, x, w, o, m, b, s, p, d, G)
+    name = f"deform_conv_transpose{dim}d" if transposed else f"deform_conv{dim}d"
+    params = [s, p, op, d, G] if transposed else [s, p, d, G]
+    ref, rg = oracle.run_reference([{"op": name, "args": [x, w, o, m, b] + params},
+                                    {"op": f"_{name}_backward", "args": [gout, x, w, o, m, b] + params}])
     kw = dict(stride=s, padding=p, dilation=d, groups=G, transposed=transposed, output_padding=op)
     assert rel_err(oracle.forward(dim, x, w, o, m, b, **kw), ref) < 1e-12
     for g, r in zip(oracle.backward(dim, gout, x, w, o, m, b, **kw), rg):

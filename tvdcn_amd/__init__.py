@@ -1,9 +1,10 @@
 """tvdcn_amd: MI355X (gfx950) deformable convolution with tvdcn's Python API.
 
-``import tvdcn_amd as tvdcn`` gives the same public names as ``import tvdcn``
-(tvdcn/__init__.py): the functional ops, the modules, the mask activations and
-the capability queries. The ops run on hand-written HIP kernels only; there is
-no CPU path.
+The implementation package behind ``import tvdcn`` (the top-level ``tvdcn`` package
+re-exports it under the reference's module names). It has the same public names as
+tvdcn/__init__.py: the functional ops, the modules, the mask activations and the
+capability queries. The ops are the native ``torch.ops.tvdcn.*`` operators; their
+GPU kernels are hand-written HIP only.
 """
 from . import ops
 from ._version import __version__

@@ -84,11 +84,15 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     if (d->batch < 0 || d->in_channels <= 0 || d->out_channels <= 0)
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "batch must be >= 0 and channels positive");
     if (d->groups <= 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "groups must be positive");
-    if (d->flags & ~(TVDCN_FLAG_CHANNELS_LAST | TVDCN_FLAG_MASK_SIGMOID))
+    if (d->flags & ~(TVDCN_FLAG_CHANNELS_LAST | TVDCN_FLAG_MASK_SIGMOID | TVDCN_FLAG_MASK_SOFTMAX))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "unknown flags");
+    if ((d->flags & TVDCN_FLAG_MASK_SIGMOID) && (d->flags & TVDCN_FLAG_MASK_SOFTMAX))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "TVDCN_FLAG_MASK_SIGMOID and TVDCN_FLAG_MASK_SOFTMAX exclude each other");
     if ((d->flags & TVDCN_FLAG_MASK_SIGMOID) && (d->mask_groups == 0 || !(d->mask_scale > 0.0) ||
                                                  !(d->mask_scale < 1e300)))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "a sigmoid mask needs a mask and a positive finite mask_scale");
+    if ((d->flags & TVDCN_FLAG_MASK_SOFTMAX) && d->mask_groups == 0)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "a softmax mask needs a mask");
     if ((d->flags & TVDCN_FLAG_CHANNELS_LAST) && d->transposed)
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "channels-last input is supported for the non-transposed ops");
     if (d->in_channels % d->groups || d->out_channels % d->groups)
@@ -152,6 +156,9 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     g.Pn = (int)Pn;
     g.Kn = (int)Kn;
     g.NP = (int)(B * Pn);
+    g.mask_act = (d->flags & TVDCN_FLAG_MASK_SIGMOID) ? MASK_ACT_SIGMOID
+                 : (d->flags & TVDCN_FLAG_MASK_SOFTMAX) ? MASK_ACT_SOFTMAX
+                                                         : 0;
     g.mask_scale = (d->flags & TVDCN_FLAG_MASK_SIGMOID) ? d->mask_scale : 0.0;
     g.dPn = make_fastdiv((uint32_t)g.Pn);
     g.dP2 = make_fastdiv((uint32_t)g.P[2]);
@@ -535,9 +542,13 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
             TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,
                                                                         at(workspace, L.wpart), grad_weight, s));
     }
-    // mask logits: the accumulated mask gradient times d(mask value) / d(logit)
+    // mask logits: the accumulated mask gradient through d(mask value) / d(logit) -- elementwise for
+    // the sigmoid, over the taps of each (batch, mask group, pixel) for the softmax
     if (gmask && (desc->flags & TVDCN_FLAG_MASK_SIGMOID))
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_mask_sigmoid_grad(dt, mask, gmask, desc->mask_scale, n_gmask, s));
+    if (gmask && (desc->flags & TVDCN_FLAG_MASK_SOFTMAX))
+        TVDCN_LAUNCH(TVDCN_KERNEL_MASK_SOFTMAX, s,
+                     launch_mask_softmax_logit_grad(dt, mask, gmask, (int64_t)g.B * g.mg, g.Kn, g.Pn, s));
     if (!direct) {
         if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, goff, grad_offset, n_goff, s));
         if (gmask) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, gmask, grad_mask, n_gmask, s));

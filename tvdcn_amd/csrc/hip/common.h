@@ -54,8 +54,14 @@ struct Geo {
     int Sn, Pn, Kn;
     int NP;                // B * Pn
     FastDiv dPn, dP2, dP12, dK2, dK12;   // divisors Pn, P[2], P[1]*P[2], K[2], K[1]*K[2]
-    double mask_scale = 0.0;   // > 0: the mask tensor holds logits; the kernels use mask_scale * sigmoid(logit)
+    // mask_act: 0 = the mask tensor holds the mask values; otherwise it holds logits, activated in the
+    // kernels' mask load: MASK_ACT_SIGMOID = mask_scale * sigmoid(logit), MASK_ACT_SOFTMAX = softmax
+    // over the Kn taps of the logit's (batch, mask group, column pixel)
+    int mask_act = 0;
+    double mask_scale = 0.0;
 };
+constexpr int MASK_ACT_SIGMOID = 1;
+constexpr int MASK_ACT_SOFTMAX = 2;
 
 // ---------------------------------------------------------------------------
 // scalar conversion
@@ -339,11 +345,12 @@ __device__ __forceinline__ GatherCorners<DIM, A> gather_corners(const Geo &g, co
     return gc;
 }
 
-// Mask value of (b, mask group, tap, column pixel): the tensor's value, or mask_scale *
-// sigmoid(value) when the mask holds logits (tvdcn/ops/activations/mask_sigmoid.py:11-21
-// applied in the load instead of as a separate pass)
-// (mask_raw: the stored value, 1 without a mask; mask_activate: the sigmoid when the mask holds
-// logits — split so that batched loads are all issued before any value is used)
+// Mask value of (b, mask group, tap, column pixel): the tensor's value, or its activation
+// when the mask holds logits (tvdcn/ops/activations/mask_sigmoid.py:11-21 and
+// mask_softmax.py:19-126 applied in the load instead of as separate passes)
+// (mask_raw: the stored value, 1 without a mask; mask_activate: the sigmoid of a logit —
+// split so that batched loads are all issued before any value is used; the softmax needs
+// every tap's logit of the pixel: mask_softmax_norm gives its max and 1 / sum)
 template <typename A, typename T>
 __device__ __forceinline__ A mask_raw(const Geo &g, const T *__restrict__ mask, int b, int mgi, int t, int p) {
     if (mask == nullptr) return A(1);
@@ -351,7 +358,7 @@ __device__ __forceinline__ A mask_raw(const Geo &g, const T *__restrict__ mask, 
 }
 template <typename A>
 __device__ __forceinline__ A mask_activate(const Geo &g, A v) {
-    if (g.mask_scale > 0.0) {   // uniform
+    if (g.mask_act == MASK_ACT_SIGMOID) {   // uniform
         // fp32: hardware exp2 and reciprocal (a few instructions, ~2 ulp), so that the rarely
         // taken branch adds little code to the kernels' hot loops
         if constexpr (std::is_same_v<A, float>)
@@ -361,8 +368,27 @@ __device__ __forceinline__ A mask_activate(const Geo &g, A v) {
     }
     return v;
 }
+// max over the Kn taps of the logits of (b, mask group, pixel), and 1 / sum_t exp(logit_t - max)
+template <typename A, typename T>
+__device__ __forceinline__ void mask_softmax_norm(const Geo &g, const T *__restrict__ mask, int b, int mgi, int p,
+                                                  A &mx, A &inv_sum) {
+    const T *ml = mask + (size_t)(b * g.mg + mgi) * g.Kn * (size_t)g.Pn + p;
+    mx = -INFINITY;
+    for (int t = 0; t < g.Kn; ++t) {
+        const A v = to_acc<A>(ml[(size_t)t * g.Pn]);
+        mx = v > mx ? v : mx;
+    }
+    A sum = A(0);
+    for (int t = 0; t < g.Kn; ++t) sum += exp(to_acc<A>(ml[(size_t)t * g.Pn]) - mx);
+    inv_sum = A(1) / sum;
+}
 template <typename A, typename T>
 __device__ __forceinline__ A mask_at(const Geo &g, const T *__restrict__ mask, int b, int mgi, int t, int p) {
+    if (mask != nullptr && g.mask_act == MASK_ACT_SOFTMAX) {
+        A mx, inv;
+        mask_softmax_norm<A, T>(g, mask, b, mgi, p, mx, inv);
+        return exp(mask_raw<A, T>(g, mask, b, mgi, t, p) - mx) * inv;
+    }
     return mask_activate<A>(g, mask_raw<A, T>(g, mask, b, mgi, t, p));
 }
 

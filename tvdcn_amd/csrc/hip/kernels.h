@@ -117,6 +117,10 @@ hipError_t launch_fill_zero(int elem_bytes, void *p, size_t n, hipStream_t s);  
 hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n, hipStream_t s);
 hipError_t launch_storage_to_acc(int dtype, const void *x, void *acc, size_t n, hipStream_t s);   // elementwise widening
 // gmask_acc (accumulation type) *= d(scale * sigmoid(logit)) / d(logit), elementwise
+// gmask_acc (accumulation type) <- y * (gmask_acc - sum_k gmask_acc_k * y_k), y = softmax over K of the
+// logits viewed as (BG, K, S): the gradient of a softmax-activated mask with respect to its logits
+hipError_t launch_mask_softmax_logit_grad(int dtype, const void *logits, void *gmask_acc, int64_t BG, int K, int64_t S,
+                                          hipStream_t s);
 hipError_t launch_mask_sigmoid_grad(int dtype, const void *logits, void *gmask_acc, double scale, size_t n,
                                     hipStream_t s);
 hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s);

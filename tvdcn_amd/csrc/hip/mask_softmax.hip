@@ -86,6 +86,35 @@ __global__ void __launch_bounds__(256) softmax_bwd_kernel(const T *__restrict__ 
     }
 }
 
+// Gradient with respect to the logits of a mask the convolution kernels softmax-activated in
+// their mask load: g (accumulation type, in place) holds d(loss)/d(y) summed over channels;
+// y is recomputed from the logits x as in the forward, then g <- y * (g - sum_k g_k * y_k).
+template <typename T, typename A>
+__global__ void __launch_bounds__(256) softmax_logit_grad_kernel(const T *__restrict__ x, A *__restrict__ g,
+                                                                 int64_t BG, int K, int64_t S) {
+    const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (i >= BG * S) return;
+    const int64_t bg = i / S, s = i - bg * S;
+    const int64_t o = bg * K * S + s;
+    A mx = -INFINITY;
+    for (int k = 0; k < K; ++k) {
+        const A v = to_acc<A>(x[o + k * S]);
+        mx = v > mx ? v : mx;
+    }
+    A sum = A(0), dot = A(0);
+    for (int k = 0; k < K; ++k) {
+        const A e = exp(to_acc<A>(x[o + k * S]) - mx);
+        sum += e;
+        dot += e * g[o + k * S];
+    }
+    const A inv = A(1) / sum;
+    dot *= inv;
+    for (int k = 0; k < K; ++k) {
+        const A y = exp(to_acc<A>(x[o + k * S]) - mx) * inv;
+        g[o + k * S] = y * (g[o + k * S] - dot);
+    }
+}
+
 template <typename F>
 hipError_t by_dtype(int dtype, F &&f) {
     switch (dtype) {
@@ -120,6 +149,19 @@ hipError_t launch_mask_softmax_bwd(int dtype, const void *y, const void *gy, voi
         using A = decltype(av);
         hipLaunchKernelGGL((softmax_bwd_kernel<T, A>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                            static_cast<const T *>(y), static_cast<const T *>(gy), static_cast<T *>(gx), BG, K, S);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_mask_softmax_logit_grad(int dtype, const void *logits, void *gmask_acc, int64_t BG, int K, int64_t S,
+                                          hipStream_t s) {
+    const int64_t n = BG * S;
+    if (n == 0) return hipSuccess;
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        hipLaunchKernelGGL((softmax_logit_grad_kernel<T, A>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                           static_cast<const T *>(logits), static_cast<A *>(gmask_acc), BG, K, S);
         return hipGetLastError();
     });
 }

@@ -392,13 +392,27 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
             geo[tl * BPX + i] = r;
         }
     }
-    // mask logits (mask_scale > 0): the thread activates the masks of its own records in a
-    // separate pass, so that the loops above keep their code when masks are plain values
-    if (mask != nullptr && g.mask_scale > 0.0) {
+    // mask logits: the thread activates the masks of its own records in a separate pass, so
+    // that the loops above keep their code when masks are plain values. The softmax takes a
+    // pixel per thread: the normaliser over all Kn taps (also those outside this pass) is
+    // formed once and applied to the pixel's records of the pass. Records of pixels outside
+    // the grid keep mask 0.
+    if (mask != nullptr && g.mask_act == MASK_ACT_SIGMOID) {
         for (int e = tid; e < n; e += nthreads) {
-            if (tile.pixel(g, wt, e % BPX) < 0) continue;   // outside the grid: mask 0
+            if (tile.pixel(g, wt, e % BPX) < 0) continue;
             float *m = reinterpret_cast<float *>(geo + e) + (DIM == 3 ? 3 : DIM);
             *m = mask_activate<float>(g, *m);
+        }
+    } else if (mask != nullptr && g.mask_act == MASK_ACT_SOFTMAX) {
+        for (int i = tid; i < BPX; i += nthreads) {
+            const int p = tile.pixel(g, wt, i);
+            if (p < 0) continue;
+            float mx, inv;
+            mask_softmax_norm<float, T>(g, mask, tile.b, tile.mgu, p, mx, inv);
+            for (int tl = 0; tl < ntaps; ++tl) {
+                float *m = reinterpret_cast<float *>(geo + tl * BPX + i) + (DIM == 3 ? 3 : DIM);
+                *m = expf(*m - mx) * inv;
+            }
         }
     }
 }

@@ -1,5 +1,5 @@
 // PyTorch-ROCm operator layer of tvdcn_amd: the reference's twelve operator
-// schemas (plus mask_softmax), registered under the `tvdcn_amd` namespace with
+// schemas (plus mask_softmax), registered under the reference's `tvdcn` namespace with
 // CUDA (= HIP on ROCm), Meta, Autograd and Autocast kernels. The CUDA kernels
 // validate, allocate outputs and workspace from the caching allocator, and call
 // the C ABI of libtvdcn_hip.so on the current HIP stream. There is no CPU
@@ -280,13 +280,19 @@ Tensor aligned(const Tensor &t) {
     return t.clone(at::MemoryFormat::Preserve);   // keeps a channels-last input channels-last
 }
 
-// mask_scale > 0: the mask holds logits, activated as mask_scale * sigmoid in the kernels
-void set_mask_sigmoid(Problem &pr, double mask_scale) {
-    if (mask_scale == 0.0) return;
-    TORCH_CHECK(mask_scale > 0.0 && std::isfinite(mask_scale), "mask_scale must be a positive finite number");
-    TORCH_CHECK(pr.mask.defined(), "a sigmoid mask needs a mask tensor");
-    pr.desc.flags |= TVDCN_FLAG_MASK_SIGMOID;
-    pr.desc.mask_scale = mask_scale;
+// activation 1 / 2: the mask holds logits, activated in the kernels as mask_scale * sigmoid /
+// as the softmax over the kernel taps of each mask group (0: the mask is used as it is)
+void set_mask_activation(Problem &pr, int64_t activation, double mask_scale) {
+    if (activation == 0) return;
+    TORCH_CHECK(pr.mask.defined(), "an activated mask needs a mask tensor");
+    if (activation == 1) {
+        TORCH_CHECK(mask_scale > 0.0 && std::isfinite(mask_scale), "mask_scale must be a positive finite number");
+        pr.desc.flags |= TVDCN_FLAG_MASK_SIGMOID;
+        pr.desc.mask_scale = mask_scale;
+    } else {
+        TORCH_CHECK(activation == 2, "unknown mask activation ", activation);
+        pr.desc.flags |= TVDCN_FLAG_MASK_SOFTMAX;
+    }
 }
 
 hipStream_t current_stream(const Tensor &t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
@@ -297,13 +303,14 @@ hipStream_t current_stream(const Tensor &t) { return c10::hip::getCurrentHIPStre
 Tensor forward_hip(int dim, bool transposed, const Tensor &input, const Tensor &weight,
                    const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
                    at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding,
-                   at::IntArrayRef dilation, int64_t groups, const char *name, double mask_scale = 0.0) {
+                   at::IntArrayRef dilation, int64_t groups, const char *name, int64_t activation = 0,
+                   double mask_scale = 0.0) {
     TORCH_CHECK(input.is_cuda(), name, ": expected a GPU (HIP) tensor");
     c10::DeviceGuard guard(input.device());
     Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
                               dilation, groups, name);
     pr.desc.dtype = dtype_code(pr.input.scalar_type());
-    set_mask_sigmoid(pr, mask_scale);
+    set_mask_activation(pr, activation, mask_scale);
     Tensor output = at::empty(out_shape(pr), pr.input.options());
     if (output.numel() > 0) {
         const size_t ws_bytes = tvdcn_deform_conv_forward_workspace_size(&pr.desc);
@@ -326,13 +333,13 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_hip(
     int dim, bool transposed, const Tensor &grad, const Tensor &input, const Tensor &weight,
     const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
     at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding, at::IntArrayRef dilation,
-    int64_t groups, const char *name, double mask_scale = 0.0) {
+    int64_t groups, const char *name, int64_t activation = 0, double mask_scale = 0.0) {
     TORCH_CHECK(input.is_cuda(), name, ": expected a GPU (HIP) tensor");
     c10::DeviceGuard guard(input.device());
     Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
                               dilation, groups, name);
     pr.desc.dtype = dtype_code(pr.input.scalar_type());
-    set_mask_sigmoid(pr, mask_scale);
+    set_mask_activation(pr, activation, mask_scale);
     Tensor g = grad.contiguous();
     if (pr.unbatched) g = g.unsqueeze(0);
     TORCH_CHECK(g.sizes() == at::IntArrayRef(out_shape(pr)), name, ": grad has shape ", g.sizes(), ", expected ",
@@ -406,8 +413,8 @@ struct Names;
 #define TVDCN_NAMES(D, TRV, F, Bw)                               \
     template <>                                                  \
     struct Names<D, TRV> {                                       \
-        static constexpr const char *fwd = "tvdcn_amd::" F;      \
-        static constexpr const char *bwd = "tvdcn_amd::" Bw;     \
+        static constexpr const char *fwd = "tvdcn::" F;      \
+        static constexpr const char *bwd = "tvdcn::" Bw;     \
         static constexpr const char *short_name = F;             \
     };
 TVDCN_NAMES(1, false, "deform_conv1d", "_deform_conv1d_backward")
@@ -745,7 +752,7 @@ class MaskSoftmaxFunction : public torch::autograd::Function<MaskSoftmaxFunction
     static Tensor forward(torch::autograd::AutogradContext *ctx, const Tensor &x, int64_t K) {
         at::AutoDispatchBelowADInplaceOrView guard;
         static auto op = c10::Dispatcher::singleton()
-                             .findSchemaOrThrow("tvdcn_amd::mask_softmax", "")
+                             .findSchemaOrThrow("tvdcn::mask_softmax", "")
                              .typed<Tensor(const Tensor &, int64_t)>();
         Tensor y = op.call(x, K);
         ctx->save_for_backward({y});
@@ -755,7 +762,7 @@ class MaskSoftmaxFunction : public torch::autograd::Function<MaskSoftmaxFunction
     static torch::autograd::variable_list backward(torch::autograd::AutogradContext *ctx,
                                                    const torch::autograd::variable_list &g) {
         static auto op = c10::Dispatcher::singleton()
-                             .findSchemaOrThrow("tvdcn_amd::_mask_softmax_backward", "")
+                             .findSchemaOrThrow("tvdcn::_mask_softmax_backward", "")
                              .typed<Tensor(const Tensor &, const Tensor &, int64_t)>();
         auto saved = ctx->get_saved_variables();
         return {op.call(g[0], saved[0], ctx->saved_data["K"].toInt()), Tensor()};
@@ -765,86 +772,100 @@ class MaskSoftmaxFunction : public torch::autograd::Function<MaskSoftmaxFunction
 Tensor mask_softmax_autograd(const Tensor &x, int64_t K) { return MaskSoftmaxFunction::apply(x, K); }
 
 // ---------------------------------------------------------------------------
-// deform_conv_sigmoid_mask: conv / transposed conv (rank from len(stride)) whose mask
-// tensor holds logits, activated as mask_scale * sigmoid in the kernels' mask load; the
-// backward's mask gradient is with respect to the logits. Used by the packed modules for
-// their default mask activation (MaskSigmoid); no counterpart op in the reference.
+// deform_conv_mask_activation: conv / transposed conv (rank from len(stride)) whose mask
+// tensor holds logits, activated in the kernels' mask load: activation 1 = mask_scale *
+// sigmoid (tvdcn's MaskSigmoid), 2 = softmax over the kernel taps of each mask group
+// (MaskSoftmax{N}d). The backward's mask gradient is with respect to the logits. Used by the
+// packed modules for those two activations; no counterpart op in the reference, whose
+// packed modules run the activation as separate passes (ops/deform_conv.py:623-626).
 // ---------------------------------------------------------------------------
-int sig_dim(at::IntArrayRef stride) {
-    TORCH_CHECK(stride.size() >= 1 && stride.size() <= 3, "deform_conv_sigmoid_mask: stride must have 1 to 3 ",
+const char *kActName = "deform_conv_mask_activation";
+
+int act_dim(at::IntArrayRef stride) {
+    TORCH_CHECK(stride.size() >= 1 && stride.size() <= 3, kActName, ": stride must have 1 to 3 ",
                 "elements (one per spatial axis)");
     return (int)stride.size();
 }
 
-Tensor sig_fwd_hip(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
-                   const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
-                   at::IntArrayRef d, int64_t g, bool tr, double scale) {
-    TORCH_CHECK(scale > 0.0, "mask_scale must be a positive finite number");
-    return forward_hip(sig_dim(s), tr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, "deform_conv_sigmoid_mask",
-                       scale);
+void check_activation(int64_t activation, double scale) {
+    TORCH_CHECK(activation == 1 || activation == 2, kActName, ": activation must be 1 (sigmoid) or 2 (softmax), got ",
+                activation);
+    TORCH_CHECK(activation != 1 || (scale > 0.0 && std::isfinite(scale)), "mask_scale must be a positive finite number");
 }
 
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> sig_bwd_hip(const Tensor &gr, const Tensor &i, const Tensor &w,
+Tensor act_fwd_hip(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+                   const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                   at::IntArrayRef d, int64_t g, bool tr, int64_t act, double scale) {
+    check_activation(act, scale);
+    return forward_hip(act_dim(s), tr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, kActName, act, scale);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> act_bwd_hip(const Tensor &gr, const Tensor &i, const Tensor &w,
                                                                const optional<Tensor> &o, const Tensor &m,
                                                                const optional<Tensor> &b, at::IntArrayRef s,
                                                                at::IntArrayRef p, at::IntArrayRef op,
-                                                               at::IntArrayRef d, int64_t g, bool tr, double scale) {
-    TORCH_CHECK(scale > 0.0, "mask_scale must be a positive finite number");
-    return backward_hip(sig_dim(s), tr, gr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g,
-                        "deform_conv_sigmoid_mask", scale);
+                                                               at::IntArrayRef d, int64_t g, bool tr, int64_t act,
+                                                               double scale) {
+    check_activation(act, scale);
+    return backward_hip(act_dim(s), tr, gr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, kActName, act, scale);
 }
 
-Tensor sig_fwd_meta(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+Tensor act_fwd_meta(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
                     const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
-                    at::IntArrayRef d, int64_t g, bool tr, double scale) {
-    TORCH_CHECK(scale > 0.0, "mask_scale must be a positive finite number");
-    return forward_meta(sig_dim(s), tr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, "deform_conv_sigmoid_mask");
+                    at::IntArrayRef d, int64_t g, bool tr, int64_t act, double scale) {
+    check_activation(act, scale);
+    return forward_meta(act_dim(s), tr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, kActName);
 }
 
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> sig_bwd_meta(const Tensor &gr, const Tensor &i, const Tensor &w,
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> act_bwd_meta(const Tensor &gr, const Tensor &i, const Tensor &w,
                                                                 const optional<Tensor> &o, const Tensor &m,
                                                                 const optional<Tensor> &b, at::IntArrayRef s,
                                                                 at::IntArrayRef p, at::IntArrayRef op,
-                                                                at::IntArrayRef d, int64_t g, bool tr, double scale) {
-    TORCH_CHECK(scale > 0.0, "mask_scale must be a positive finite number");
-    return backward_meta(sig_dim(s), tr, gr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g,
-                         "deform_conv_sigmoid_mask");
+                                                                at::IntArrayRef d, int64_t g, bool tr, int64_t act,
+                                                                double scale) {
+    check_activation(act, scale);
+    return backward_meta(act_dim(s), tr, gr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, kActName);
 }
 
-using SigFwdSig = Tensor(const Tensor &, const Tensor &, const optional<Tensor> &, const Tensor &,
+using ActFwdSig = Tensor(const Tensor &, const Tensor &, const optional<Tensor> &, const Tensor &,
                          const optional<Tensor> &, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef,
-                         int64_t, bool, double);
-using SigBwdSig = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor>(
+                         int64_t, bool, int64_t, double);
+using ActBwdSig = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor>(
     const Tensor &, const Tensor &, const Tensor &, const optional<Tensor> &, const Tensor &, const optional<Tensor> &,
-    at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t, bool, double);
+    at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, at::IntArrayRef, int64_t, bool, int64_t, double);
 
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> sig_call_backward(
+Tensor act_call_forward(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+                        const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                        at::IntArrayRef d, int64_t g, bool tr, int64_t act, double scale) {
+    static auto fop =
+        c10::Dispatcher::singleton().findSchemaOrThrow("tvdcn::deform_conv_mask_activation", "").typed<ActFwdSig>();
+    return fop.call(i, w, o, m, b, s, p, op, d, g, tr, act, scale);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> act_call_backward(
     const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
     const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op, at::IntArrayRef d, int64_t g,
-    bool tr, double scale) {
+    bool tr, int64_t act, double scale) {
     static auto bop = c10::Dispatcher::singleton()
-                          .findSchemaOrThrow("tvdcn_amd::_deform_conv_sigmoid_mask_backward", "")
-                          .typed<SigBwdSig>();
-    return bop.call(gr, i, w, o, m, b, s, p, op, d, g, tr, scale);
+                          .findSchemaOrThrow("tvdcn::_deform_conv_mask_activation_backward", "")
+                          .typed<ActBwdSig>();
+    return bop.call(gr, i, w, o, m, b, s, p, op, d, g, tr, act, scale);
 }
 
-class SigmoidMaskFunction : public torch::autograd::Function<SigmoidMaskFunction> {
+class MaskActivationFunction : public torch::autograd::Function<MaskActivationFunction> {
    public:
     static torch::autograd::Variable forward(torch::autograd::AutogradContext *ctx, const Tensor &input,
                                              const Tensor &weight, const optional<Tensor> &offset,
                                              const Tensor &mask, const optional<Tensor> &bias, at::IntArrayRef stride,
                                              at::IntArrayRef padding, at::IntArrayRef out_pad,
                                              at::IntArrayRef dilation, int64_t groups, bool transposed,
-                                             double scale) {
+                                             int64_t activation, double scale) {
         at::AutoDispatchBelowADInplaceOrView guard;
-        static auto fop = c10::Dispatcher::singleton()
-                              .findSchemaOrThrow("tvdcn_amd::deform_conv_sigmoid_mask", "")
-                              .typed<SigFwdSig>();
         const int dim = (int)stride.size();
         const bool cl = keeps_cl_copy(input, dim, transposed);
         const Tensor x = cl ? cl_copy(input, dim, true) : input;
-        Tensor output =
-            fop.call(x, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups, transposed, scale);
+        Tensor output = act_call_forward(x, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups,
+                                         transposed, activation, scale);
         ctx->save_for_backward({x, weight, offset.value_or(Tensor()), mask, bias.value_or(Tensor())});
         ctx->saved_data["cl_copy"] = cl;
         ctx->saved_data["stride"] = stride.vec();
@@ -853,6 +874,7 @@ class SigmoidMaskFunction : public torch::autograd::Function<SigmoidMaskFunction
         ctx->saved_data["dilation"] = dilation.vec();
         ctx->saved_data["groups"] = groups;
         ctx->saved_data["transposed"] = transposed;
+        ctx->saved_data["activation"] = activation;
         ctx->saved_data["scale"] = scale;
         return output;
     }
@@ -860,20 +882,20 @@ class SigmoidMaskFunction : public torch::autograd::Function<SigmoidMaskFunction
     static torch::autograd::variable_list backward(torch::autograd::AutogradContext *ctx,
                                                    const torch::autograd::variable_list &grad_output) {
         auto saved = ctx->get_saved_variables();
-        auto grads = sig_call_backward(
+        auto grads = act_call_backward(
             grad_output[0], saved[0], saved[1], opt(saved[2]), saved[3], opt(saved[4]),
             ctx->saved_data["stride"].toIntVector(), ctx->saved_data["padding"].toIntVector(),
             ctx->saved_data["output_padding"].toIntVector(), ctx->saved_data["dilation"].toIntVector(),
             ctx->saved_data["groups"].toInt(), ctx->saved_data["transposed"].toBool(),
-            ctx->saved_data["scale"].toDouble());
+            ctx->saved_data["activation"].toInt(), ctx->saved_data["scale"].toDouble());
         if (ctx->saved_data["cl_copy"].toBool() && std::get<0>(grads).defined())
             std::get<0>(grads) = cl_copy(std::get<0>(grads), (int)saved[0].dim() - 2, false);
         return {std::get<0>(grads), std::get<1>(grads), std::get<2>(grads), std::get<3>(grads), std::get<4>(grads),
-                Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+                Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
     }
 };
 
-class SigmoidMaskBackwardFunction : public torch::autograd::Function<SigmoidMaskBackwardFunction> {
+class MaskActivationBackwardFunction : public torch::autograd::Function<MaskActivationBackwardFunction> {
    public:
     static torch::autograd::variable_list forward(torch::autograd::AutogradContext *, const Tensor &grad,
                                                   const Tensor &input, const Tensor &weight,
@@ -881,51 +903,49 @@ class SigmoidMaskBackwardFunction : public torch::autograd::Function<SigmoidMask
                                                   const optional<Tensor> &bias, at::IntArrayRef stride,
                                                   at::IntArrayRef padding, at::IntArrayRef out_pad,
                                                   at::IntArrayRef dilation, int64_t groups, bool transposed,
-                                                  double scale) {
+                                                  int64_t activation, double scale) {
         at::AutoDispatchBelowADInplaceOrView guard;
-        auto r = sig_call_backward(grad, input, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups,
-                                   transposed, scale);
+        auto r = act_call_backward(grad, input, weight, offset, mask, bias, stride, padding, out_pad, dilation, groups,
+                                   transposed, activation, scale);
         auto ph = [&](const Tensor &t) { return t.defined() ? t : at::empty({0}, input.options()); };
         return {std::get<0>(r), std::get<1>(r), ph(std::get<2>(r)), std::get<3>(r), ph(std::get<4>(r))};
     }
     static torch::autograd::variable_list backward(torch::autograd::AutogradContext *,
                                                    const torch::autograd::variable_list &) {
-        TORCH_CHECK(false, "double backwards on deform_conv_sigmoid_mask not supported");
+        TORCH_CHECK(false, "double backwards on ", kActName, " not supported");
         return {};
     }
 };
 
-Tensor sig_fwd_autograd(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+Tensor act_fwd_autograd(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
                         const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
-                        at::IntArrayRef d, int64_t g, bool tr, double scale) {
-    return SigmoidMaskFunction::apply(i, w, o, m, b, s, p, op, d, g, tr, scale);
+                        at::IntArrayRef d, int64_t g, bool tr, int64_t act, double scale) {
+    return MaskActivationFunction::apply(i, w, o, m, b, s, p, op, d, g, tr, act, scale);
 }
 
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> sig_bwd_autograd(const Tensor &gr, const Tensor &i,
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> act_bwd_autograd(const Tensor &gr, const Tensor &i,
                                                                     const Tensor &w, const optional<Tensor> &o,
                                                                     const Tensor &m, const optional<Tensor> &b,
                                                                     at::IntArrayRef s, at::IntArrayRef p,
                                                                     at::IntArrayRef op, at::IntArrayRef d, int64_t g,
-                                                                    bool tr, double scale) {
-    auto r = SigmoidMaskBackwardFunction::apply(gr, i, w, o, m, b, s, p, op, d, g, tr, scale);
+                                                                    bool tr, int64_t act, double scale) {
+    auto r = MaskActivationBackwardFunction::apply(gr, i, w, o, m, b, s, p, op, d, g, tr, act, scale);
     const bool has_off = o.has_value() && o->defined();
     const bool has_bias = b.has_value() && b->defined();
     return {r[0], r[1], has_off ? r[2] : Tensor(), r[3], has_bias ? r[4] : Tensor()};
 }
 
-Tensor sig_fwd_autocast(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+Tensor act_fwd_autocast(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
                         const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
-                        at::IntArrayRef d, int64_t g, bool tr, double scale) {
+                        at::IntArrayRef d, int64_t g, bool tr, int64_t act, double scale) {
     c10::impl::ExcludeDispatchKeyGuard no_autocast(c10::DispatchKey::Autocast);
     auto f32 = [](const Tensor &t) { return at::autocast::cached_cast(at::kFloat, t, c10::DeviceType::CUDA); };
     auto f32o = [&](const optional<Tensor> &t) -> optional<Tensor> {
         if (!t.has_value() || !t->defined()) return t;
         return f32(*t);
     };
-    static auto fop = c10::Dispatcher::singleton()
-                          .findSchemaOrThrow("tvdcn_amd::deform_conv_sigmoid_mask", "")
-                          .typed<SigFwdSig>();
-    return fop.call(f32(i), f32(w), f32o(o), f32(m), f32o(b), s, p, op, d, g, tr, scale).to(i.scalar_type());
+    return act_call_forward(f32(i), f32(w), f32o(o), f32(m), f32o(b), s, p, op, d, g, tr, act, scale)
+        .to(i.scalar_type());
 }
 
 int64_t hip_version() { return tvdcn_hip_version(); }
@@ -953,7 +973,7 @@ std::string arch_flags() { return tvdcn_arch_flags(); }
     "Tensor? mask=None, Tensor? bias=None, SymInt[" #D "] stride=1, SymInt[" #D "] padding=0, SymInt[" #D      \
     "] output_padding=0, SymInt[" #D "] dilation=1, SymInt groups=1) -> (Tensor, Tensor, Tensor, Tensor, Tensor)"
 
-TORCH_LIBRARY(tvdcn_amd, m) {
+TORCH_LIBRARY(tvdcn, m) {
     m.def(TVDCN_CONV_SCHEMA(1));
     m.def(TVDCN_CONV_BWD_SCHEMA(1));
     m.def(TVDCN_CONV_SCHEMA(2));
@@ -966,12 +986,12 @@ TORCH_LIBRARY(tvdcn_amd, m) {
     m.def(TVDCN_TR_BWD_SCHEMA(2));
     m.def(TVDCN_TR_SCHEMA(3));
     m.def(TVDCN_TR_BWD_SCHEMA(3));
-    m.def("deform_conv_sigmoid_mask(Tensor input, Tensor weight, Tensor? offset, Tensor mask, Tensor? bias, "
+    m.def("deform_conv_mask_activation(Tensor input, Tensor weight, Tensor? offset, Tensor mask, Tensor? bias, "
           "SymInt[] stride, SymInt[] padding, SymInt[] output_padding, SymInt[] dilation, SymInt groups, "
-          "bool transposed, float mask_scale) -> Tensor");
-    m.def("_deform_conv_sigmoid_mask_backward(Tensor grad, Tensor input, Tensor weight, Tensor? offset, "
+          "bool transposed, int activation, float mask_scale) -> Tensor");
+    m.def("_deform_conv_mask_activation_backward(Tensor grad, Tensor input, Tensor weight, Tensor? offset, "
           "Tensor mask, Tensor? bias, SymInt[] stride, SymInt[] padding, SymInt[] output_padding, "
-          "SymInt[] dilation, SymInt groups, bool transposed, float mask_scale) "
+          "SymInt[] dilation, SymInt groups, bool transposed, int activation, float mask_scale) "
           "-> (Tensor, Tensor, Tensor, Tensor, Tensor)");
     m.def("mask_softmax(Tensor mask, int kernel_numel) -> Tensor");
     m.def("_mask_softmax_backward(Tensor grad, Tensor output, int kernel_numel) -> Tensor");
@@ -994,41 +1014,41 @@ using Tr3 = Kernels<3, true>;
     m.impl("deform_conv_transpose" #D "d", TORCH_FN(tvdcn_amd::Tr##D::KEYFN_F##_t));          \
     m.impl("_deform_conv_transpose" #D "d_backward", TORCH_FN(tvdcn_amd::Tr##D::KEYFN_B##_t));
 
-TORCH_LIBRARY_IMPL(tvdcn_amd, CUDA, m) {
+TORCH_LIBRARY_IMPL(tvdcn, CUDA, m) {
     TVDCN_IMPL_CONV(1, fwd_hip, bwd_hip)
     TVDCN_IMPL_CONV(2, fwd_hip, bwd_hip)
     TVDCN_IMPL_CONV(3, fwd_hip, bwd_hip)
-    m.impl("deform_conv_sigmoid_mask", TORCH_FN(tvdcn_amd::sig_fwd_hip));
-    m.impl("_deform_conv_sigmoid_mask_backward", TORCH_FN(tvdcn_amd::sig_bwd_hip));
+    m.impl("deform_conv_mask_activation", TORCH_FN(tvdcn_amd::act_fwd_hip));
+    m.impl("_deform_conv_mask_activation_backward", TORCH_FN(tvdcn_amd::act_bwd_hip));
     m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_hip));
     m.impl("_mask_softmax_backward", TORCH_FN(tvdcn_amd::mask_softmax_backward_hip));
 }
 
-TORCH_LIBRARY_IMPL(tvdcn_amd, Meta, m) {
+TORCH_LIBRARY_IMPL(tvdcn, Meta, m) {
     TVDCN_IMPL_CONV(1, fwd_meta, bwd_meta)
     TVDCN_IMPL_CONV(2, fwd_meta, bwd_meta)
     TVDCN_IMPL_CONV(3, fwd_meta, bwd_meta)
-    m.impl("deform_conv_sigmoid_mask", TORCH_FN(tvdcn_amd::sig_fwd_meta));
-    m.impl("_deform_conv_sigmoid_mask_backward", TORCH_FN(tvdcn_amd::sig_bwd_meta));
+    m.impl("deform_conv_mask_activation", TORCH_FN(tvdcn_amd::act_fwd_meta));
+    m.impl("_deform_conv_mask_activation_backward", TORCH_FN(tvdcn_amd::act_bwd_meta));
     m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_meta));
     m.impl("_mask_softmax_backward", TORCH_FN(tvdcn_amd::mask_softmax_backward_meta));
 }
 
-TORCH_LIBRARY_IMPL(tvdcn_amd, Autograd, m) {
+TORCH_LIBRARY_IMPL(tvdcn, Autograd, m) {
     TVDCN_IMPL_CONV(1, fwd_ag, bwd_ag)
     TVDCN_IMPL_CONV(2, fwd_ag, bwd_ag)
     TVDCN_IMPL_CONV(3, fwd_ag, bwd_ag)
-    m.impl("deform_conv_sigmoid_mask", TORCH_FN(tvdcn_amd::sig_fwd_autograd));
-    m.impl("_deform_conv_sigmoid_mask_backward", TORCH_FN(tvdcn_amd::sig_bwd_autograd));
+    m.impl("deform_conv_mask_activation", TORCH_FN(tvdcn_amd::act_fwd_autograd));
+    m.impl("_deform_conv_mask_activation_backward", TORCH_FN(tvdcn_amd::act_bwd_autograd));
     m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_autograd));
 }
 
-TORCH_LIBRARY_IMPL(tvdcn_amd, Autocast, m) {
+TORCH_LIBRARY_IMPL(tvdcn, Autocast, m) {
     m.impl("deform_conv1d", TORCH_FN(tvdcn_amd::Conv1::fwd_ac_c));
     m.impl("deform_conv2d", TORCH_FN(tvdcn_amd::Conv2::fwd_ac_c));
     m.impl("deform_conv3d", TORCH_FN(tvdcn_amd::Conv3::fwd_ac_c));
     m.impl("deform_conv_transpose1d", TORCH_FN(tvdcn_amd::Tr1::fwd_ac_t));
     m.impl("deform_conv_transpose2d", TORCH_FN(tvdcn_amd::Tr2::fwd_ac_t));
     m.impl("deform_conv_transpose3d", TORCH_FN(tvdcn_amd::Tr3::fwd_ac_t));
-    m.impl("deform_conv_sigmoid_mask", TORCH_FN(tvdcn_amd::sig_fwd_autocast));
+    m.impl("deform_conv_mask_activation", TORCH_FN(tvdcn_amd::act_fwd_autocast));
 }

@@ -3,9 +3,14 @@
 Mirrors tvdcn/extension.py (``has_ops``, ``with_cuda``, ``cuda_version``,
 ``cuda_arch_list``, ``_assert_has_ops``; tvdcn/extension.py:61-188). The library
 is ``tvdcn_amd/_C.so``, built in-tree by ``tvdcn_amd/_build.py``; it registers the
-``torch.ops.tvdcn_amd`` operators and links ``libtvdcn_hip.so`` (the gfx950 HIP
-kernels behind the C ABI in ``include/tvdcn_hip.h``). There is no fallback: if
-the library is missing every op raises.
+``torch.ops.tvdcn`` operators (the reference's namespace and schemas) and links
+``libtvdcn_hip.so`` (the gfx950 HIP kernels behind the C ABI in
+``include/tvdcn_hip.h``). There is no fallback: if the library is missing every op
+raises.
+
+``_has_ops`` is a function whose body is a constant, rebound once the library loads
+(as tvdcn/extension.py:55-82 does), so that TorchScript can compile
+``_assert_has_ops`` into scripted modules.
 """
 import os
 from typing import List
@@ -20,15 +25,24 @@ _HAS_OPS = False
 _LOAD_ERROR = None
 
 
+def _has_ops() -> bool:
+    return False
+
+
+def _has_ops_loaded() -> bool:
+    return True
+
+
 def _load() -> bool:
     """Loads ``_C.so`` once it exists; safe to call again (e.g. right after a build)."""
-    global _HAS_OPS, _LOAD_ERROR
+    global _HAS_OPS, _LOAD_ERROR, _has_ops
     if _HAS_OPS:
         return True
     try:
         if os.path.exists(_LIB_PATH):
             torch.ops.load_library(_LIB_PATH)
             _HAS_OPS = True
+            _has_ops = _has_ops_loaded
             _LOAD_ERROR = None
         else:
             _LOAD_ERROR = f"{_LIB_PATH} does not exist"
@@ -40,10 +54,10 @@ def _load() -> bool:
 _load()
 
 
-def _assert_has_ops():
-    if not _HAS_OPS:
+def _assert_has_ops() -> None:
+    if not _has_ops():
         raise RuntimeError(
-            "Couldn't load the tvdcn_amd native ops (" + str(_LOAD_ERROR) + "). Build them with:\n"
+            "Couldn't load the tvdcn native ops (tvdcn_amd/_C.so). Build them with:\n"
             "\tpython -m tvdcn_amd._build")
 
 
@@ -59,7 +73,7 @@ def cuda_version() -> int:
     """
     if not _HAS_OPS:
         return -1
-    return torch.ops.tvdcn_amd._cuda_version()
+    return torch.ops.tvdcn._cuda_version()
 
 
 def with_cuda() -> bool:
@@ -71,4 +85,4 @@ def cuda_arch_list() -> List[str]:
     """Offload targets the kernels were compiled for (``['gfx950']``)."""
     if not _HAS_OPS:
         return []
-    return torch.ops.tvdcn_amd._cuda_arch_flags().split()
+    return torch.ops.tvdcn._cuda_arch_flags().split()

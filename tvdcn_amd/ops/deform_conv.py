@@ -2,11 +2,17 @@
 
 Same signatures, defaults and error behaviour as tvdcn/ops/deform_conv.py
 (functions :30-199, modules :206-751). The functions dispatch to
-``torch.ops.tvdcn_amd.deform_conv{N}d`` whose GPU kernel is the fused gfx950
+``torch.ops.tvdcn.deform_conv{N}d`` whose GPU kernel is the fused gfx950
 gather-GEMM (forward) and the fused grad-columns / scatter / weight-gradient
-kernels (backward).
+kernels (backward). The modules compile with ``torch.jit.script``.
+
+The packed modules differ from the reference in one way that does not change
+their results: when their mask activation is the default ``MaskSigmoid`` or a
+``MaskSoftmax{N}d`` over the convolution's own taps, the activation runs inside the
+kernels' mask load (op ``tvdcn::deform_conv_mask_activation``) instead of as
+separate passes over the mask, and the gradient flows to the generator's logits.
 """
-from typing import Callable, Optional, Union
+from typing import Callable, List, Optional, Tuple, Union
 
 import torch
 import torch.nn.functional as F
@@ -18,7 +24,7 @@ from torch.nn.modules.utils import _pair, _single, _triple
 
 from .activations import MaskSigmoid, MaskSoftmax1d, MaskSoftmax2d, MaskSoftmax3d
 from ..extension import _assert_has_ops
-from ..utils import _log_api_usage_once
+from ..utils import _ints1, _ints2, _ints3, _log_api_usage_once
 
 __all__ = [
     "deform_conv1d", "deform_conv2d", "deform_conv3d",
@@ -26,68 +32,90 @@ __all__ = [
     "PackedDeformConv1d", "PackedDeformConv2d", "PackedDeformConv3d",
 ]
 
-_NTUPLE = {1: _single, 2: _pair, 3: _triple}
-_MASK_SOFTMAX = {1: MaskSoftmax1d, 2: MaskSoftmax2d, 3: MaskSoftmax3d}
-
-
-def _call(dim: int, fn, input, weight, offset, mask, bias, stride, padding, dilation, groups) -> Tensor:
-    if not torch.jit.is_scripting() and not torch.jit.is_tracing():
-        _log_api_usage_once(fn)
-    _assert_has_ops()
-    op = getattr(torch.ops.tvdcn_amd, f"deform_conv{dim}d")
-    nt = _NTUPLE[dim]
-    return op(input, weight, offset, mask, bias, nt(stride), nt(padding), nt(dilation), groups)
-
 
 def deform_conv1d(input: Tensor, weight: Tensor, offset: Optional[Tensor] = None, mask: Optional[Tensor] = None,
-                  bias: Optional[Tensor] = None, stride: _size_1_t = 1, padding: _size_1_t = 0,
-                  dilation: _size_1_t = 1, groups: int = 1) -> Tensor:
+                  bias: Optional[Tensor] = None, stride: Union[int, Tuple[int]] = 1,
+                  padding: Union[int, Tuple[int]] = 0, dilation: Union[int, Tuple[int]] = 1,
+                  groups: int = 1) -> Tensor:
     r"""1D deformable convolution.
 
     input (B, Cin, W); weight (Cout, Cin // groups, kw); offset (B, offset_groups * kw, out_w);
     mask (B, mask_groups * kw, out_w); bias (Cout,). Returns (B, Cout, out_w).
     """
-    return _call(1, deform_conv1d, input, weight, offset, mask, bias, stride, padding, dilation, groups)
+    if not torch.jit.is_scripting() and not torch.jit.is_tracing():
+        _log_api_usage_once(deform_conv1d)
+    _assert_has_ops()
+    return torch.ops.tvdcn.deform_conv1d(input, weight, offset, mask, bias, _ints1(stride), _ints1(padding),
+                                         _ints1(dilation), groups)
 
 
 def deform_conv2d(input: Tensor, weight: Tensor, offset: Optional[Tensor] = None, mask: Optional[Tensor] = None,
-                  bias: Optional[Tensor] = None, stride: _size_2_t = 1, padding: _size_2_t = 0,
-                  dilation: _size_2_t = 1, groups: int = 1) -> Tensor:
+                  bias: Optional[Tensor] = None, stride: Union[int, Tuple[int, int]] = 1,
+                  padding: Union[int, Tuple[int, int]] = 0, dilation: Union[int, Tuple[int, int]] = 1,
+                  groups: int = 1) -> Tensor:
     r"""2D deformable convolution (DCNv1 / DCNv2; https://arxiv.org/abs/1703.06211, https://arxiv.org/abs/1811.11168).
 
     input (B, Cin, H, W); weight (Cout, Cin // groups, kh, kw);
     offset (B, 2 * offset_groups * kh * kw, out_h, out_w), channel ((g * kh + i) * kw + j) * 2 + {0: dy, 1: dx};
     mask (B, mask_groups * kh * kw, out_h, out_w); bias (Cout,). Returns (B, Cout, out_h, out_w).
     """
-    return _call(2, deform_conv2d, input, weight, offset, mask, bias, stride, padding, dilation, groups)
+    if not torch.jit.is_scripting() and not torch.jit.is_tracing():
+        _log_api_usage_once(deform_conv2d)
+    _assert_has_ops()
+    return torch.ops.tvdcn.deform_conv2d(input, weight, offset, mask, bias, _ints2(stride), _ints2(padding),
+                                         _ints2(dilation), groups)
 
 
 def deform_conv3d(input: Tensor, weight: Tensor, offset: Optional[Tensor] = None, mask: Optional[Tensor] = None,
-                  bias: Optional[Tensor] = None, stride: _size_3_t = 1, padding: _size_3_t = 0,
-                  dilation: _size_3_t = 1, groups: int = 1) -> Tensor:
+                  bias: Optional[Tensor] = None, stride: Union[int, Tuple[int, int, int]] = 1,
+                  padding: Union[int, Tuple[int, int, int]] = 0, dilation: Union[int, Tuple[int, int, int]] = 1,
+                  groups: int = 1) -> Tensor:
     r"""3D deformable convolution.
 
     input (B, Cin, D, H, W); weight (Cout, Cin // groups, kd, kh, kw);
     offset (B, 3 * offset_groups * kd * kh * kw, out_d, out_h, out_w) with directions (dz, dy, dx);
     mask (B, mask_groups * kd * kh * kw, out_d, out_h, out_w); bias (Cout,).
     """
-    return _call(3, deform_conv3d, input, weight, offset, mask, bias, stride, padding, dilation, groups)
-
-
-_FUNCTIONAL = {1: deform_conv1d, 2: deform_conv2d, 3: deform_conv3d}
-
-
-def _deform_conv_sigmoid_mask(dim: int, input: Tensor, weight: Tensor, offset: Optional[Tensor], mask_logits: Tensor,
-                              bias: Optional[Tensor], stride, padding, output_padding, dilation, groups: int,
-                              transposed: bool, mask_scale: float) -> Tensor:
-    """Deformable (transposed) convolution whose mask is ``mask_scale * sigmoid(mask_logits)``, the
-    activation applied in the kernels' mask load (the packed modules' default ``MaskSigmoid``,
-    tvdcn/ops/deform_conv.py:502-505, without its separate passes). Gradients flow to the logits."""
+    if not torch.jit.is_scripting() and not torch.jit.is_tracing():
+        _log_api_usage_once(deform_conv3d)
     _assert_has_ops()
-    nt = _NTUPLE[dim]
-    return torch.ops.tvdcn_amd.deform_conv_sigmoid_mask(input, weight, offset, mask_logits, bias, nt(stride),
-                                                        nt(padding), nt(output_padding), nt(dilation), groups,
-                                                        transposed, float(mask_scale))
+    return torch.ops.tvdcn.deform_conv3d(input, weight, offset, mask, bias, _ints3(stride), _ints3(padding),
+                                         _ints3(dilation), groups)
+
+
+# mask activations the kernels can apply in their mask load (codes of tvdcn::deform_conv_mask_activation;
+# the scripted methods below write 0 for _FUSED_NONE: TorchScript reads no module-level ints)
+_FUSED_NONE = 0
+_FUSED_SIGMOID = 1
+_FUSED_SOFTMAX = 2
+
+
+def _deform_conv_mask_activation(input: Tensor, weight: Tensor, offset: Optional[Tensor], mask_logits: Tensor,
+                                 bias: Optional[Tensor], stride: List[int], padding: List[int],
+                                 output_padding: List[int], dilation: List[int], groups: int, transposed: bool,
+                                 activation: int, scale: float) -> Tensor:
+    """Deformable (transposed) convolution whose mask is an activation of ``mask_logits``, applied in the
+    kernels' mask load: ``scale * sigmoid`` (activation 1, tvdcn's ``MaskSigmoid``) or the softmax over
+    the kernel taps of each mask group (activation 2, ``MaskSoftmax{N}d``). Gradients flow to the logits."""
+    _assert_has_ops()
+    return torch.ops.tvdcn.deform_conv_mask_activation(input, weight, offset, mask_logits, bias, stride, padding,
+                                                       output_padding, dilation, groups, transposed, activation,
+                                                       scale)
+
+
+def _mask_fusion_of(activation: Optional[Callable], kernel_size: Tuple[int, ...]) -> Tuple[int, float]:
+    """(code, scale) of a mask activation the kernels apply themselves; (0, 0.0) for any other.
+
+    Only the exact classes qualify (a subclass may change ``forward``). A non-positive sigmoid scale
+    is left to ``MaskSigmoid`` itself, which raises the reference's ``ValueError``."""
+    if type(activation) is MaskSigmoid:
+        if activation.scale > 0:
+            return _FUSED_SIGMOID, float(activation.scale)
+        return _FUSED_NONE, 0.0
+    if type(activation) in (MaskSoftmax1d, MaskSoftmax2d, MaskSoftmax3d):
+        if tuple(activation.kernel_size) == tuple(kernel_size):
+            return _FUSED_SOFTMAX, 0.0
+    return _FUSED_NONE, 0.0
 
 
 class _DeformConvNd(_ConvNd):
@@ -132,117 +160,145 @@ class _DeformConvNd(_ConvNd):
         return s.format(**self.__dict__)
 
 
-class _DeformConvDim(_DeformConvNd):
-    """Rank-specific deformable convolution module; ``_dim`` is set by the subclasses."""
-    _dim = 0
-
-    def __init__(self, in_channels: int, out_channels: int, kernel_size, stride=1, padding=0, dilation=1,
-                 groups: int = 1, bias: bool = True, padding_mode: str = "zeros", device=None, dtype=None) -> None:
-        nt = _NTUPLE[self._dim]
-        super().__init__(in_channels, out_channels, nt(kernel_size), nt(stride),
-                         padding if isinstance(padding, str) else nt(padding), nt(dilation), False, nt(0),
-                         groups, bias, padding_mode, device=device, dtype=dtype)
-
-    def _conv_forward(self, input: Tensor, weight: Tensor, offset: Optional[Tensor], mask: Optional[Tensor],
-                      bias: Optional[Tensor], mask_sigmoid_scale: Optional[float] = None) -> Tensor:
-        if mask_sigmoid_scale is not None:
-            # mask holds logits: the sigmoid runs inside the kernels
-            padding = self.padding
-            if self.padding_mode != "zeros":
-                input = F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode)
-                padding = (0,) * self._dim
-            return _deform_conv_sigmoid_mask(self._dim, input, weight, offset, mask, bias, self.stride, padding,
-                                             (0,) * self._dim, self.dilation, self.groups, False, mask_sigmoid_scale)
-        fn = _FUNCTIONAL[self._dim]
-        if self.padding_mode != "zeros":
-            # non-zero padding modes: pad explicitly, then convolve without padding
-            return fn(F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode), weight, offset,
-                      mask, bias, self.stride, (0,) * self._dim, self.dilation, self.groups)
-        return fn(input, weight, offset, mask, bias, self.stride, self.padding, self.dilation, self.groups)
-
-
-class DeformConv1d(_DeformConvDim):
+class DeformConv1d(_DeformConvNd):
     """See :func:`deform_conv1d`."""
-    _dim = 1
 
     def __init__(self, in_channels: int, out_channels: int, kernel_size: _size_1_t, stride: _size_1_t = 1,
                  padding: Union[str, _size_1_t] = 0, dilation: _size_1_t = 1, groups: int = 1, bias: bool = True,
                  padding_mode: str = "zeros", device=None, dtype=None) -> None:
-        super().__init__(in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
-                         padding_mode, device, dtype)
+        super().__init__(in_channels, out_channels, _single(kernel_size), _single(stride),
+                         padding if isinstance(padding, str) else _single(padding), _single(dilation), False,
+                         _single(0), groups, bias, padding_mode, device=device, dtype=dtype)
+
+    def _conv_forward(self, input: Tensor, weight: Tensor, offset: Optional[Tensor], mask: Optional[Tensor],
+                      bias: Optional[Tensor]) -> Tensor:
+        if self.padding_mode != "zeros":
+            # non-zero padding modes: pad explicitly, then convolve without padding
+            return deform_conv1d(F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode),
+                                 weight, offset, mask, bias, self.stride, (0,), self.dilation, self.groups)
+        return deform_conv1d(input, weight, offset, mask, bias, self.stride, self.padding, self.dilation,
+                             self.groups)
+
+    def _conv_forward_mask_activation(self, input: Tensor, weight: Tensor, offset: Optional[Tensor],
+                                      mask_logits: Tensor, bias: Optional[Tensor], activation: int,
+                                      scale: float) -> Tensor:
+        padding = self.padding
+        if self.padding_mode != "zeros":
+            input = F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode)
+            padding = (0,)
+        return _deform_conv_mask_activation(input, weight, offset, mask_logits, bias, _ints1(self.stride),
+                                            _ints1(padding), [0], _ints1(self.dilation), self.groups, False,
+                                            activation, scale)
 
 
-class DeformConv2d(_DeformConvDim):
+class DeformConv2d(_DeformConvNd):
     """See :func:`deform_conv2d`."""
-    _dim = 2
 
     def __init__(self, in_channels: int, out_channels: int, kernel_size: _size_2_t, stride: _size_2_t = 1,
                  padding: Union[str, _size_2_t] = 0, dilation: _size_2_t = 1, groups: int = 1, bias: bool = True,
                  padding_mode: str = "zeros", device=None, dtype=None) -> None:
-        super().__init__(in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
-                         padding_mode, device, dtype)
+        super().__init__(in_channels, out_channels, _pair(kernel_size), _pair(stride),
+                         padding if isinstance(padding, str) else _pair(padding), _pair(dilation), False,
+                         _pair(0), groups, bias, padding_mode, device=device, dtype=dtype)
+
+    def _conv_forward(self, input: Tensor, weight: Tensor, offset: Optional[Tensor], mask: Optional[Tensor],
+                      bias: Optional[Tensor]) -> Tensor:
+        if self.padding_mode != "zeros":
+            return deform_conv2d(F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode),
+                                 weight, offset, mask, bias, self.stride, (0, 0), self.dilation, self.groups)
+        return deform_conv2d(input, weight, offset, mask, bias, self.stride, self.padding, self.dilation,
+                             self.groups)
+
+    def _conv_forward_mask_activation(self, input: Tensor, weight: Tensor, offset: Optional[Tensor],
+                                      mask_logits: Tensor, bias: Optional[Tensor], activation: int,
+                                      scale: float) -> Tensor:
+        padding = self.padding
+        if self.padding_mode != "zeros":
+            input = F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode)
+            padding = (0, 0)
+        return _deform_conv_mask_activation(input, weight, offset, mask_logits, bias, _ints2(self.stride),
+                                            _ints2(padding), [0, 0], _ints2(self.dilation), self.groups, False,
+                                            activation, scale)
 
 
-class DeformConv3d(_DeformConvDim):
+class DeformConv3d(_DeformConvNd):
     """See :func:`deform_conv3d`."""
-    _dim = 3
 
     def __init__(self, in_channels: int, out_channels: int, kernel_size: _size_3_t, stride: _size_3_t = 1,
                  padding: Union[str, _size_3_t] = 0, dilation: _size_3_t = 1, groups: int = 1, bias: bool = True,
                  padding_mode: str = "zeros", device=None, dtype=None) -> None:
-        super().__init__(in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
-                         padding_mode, device, dtype)
+        super().__init__(in_channels, out_channels, _triple(kernel_size), _triple(stride),
+                         padding if isinstance(padding, str) else _triple(padding), _triple(dilation), False,
+                         _triple(0), groups, bias, padding_mode, device=device, dtype=dtype)
+
+    def _conv_forward(self, input: Tensor, weight: Tensor, offset: Optional[Tensor], mask: Optional[Tensor],
+                      bias: Optional[Tensor]) -> Tensor:
+        if self.padding_mode != "zeros":
+            return deform_conv3d(F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode),
+                                 weight, offset, mask, bias, self.stride, (0, 0, 0), self.dilation, self.groups)
+        return deform_conv3d(input, weight, offset, mask, bias, self.stride, self.padding, self.dilation,
+                             self.groups)
+
+    def _conv_forward_mask_activation(self, input: Tensor, weight: Tensor, offset: Optional[Tensor],
+                                      mask_logits: Tensor, bias: Optional[Tensor], activation: int,
+                                      scale: float) -> Tensor:
+        padding = self.padding
+        if self.padding_mode != "zeros":
+            input = F.pad(input, self._reversed_padding_repeated_twice, mode=self.padding_mode)
+            padding = (0, 0, 0)
+        return _deform_conv_mask_activation(input, weight, offset, mask_logits, bias, _ints3(self.stride),
+                                            _ints3(padding), [0, 0, 0], _ints3(self.dilation), self.groups, False,
+                                            activation, scale)
 
 
-def _check_packed_groups(in_channels: int, out_channels: int, offset_groups: int, mask_groups: int) -> None:
-    for what, n in (("offset_groups", offset_groups), ("mask_groups", mask_groups)):
-        if in_channels % n != 0:
-            raise ValueError(f"in_channels must be divisible by {what}")
-        if out_channels % n != 0:
-            raise ValueError(f"out_channels must be divisible by {what}")
+class _PackedGenerators:
+    """What the packed modules share (tvdcn/ops/deform_conv.py:392-510 and twins): the zero-initialised
+    offset / mask generator convolutions, the mask activation and its fusion into the kernels.
 
-
-def _resolve_mask_activation(mask_activation, dim: int, kernel_size):
-    if isinstance(mask_activation, str):
-        if mask_activation == "sigmoid":
-            return MaskSigmoid(scale=2.)
-        if mask_activation == "softmax":
-            return _MASK_SOFTMAX[dim](kernel_size)
-        raise ValueError('only "sigmoid" and "softmax" activations are supported for mask')
-    return mask_activation
-
-
-class _PackedMixin:
-    """Shared parts of the packed modules: zero-initialised offset/mask generators
-    (tvdcn/ops/deform_conv.py:392-510 and twins)."""
+    ``_mask_fusion`` decides at every eager call from the current ``mask_activation``; a scripted module
+    keeps the decision taken when it was scripted (``__prepare_scriptable__``), as it keeps every other
+    attribute's value."""
 
     def _setup_generators(self, dim: int, offset_groups: int, mask_groups: int, generator_bias: bool,
-                          deformable: bool, modulated: bool, offset_activation, mask_activation, conv_kwargs,
-                          device, dtype) -> None:
-        _check_packed_groups(self.in_channels, self.out_channels, offset_groups, mask_groups)
+                          deformable: bool, modulated: bool, offset_activation, mask_activation, kernel_size,
+                          stride, padding, dilation, device, dtype) -> None:
+        for what, n in (("offset_groups", offset_groups), ("mask_groups", mask_groups)):
+            if self.in_channels % n != 0:
+                raise ValueError(f"in_channels must be divisible by {what}")
+            if self.out_channels % n != 0:
+                raise ValueError(f"out_channels must be divisible by {what}")
         if isinstance(offset_activation, str):
             raise ValueError("currently, no activation is supported for offset")
-        mask_activation = _resolve_mask_activation(mask_activation, dim, self.kernel_size)
+        if isinstance(mask_activation, str):
+            if mask_activation == "sigmoid":
+                mask_activation = MaskSigmoid(scale=2.)
+            elif mask_activation == "softmax":
+                mask_activation = (MaskSoftmax1d, MaskSoftmax2d, MaskSoftmax3d)[dim - 1](self.kernel_size)
+            else:
+                raise ValueError('only "sigmoid" and "softmax" activations are supported for mask')
         self.offset_groups = offset_groups
         self.mask_groups = mask_groups
         self.deformable = deformable
         self.modulated = modulated
-        conv_cls = {1: nn.Conv1d, 2: nn.Conv2d, 3: nn.Conv3d}[dim]
+        conv = (nn.Conv1d, nn.Conv2d, nn.Conv3d)[dim - 1]
         taps = 1
         for k in self.kernel_size:
             taps *= k
         if deformable:
-            self.offset_generator = conv_cls(self.in_channels, dim * taps * offset_groups, groups=offset_groups,
-                                             bias=generator_bias, device=device, dtype=dtype, **conv_kwargs)
+            self.offset_generator = conv(self.in_channels, dim * taps * offset_groups, kernel_size=kernel_size,
+                                         stride=stride, padding=padding, dilation=dilation, groups=offset_groups,
+                                         bias=generator_bias, device=device, dtype=dtype)
         else:
             self.register_module("offset_generator", None)
         if modulated:
-            self.mask_generator = conv_cls(self.in_channels, taps * mask_groups, groups=mask_groups,
-                                           bias=generator_bias, device=device, dtype=dtype, **conv_kwargs)
+            self.mask_generator = conv(self.in_channels, taps * mask_groups, kernel_size=kernel_size,
+                                       stride=stride, padding=padding, dilation=dilation, groups=mask_groups,
+                                       bias=generator_bias, device=device, dtype=dtype)
         else:
             self.register_module("mask_generator", None)
         self.offset_activation = offset_activation
         self.mask_activation = mask_activation
+        self._fused_mask_activation, self._fused_mask_scale = _mask_fusion_of(mask_activation, self.kernel_size)
         self.reset_parameters()
 
     def _reset_generators(self) -> None:
@@ -252,58 +308,117 @@ class _PackedMixin:
                 if gen.bias is not None:
                     init.zeros_(gen.bias)
 
-    def _generate(self, input: Tensor):
-        """offset, mask and the mask's sigmoid scale: a ``MaskSigmoid`` activation (the default) is
-        left to the kernels, which apply it in their mask load — the mask is then returned as
-        logits with the scale; any other activation is applied here (scale None)."""
-        offset = mask = scale = None
+    def __prepare_scriptable__(self):
+        self._fused_mask_activation, self._fused_mask_scale = _mask_fusion_of(self.mask_activation,
+                                                                              self.kernel_size)
+        return self
+
+    def _mask_fusion(self) -> Tuple[int, float]:
+        if not torch.jit.is_scripting():
+            return _mask_fusion_of(self.mask_activation, self.kernel_size)
+        return self._fused_mask_activation, self._fused_mask_scale
+
+    def _generate(self, input: Tensor) -> Tuple[Optional[Tensor], Optional[Tensor], int, float]:
+        """(offset, mask, fused activation code, scale); with a non-zero code the mask holds the logits."""
+        offset: Optional[Tensor] = None
         if self.deformable and self.offset_generator is not None:
             offset = self.offset_generator(input)
             if self.offset_activation is not None:
                 offset = self.offset_activation(offset)
+        mask: Optional[Tensor] = None
         if self.modulated and self.mask_generator is not None:
             mask = self.mask_generator(input)
-            if type(self.mask_activation) is MaskSigmoid:
-                scale = self.mask_activation.scale
-            elif self.mask_activation is not None:
+            fused, scale = self._mask_fusion()
+            if fused != 0:
+                return offset, mask, fused, scale
+            if self.mask_activation is not None:
                 mask = self.mask_activation(mask)
-        return offset, mask, scale
+        return offset, mask, 0, 0.0
 
 
-def _make_packed(base, dim: int, doc: str):
-    class _Packed(_PackedMixin, base):
-        __doc__ = doc
+class PackedDeformConv1d(_PackedGenerators, DeformConv1d):
+    """Packed version of :class:`DeformConv1d`."""
 
-        def __init__(self, in_channels: int, out_channels: int, kernel_size, stride=1, padding=0, dilation=1,
-                     groups: int = 1, offset_groups: int = 1, mask_groups: int = 1, bias: bool = True,
-                     generator_bias: bool = False, deformable: bool = True, modulated: bool = False,
-                     offset_activation: Optional[Union[str, Callable]] = None,
-                     mask_activation: Optional[Union[str, Callable]] = "sigmoid", padding_mode: str = "zeros",
-                     device=None, dtype=None) -> None:
-            base.__init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
-                          padding_mode, device, dtype)
-            # the generators see the same receptive field as the deformable conv
-            conv_kwargs = dict(kernel_size=self.kernel_size, stride=self.stride, padding=self.padding,
-                               dilation=self.dilation)
-            self._setup_generators(dim, offset_groups, mask_groups, generator_bias, deformable, modulated,
-                                   offset_activation, mask_activation, conv_kwargs, device, dtype)
+    def __init__(self, in_channels: int, out_channels: int, kernel_size: _size_1_t, stride: _size_1_t = 1,
+                 padding: Union[str, _size_1_t] = 0, dilation: _size_1_t = 1, groups: int = 1,
+                 offset_groups: int = 1, mask_groups: int = 1, bias: bool = True, generator_bias: bool = False,
+                 deformable: bool = True, modulated: bool = False,
+                 offset_activation: Optional[Union[str, Callable]] = None,
+                 mask_activation: Optional[Union[str, Callable]] = "sigmoid", padding_mode: str = "zeros",
+                 device=None, dtype=None) -> None:
+        DeformConv1d.__init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
+                              padding_mode, device, dtype)
+        # the generators see the same receptive field as the deformable convolution
+        self._setup_generators(1, offset_groups, mask_groups, generator_bias, deformable, modulated,
+                               offset_activation, mask_activation, self.kernel_size, self.stride, self.padding,
+                               self.dilation, device, dtype)
 
-        def reset_parameters(self) -> None:
-            if not hasattr(self, "modulated"):
-                return
-            base.reset_parameters(self)
-            self._reset_generators()
+    def reset_parameters(self) -> None:
+        if not hasattr(self, "modulated"):
+            return
+        DeformConv1d.reset_parameters(self)
+        self._reset_generators()
 
-        def forward(self, input: Tensor) -> Tensor:
-            offset, mask, scale = self._generate(input)
-            return self._conv_forward(input, self.weight, offset, mask, self.bias, mask_sigmoid_scale=scale)
+    def forward(self, input: Tensor) -> Tensor:
+        offset, mask, fused, scale = self._generate(input)
+        if fused != 0 and mask is not None:
+            return self._conv_forward_mask_activation(input, self.weight, offset, mask, self.bias, fused, scale)
+        return self._conv_forward(input, self.weight, offset, mask, self.bias)
 
-    return _Packed
+
+class PackedDeformConv2d(_PackedGenerators, DeformConv2d):
+    """Packed version of :class:`DeformConv2d`."""
+
+    def __init__(self, in_channels: int, out_channels: int, kernel_size: _size_2_t, stride: _size_2_t = 1,
+                 padding: Union[str, _size_2_t] = 0, dilation: _size_2_t = 1, groups: int = 1,
+                 offset_groups: int = 1, mask_groups: int = 1, bias: bool = True, generator_bias: bool = False,
+                 deformable: bool = True, modulated: bool = False,
+                 offset_activation: Optional[Union[str, Callable]] = None,
+                 mask_activation: Optional[Union[str, Callable]] = "sigmoid", padding_mode: str = "zeros",
+                 device=None, dtype=None) -> None:
+        DeformConv2d.__init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
+                              padding_mode, device, dtype)
+        self._setup_generators(2, offset_groups, mask_groups, generator_bias, deformable, modulated,
+                               offset_activation, mask_activation, self.kernel_size, self.stride, self.padding,
+                               self.dilation, device, dtype)
+
+    def reset_parameters(self) -> None:
+        if not hasattr(self, "modulated"):
+            return
+        DeformConv2d.reset_parameters(self)
+        self._reset_generators()
+
+    def forward(self, input: Tensor) -> Tensor:
+        offset, mask, fused, scale = self._generate(input)
+        if fused != 0 and mask is not None:
+            return self._conv_forward_mask_activation(input, self.weight, offset, mask, self.bias, fused, scale)
+        return self._conv_forward(input, self.weight, offset, mask, self.bias)
 
 
-PackedDeformConv1d = _make_packed(DeformConv1d, 1, "Packed version of :class:`DeformConv1d`.")
-PackedDeformConv1d.__name__ = PackedDeformConv1d.__qualname__ = "PackedDeformConv1d"
-PackedDeformConv2d = _make_packed(DeformConv2d, 2, "Packed version of :class:`DeformConv2d`.")
-PackedDeformConv2d.__name__ = PackedDeformConv2d.__qualname__ = "PackedDeformConv2d"
-PackedDeformConv3d = _make_packed(DeformConv3d, 3, "Packed version of :class:`DeformConv3d`.")
-PackedDeformConv3d.__name__ = PackedDeformConv3d.__qualname__ = "PackedDeformConv3d"
+class PackedDeformConv3d(_PackedGenerators, DeformConv3d):
+    """Packed version of :class:`DeformConv3d`."""
+
+    def __init__(self, in_channels: int, out_channels: int, kernel_size: _size_3_t, stride: _size_3_t = 1,
+                 padding: Union[str, _size_3_t] = 0, dilation: _size_3_t = 1, groups: int = 1,
+                 offset_groups: int = 1, mask_groups: int = 1, bias: bool = True, generator_bias: bool = False,
+                 deformable: bool = True, modulated: bool = False,
+                 offset_activation: Optional[Union[str, Callable]] = None,
+                 mask_activation: Optional[Union[str, Callable]] = "sigmoid", padding_mode: str = "zeros",
+                 device=None, dtype=None) -> None:
+        DeformConv3d.__init__(self, in_channels, out_channels, kernel_size, stride, padding, dilation, groups, bias,
+                              padding_mode, device, dtype)
+        self._setup_generators(3, offset_groups, mask_groups, generator_bias, deformable, modulated,
+                               offset_activation, mask_activation, self.kernel_size, self.stride, self.padding,
+                               self.dilation, device, dtype)
+
+    def reset_parameters(self) -> None:
+        if not hasattr(self, "modulated"):
+            return
+        DeformConv3d.reset_parameters(self)
+        self._reset_generators()
+
+    def forward(self, input: Tensor) -> Tensor:
+        offset, mask, fused, scale = self._generate(input)
+        if fused != 0 and mask is not None:
+            return self._conv_forward_mask_activation(input, self.weight, offset, mask, self.bias, fused, scale)
+        return self._conv_forward(input, self.weight, offset, mask, self.bias)
