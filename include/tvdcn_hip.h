@@ -119,6 +119,26 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
                                        void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Allocation-free variant of tvdcn_deform_conv_forward. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, checks and results as
+ * tvdcn_deform_conv_forward minus the workspace: the forward's scratch memory (the channels-last
+ * copy of the input, the weight re-layout, the split accumulator) is a library-owned device array
+ * of TVDCN_SCRATCH_BYTES per GPU, held until the process ends; its address is looked up at the
+ * first call on each device. A problem whose forward workspace
+ * (tvdcn_deform_conv_forward_workspace_size) exceeds TVDCN_SCRATCH_BYTES returns
+ * TVDCN_STATUS_WORKSPACE_TOO_SMALL with a message naming both sizes (a float32 input passed
+ * channels-last, TVDCN_FLAG_CHANNELS_LAST, needs no input copy: only the weight re-layout).
+ * Every call on a GPU uses that GPU's one array: calls that overlap on one GPU (other streams,
+ * other host threads) race and must be serialised by the caller. No hipMalloc / hipFree, no
+ * allocating library call.
+ */
+#define TVDCN_SCRATCH_BYTES (64u << 20)
+tvdcn_status tvdcn_deform_conv_forward_noalloc(const tvdcn_conv_desc *desc, const void *input, const void *weight,
+                                               const void *offset, const void *mask, const void *bias, void *output,
+                                               void *stream);
+
+/*
  * Backward (the `_..._backward` schemas). Replaces ops/cuda/deform_conv2d_kernel.cpp:387-642,
  * ops/cuda/deform_conv_transpose2d_kernel.cpp:374-636 and their 1D/3D twins.
  * grad_offset must be NULL iff offset is NULL, grad_mask iff mask is NULL;

@@ -1,5 +1,17 @@
-"""Shared test helpers: case construction and norm-wise error metrics."""
+"""Shared test helpers: case construction, norm-wise error metrics, the C ABI descriptor."""
+import ctypes
+
 import torch
+
+
+class Desc(ctypes.Structure):
+    """tvdcn_conv_desc of include/tvdcn_hip.h"""
+    _fields_ = [("dim", ctypes.c_int32), ("transposed", ctypes.c_int32), ("dtype", ctypes.c_int32),
+                ("flags", ctypes.c_int32), ("batch", ctypes.c_int64), ("in_channels", ctypes.c_int64),
+                ("out_channels", ctypes.c_int64), ("groups", ctypes.c_int64), ("offset_groups", ctypes.c_int64),
+                ("mask_groups", ctypes.c_int64), ("in_size", ctypes.c_int64 * 3), ("kernel", ctypes.c_int64 * 3),
+                ("stride", ctypes.c_int64 * 3), ("padding", ctypes.c_int64 * 3), ("dilation", ctypes.c_int64 * 3),
+                ("output_padding", ctypes.c_int64 * 3), ("mask_scale", ctypes.c_double)]
 
 
 def rel_err(a, ref):

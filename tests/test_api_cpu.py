@@ -19,6 +19,7 @@ import torch
 import tvdcn
 from tvdcn import extension
 from oracle import oracle
+from helpers import Desc
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "tvdcn_hip.h")
@@ -49,13 +50,6 @@ def test_c_abi_exports_every_declared_function(lib):
         assert hasattr(lib, n), n
 
 
-class Desc(ctypes.Structure):
-    _fields_ = [("dim", ctypes.c_int32), ("transposed", ctypes.c_int32), ("dtype", ctypes.c_int32),
-                ("flags", ctypes.c_int32), ("batch", ctypes.c_int64), ("in_channels", ctypes.c_int64),
-                ("out_channels", ctypes.c_int64), ("groups", ctypes.c_int64), ("offset_groups", ctypes.c_int64),
-                ("mask_groups", ctypes.c_int64), ("in_size", ctypes.c_int64 * 3), ("kernel", ctypes.c_int64 * 3),
-                ("stride", ctypes.c_int64 * 3), ("padding", ctypes.c_int64 * 3), ("dilation", ctypes.c_int64 * 3),
-                ("output_padding", ctypes.c_int64 * 3), ("mask_scale", ctypes.c_double)]
 
 
 def cfg2_desc(**over):

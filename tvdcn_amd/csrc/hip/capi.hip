@@ -342,44 +342,25 @@ tvdcn_status layout_copy(bool to_cl, int32_t dtype, int64_t batch, int64_t chann
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_from_channels_last(kF32, input, output, nullptr, B, C, Sn, s));
     return TVDCN_STATUS_SUCCESS;
 }
-}  // namespace
 
-extern "C" {
-
-tvdcn_status tvdcn_conv_output_size(const tvdcn_conv_desc *desc, int64_t out_size[3]) {
-    int64_t tmp[3] = {1, 1, 1};
-    tvdcn_status st = output_size(desc, tmp);
-    if (st == TVDCN_STATUS_SUCCESS && out_size)
-        for (int i = 0; i < 3; ++i) out_size[i] = tmp[i];
-    return st;
-}
-
-size_t tvdcn_deform_conv_forward_workspace_size(const tvdcn_conv_desc *desc) {
-    Plan pl;
-    if (make_plan(desc, pl)) return 0;
-    return layout(pl, false).total;
-}
-
-size_t tvdcn_deform_conv_backward_workspace_size(const tvdcn_conv_desc *desc) {
-    Plan pl;
-    if (make_plan(desc, pl)) return 0;
-    return layout(pl, true).total;
-}
-
-tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *input, const void *weight,
-                                       const void *offset, const void *mask, const void *bias, void *output,
-                                       void *workspace, size_t workspace_bytes, void *stream) {
-    Plan pl;
-    tvdcn_status st = make_plan(desc, pl);
-    if (st) return st;
-    const Geo &g = pl.g;
-    if (g.B == 0) return TVDCN_STATUS_SUCCESS;   // empty batch: empty output, nothing to do
+tvdcn_status check_forward_pointers(const tvdcn_conv_desc *desc, const void *offset, const void *mask) {
     if ((desc->offset_groups == 0) != (offset == nullptr))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "offset pointer and offset_groups disagree");
     if ((desc->mask_groups == 0) != (mask == nullptr))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "mask pointer and mask_groups disagree");
+    return TVDCN_STATUS_SUCCESS;
+}
+
+// Forward on a validated plan (batch > 0, pointers checked) with a workspace of at least layout(pl, false).total
+// bytes; shared by tvdcn_deform_conv_forward (caller's workspace) and
+// tvdcn_deform_conv_forward_noalloc (the per-device scratch array). Every workspace byte the
+// kernels read is written first in the same call (the zero-filled accumulator by a fill kernel),
+// so the workspace may hold anything on entry.
+tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const void *input, const void *weight,
+                             const void *offset, const void *mask, const void *bias, void *output, void *workspace,
+                             void *stream) {
+    const Geo &g = pl.g;
     const Layout L = layout(pl, false);
-    if (workspace_bytes < L.total) return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
     if (!input || !weight || !output) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
     if (!aligned16(input) || !aligned16(workspace))
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "input and workspace must be 16-byte aligned");
@@ -427,6 +408,93 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
     return TVDCN_STATUS_SUCCESS;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of tvdcn_deform_conv_forward_noalloc: one array per GPU in the code object's
+// device memory, held until the process ends. Its device address is looked up once per
+// device (hipGetSymbolAddress, with that device current) at the entry point's first call on
+// the device, and only that address is handed to kernels (the array's name is a host-side
+// stand-in in host code).
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[TVDCN_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+tvdcn_status scratch_of_current_device(void **out) {
+    static std::mutex mu;
+    static void *ptrs[kMaxDevices] = {};
+    int dev = -1;
+    TVDCN_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(TVDCN_STATUS_NOT_SUPPORTED, "forward_noalloc: device index above 63");
+    std::lock_guard<std::mutex> lk(mu);
+    if (ptrs[dev] == nullptr) {
+        void *p = nullptr;
+        TVDCN_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (p == nullptr) return fail(TVDCN_STATUS_HIP_ERROR, "forward_noalloc: no device address for the scratch array");
+        ptrs[dev] = p;
+    }
+    *out = ptrs[dev];
+    return TVDCN_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+tvdcn_status tvdcn_conv_output_size(const tvdcn_conv_desc *desc, int64_t out_size[3]) {
+    int64_t tmp[3] = {1, 1, 1};
+    tvdcn_status st = output_size(desc, tmp);
+    if (st == TVDCN_STATUS_SUCCESS && out_size)
+        for (int i = 0; i < 3; ++i) out_size[i] = tmp[i];
+    return st;
+}
+
+size_t tvdcn_deform_conv_forward_workspace_size(const tvdcn_conv_desc *desc) {
+    Plan pl;
+    if (make_plan(desc, pl)) return 0;
+    return layout(pl, false).total;
+}
+
+size_t tvdcn_deform_conv_backward_workspace_size(const tvdcn_conv_desc *desc) {
+    Plan pl;
+    if (make_plan(desc, pl)) return 0;
+    return layout(pl, true).total;
+}
+
+tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *input, const void *weight,
+                                       const void *offset, const void *mask, const void *bias, void *output,
+                                       void *workspace, size_t workspace_bytes, void *stream) {
+    Plan pl;
+    tvdcn_status st = make_plan(desc, pl);
+    if (st) return st;
+    if (pl.g.B == 0) return TVDCN_STATUS_SUCCESS;   // empty batch: empty output, nothing to do
+    st = check_forward_pointers(desc, offset, mask);
+    if (st) return st;
+    if (workspace_bytes < layout(pl, false).total) return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
+    return forward_planned(pl, desc, input, weight, offset, mask, bias, output, workspace, stream);
+}
+
+tvdcn_status tvdcn_deform_conv_forward_noalloc(const tvdcn_conv_desc *desc, const void *input, const void *weight,
+                                               const void *offset, const void *mask, const void *bias, void *output,
+                                               void *stream) {
+    Plan pl;
+    tvdcn_status st = make_plan(desc, pl);
+    if (st) return st;
+    if (pl.g.B == 0) return TVDCN_STATUS_SUCCESS;
+    st = check_forward_pointers(desc, offset, mask);
+    if (st) return st;
+    const size_t need = layout(pl, false).total;
+    if (need > (size_t)TVDCN_SCRATCH_BYTES)
+        return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL,
+                    "forward_noalloc: this problem needs " + std::to_string(need) +
+                        " bytes of scratch; the library's per-GPU scratch holds " +
+                        std::to_string((size_t)TVDCN_SCRATCH_BYTES) +
+                        " (use tvdcn_deform_conv_forward with a workspace)");
+    void *ws = nullptr;
+    st = scratch_of_current_device(&ws);
+    if (st) return st;
+    return forward_planned(pl, desc, input, weight, offset, mask, bias, output, ws, stream);
+}
 tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void *grad_out, const void *input,
                                         const void *weight, const void *offset, const void *mask, void *grad_input,
                                         void *grad_weight, void *grad_offset, void *grad_mask, void *grad_bias,
