@@ -4,13 +4,14 @@ The C ABI launches only kernels on the caller's stream (fills are kernels, no me
 host synchronisation) and the torch layer takes every buffer from the caching allocator, so a
 forward + backward can be captured once and replayed. Each replay runs on inputs rewritten in
 place between replays (with eager work and synchronisations in between) and is checked
-against the eager ops on the same inputs.
+against the float64 oracle on the same inputs (and against the eager ops).
 """
 import pytest
 import torch
 
 import tvdcn
-from helpers import make_case, rel_err
+from oracle import oracle
+from helpers import make_case, oracle_conv, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -67,15 +68,22 @@ def test_hip_graph_capture_and_replay_fp32(dim, transposed):
         torch.cuda.synchronize()
         ref = run()
         torch.cuda.synchronize()
-        for name, a, r in zip(("output",) + tuple("grad_" + n for n in names), outs, ref):
+        host = [st[n].double().cpu() for n in names]
+        kw = dict(stride=[1] * dim, padding=[1] * dim, dilation=[1] * dim, groups=1, transposed=transposed,
+                  output_padding=[0] * dim)
+        o_ref = [oracle.forward(dim, *host, **kw)] + list(oracle.backward(dim, gy.double().cpu(), *host, **kw))
+        for i, (name, a, r, o) in enumerate(zip(("output",) + tuple("grad_" + n for n in names), outs, ref, o_ref)):
             assert r is not None and a is not None, name
+            e = rel_err(a.double().cpu(), o)
+            assert e < (1e-5 if i == 0 else 1e-4), f"replay {rep}: {name} rel err {e} (oracle)"
             e = rel_err(a.double().cpu(), r.double().cpu())
-            assert e < 1e-5, f"replay {rep}: {name} rel err {e}"
+            assert e < 1e-5, f"replay {rep}: {name} rel err {e} (eager)"
 
 
 def test_torch_compile_on_gpu_fp32():
     """torch.compile (aot_eager, fullgraph) of a forward + backward runs the same HIP kernels as
-    eager execution."""
+    eager execution: the loss gradients against the float64 oracle (differentiable through
+    helpers.oracle_conv) and against eager execution."""
     torch._dynamo.reset()
     case = make_case(2, False, batch=2, cin=32, cout=32, kernel=[3, 3], stride=[1, 1], padding=[1, 1],
                      dilation=[1, 1], in_size=[14, 12], out_pad=[0, 0], seed=610)
@@ -92,6 +100,10 @@ def test_torch_compile_on_gpu_fp32():
     comp = leaves()
     torch.compile(f, backend="aot_eager", fullgraph=True)(*comp).backward()
     torch.cuda.synchronize()
-    for n, a, r in zip(names, comp, eager):
+    ref = [case[n].to(torch.float32).double().requires_grad_(True) for n in names]
+    (oracle_conv(2, *ref, [1, 1], [1, 1], [1, 1], 1) ** 2).sum().backward()
+    for n, a, r, o in zip(names, comp, eager, ref):
+        e = rel_err(a.grad.double().cpu(), o.grad)
+        assert e < 1e-4, f"grad_{n} rel err {e} (oracle)"
         e = rel_err(a.grad.double().cpu(), r.grad.double().cpu())
-        assert e < 1e-5, f"grad_{n} rel err {e}"
+        assert e < 1e-5, f"grad_{n} rel err {e} (eager)"

@@ -13,7 +13,7 @@ import torch
 import tvdcn
 from tvdcn.ops.deform_conv import _deform_conv_mask_activation
 from helpers import make_case, mask_activation_f64, oracle_conv, rel_err
-from test_gpu_parity import TOL
+from test_gpu_parity import TOL, half_position_offsets
 
 pytestmark = pytest.mark.gpu
 
@@ -25,6 +25,9 @@ def _oracle_activated(case, dim, transposed, vals, activation, scale):
     """float64 reference on CPU leaves; returns (out, leaves)"""
     leaves = [None if v is None else v.detach().double().cpu().requires_grad_(True) for v in vals]
     x, w, o, logits, b = leaves
+    if o is not None and vals[2].dtype == torch.float16:
+        # float16 sampling positions are rounded to half precision (as the reference's c10::Half)
+        o = o + (half_position_offsets(case, o.detach()) - o.detach())
     kn = 1
     for k in w.shape[2:]:
         kn *= k

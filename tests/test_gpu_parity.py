@@ -3,7 +3,8 @@ tvdcn's CPU algorithm, itself pinned to the reference build and the golden fixtu
 
 Tolerances (norm-wise, see helpers.rel_err): float64 1e-9; float32 forward 1e-5 and
 backward 1e-4 (atomic ordering); float16 / bfloat16 1e-2 against the oracle run on
-the same rounded inputs.
+the same rounded inputs (float16: and sampling positions rounded to half precision, as the
+reference's c10::Half arithmetic rounds them).
 """
 import itertools
 
@@ -41,9 +42,37 @@ def run_gpu(case, dtype, grad_out=None):
     return out, [t.grad if t is not None else None for t in ts], grad_out
 
 
+def half_position_offsets(case, offset):
+    """Offsets that put the float64 oracle's sampling positions where float16 arithmetic puts them:
+    base + offset rounded once to half precision, as the reference forms `y + offset` in c10::Half
+    (cpu/deform_conv2d_common_kernels.cpp:407-411, cuda/deform_conv2d_common_kernels.cu:170-178) and the
+    kernels do for float16 inputs. The gradient reported for an offset is the one at that position."""
+    dim = case["dim"]
+    ks = list(case["weight"].shape[2:])
+    grid = list(offset.shape[2:])
+    B, ch = offset.shape[:2]
+    kn = 1
+    for k in ks:
+        kn *= k
+    og = ch // (dim * kn)
+    taps = torch.tensor(list(__import__("itertools").product(*[range(k) for k in ks])))   # (kn, dim)
+    pos = offset.reshape(B, og, kn, dim, *grid).clone()
+    for a in range(dim):
+        shape = [1] * dim
+        shape[a] = grid[a]
+        p = torch.arange(grid[a], dtype=torch.float64).reshape(shape)
+        base = p * case["stride"][a] - case["padding"][a] + \
+            taps[:, a].double().reshape([kn] + [1] * dim) * case["dilation"][a]   # (kn, *grid)
+        exact = pos[:, :, :, a] + base
+        pos[:, :, :, a] = exact.to(torch.float16).double() - base
+    return pos.reshape(offset.shape)
+
+
 def run_oracle(case, grad_out, dtype):
     cast = (lambda t: None if t is None else t.to(dtype).double())
     args = [cast(case[n]) for n in ("input", "weight", "offset", "mask", "bias")]
+    if dtype == torch.float16 and args[2] is not None:
+        args[2] = half_position_offsets(case, args[2])
     kw = dict(stride=case["stride"], padding=case["padding"], dilation=case["dilation"], groups=case["groups"],
               transposed=case["transposed"], output_padding=case["output_padding"])
     out = oracle.forward(case["dim"], *args, **kw)
@@ -148,3 +177,34 @@ def test_mask_softmax_matches_torch_softmax():
         y.backward(gy)
         yr.backward(gy)
         assert rel_err(x.grad, xr.grad) < 1e-12
+
+
+@pytest.mark.parametrize("dim,transposed", [(2, False), (2, True), (1, False), (3, False)])
+def test_autocast_runs_in_float32_and_casts_back(dim, transposed):
+    """Under torch.autocast("cuda"), float16 inputs run in float32 and the result is cast back to the
+    input's type (autocast/deform_conv2d_kernel.cpp:9-38): the same numbers as the float32 op on the
+    widened inputs, cast to float16; gradients reach the float16 leaves; float32 against the oracle."""
+    case = make_case(dim, transposed, batch=2, cin=16, cout=16, seed=700 + dim)
+    names = ("input", "weight", "offset", "mask", "bias")
+    fn = getattr(tvdcn, f"deform_conv_transpose{dim}d" if transposed else f"deform_conv{dim}d")
+    kw = dict(stride=case["stride"], padding=case["padding"], dilation=case["dilation"], groups=case["groups"])
+    if transposed:
+        kw["output_padding"] = case["output_padding"]
+    ts16 = [case[n].to(DEV, torch.float16).requires_grad_(True) for n in names]
+    with torch.autocast("cuda", dtype=torch.float16):
+        y = fn(*ts16, **kw)
+    assert y.dtype == torch.float16
+    ts32 = [t.detach().float().requires_grad_(True) for t in ts16]
+    y32 = fn(*ts32, **kw)
+    assert torch.equal(y, y32.half())
+    g = torch.rand(y.shape, generator=torch.Generator().manual_seed(7), dtype=torch.float64)
+    y.backward(g.to(DEV, torch.float16))
+    y32.backward(g.to(DEV, torch.float16).float())
+    torch.cuda.synchronize()
+    for n, a, b in zip(names, ts16, ts32):
+        assert a.grad is not None and a.grad.dtype == torch.float16, n
+        # float atomics in the offset / mask gradients: not bit-reproducible from run to run
+        assert rel_err(a.grad, b.grad.half()) < 1e-3, n
+    rounded = {k: (v.half().double() if isinstance(v, torch.Tensor) else v) for k, v in case.items()}
+    ref_out, _ = run_oracle(rounded, g, torch.float64)
+    assert rel_err(y32, ref_out) < 1e-5

@@ -28,12 +28,16 @@
 //     s_c = 29 - ceil(log2 B_c), B_c = sum of |G * mask| over every (pixel, tap)
 //     accumulated so far: a bilinear corner weight is at most 1 and each (pixel,
 //     tap) reaches a cell through at most one corner, so every cell sum stays
-//     below 2^29 (no overflow) and is rounded at B_c * 2^-29 per term (~1e-9 B_c).
+//     below 2^29 (no overflow); each term is rounded to the unit 2^-s_c <= 2^-28 B_c.
 //     Integer sums are also order independent. When a pass of taps grows B_c,
-//     the values already held are shifted down to the new scale. A non-finite
-//     bound sends the pass to global float atomics (after flushing what the
-//     window holds) so that inf/nan propagate as in the reference. Corners
-//     outside the window go to global float atomics.
+//     the values already held are shifted down to the new scale (rounded to
+//     nearest). The unit is relative to the tile's bound, not to each cell, so a
+//     pass in which one term |G * mask| exceeds 2^-6 of its channel's bound (a
+//     gradient spike: the bound would be the spike's, and quiet cells of the tile
+//     would be rounded at it) does not use the window; neither does a pass with a
+//     non-finite bound (inf/nan must propagate as in the reference). Such a pass
+//     goes to global float atomics, after the window flushes what it holds.
+//     Corners outside the window go to global float atomics.
 //   * The window (sampled-grid box around the tile's undeformed footprint plus a
 //     margin R per axis) accumulates over all passes of the tile and is flushed
 //     once: one float atomic per non-zero (cell, channel), 16 consecutive channels
@@ -61,9 +65,11 @@ static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
 static_assert(NT == BC * 32, "window rescale: 32 threads per channel");
 
 // LDS words ahead of the windows: geometry table [WIN_TMAX][BPX] x (position, mask),
-// per-wave channel bounds, scale exponents
+// per-wave channel bounds, scale exponents and flags, held bounds, rescale shifts,
+// largest terms
 constexpr int GEO_WORDS = WIN_TMAX * BPX * 4;
-constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + 3 * BC + 4;
+constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + 4 * BC + 4;
+constexpr int SPIKE_BITS = 6;     // a term above 2^-SPIKE_BITS of its channel's bound: no window
 
 // Offset / mask gradient terms of one (pixel, tap) as the reference's corner sums, from
 // gk[k] = G contracted with X at corner k (k = 2 * y bit + x bit in 2D, x bit in 1D):
@@ -113,6 +119,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     int *scl = reinterpret_cast<int *>(bsum + NW * BC);        // [BC] scale exponents, [BC] = non-finite flag
     float *btot = bsum + NW * BC + BC + 4;                     // [BC] bound of what the window holds
     int *shift = reinterpret_cast<int *>(btot + BC);           // [BC] rescale of the window for a pass
+    int *bmax = shift + BC;                                    // [BC] largest |G * mask| (float bits, >= 0)
     float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X window (COORD)
     int *iwin = reinterpret_cast<int *>(xwin + (COORD ? wt.cells * XS : 0));   // [BC][cst] fixed point
     const int cst = fix_stride(wt.cells);
@@ -140,6 +147,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     if constexpr (COORD) fill_xwin(g, wt, tile, xb, xwin, tid, NT);
     if constexpr (SCATTER) {
         for (int i = tid; i < BC * cst; i += NT) iwin[i] = 0;
+        if (tid < BC) bmax[tid] = 0;
     }
 
     // ---- K-loop operands, straight to registers ---------------------------------
@@ -307,7 +315,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
         int sexp[4] = {0, 0, 0, 0};   // scale exponents of this lane's channels c0 + mq + v
         bool use_window = false;
         if constexpr (SCATTER) {
-            float part[4] = {0.f, 0.f, 0.f, 0.f};
+            float part[4] = {0.f, 0.f, 0.f, 0.f}, pmax[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int pb = 0; pb < PB; ++pb) {
                 const int i = wave * (PB * 16) + pb * 16 + (lane & 15);
@@ -316,18 +324,30 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     if (tp < ntaps && zp[pb] >= 0) {
                         const float mk = fabsf(rec_mask<DIM>(geo[tp * BPX + i]));
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) part[v] += fabsf(acc[tp][pb][v]) * mk;
+                        for (int v = 0; v < 4; ++v) {
+                            const float a = fabsf(acc[tp][pb][v]) * mk;
+                            part[v] += a;
+                            pmax[v] = fmaxf(pmax[v], a);
+                        }
                     }
                 }
             }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
 #pragma unroll
-                for (int m = 1; m < 16; m <<= 1) part[v] += __shfl_xor(part[v], m);
+                for (int m = 1; m < 16; m <<= 1) {
+                    part[v] += __shfl_xor(part[v], m);
+                    pmax[v] = fmaxf(pmax[v], __shfl_xor(pmax[v], m));
+                }
             }
             if ((lane & 15) == 0) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) bsum[wave * BC + mq + v] = part[v];
+                for (int v = 0; v < 4; ++v) {
+                    bsum[wave * BC + mq + v] = part[v];
+                    // non-negative floats order as their bit patterns (a nan has an exponent of
+                    // all ones: it lands above every finite value, and the bound is not finite)
+                    atomicMax(bmax + mq + v, __float_as_int(pmax[v]));
+                }
             }
             __syncthreads();
             if (tid < BC) {
@@ -335,8 +355,11 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 #pragma unroll
                 for (int w = 0; w < NW; ++w) bc += bsum[w * BC + tid];
                 const float tot = (win_data ? btot[tid] : 0.f) + bc;
-                // the pass uses the window only if every bound is finite (ballot over 16 lanes)
-                const unsigned long long bad = __ballot(!isfinite(tot));
+                const float big = __int_as_float(bmax[tid]);
+                bmax[tid] = 0;   // for the next pass (read after this pass's last barrier)
+                // the pass uses the window only if every bound is finite and no term of any
+                // channel exceeds 2^-SPIKE_BITS of its bound (ballot over 16 lanes)
+                const unsigned long long bad = __ballot(!isfinite(tot) || big > ldexpf(tot, -SPIKE_BITS));
                 int e = 0;
                 if (tot > 0.f && isfinite(tot)) frexpf(tot, &e);   // tot < 2^e
                 shift[tid] = 0;
@@ -349,16 +372,20 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
             }
             __syncthreads();
             if (scl[BC] != 0) {
-                // not finite: what the window holds goes out at its scale, the pass goes to
-                // global float atomics (inf / nan propagate as in the reference)
+                // not finite, or a spike: what the window holds goes out at its scale, the pass
+                // goes to global float atomics (inf / nan propagate as in the reference)
                 if (win_data) flush_window(true);
                 win_data = false;
             } else {
                 if (win_data) {
-                    // arithmetic shifts (rounding down by under one unit of the new scale)
+                    // rescale to nearest (halves up); a shift of 31 or more leaves under half a unit
                     const int c = tid >> 5, sh = shift[c];
-                    if (sh > 0)
-                        for (int cell = tid & 31; cell < cst; cell += 32) iwin[c * cst + cell] >>= sh;
+                    if (sh > 0) {
+                        for (int cell = tid & 31; cell < cst; cell += 32) {
+                            const int v = iwin[c * cst + cell];   // |v| < 2^29
+                            iwin[c * cst + cell] = sh >= 31 ? 0 : (v + (1 << (sh - 1))) >> sh;
+                        }
+                    }
                     __syncthreads();
                 }
                 use_window = wt.cells > 0;

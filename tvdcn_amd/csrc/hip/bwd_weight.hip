@@ -126,7 +126,7 @@ bwd_weight_kernel(const Geo g, const T *__restrict__ z, const A *__restrict__ xc
         Point<DIM, A> pt = sample_point<DIM, A, T>(g, nullptr, st.b2, st.p2, t, 0);
         if (deformable) {
 #pragma unroll
-            for (int a = 0; a < DIM; ++a) pt.pos[a] += st.off[a];
+            for (int a = 0; a < DIM; ++a) pt.pos[a] = round_position<T, A>(pt.pos[a] + st.off[a]);
         }
         st.gc = gather_corners<DIM, A>(g, axis_weights<DIM, A>(g, pt, deformable));
         st.mk = st.mraw;

@@ -219,6 +219,19 @@ __device__ __forceinline__ void decompose_pix(const Geo &g, int p, int pp[DIM]) 
     }
 }
 
+// A sample position in the arithmetic of the input's type, as the reference's kernels form
+// `y + offset` in scalar_t (tvdcn/csrc/ops/cuda/deform_conv2d_common_kernels.cu:170-178): an exact
+// float sum of the integer base and the offset, rounded once to the type -- float32 by the float
+// addition itself, float16 to half precision (c10::Half arithmetic), float64 exact. bfloat16 has no
+// reference path (its dispatch excludes the type): its positions stay float32.
+template <typename T, typename A>
+__device__ __forceinline__ A round_position(A v) {
+    if constexpr (std::is_same_v<T, __half>)
+        return static_cast<A>(__half2float(__float2half(static_cast<float>(v))));
+    else
+        return v;
+}
+
 // Integer base point h*stride - pad + i*dilation per axis
 // (deform_conv2d_common_kernels.cu:171-172) plus the offsets of group ogi
 // (offset channel ((ogi*Kn + t)*DIM + axis), deform_conv2d_kernel.cpp:278-286).
@@ -238,7 +251,7 @@ __device__ __forceinline__ Point<DIM, A> sample_point(const Geo &g, const T *__r
     if (offset != nullptr) {
         const T *o = offset + ((size_t)(b * g.og + ogi) * g.Kn + t) * DIM * (size_t)g.Pn + p;
 #pragma unroll
-        for (int a = 0; a < DIM; ++a) pt.pos[a] += to_acc<A>(o[(size_t)a * g.Pn]);
+        for (int a = 0; a < DIM; ++a) pt.pos[a] = round_position<T, A>(pt.pos[a] + to_acc<A>(o[(size_t)a * g.Pn]));
     }
     return pt;
 }

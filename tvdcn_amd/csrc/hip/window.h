@@ -354,7 +354,7 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
                 for (int a = 0; a < DIM; ++a) {
                     const int ee = 3 - DIM + a;
                     pt.base[a] = pp[a] * g.st[ee] - g.pad[ee] + kk[a] * g.dil[ee];
-                    pt.pos[a] = (float)pt.base[a] + ov[j][a];
+                    pt.pos[a] = round_position<T, float>((float)pt.base[a] + ov[j][a]);
                     r[a] = pt.pos[a];
                 }
                 mk = mv[j];
