@@ -43,7 +43,7 @@ typedef enum {
     TVDCN_STATUS_SUCCESS = 0,
     TVDCN_STATUS_INVALID_ARGUMENT = 1,   /* shape / parameter check failed (RuntimeError in the reference) */
     TVDCN_STATUS_WORKSPACE_TOO_SMALL = 2,
-    TVDCN_STATUS_NOT_SUPPORTED = 3,      /* e.g. a tensor above 2^31 - 1 elements */
+    TVDCN_STATUS_NOT_SUPPORTED = 3,      /* e.g. one image's tensor above the batch-block limit */
     TVDCN_STATUS_HIP_ERROR = 4           /* a kernel launch failed */
 } tvdcn_status;
 
@@ -104,9 +104,20 @@ typedef struct {
  * when the descriptor fails the reference's shape checks. */
 tvdcn_status tvdcn_conv_output_size(const tvdcn_conv_desc *desc, int64_t out_size[3]);
 
-/* Bytes of workspace needed by tvdcn_deform_conv_forward / _backward. */
+/* Bytes of workspace needed by tvdcn_deform_conv_forward / _backward (0 when the descriptor is
+ * invalid). The kernels index in 32 bits: the entry points run the batch in blocks of images whose
+ * tensors hold at most tvdcn_set_max_block_elements' limit of elements each (2^31 - 1 by default;
+ * the weight gradient is accumulated over the blocks), and the workspace serves one block at a
+ * time. The reference blocks its batch as well (n_parallel_imgs, ops/utils/parallel_helpers.h:7-16,
+ * ops/cuda/deform_conv2d_kernel.cpp:149). One image above the limit is TVDCN_STATUS_NOT_SUPPORTED. */
 size_t tvdcn_deform_conv_forward_workspace_size(const tvdcn_conv_desc *desc);
 size_t tvdcn_deform_conv_backward_workspace_size(const tvdcn_conv_desc *desc);
+
+/* Sets the largest element count of any batch-sized tensor in one batch block (1 .. 2^31 - 1;
+ * default 2^31 - 1): a lower limit means smaller blocks and a smaller workspace. Process-wide;
+ * call it while no entry point runs. Counterpart of the reference's kMaxParallelImgs
+ * (ops/utils/parallel_helpers.h:7-16), counted in elements instead of images. */
+tvdcn_status tvdcn_set_max_block_elements(int64_t max_elements);
 
 /*
  * Forward of deform_conv{1,2,3}d / deform_conv_transpose{1,2,3}d.

@@ -591,3 +591,41 @@ def test_c_abi_layout_copy_argument_checks(lib):
         assert lib.tvdcn_last_error() == b""
         assert fn(0, 2, 3, 4, None, None, None) != 0                          # null pointers
         assert b"null pointer" in lib.tvdcn_last_error()
+
+
+def test_c_abi_batch_blocks_beyond_32_bit_indexing(lib):
+    """A descriptor above 2^31 elements (B=128, C=256, 256x256 float32: 2^31 input elements) plans
+    in batch blocks: the workspace queries succeed and serve one block; lowering the block limit
+    shrinks the workspace; one image above the limit is refused; the limit's range is checked."""
+    lib.tvdcn_deform_conv_forward_workspace_size.restype = ctypes.c_size_t
+    lib.tvdcn_deform_conv_backward_workspace_size.restype = ctypes.c_size_t
+    lib.tvdcn_set_max_block_elements.argtypes = [ctypes.c_int64]
+    lib.tvdcn_set_max_block_elements.restype = ctypes.c_int
+    lib.tvdcn_last_error.restype = ctypes.c_char_p
+    big = cfg2_desc(batch=128)
+    for i in range(2):
+        big.in_size[i] = 256
+    assert 128 * 256 * 256 * 256 >= 2 ** 31
+    fw = lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(big))
+    bw = lib.tvdcn_deform_conv_backward_workspace_size(ctypes.byref(big))
+    half = cfg2_desc(batch=64)   # the largest block below 2^31 elements: 127 images, a remainder of 1
+    for i in range(2):
+        half.in_size[i] = 256
+    assert fw > 0 and bw > 0
+    assert fw <= lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(half)) * 2
+    try:
+        per_image = 256 * 256 * 256
+        assert lib.tvdcn_set_max_block_elements(4 * per_image) == 0
+        fw4 = lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(big))
+        assert 0 < fw4 < fw / 16
+        assert lib.tvdcn_set_max_block_elements(per_image - 1) == 0
+        assert lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(big)) == 0
+        out = (ctypes.c_int64 * 3)()
+        st = lib.tvdcn_deform_conv_forward(ctypes.byref(big), None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                           None, None, None, ctypes.c_size_t(0), None)
+        assert st == 3 and b"32 bits" in lib.tvdcn_last_error()
+        assert lib.tvdcn_set_max_block_elements(0) == 1
+        assert lib.tvdcn_set_max_block_elements(2 ** 31) == 1
+    finally:
+        assert lib.tvdcn_set_max_block_elements(2 ** 31 - 1) == 0
+    assert lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(big)) == fw

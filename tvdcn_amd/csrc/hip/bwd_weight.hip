@@ -287,7 +287,8 @@ bwd_weight_kernel(const Geo g, const T *__restrict__ z, const A *__restrict__ xc
 // 32-bit index arithmetic: the weight's element count and the unit count fit in int.
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) weight_reduce_kernel(const A *__restrict__ part, T *__restrict__ gw, int k_splits,
-                                                            int G, int Kn, int Mg, int Cg, int ups, int n_sp, int tpp) {
+                                                            int G, int Kn, int Mg, int Cg, int ups, int n_sp, int tpp,
+                                                            bool accumulate) {
     const int per_split = G * Kn * Mg * Cg;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < per_split; i += gridDim.x * blockDim.x) {
         const int c = i % Cg;
@@ -303,19 +304,20 @@ __global__ void __launch_bounds__(256) weight_reduce_kernel(const A *__restrict_
         }
         A sum = A(0);
         for (int ks = ks0; ks < ks1; ++ks) sum += part[(size_t)ks * per_split + i];
-        gw[(((size_t)grp * Mg + m) * Cg + c) * Kn + t] = from_acc<T, A>(sum);
+        T *dst = gw + (((size_t)grp * Mg + m) * Cg + c) * Kn + t;
+        *dst = from_acc<T, A>(accumulate ? to_acc<A>(*dst) + sum : sum);
     }
 }
 
 template <typename T, typename A>
-hipError_t launch_reduce(const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s, int ups, int n_sp,
-                         int tpp) {
+hipError_t launch_reduce(const Geo &g, int k_splits, const void *part, void *gw, bool accumulate, hipStream_t s, int ups,
+                         int n_sp, int tpp) {
     if (ups > 0 && (n_sp <= 0 || tpp <= 0)) return hipErrorInvalidValue;
     const size_t n = (size_t)g.G * g.Kn * g.Mg * g.Cg;
     if (n > (size_t)INT_MAX) return hipErrorInvalidValue;
     const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL((weight_reduce_kernel<T, A>), dim3(blocks), dim3(256), 0, s, static_cast<const A *>(part),
-                       static_cast<T *>(gw), k_splits, g.G, g.Kn, g.Mg, g.Cg, ups, n_sp, tpp);
+                       static_cast<T *>(gw), k_splits, g.G, g.Kn, g.Mg, g.Cg, ups, n_sp, tpp, accumulate);
     return hipGetLastError();
 }
 
@@ -353,7 +355,7 @@ hipError_t launch_w(const Geo &g, const WeightTiles &tl, const void *z, const vo
 
 template <typename T, typename A>
 hipError_t launch_d(int dim, const Geo &g, const WeightTiles &tl, const void *z, const void *xcl, const void *offset,
-                    const void *mask, void *part, void *gw, hipStream_t s) {
+                    const void *mask, void *part, void *gw, bool accumulate, hipStream_t s) {
     hipError_t e = hipErrorInvalidValue;
     switch (dim) {
         case 1: e = launch_w<1, T, A>(g, tl, z, xcl, offset, mask, part, s); break;
@@ -361,7 +363,7 @@ hipError_t launch_d(int dim, const Geo &g, const WeightTiles &tl, const void *z,
         case 3: e = launch_w<3, T, A>(g, tl, z, xcl, offset, mask, part, s); break;
     }
     if (e != hipSuccess) return e;
-    return launch_reduce<T, A>(g, tl.k_splits, part, gw, s, 0, 0, 0);
+    return launch_reduce<T, A>(g, tl.k_splits, part, gw, accumulate, s, 0, 0, 0);
 }
 
 }  // namespace
@@ -389,24 +391,26 @@ WeightTiles plan_weight(const Geo &g, int dtype) {
     return t;
 }
 
-hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s,
+hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, bool accumulate,
+                                hipStream_t s,
                                 int ups, int n_sp, int tpp) {
     switch (dtype) {
-        case kF32: return launch_reduce<float, float>(g, k_splits, part, gw, s, ups, n_sp, tpp);
-        case kF64: return launch_reduce<double, double>(g, k_splits, part, gw, s, ups, n_sp, tpp);
-        case kF16: return launch_reduce<__half, float>(g, k_splits, part, gw, s, ups, n_sp, tpp);
-        case kBF16: return launch_reduce<__hip_bfloat16, float>(g, k_splits, part, gw, s, ups, n_sp, tpp);
+        case kF32: return launch_reduce<float, float>(g, k_splits, part, gw, accumulate, s, ups, n_sp, tpp);
+        case kF64: return launch_reduce<double, double>(g, k_splits, part, gw, accumulate, s, ups, n_sp, tpp);
+        case kF16: return launch_reduce<__half, float>(g, k_splits, part, gw, accumulate, s, ups, n_sp, tpp);
+        case kBF16: return launch_reduce<__hip_bfloat16, float>(g, k_splits, part, gw, accumulate, s, ups, n_sp, tpp);
     }
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_bwd_weight(int dtype, int dim, const Geo &g, const WeightTiles &t, const void *z, const void *xcl,
-                             const void *offset, const void *mask, void *part, void *gw, hipStream_t s) {
+                             const void *offset, const void *mask, void *part, void *gw, bool accumulate,
+                             hipStream_t s) {
     switch (dtype) {
-        case kF32: return launch_d<float, float>(dim, g, t, z, xcl, offset, mask, part, gw, s);
-        case kF64: return launch_d<double, double>(dim, g, t, z, xcl, offset, mask, part, gw, s);
-        case kF16: return launch_d<__half, float>(dim, g, t, z, xcl, offset, mask, part, gw, s);
-        case kBF16: return launch_d<__hip_bfloat16, float>(dim, g, t, z, xcl, offset, mask, part, gw, s);
+        case kF32: return launch_d<float, float>(dim, g, t, z, xcl, offset, mask, part, gw, accumulate, s);
+        case kF64: return launch_d<double, double>(dim, g, t, z, xcl, offset, mask, part, gw, accumulate, s);
+        case kF16: return launch_d<__half, float>(dim, g, t, z, xcl, offset, mask, part, gw, accumulate, s);
+        case kBF16: return launch_d<__hip_bfloat16, float>(dim, g, t, z, xcl, offset, mask, part, gw, accumulate, s);
     }
     return hipErrorInvalidValue;
 }

@@ -372,7 +372,7 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
 
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
-                                 void *gw, hipStream_t s) {
+                                 void *gw, bool accumulate, hipStream_t s) {
     hipError_t e = hipErrorInvalidValue;
     switch (dtype) {
         case kF32: e = launch_d<float>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
@@ -380,7 +380,8 @@ hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTile
         case kBF16: e = launch_d<__hip_bfloat16>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
     }
     if (e != hipSuccess) return e;
-    return launch_weight_reduce(dtype, g, ww.n_split, part, gw, s, ww.units_per_split, ww.n_spatial, wt.tpp);
+    return launch_weight_reduce(dtype, g, ww.n_split, part, gw, accumulate, s, ww.units_per_split, ww.n_spatial,
+                                wt.tpp);
 }
 
 }  // namespace tvdcn_hip

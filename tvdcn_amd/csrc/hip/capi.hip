@@ -6,6 +6,8 @@
 #include <string>
 #include <cstring>
 #include <climits>
+#include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -77,7 +79,8 @@ struct Plan {
 
 bool fits_int(int64_t v) { return v >= 0 && v <= (int64_t)INT_MAX; }
 
-tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
+// Plan of one batch block of `batch` images (the descriptor's other fields as given).
+tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl, int64_t batch) {
     tvdcn_status st = output_size(d, pl.out_size);
     if (st) return st;
     if (d->dtype < 0 || d->dtype > 3) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "unknown dtype");
@@ -127,8 +130,8 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
         dl3[e] = d->dilation[i];
     }
     const int64_t Sn = S3[0] * S3[1] * S3[2], Pn = P3[0] * P3[1] * P3[2], Kn = K3[0] * K3[1] * K3[2];
-    const int64_t B = d->batch;
-    // int32 indexing inside the kernels: every tensor must stay below 2^31 elements
+    const int64_t B = batch;
+    // int32 indexing inside the kernels: every tensor of the block must stay below 2^31 elements
     const int64_t biggest[] = {B * C * Sn, B * M * Pn, M * (C / d->groups) * Kn,
                                B * (d->offset_groups ? d->offset_groups : 1) * Kn * d->dim * Pn,
                                B * (d->mask_groups ? d->mask_groups : 1) * Kn * Pn};
@@ -178,6 +181,59 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl) {
     pl.wn_w = win_resize(pl.wn_s, g, pl.dim, weight_win_fixed_bytes(g, pl.dim, pl.wn_s.tpp), x_window_cell_bytes());
     pl.ww = plan_weight_win(g, pl.wn_w, pl.dim);
     pl.fw = plan_fwd_win(g, pl.wn_s, pl.dim, pl.wn_f);
+    return TVDCN_STATUS_SUCCESS;
+}
+
+// ---------------------------------------------------------------------------
+// Batch blocks. The kernels index in 32 bits, so the entry points run the batch in blocks of
+// images whose batch-sized tensors and workspace buffers stay at or below g_block_limit
+// elements (2^31 - 1 unless tvdcn_set_max_block_elements lowers it); the weight gradient is
+// accumulated across blocks. The reference blocks its batch too, by n_parallel_imgs
+// (cuda/deform_conv2d_kernel.cpp:149, utils/parallel_helpers.h:7-16), for its columns buffer.
+// ---------------------------------------------------------------------------
+std::atomic<int64_t> g_block_limit{INT_MAX};
+
+int64_t mul_sat(int64_t a, int64_t b) {   // a * b for a, b >= 0, saturating at INT64_MAX
+    if (a == 0 || b == 0) return 0;
+    return a > INT64_MAX / b ? INT64_MAX : a * b;
+}
+
+// per-image element counts of the user tensors: input, output, offset, mask
+struct ImageElems {
+    int64_t in = 1, out = 1, offset = 0, mask = 0;
+    int64_t largest() const { return std::max(std::max(in, out), std::max(offset, mask)); }
+};
+
+ImageElems image_elems(const tvdcn_conv_desc *d, const int64_t out_size[3]) {
+    ImageElems e;
+    int64_t si = 1, so = 1, kn = 1;
+    for (int i = 0; i < d->dim; ++i) {
+        si = mul_sat(si, d->in_size[i]);
+        so = mul_sat(so, out_size[i]);
+        kn = mul_sat(kn, d->kernel[i]);
+    }
+    const int64_t grid = d->transposed ? si : so;   // offsets / masks live on the column grid
+    e.in = mul_sat(d->in_channels, si);
+    e.out = mul_sat(d->out_channels, so);
+    e.offset = mul_sat(mul_sat(d->offset_groups, mul_sat(kn, d->dim)), grid);
+    e.mask = mul_sat(mul_sat(d->mask_groups, kn), grid);
+    return e;
+}
+
+// images per block (>= 1 for a non-empty batch): every buffer of the kernels is as large as
+// one of the user tensors or batch-independent, so the user tensors' per-image sizes decide
+tvdcn_status batch_block(const tvdcn_conv_desc *d, int64_t &block, ImageElems *elems = nullptr) {
+    int64_t out[3] = {1, 1, 1};
+    tvdcn_status st = output_size(d, out);
+    if (st) return st;
+    if (d->batch < 0) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "batch must be >= 0 and channels positive");
+    const ImageElems e = image_elems(d, out);
+    if (elems) *elems = e;
+    const int64_t lim = g_block_limit.load();
+    if (e.largest() > lim)
+        return fail(TVDCN_STATUS_NOT_SUPPORTED, "one image's tensors exceed " + std::to_string(lim) +
+                                                    " elements (the kernels index in 32 bits)");
+    block = d->batch == 0 ? 0 : std::max<int64_t>(1, std::min<int64_t>(d->batch, lim / std::max<int64_t>(e.largest(), 1)));
     return TVDCN_STATUS_SUCCESS;
 }
 
@@ -408,127 +464,18 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
     return TVDCN_STATUS_SUCCESS;
 }
 
-// ---------------------------------------------------------------------------
-// Scratch of tvdcn_deform_conv_forward_noalloc: one array per GPU in the code object's
-// device memory, held until the process ends. Its device address is looked up once per
-// device (hipGetSymbolAddress, with that device current) at the entry point's first call on
-// the device, and only that address is handed to kernels (the array's name is a host-side
-// stand-in in host code).
-// ---------------------------------------------------------------------------
-static __device__ __align__(256) unsigned char scratch[TVDCN_SCRATCH_BYTES];
-
-constexpr int kMaxDevices = 64;
-
-tvdcn_status scratch_of_current_device(void **out) {
-    static std::mutex mu;
-    static void *ptrs[kMaxDevices] = {};
-    int dev = -1;
-    TVDCN_CHECK_HIP(hipGetDevice(&dev));
-    if (dev < 0 || dev >= kMaxDevices)
-        return fail(TVDCN_STATUS_NOT_SUPPORTED, "forward_noalloc: device index above 63");
-    std::lock_guard<std::mutex> lk(mu);
-    if (ptrs[dev] == nullptr) {
-        void *p = nullptr;
-        TVDCN_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-        if (p == nullptr) return fail(TVDCN_STATUS_HIP_ERROR, "forward_noalloc: no device address for the scratch array");
-        ptrs[dev] = p;
-    }
-    *out = ptrs[dev];
-    return TVDCN_STATUS_SUCCESS;
-}
-
-}  // namespace
-
-extern "C" {
-
-tvdcn_status tvdcn_conv_output_size(const tvdcn_conv_desc *desc, int64_t out_size[3]) {
-    int64_t tmp[3] = {1, 1, 1};
-    tvdcn_status st = output_size(desc, tmp);
-    if (st == TVDCN_STATUS_SUCCESS && out_size)
-        for (int i = 0; i < 3; ++i) out_size[i] = tmp[i];
-    return st;
-}
-
-size_t tvdcn_deform_conv_forward_workspace_size(const tvdcn_conv_desc *desc) {
-    Plan pl;
-    if (make_plan(desc, pl)) return 0;
-    return layout(pl, false).total;
-}
-
-size_t tvdcn_deform_conv_backward_workspace_size(const tvdcn_conv_desc *desc) {
-    Plan pl;
-    if (make_plan(desc, pl)) return 0;
-    return layout(pl, true).total;
-}
-
-tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *input, const void *weight,
-                                       const void *offset, const void *mask, const void *bias, void *output,
-                                       void *workspace, size_t workspace_bytes, void *stream) {
-    Plan pl;
-    tvdcn_status st = make_plan(desc, pl);
-    if (st) return st;
-    if (pl.g.B == 0) return TVDCN_STATUS_SUCCESS;   // empty batch: empty output, nothing to do
-    st = check_forward_pointers(desc, offset, mask);
-    if (st) return st;
-    if (workspace_bytes < layout(pl, false).total) return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
-    return forward_planned(pl, desc, input, weight, offset, mask, bias, output, workspace, stream);
-}
-
-tvdcn_status tvdcn_deform_conv_forward_noalloc(const tvdcn_conv_desc *desc, const void *input, const void *weight,
-                                               const void *offset, const void *mask, const void *bias, void *output,
-                                               void *stream) {
-    Plan pl;
-    tvdcn_status st = make_plan(desc, pl);
-    if (st) return st;
-    if (pl.g.B == 0) return TVDCN_STATUS_SUCCESS;
-    st = check_forward_pointers(desc, offset, mask);
-    if (st) return st;
-    const size_t need = layout(pl, false).total;
-    if (need > (size_t)TVDCN_SCRATCH_BYTES)
-        return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL,
-                    "forward_noalloc: this problem needs " + std::to_string(need) +
-                        " bytes of scratch; the library's per-GPU scratch holds " +
-                        std::to_string((size_t)TVDCN_SCRATCH_BYTES) +
-                        " (use tvdcn_deform_conv_forward with a workspace)");
-    void *ws = nullptr;
-    st = scratch_of_current_device(&ws);
-    if (st) return st;
-    return forward_planned(pl, desc, input, weight, offset, mask, bias, output, ws, stream);
-}
-tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void *grad_out, const void *input,
-                                        const void *weight, const void *offset, const void *mask, void *grad_input,
-                                        void *grad_weight, void *grad_offset, void *grad_mask, void *grad_bias,
-                                        void *workspace, size_t workspace_bytes, void *stream) {
-    Plan pl;
-    tvdcn_status st = make_plan(desc, pl);
-    if (st) return st;
+// Backward of one batch block on its plan (pointers at the block's first image), except the
+// bias gradient; the weight gradient is written (first block) or added (accumulate_weight).
+tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const void *grad_out, const void *input,
+                              const void *weight, const void *offset, const void *mask, void *grad_input,
+                              void *grad_weight, void *grad_offset, void *grad_mask, void *workspace, void *stream,
+                              bool accumulate_weight) {
     const Geo &g = pl.g;
+    const Layout L = layout(pl, true);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int dt = pl.dtype;
-    if (g.B == 0) {
-        // empty batch: the reference returns zero weight / bias gradients; the
-        // batch-sized tensors are empty (their pointers may be null)
-        if (!grad_weight) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
-        g_last_error.clear();
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
-                     launch_fill_zero((int)elem_size(dt), grad_weight, (size_t)g.M * g.Cg * g.Kn, s));
-        if (grad_bias)
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
-                         launch_fill_zero((int)elem_size(dt), grad_bias, (size_t)desc->out_channels, s));
-        return TVDCN_STATUS_SUCCESS;
-    }
-    if ((desc->offset_groups == 0) != (offset == nullptr) || (offset == nullptr) != (grad_offset == nullptr))
-        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "offset / grad_offset pointers and offset_groups disagree");
-    if ((desc->mask_groups == 0) != (mask == nullptr) || (mask == nullptr) != (grad_mask == nullptr))
-        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "mask / grad_mask pointers and mask_groups disagree");
-    const Layout L = layout(pl, true);
-    if (workspace_bytes < L.total) return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
-    if (!grad_out || !input || !weight || !grad_input || !grad_weight)
-        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
-    if (!aligned16(workspace)) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
     const int ab = (int)acc_size(dt);
     const bool direct = acc_is_storage(dt);
-    g_last_error.clear();
 
     const size_t n_goff = g.og ? (size_t)g.B * g.og * g.Kn * pl.dim * g.Pn : 0;
     const size_t n_gmask = g.mg ? (size_t)g.B * g.mg * g.Kn * g.Pn : 0;
@@ -605,10 +552,12 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
         }
         if (pl.ww.ok)
             TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight_win(dt, pl.dim, g, pl.wn_w, pl.ww, Z, xcl, offset,
-                                                                            mask, at(workspace, L.wpart), grad_weight, s));
+                                                                            mask, at(workspace, L.wpart), grad_weight,
+                                                                            accumulate_weight, s));
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,
-                                                                        at(workspace, L.wpart), grad_weight, s));
+                                                                        at(workspace, L.wpart), grad_weight,
+                                                                        accumulate_weight, s));
     }
     // mask logits: the accumulated mask gradient through d(mask value) / d(logit) -- elementwise for
     // the sigmoid, over the taps of each (batch, mask group, pixel) for the softmax
@@ -621,12 +570,209 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
         if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, goff, grad_offset, n_goff, s));
         if (gmask) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, gmask, grad_mask, n_gmask, s));
     }
+    return TVDCN_STATUS_SUCCESS;
+}
+
+// Workspace bytes of a call: the largest of its blocks' layouts (a full block and the remainder).
+size_t workspace_bytes_of(const tvdcn_conv_desc *desc, bool backward) {
+    int64_t block = 0;
+    if (batch_block(desc, block)) return 0;
+    Plan pl;
+    if (make_plan(desc, pl, block)) return 0;
+    size_t n = layout(pl, backward).total;
+    const int64_t tail = block > 0 ? desc->batch % block : 0;
+    if (tail > 0) {
+        Plan pt;
+        if (make_plan(desc, pt, tail)) return 0;
+        n = std::max(n, layout(pt, backward).total);
+    }
+    return n;
+}
+
+// The forward over the batch blocks (pointers checked, workspace large enough).
+tvdcn_status forward_blocks(const tvdcn_conv_desc *desc, int64_t block, const void *input, const void *weight,
+                            const void *offset, const void *mask, const void *bias, void *output, void *workspace,
+                            void *stream) {
+    ImageElems ie;
+    int64_t blk = 0;
+    tvdcn_status st = batch_block(desc, blk, &ie);
+    if (st) return st;
+    const size_t es = elem_size(desc->dtype);
+    auto adv = [](const void *p, size_t bytes) -> void * {
+        return p ? static_cast<char *>(const_cast<void *>(p)) + bytes : nullptr;
+    };
+    for (int64_t b0 = 0; b0 < desc->batch; b0 += block) {
+        const int64_t nb = std::min<int64_t>(block, desc->batch - b0);
+        Plan pl;
+        st = make_plan(desc, pl, nb);
+        if (st) return st;
+        st = forward_planned(pl, desc, adv(input, b0 * ie.in * es), weight, adv(offset, b0 * ie.offset * es),
+                             adv(mask, b0 * ie.mask * es), bias, adv(output, b0 * ie.out * es), workspace, stream);
+        if (st) return st;
+    }
+    return TVDCN_STATUS_SUCCESS;
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of tvdcn_deform_conv_forward_noalloc: one array per GPU in the code object's
+// device memory, held until the process ends. Its device address is looked up once per
+// device (hipGetSymbolAddress, with that device current) at the entry point's first call on
+// the device, and only that address is handed to kernels (the array's name is a host-side
+// stand-in in host code).
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[TVDCN_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+tvdcn_status scratch_of_current_device(void **out) {
+    static std::mutex mu;
+    static void *ptrs[kMaxDevices] = {};
+    int dev = -1;
+    TVDCN_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(TVDCN_STATUS_NOT_SUPPORTED, "forward_noalloc: device index above 63");
+    std::lock_guard<std::mutex> lk(mu);
+    if (ptrs[dev] == nullptr) {
+        void *p = nullptr;
+        TVDCN_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (p == nullptr) return fail(TVDCN_STATUS_HIP_ERROR, "forward_noalloc: no device address for the scratch array");
+        ptrs[dev] = p;
+    }
+    *out = ptrs[dev];
+    return TVDCN_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+tvdcn_status tvdcn_conv_output_size(const tvdcn_conv_desc *desc, int64_t out_size[3]) {
+    int64_t tmp[3] = {1, 1, 1};
+    tvdcn_status st = output_size(desc, tmp);
+    if (st == TVDCN_STATUS_SUCCESS && out_size)
+        for (int i = 0; i < 3; ++i) out_size[i] = tmp[i];
+    return st;
+}
+
+size_t tvdcn_deform_conv_forward_workspace_size(const tvdcn_conv_desc *desc) {
+    return workspace_bytes_of(desc, false);
+}
+
+size_t tvdcn_deform_conv_backward_workspace_size(const tvdcn_conv_desc *desc) {
+    return workspace_bytes_of(desc, true);
+}
+
+tvdcn_status tvdcn_set_max_block_elements(int64_t max_elements) {
+    if (max_elements < 1 || max_elements > INT_MAX)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "max_elements must be in [1, 2^31 - 1]");
+    g_block_limit.store(max_elements);
+    return TVDCN_STATUS_SUCCESS;
+}
+
+tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *input, const void *weight,
+                                       const void *offset, const void *mask, const void *bias, void *output,
+                                       void *workspace, size_t workspace_bytes, void *stream) {
+    int64_t block = 0;
+    tvdcn_status st = batch_block(desc, block);
+    if (st) return st;
+    Plan pl;
+    st = make_plan(desc, pl, block);
+    if (st) return st;
+    if (desc->batch == 0) return TVDCN_STATUS_SUCCESS;   // empty batch: empty output, nothing to do
+    st = check_forward_pointers(desc, offset, mask);
+    if (st) return st;
+    if (workspace_bytes < workspace_bytes_of(desc, false))
+        return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
+    return forward_blocks(desc, block, input, weight, offset, mask, bias, output, workspace, stream);
+}
+
+tvdcn_status tvdcn_deform_conv_forward_noalloc(const tvdcn_conv_desc *desc, const void *input, const void *weight,
+                                               const void *offset, const void *mask, const void *bias, void *output,
+                                               void *stream) {
+    int64_t block = 0;
+    tvdcn_status st = batch_block(desc, block);
+    if (st) return st;
+    Plan pl;
+    st = make_plan(desc, pl, block);
+    if (st) return st;
+    if (desc->batch == 0) return TVDCN_STATUS_SUCCESS;
+    st = check_forward_pointers(desc, offset, mask);
+    if (st) return st;
+    const size_t need = workspace_bytes_of(desc, false);
+    if (need > (size_t)TVDCN_SCRATCH_BYTES)
+        return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL,
+                    "forward_noalloc: this problem needs " + std::to_string(need) +
+                        " bytes of scratch; the library's per-GPU scratch holds " +
+                        std::to_string((size_t)TVDCN_SCRATCH_BYTES) +
+                        " (use tvdcn_deform_conv_forward with a workspace)");
+    void *ws = nullptr;
+    st = scratch_of_current_device(&ws);
+    if (st) return st;
+    return forward_blocks(desc, block, input, weight, offset, mask, bias, output, ws, stream);
+}
+
+tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void *grad_out, const void *input,
+                                        const void *weight, const void *offset, const void *mask, void *grad_input,
+                                        void *grad_weight, void *grad_offset, void *grad_mask, void *grad_bias,
+                                        void *workspace, size_t workspace_bytes, void *stream) {
+    int64_t block = 0;
+    ImageElems ie;
+    tvdcn_status st = batch_block(desc, block, &ie);
+    if (st) return st;
+    Plan pl;
+    st = make_plan(desc, pl, block);
+    if (st) return st;
+    const Geo &g = pl.g;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int dt = pl.dtype;
+    if (desc->batch == 0) {
+        // empty batch: the reference returns zero weight / bias gradients; the
+        // batch-sized tensors are empty (their pointers may be null)
+        if (!grad_weight) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
+        g_last_error.clear();
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                     launch_fill_zero((int)elem_size(dt), grad_weight, (size_t)g.M * g.Cg * g.Kn, s));
+        if (grad_bias)
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                         launch_fill_zero((int)elem_size(dt), grad_bias, (size_t)desc->out_channels, s));
+        return TVDCN_STATUS_SUCCESS;
+    }
+    if ((desc->offset_groups == 0) != (offset == nullptr) || (offset == nullptr) != (grad_offset == nullptr))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "offset / grad_offset pointers and offset_groups disagree");
+    if ((desc->mask_groups == 0) != (mask == nullptr) || (mask == nullptr) != (grad_mask == nullptr))
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "mask / grad_mask pointers and mask_groups disagree");
+    if (workspace_bytes < workspace_bytes_of(desc, true))
+        return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
+    if (!grad_out || !input || !weight || !grad_input || !grad_weight)
+        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
+    if (!aligned16(workspace)) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    if (!fits_int(desc->batch)) return fail(TVDCN_STATUS_NOT_SUPPORTED, "batch above 2^31 - 1");
+    g_last_error.clear();
+    // per image: X / grad_input and Z follow the op's input and output tensors
+    const size_t es = elem_size(dt);
+    const size_t in_b = (size_t)ie.in * es, out_b = (size_t)ie.out * es, off_b = (size_t)ie.offset * es,
+                 mask_b = (size_t)ie.mask * es;
+    auto adv = [](const void *p, size_t bytes) -> void * {
+        return p ? static_cast<char *>(const_cast<void *>(p)) + bytes : nullptr;
+    };
+    for (int64_t b0 = 0; b0 < desc->batch; b0 += block) {
+        const int64_t nb = std::min<int64_t>(block, desc->batch - b0);
+        Plan bp;
+        st = nb == block ? TVDCN_STATUS_SUCCESS : make_plan(desc, bp, nb);
+        if (st) return st;
+        st = backward_planned(nb == block ? pl : bp, desc, adv(grad_out, b0 * out_b), adv(input, b0 * in_b), weight,
+                              adv(offset, b0 * off_b), adv(mask, b0 * mask_b), adv(grad_input, b0 * in_b),
+                              grad_weight, adv(grad_offset, b0 * off_b), adv(grad_mask, b0 * mask_b), workspace, stream,
+                              b0 > 0);
+        if (st) return st;
+    }
     if (grad_bias) {
-        // grad_out is (B, Cout, *out_size): conv Cout = M on the column grid,
-        // transposed Cout = C on the sampled grid
-        const int Cout = pl.transposed ? g.C : g.M;
+        // grad_out is (B, Cout, *out_size) over the whole batch (the kernel indexes in 64 bits):
+        // conv Cout = M on the column grid, transposed Cout = C on the sampled grid
+        const int Cout = (int)desc->out_channels;
         const int So = pl.transposed ? g.Sn : g.Pn;
-        TVDCN_LAUNCH(TVDCN_KERNEL_BIAS_GRAD, s, launch_bias_grad(dt, grad_out, grad_bias, g.B, Cout, So, s));
+        TVDCN_LAUNCH(TVDCN_KERNEL_BIAS_GRAD, s,
+                     launch_bias_grad(dt, grad_out, grad_bias, (int)desc->batch, Cout, So, s));
     }
     return TVDCN_STATUS_SUCCESS;
 }

@@ -144,16 +144,18 @@ hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles 
                                const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s);
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
-                                 void *gw, hipStream_t s);
+                                 void *gw, bool accumulate, hipStream_t s);
 // gw (storage type, layout (M, Cg, Kn)) = sum over k_splits of part[ks][G][Kn][Mg][Cg]
 // dW = sum over splits of the partials; with units_per_split > 0 (windowed kernel) tap t sums only
 // the splits whose unit range meets its pass (t / tpp) over n_spatial tiles
-hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, hipStream_t s,
-                                int units_per_split = 0, int n_spatial = 0, int tpp = 0);
+// (accumulate: gw += that sum, for batch blocks after the first)
+hipError_t launch_weight_reduce(int dtype, const Geo &g, int k_splits, const void *part, void *gw, bool accumulate,
+                                hipStream_t s, int units_per_split = 0, int n_spatial = 0, int tpp = 0);
 // writes split partials to `part` (WeightTiles::part_elems accumulator elements),
 // then reduces them into gw (storage type, layout (M, Cg, Kn))
 hipError_t launch_bwd_weight(int dtype, int dim, const Geo &g, const WeightTiles &t, const void *z, const void *xcl,
-                             const void *offset, const void *mask, void *part, void *gw, hipStream_t s);
+                             const void *offset, const void *mask, void *part, void *gw, bool accumulate,
+                             hipStream_t s);
 
 // mask_softmax (mask_softmax.hip)
 hipError_t launch_mask_softmax_fwd(int dtype, const void *x, void *y, int64_t BG, int K, int64_t S, hipStream_t s);

@@ -484,7 +484,8 @@ bool keeps_cl_copy(const Tensor &x, int dim, bool transposed) {
     if (c10::impl::dispatch_mode_enabled() || x.key_set().has(c10::DispatchKey::Python) ||
         at::functionalization::impl::isFunctionalTensor(x))
         return false;
-    return x.size(1) > 1 && x.numel() > x.size(0) * x.size(1);   // else both orders coincide
+    // (the layout copy indexes in 32 bits; larger inputs keep the plain path, which batch-blocks)
+    return x.size(1) > 1 && x.numel() > x.size(0) * x.size(1) && x.numel() <= INT32_MAX;   // else both orders coincide
 }
 
 Tensor cl_copy(const Tensor &x, int dim, bool to_cl) {
