@@ -203,7 +203,8 @@ def test_layout_copies_through_c_abi():
 
 @pytest.mark.parametrize("dim", [1, 2, 3])
 def test_forward_copy_kept_for_backward(dim):
-    """float32 NC<spatial> inputs: the forward's channels-last copy serves the backward, and
+    """float32 NC<spatial> inputs with the opt-in kept copy (set_keep_channels_last_copy): the
+    forward's channels-last copy serves the backward, and
     grad_input comes back in the input's own (NC<spatial>) order with the numbers of the
     backward op called on the original input, and of the float64 oracle."""
     in_size = {1: [70], 2: [20, 18], 3: [6, 10, 9]}[dim]
@@ -219,7 +220,11 @@ def test_forward_copy_kept_for_backward(dim):
     gy = torch.randn(y_ref.shape, device="cuda:0")
     ref = bwd(gy, *ts, *params)
     leaves = [t.clone().requires_grad_(True) for t in ts]
-    y = fwd(*leaves, *params)
+    previous = tvdcn.set_keep_channels_last_copy(True)
+    try:
+        y = fwd(*leaves, *params)
+    finally:
+        tvdcn.set_keep_channels_last_copy(previous)
     y.backward(gy)
     torch.cuda.synchronize()
     assert leaves[0].grad.is_contiguous()
@@ -386,3 +391,19 @@ def test_scatter_elementwise_under_gradient_spikes_fp32(dim, spike):
     assert e <= 4 * e_ref + 1e-5
     for name, gr, r in zip(("weight", "offset", "mask", "bias"), grads[1:], ref[1:]):
         assert rel_err(gr, r) < TOL[torch.float32][1], name
+
+
+def test_saved_input_version_check_by_default():
+    """By default the autograd node saves the input itself, as the reference does
+    (autograd/deform_conv2d_kernel.cpp:35): changing it in place after the forward makes the backward
+    raise torch's version-counter error."""
+    case = make_case(2, False, batch=2, cin=32, cout=48, kernel=[3, 3], stride=[1, 1], padding=[1, 1],
+                     dilation=[1, 1], in_size=[12, 10], out_pad=[0, 0], seed=590)
+    ts = [case[n].to("cuda:0", torch.float32).requires_grad_(n != "input")
+          for n in ("input", "weight", "offset", "mask", "bias")]
+    x = ts[0].clone().requires_grad_(True)
+    xin = x * 1.0    # a non-leaf input that can be changed in place
+    y = tvdcn.deform_conv2d(xin, *ts[1:], padding=1)
+    xin.add_(1.0)
+    with pytest.raises(RuntimeError, match="modified by an inplace operation"):
+        y.sum().backward()

@@ -12,7 +12,8 @@ import sys as _sys
 import tvdcn_amd as _impl
 from tvdcn_amd import _version, extension, ops, utils  # noqa: F401
 from tvdcn_amd._version import __version__  # noqa: F401
-from tvdcn_amd.extension import _HAS_OPS, cuda_arch_list, cuda_version, has_ops, with_cuda  # noqa: F401
+from tvdcn_amd.extension import (  # noqa: F401
+    _HAS_OPS, cuda_arch_list, cuda_version, has_ops, set_keep_channels_last_copy, with_cuda)
 from tvdcn_amd.ops import *  # noqa: F401,F403
 
 for _name in ("ops", "ops.activations", "ops.activations.mask_sigmoid", "ops.activations.mask_softmax",

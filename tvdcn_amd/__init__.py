@@ -8,5 +8,5 @@ GPU kernels are hand-written HIP only.
 """
 from . import ops
 from ._version import __version__
-from .extension import _HAS_OPS, cuda_arch_list, cuda_version, has_ops, with_cuda
+from .extension import _HAS_OPS, cuda_arch_list, cuda_version, has_ops, set_keep_channels_last_copy, with_cuda
 from .ops import *  # noqa: F401,F403

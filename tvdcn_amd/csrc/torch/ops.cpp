@@ -23,6 +23,7 @@
 #include <torch/autograd.h>
 #include <torch/library.h>
 
+#include <atomic>
 #include <cmath>
 #include <sstream>
 #include <string>
@@ -471,11 +472,20 @@ Tensor call_forward(const Tensor &input, const Tensor &weight, const optional<Te
 
 optional<Tensor> opt(const Tensor &t) { return t.defined() ? optional<Tensor>(t) : optional<Tensor>(); }
 
-// float32 2D / 3D conv inputs in NC<spatial> order: the forward makes the channels-last copy
-// that the kernels sample (tvdcn_to_channels_last) and keeps it for the backward, which would
-// otherwise make the same copy again; the backward writes grad_input channels-last and brings
-// it back to NC<spatial> (tvdcn_from_channels_last). Every other input passes through as it is.
+// Opt-in (tvdcn::_set_keep_input_copy): for float32 1D / 2D / 3D conv inputs in NC<spatial> order
+// the forward makes the channels-last copy that the kernels sample (tvdcn_to_channels_last) and
+// the autograd node saves it instead of the input, so that the backward skips its own copy; the
+// backward writes grad_input channels-last and brings it back to NC<spatial>
+// (tvdcn_from_channels_last). It costs one |input| of device memory per layer until the backward
+// runs (the caller usually holds the input too), and an in-place change of the input after the
+// forward is no longer detected; off by default, the node saves the input as the reference does
+// (autograd/deform_conv2d_kernel.cpp:35).
+std::atomic<bool> g_keep_input_copy{false};
+
+bool set_keep_input_copy(bool enable) { return g_keep_input_copy.exchange(enable); }
+
 bool keeps_cl_copy(const Tensor &x, int dim, bool transposed) {
+    if (!g_keep_input_copy.load()) return false;
     if (transposed || dim < 1 || dim > 3 || !x.is_cuda() || x.scalar_type() != at::kFloat ||
         x.dim() != dim + 2 || !x.is_contiguous() || x.numel() == 0)
         return false;
@@ -996,6 +1006,7 @@ TORCH_LIBRARY(tvdcn, m) {
           "-> (Tensor, Tensor, Tensor, Tensor, Tensor)");
     m.def("mask_softmax(Tensor mask, int kernel_numel) -> Tensor");
     m.def("_mask_softmax_backward(Tensor grad, Tensor output, int kernel_numel) -> Tensor");
+    m.def("_set_keep_input_copy", &tvdcn_amd::set_keep_input_copy);
     m.def("_cuda_version", &tvdcn_amd::hip_version);
     m.def("_cuda_arch_flags", &tvdcn_amd::arch_flags);
 }

@@ -86,3 +86,16 @@ def cuda_arch_list() -> List[str]:
     if not _HAS_OPS:
         return []
     return torch.ops.tvdcn._cuda_arch_flags().split()
+
+
+def set_keep_channels_last_copy(enabled: bool) -> bool:
+    """Opt-in memory-for-time trade of the float32 convolutions (no counterpart in the reference):
+    when enabled, the forward keeps the channels-last copy of its input that the kernels sample, and
+    the autograd node saves it instead of the input (the reference saves the input,
+    autograd/deform_conv2d_kernel.cpp:35), so that the backward skips its own layout copy (about 1%
+    of a forward + backward at BASELINE configs[1]). It holds one more |input| of device memory per
+    layer until the backward runs, and an in-place change of the input after the forward goes
+    undetected. Off by default. Returns the previous setting."""
+    _assert_has_ops()
+    return torch.ops.tvdcn._set_keep_input_copy(bool(enabled))
+
