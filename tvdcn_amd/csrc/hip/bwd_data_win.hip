@@ -31,12 +31,15 @@
 //     below 2^29 (no overflow); each term is rounded to the unit 2^-s_c <= 2^-28 B_c.
 //     Integer sums are also order independent. When a pass of taps grows B_c,
 //     the values already held are shifted down to the new scale (rounded to
-//     nearest). The unit is relative to the tile's bound, not to each cell, so a
-//     pass in which one term |G * mask| exceeds 2^-6 of its channel's bound (a
-//     gradient spike: the bound would be the spike's, and quiet cells of the tile
-//     would be rounded at it) does not use the window; neither does a pass with a
-//     non-finite bound (inf/nan must propagate as in the reference). Such a pass
-//     goes to global float atomics, after the window flushes what it holds.
+//     nearest). The unit is relative to the tile's bound, not to each cell, so
+//     terms |G * mask| above 2^6 times the typical term of their (pass, channel)
+//     (gradient spikes: the bound would be theirs, and the quiet cells of the tile
+//     would be rounded at it) bypass the window: they go to global float atomics,
+//     and the bound covers the terms that stay. The typical term is 2 to the mean
+//     binary exponent of the 128 per-lane mean terms (a geometric mean, which a
+//     minority of spikes barely moves: each lane holds 2 pixels x the pass's taps). A pass with a non-finite bound (inf/nan must
+//     propagate as in the reference) does not use the window at all: it goes to
+//     global float atomics, after the window flushes what it holds.
 //     Corners outside the window go to global float atomics.
 //   * The window (sampled-grid box around the tile's undeformed footprint plus a
 //     margin R per axis) accumulates over all passes of the tile and is flushed
@@ -65,11 +68,12 @@ static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
 static_assert(NT == BC * 32, "window rescale: 32 threads per channel");
 
 // LDS words ahead of the windows: geometry table [WIN_TMAX][BPX] x (position, mask),
-// per-wave channel bounds, scale exponents and flags, held bounds, rescale shifts,
-// largest terms
+// per-wave channel bounds, scale exponents and flags, held bounds, rescale shifts (or
+// spike thresholds), largest terms, exponent statistics
 constexpr int GEO_WORDS = WIN_TMAX * BPX * 4;
-constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + 4 * BC + 4;
-constexpr int SPIKE_BITS = 6;     // a term above 2^-SPIKE_BITS of its channel's bound: no window
+constexpr int FIXED_WORDS = GEO_WORDS + NW * BC + 5 * BC + 4;
+// a term above 2^SPIKE_BITS x 2^(mean exponent of the per-lane mean terms of its pass) is a spike
+constexpr int SPIKE_BITS = 6;
 
 // Offset / mask gradient terms of one (pixel, tap) as the reference's corner sums, from
 // gk[k] = G contracted with X at corner k (k = 2 * y bit + x bit in 2D, x bit in 1D):
@@ -105,6 +109,30 @@ __device__ __forceinline__ float row_sum4(float v) {
     return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// Reduction over each row of 16 lanes (the lanes of one channel quad's 16 pixels), the
+// result in every lane of the row: DPP quad xor 1, quad xor 2, half-row mirror, row
+// mirror (VALU only; a shuffle goes through the LDS crossbar)
+template <typename F>
+__device__ __forceinline__ unsigned row_reduce16(unsigned v, F op) {
+    v = op(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, true));
+    v = op(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, true));
+    v = op(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, true));
+    return op(v, (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+    return __uint_as_float(row_reduce16(__float_as_uint(v), [](unsigned a, unsigned b) {
+        return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+    }));
+}
+__device__ __forceinline__ float row_max16(float v) {
+    return __uint_as_float(row_reduce16(__float_as_uint(v), [](unsigned a, unsigned b) {
+        return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    }));
+}
+__device__ __forceinline__ unsigned row_sum16(unsigned v) {
+    return row_reduce16(v, [](unsigned a, unsigned b) { return a + b; });
+}
+
 template <int DIM, typename T, bool SCATTER, bool COORD>
 __global__ void __launch_bounds__(NT)
 bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wchunks,
@@ -116,10 +144,14 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     extern __shared__ float smem[];
     acc4 *geo = reinterpret_cast<acc4 *>(smem);                // [TMAX][BPX] sampling table (window.h)
     float *bsum = smem + GEO_WORDS;                            // [NW][BC] partial bounds
-    int *scl = reinterpret_cast<int *>(bsum + NW * BC);        // [BC] scale exponents, [BC] = non-finite flag
+    int *scl = reinterpret_cast<int *>(bsum + NW * BC);        // [BC] scale exponents, then the non-finite
+                                                               // flag [BC] and the spike flag [BC + 1]
     float *btot = bsum + NW * BC + BC + 4;                     // [BC] bound of what the window holds
     int *shift = reinterpret_cast<int *>(btot + BC);           // [BC] rescale of the window for a pass
+    // [BC] spike thresholds of a pass with spikes, read before its rescale shifts are written
+    float *thr = reinterpret_cast<float *>(shift);
     int *bmax = shift + BC;                                    // [BC] largest |G * mask| (float bits, >= 0)
+    unsigned *bexp = reinterpret_cast<unsigned *>(bmax + BC);  // [BC] exponent sums + (counts << 20)
     float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X window (COORD)
     int *iwin = reinterpret_cast<int *>(xwin + (COORD ? wt.cells * XS : 0));   // [BC][cst] fixed point
     const int cst = fix_stride(wt.cells);
@@ -147,7 +179,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     if constexpr (COORD) fill_xwin(g, wt, tile, xb, xwin, tid, NT);
     if constexpr (SCATTER) {
         for (int i = tid; i < BC * cst; i += NT) iwin[i] = 0;
-        if (tid < BC) bmax[tid] = 0;
+        if (tid < BC) {
+            bmax[tid] = 0;
+            bexp[tid] = 0u;
+        }
     }
 
     // ---- K-loop operands, straight to registers ---------------------------------
@@ -311,55 +346,77 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 
         // ---- fixed-point scale per channel: the bound covers this pass plus everything
         //      the window already holds; when it grows, the held values are shifted down
-        //      to the new (smaller or equal) scale
+        //      to the new (smaller or equal) scale. Terms above the spike threshold th of
+        //      their channel bypass the window and the bound.
         int sexp[4] = {0, 0, 0, 0};   // scale exponents of this lane's channels c0 + mq + v
-        bool use_window = false;
+        float th[4] = {0.f, 0.f, 0.f, 0.f};   // spike thresholds of this lane's channels
+        bool use_window = false, spikes = false;
         if constexpr (SCATTER) {
-            float part[4] = {0.f, 0.f, 0.f, 0.f}, pmax[4] = {0.f, 0.f, 0.f, 0.f};
+            // first sweep: per-channel sum of the terms (a nan makes it non-finite), their
+            // maximum, and over the lanes the sum of the biased exponents of the nonzero lane
+            // means + (their count << 20) (128 lanes of exponent < 2^8: no carry); otherwise
+            // the sum of the terms at or below lim[v]
+            auto bound_sweep = [&](const float (&lim)[4], bool with_max) {
+                float part[4] = {0.f, 0.f, 0.f, 0.f}, pmax[4] = {0.f, 0.f, 0.f, 0.f};
+                unsigned ex[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int pb = 0; pb < PB; ++pb) {
-                const int i = wave * (PB * 16) + pb * 16 + (lane & 15);
+                for (int pb = 0; pb < PB; ++pb) {
+                    const int i = wave * (PB * 16) + pb * 16 + (lane & 15);
 #pragma unroll
-                for (int tp = 0; tp < TMAX; ++tp) {
-                    if (tp < ntaps && zp[pb] >= 0) {
-                        const float mk = fabsf(rec_mask<DIM>(geo[tp * BPX + i]));
+                    for (int tp = 0; tp < TMAX; ++tp) {
+                        if (tp < ntaps && zp[pb] >= 0) {
+                            const float mk = fabsf(rec_mask<DIM>(geo[tp * BPX + i]));
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            const float a = fabsf(acc[tp][pb][v]) * mk;
-                            part[v] += a;
-                            pmax[v] = fmaxf(pmax[v], a);
+                            for (int v = 0; v < 4; ++v) {
+                                const float a = fabsf(acc[tp][pb][v]) * mk;
+                                if (with_max) {
+                                    part[v] += a;
+                                    pmax[v] = fmaxf(pmax[v], a);
+                                } else {
+                                    part[v] += a <= lim[v] ? a : 0.f;
+                                }
+                            }
                         }
                     }
                 }
-            }
+                if (with_max) {
+                    // terms of the lane (per channel): the pass's taps at each valid pixel
+                    int npx = 0;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
+                    for (int pb = 0; pb < PB; ++pb) npx += zp[pb] >= 0;
+                    const float inv = npx > 0 ? __frcp_rn((float)(npx * ntaps)) : 0.f;
 #pragma unroll
-                for (int m = 1; m < 16; m <<= 1) {
-                    part[v] += __shfl_xor(part[v], m);
-                    pmax[v] = fmaxf(pmax[v], __shfl_xor(pmax[v], m));
+                    for (int v = 0; v < 4; ++v) {
+                        const unsigned e = __float_as_uint(part[v] * inv) >> 23;
+                        ex[v] = e != 0u ? e + (1u << 20) : 0u;
+                    }
                 }
-            }
-            if ((lane & 15) == 0) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    bsum[wave * BC + mq + v] = part[v];
-                    // non-negative floats order as their bit patterns (a nan has an exponent of
-                    // all ones: it lands above every finite value, and the bound is not finite)
-                    atomicMax(bmax + mq + v, __float_as_int(pmax[v]));
+                    part[v] = row_sum16(part[v]);
+                    if (with_max) {
+                        pmax[v] = row_max16(pmax[v]);
+                        ex[v] = row_sum16(ex[v]);
+                    }
                 }
-            }
-            __syncthreads();
-            if (tid < BC) {
-                float bc = 0.f;
+                if ((lane & 15) == 0) {
 #pragma unroll
-                for (int w = 0; w < NW; ++w) bc += bsum[w * BC + tid];
+                    for (int v = 0; v < 4; ++v) {
+                        bsum[wave * BC + mq + v] = part[v];
+                        if (with_max) {
+                            // non-negative floats order as their bit patterns (a nan has an
+                            // exponent of all ones: it lands above every finite value)
+                            atomicMax(bmax + mq + v, __float_as_int(pmax[v]));
+                            atomicAdd(bexp + mq + v, ex[v]);
+                        }
+                    }
+                }
+            };
+            // scale of the pass from its (kept) bound bc, channel tid of wave 0's first 16 lanes
+            auto set_scale = [&](float bc) {
                 const float tot = (win_data ? btot[tid] : 0.f) + bc;
-                const float big = __int_as_float(bmax[tid]);
-                bmax[tid] = 0;   // for the next pass (read after this pass's last barrier)
-                // the pass uses the window only if every bound is finite and no term of any
-                // channel exceeds 2^-SPIKE_BITS of its bound (ballot over 16 lanes)
-                const unsigned long long bad = __ballot(!isfinite(tot) || big > ldexpf(tot, -SPIKE_BITS));
+                // the pass uses the window only if every bound is finite (ballot over 16 lanes)
+                const unsigned long long bad = __ballot(!isfinite(tot));
                 int e = 0;
                 if (tot > 0.f && isfinite(tot)) frexpf(tot, &e);   // tot < 2^e
                 shift[tid] = 0;
@@ -369,13 +426,55 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     btot[tid] = tot;
                 }
                 if (tid == 0) scl[BC] = bad != 0ull;
+            };
+            const float no_lim[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+            bound_sweep(no_lim, true);
+            __syncthreads();
+            if (tid < BC) {
+                float bc = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) bc += bsum[w * BC + tid];
+                const unsigned es = bexp[tid];
+                const float big = __int_as_float(bmax[tid]);
+                bmax[tid] = 0;   // for the next pass (read after this pass's last barrier)
+                bexp[tid] = 0u;
+                // threshold 2^(mean unbiased exponent of the lane means + SPIKE_BITS), the mean
+                // rounded down (exact: integers below 2^24, a correctly rounded quotient of
+                // denominator <= 128 is an integer only when the true quotient is)
+                const float cnt = (float)(es >> 20), esum = (float)(es & ((1u << 20) - 1u));
+                const float lim = cnt > 0.f ? ldexpf(1.f, (int)floorf(esum / cnt) - 127 + SPIKE_BITS) : INFINITY;
+                const bool spike = isfinite(bc) && big > lim;
+                thr[tid] = spike ? lim : INFINITY;
+                const unsigned long long any = __ballot(spike);
+                if (any == 0ull) set_scale(bc);   // no spike: the bound is final
+                if (tid == 0) scl[BC + 1] = any != 0ull;
             }
             __syncthreads();
-            if (scl[BC] != 0) {
-                // not finite, or a spike: what the window holds goes out at its scale, the pass
-                // goes to global float atomics (inf / nan propagate as in the reference)
+            // both flags in one read: non-finite [BC], spikes [BC + 1]
+            const int2 flags = *reinterpret_cast<const int2 *>(scl + BC);
+            spikes = flags.y != 0;
+            bool nonfinite = flags.x != 0;
+            if (spikes) {
+                // bound of the terms that stay in the window
+#pragma unroll
+                for (int v = 0; v < 4; ++v) th[v] = thr[mq + v];
+                bound_sweep(th, false);
+                __syncthreads();
+                if (tid < BC) {
+                    float bc = 0.f;
+#pragma unroll
+                    for (int w = 0; w < NW; ++w) bc += bsum[w * BC + tid];
+                    set_scale(bc);
+                }
+                __syncthreads();
+                nonfinite = scl[BC] != 0;
+            }
+            if (nonfinite) {
+                // not finite: what the window holds goes out at its scale, the pass goes to
+                // global float atomics (inf / nan propagate as in the reference)
                 if (win_data) flush_window(true);
                 win_data = false;
+                spikes = false;
             } else {
                 if (win_data) {
                     // rescale to nearest (halves up); a shift of 31 or more leaves under half a unit
@@ -421,12 +520,26 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 const float mk = rec_mask<DIM>(r);
                 const acc4 gv = gt[pb];
                 const int fc = rec_fast_cell<DIM>(r);
+                // channels whose term is a spike of the pass: global float atomics (nan included)
+                bool sp[4] = {false, false, false, false};
+                bool lane_spike = false;
+                if constexpr (SCATTER) {
+                    if (spikes) {
+                        const float am = fabsf(mk);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            sp[v] = !(fabsf(gv[v]) * am <= th[v]);
+                            lane_spike = lane_spike || sp[v];
+                        }
+                    }
+                }
                 float qv[DIM + 1];
                 bool done = false;
                 if constexpr (DIM == 3) {
-                    if (!SCATTER || use_window) {
+                    if (!SCATTER || (use_window && !lane_spike)) {
                         // 3D: one branch-light path for every lane (window margins of about one
-                        // cell: most waves hold a lane with a corner outside the window)
+                        // cell: most waves hold a lane with a corner outside the window); lanes
+                        // holding a spike take the general path
                         done = true;
                         const Corners3 cr(g, wt, tile, r, deformable);
                         if constexpr (COORD) {
@@ -476,7 +589,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                             }
                         }
                     }
-                } else if (fc >= 0 && (!SCATTER || use_window)) {
+                } else if (fc >= 0 && (!SCATTER || use_window) && !lane_spike) {
                     done = true;
                     // fast path: every corner cell is in the window (zeros / dropped
                     // outside the grid), plain bilinear formulas
@@ -593,8 +706,12 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                 if (use_window && loc[k] >= 0) {
                                     unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + loc[k]);
 #pragma unroll
-                                    for (int v = 0; v < 4; ++v)
-                                        atomicAdd(dst + v * cst, (unsigned int)fixed_round(ldexpf(s * gv[v], sexp[v])));
+                                    for (int v = 0; v < 4; ++v) {
+                                        if (sp[v])
+                                            atomic_add(gdst + (size_t)gidx[k] * g.C + v, s * gv[v]);
+                                        else
+                                            atomicAdd(dst + v * cst, (unsigned int)fixed_round(ldexpf(s * gv[v], sexp[v])));
+                                    }
                                 } else {
                                     float *dst = gdst + (size_t)gidx[k] * g.C;
 #pragma unroll

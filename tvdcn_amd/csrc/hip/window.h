@@ -404,6 +404,10 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
             *m = mask_activate<float>(g, *m);
         }
     } else if (mask != nullptr && g.mask_act == MASK_ACT_SOFTMAX) {
+        // a pixel's records of the pass were written by other threads (record e belongs to
+        // thread e mod nthreads): every caller runs fill_geo with the whole workgroup, under
+        // uniform control flow
+        __syncthreads();
         for (int i = tid; i < BPX; i += nthreads) {
             const int p = tile.pixel(g, wt, i);
             if (p < 0) continue;
