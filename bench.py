@@ -367,6 +367,8 @@ def main():
                     help="instead of the metric line, print one JSON line per BASELINE config 2-5 (cfg5 also in "
                          "fp16 / bf16): forward and forward+backward ms, TFLOP/s, fraction of fp32 MFMA peak and "
                          "per-kernel-family rooflines")
+    ap.add_argument("--only", type=int, default=0, metavar="N",
+                    help="with --configs: only BASELINE config N (2-5; cfg5 in all three dtypes)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 5 times (reference for the rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE scale) and exit")
@@ -389,6 +391,8 @@ def main():
 
     if args.configs:
         for n, dt in SUITE:
+            if args.only and n != args.only:
+                continue
             print(f"[bench] suite cfg{n} {dt}", file=sys.stderr, flush=True)
             print(json.dumps(run_suite_case(n, dt, args.steps, args.warmup, cpu=not args.no_cpu_baseline)),
                   flush=True)

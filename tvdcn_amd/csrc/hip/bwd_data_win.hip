@@ -14,10 +14,19 @@
 // 256 in 1D, 4x8x8 in 3D) x 16 sampled-side channels x every tap; eight waves
 // (two per SIMD, so one wave's loads overlap the other's MFMAs), each owning 32
 // pixels; one workgroup per CU (the window takes most of the 160 KB of LDS).
-//   * K loop over the GEMM-side channels m, 16 per step, operands straight from
-//     global memory into registers (next step prefetched while the MFMAs of the
-//     current one run): wave w computes Gt[c][px] for its 32 pixels, so each lane
-//     holds four consecutive channels of one pixel per (tap, 16-pixel block).
+//   * K loop over the GEMM-side channels m, operands straight from global memory
+//     into registers (the next step's prefetched while the MFMAs of the current one
+//     run): wave w computes Gt[c][px] for its 32 pixels, so each lane holds four
+//     consecutive channels of one pixel per (tap, 16-pixel block). It runs on
+//     16x16x32 MFMAs, 32 channels per step, from 16-bit operands laid out by
+//     z_split_kernel / weight_split_kernel: fp16 and bf16 tensors as they are, fp32
+//     tensors as three bf16 pieces each, of whose nine cross products the six with
+//     i + j <= 2 are summed (the rest are below 2^-25 of the product, under fp32's own
+//     rounding; 6 MFMAs at 16 cycles against 8 fp32 16x16x4 MFMAs at 32 cycles per 32
+//     channels). An fp32 operand that is not finite or would round past the bf16
+//     range (a device flag set by the layout kernels) sends the launch down the fp32
+//     loop (16x16x4 MFMAs, 16 channels per step), which keeps the reference's inf/nan
+//     propagation.
 //   * Epilogue per tap: the geometry of the 256 pixels (one per thread) goes to an
 //     LDS table. The offset/mask gradients are formed in the MFMA layout (4
 //     channels in-lane, two shuffles across the channel quads, one atomic per
@@ -37,8 +46,9 @@
 //     would be rounded at it) bypass the window: they go to global float atomics,
 //     and the bound covers the terms that stay. The typical term is 2 to the mean
 //     binary exponent of the 128 per-lane mean terms (a geometric mean, which a
-//     minority of spikes barely moves: each lane holds 2 pixels x the pass's taps). A pass with a non-finite bound (inf/nan must
-//     propagate as in the reference) does not use the window at all: it goes to
+//     minority of spikes barely moves: each lane holds 2 pixels x the pass's taps).
+//     In 3D a pass with spikes does not use the window. Neither does a pass with a
+//     non-finite bound (inf/nan must propagate as in the reference): it goes to
 //     global float atomics, after the window flushes what it holds.
 //     Corners outside the window go to global float atomics.
 //   * The window (sampled-grid box around the tile's undeformed footprint plus a
@@ -109,6 +119,115 @@ __device__ __forceinline__ float row_sum4(float v) {
     return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// ---- 16-bit MFMA operands --------------------------------------------------------------
+// An fp32 value as three bf16 pieces, each rounded to nearest even from what the previous
+// ones leave: v = p0 + p1 + p2 + r, |r| <= 2^-27 |v| (each piece holds the next 8
+// significant bits; the residuals are exact in fp32). The products p_i * q_j with
+// i + j <= 2 are exact in the MFMA's fp32 accumulation; the three left out are below
+// 2^-25 |v w| together. `bad`: not finite, or rounds past the largest bf16.
+__device__ __forceinline__ uint32_t bf16_rne_bits(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ bool bf16_split_bad(float v) {
+    return (__float_as_uint(v) & 0x7FFFFFFFu) >= 0x7F7F8000u;
+}
+__device__ __forceinline__ void split3(float v, uint32_t (&p)[3]) {
+    float r = v;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        p[k] = bf16_rne_bits(r);
+        r -= __uint_as_float(p[k] << 16);
+    }
+}
+template <typename T> __device__ __forceinline__ uint32_t bits16(float v) {
+    if constexpr (std::is_same<T, __half>::value) return __half_as_ushort(__float2half(v));
+    else return bf16_rne_bits(v);   // bf16 storage: exact (v came from a bf16)
+}
+template <typename T> constexpr int npiece_of() { return std::is_same<T, float>::value ? 3 : 1; }
+
+// Eight 16-bit operand values of a lane (K = 8 * (lane / 16) .. + 7) from eight floats: piece k
+// of each value, packed two per dword (the lower K in the low half). Returns whether any value
+// is bad for the split.
+template <typename T, int NP>
+__device__ __forceinline__ bool pack_pieces(const float (&v)[8], uint4 (&out)[NP]) {
+    uint32_t w[NP][4];
+    bool bad = false;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        uint32_t lo[NP], hi[NP];
+        if constexpr (NP == 3) {
+            uint32_t a[3], b[3];
+            split3(v[e], a);
+            split3(v[e + 1], b);
+            bad = bad || bf16_split_bad(v[e]) || bf16_split_bad(v[e + 1]);
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                lo[k] = a[k];
+                hi[k] = b[k];
+            }
+        } else {
+            lo[0] = bits16<T>(v[e]);
+            hi[0] = bits16<T>(v[e + 1]);
+        }
+#pragma unroll
+        for (int k = 0; k < NP; ++k) w[k][e >> 1] = (lo[k] & 0xFFFFu) | (hi[k] << 16);
+    }
+#pragma unroll
+    for (int k = 0; k < NP; ++k) out[k] = uint4{w[k][0], w[k][1], w[k][2], w[k][3]};
+    return bad;
+}
+
+// D += A * B on one 16x16x32 MFMA: bf16 operands (fp32 pieces, bf16 tensors) or fp16
+template <typename T> __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
+    if constexpr (std::is_same<T, __half>::value) {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+    } else {
+        typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b), c, 0, 0,
+                                                        0);
+    }
+}
+
+// Z (B, G * Mg, Pn) -> zs [B][G][ms32][Pn][NP][32]: per pixel and 32-channel step, the NP pieces
+// of its 32 channels (zero past Mg), each as 4 lane groups of 8 (the 16x16x32 B-operand layout).
+// Block = 64 pixels of one (image, group, step), transposed through LDS.
+template <typename T, int NP>
+__global__ void __launch_bounds__(256)
+z_split_kernel(const T *__restrict__ z, uint16_t *__restrict__ zs, int *flag, int G, int Mg, int Pn, int ms32,
+               int pblocks) {
+    __shared__ float tile[32][65];
+    const long long bid = blockIdx.x;
+    const int pb = (int)(bid % pblocks);
+    const long long bgs = bid / pblocks;   // (b * G + grp) * ms32 + step
+    const int st = (int)(bgs % ms32);
+    const long long bg = bgs / ms32;
+    const int grp = (int)(bg % G);
+    const long long b = bg / G;
+    const int p0 = pb * 64;
+    const T *src = z + ((size_t)b * G + grp) * (size_t)Mg * Pn;
+    for (int i = threadIdx.x; i < 32 * 64; i += 256) {
+        const int ml = i >> 6, pl = i & 63;
+        const int m = st * 32 + ml, p = p0 + pl;
+        float v = 0.f;
+        if (m < Mg && p < Pn) v = to_acc<float>(src[(size_t)m * Pn + p]);
+        tile[ml][pl] = v;
+    }
+    __syncthreads();
+    const int pl = threadIdx.x >> 2, q = threadIdx.x & 3, p = p0 + pl;
+    if (p >= Pn) return;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = tile[q * 8 + e][pl];
+    uint4 out[NP];
+    const bool bad = pack_pieces<T, NP>(v, out);
+    uint16_t *dst = zs + ((size_t)bgs * Pn + p) * (NP * 32) + q * 8;
+#pragma unroll
+    for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + k * 32) = out[k];
+    if (NP == 3 && bad) atomicOr(flag, 1);
+}
+
 // Reduction over each row of 16 lanes (the lanes of one channel quad's 16 pixels), the
 // result in every lane of the row: DPP quad xor 1, quad xor 2, half-row mirror, row
 // mirror (VALU only; a shuffle goes through the LDS crossbar)
@@ -135,9 +254,10 @@ __device__ __forceinline__ unsigned row_sum16(unsigned v) {
 
 template <int DIM, typename T, bool SCATTER, bool COORD>
 __global__ void __launch_bounds__(NT)
-bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wchunks,
-                    const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
-                    float *__restrict__ gx_cl, float *__restrict__ goff, float *__restrict__ gmask) {
+bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wchunks, const uint16_t *zs,
+                    const uint16_t *wsplit, const int *flag, const float *__restrict__ xcl,
+                    const T *__restrict__ offset, const T *__restrict__ mask, float *__restrict__ gx_cl,
+                    float *__restrict__ goff, float *__restrict__ gmask) {
     constexpr int NC = 1 << DIM;
     constexpr int TMAX = WIN_TMAX;
 
@@ -171,6 +291,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     tile.init(g, wt, L % n_sp, ct, L / n_sp);
     const int b = tile.b, grp = tile.grp, c0 = tile.c0, cg0 = tile.cg0, ogu = tile.ogu, mgu = tile.mgu;
     const bool deformable = offset != nullptr;
+    // the 16-bit K loop when its operands were laid out, and (fp32) none was flagged
+    const int use16_flag = zs != nullptr && (flag == nullptr || *flag == 0);
     const bool cq_ok = c0 + mq < g.Cg;           // Cg % 4 == 0: a channel quad is all in or all out
     const float *xb = xcl + (size_t)b * g.Sn * g.C + cg0;
 
@@ -335,13 +457,87 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 }
             }
         };
-        const bool mpad = g.Mg % BM != 0;
-        if (ntaps == TMAX && !mpad)
-            kloop(std::true_type(), std::false_type());
-        else if (!mpad)
-            kloop(std::false_type(), std::false_type());
-        else
-            kloop(std::false_type(), std::true_type());
+        // ---- 16-bit K loop: 16x16x32 MFMAs over 32 channels per step, operands straight
+        //      from the split layouts into registers; Z of the next step and the weight
+        //      fragment one tap ahead (of the (step, tap) sequence) in flight
+        auto kloop16 = [&]() {
+            constexpr int NP = npiece_of<T>();
+            const int ms32 = wt.ms32;
+            const size_t zstep = (size_t)g.Pn * (NP * 32);
+            const uint16_t *zl[PB];
+#pragma unroll
+            for (int pb = 0; pb < PB; ++pb)
+                zl[pb] = zs + ((size_t)(b * g.G + grp) * ms32 * g.Pn + (zp[pb] < 0 ? 0 : zp[pb])) * (NP * 32) + q * 8;
+            const uint16_t *wl = wsplit + ((size_t)(grp * wt.c_tiles + ct) * ms32 * g.Kn + t0) * (NP * 512) + lane * 8;
+            auto wfrag = [&](int st, int tl, uint4 (&f)[NP]) {
+                const uint16_t *pw = wl + ((size_t)min(st, ms32 - 1) * g.Kn + tl) * (NP * 512);
+#pragma unroll
+                for (int k = 0; k < NP; ++k) f[k] = *reinterpret_cast<const uint4 *>(pw + k * 512);
+            };
+            auto zfrag = [&](int st, uint4 (&f)[PB][NP]) {
+#pragma unroll
+                for (int pb = 0; pb < PB; ++pb)
+#pragma unroll
+                    for (int k = 0; k < NP; ++k)
+                        f[pb][k] = *reinterpret_cast<const uint4 *>(zl[pb] + (size_t)st * zstep + k * 32);
+            };
+            uint4 zc[PB][NP], zn[PB][NP], w0[NP], w1[NP];
+            zfrag(0, zc);
+            wfrag(0, 0, w0);
+            // (ps, pt): the next weight fragment of the (step, tap) sequence to load
+            int ps = 0, pt = 1;
+            if (pt == ntaps) {
+                pt = 0;
+                ++ps;
+            }
+            for (int st = 0; st < ms32; ++st) {
+                zfrag(min(st + 1, ms32 - 1), zn);
+                issue_fence();
+#pragma unroll
+                for (int tp = 0; tp < TMAX; ++tp) {
+                    if (tp >= ntaps) break;
+                    wfrag(ps, pt, w1);
+                    if (++pt == ntaps) {
+                        pt = 0;
+                        ++ps;
+                    }
+#pragma unroll
+                    for (int pb = 0; pb < PB; ++pb) {
+                        if constexpr (NP == 3) {
+                            // smallest products first: (2,0) (1,1) (0,2) (1,0) (0,1) (0,0)
+                            acc[tp][pb] = mfma16x16x32<T>(w0[2], zc[pb][0], acc[tp][pb]);
+                            acc[tp][pb] = mfma16x16x32<T>(w0[1], zc[pb][1], acc[tp][pb]);
+                            acc[tp][pb] = mfma16x16x32<T>(w0[0], zc[pb][2], acc[tp][pb]);
+                            acc[tp][pb] = mfma16x16x32<T>(w0[1], zc[pb][0], acc[tp][pb]);
+                            acc[tp][pb] = mfma16x16x32<T>(w0[0], zc[pb][1], acc[tp][pb]);
+                        }
+                        acc[tp][pb] = mfma16x16x32<T>(w0[0], zc[pb][0], acc[tp][pb]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int k = 0; k < NP; ++k) w0[k] = w1[k];
+                }
+#pragma unroll
+                for (int pb = 0; pb < PB; ++pb)
+#pragma unroll
+                    for (int k = 0; k < NP; ++k) zc[pb][k] = zn[pb][k];
+            }
+        };
+        // (opaque to the optimiser: the choice is made per pass rather than by two copies of
+        // the whole pass loop)
+        int use16 = __builtin_amdgcn_readfirstlane(use16_flag);
+        asm volatile("" : "+s"(use16));
+        if (use16) {
+            kloop16();
+        } else {
+            const bool mpad = g.Mg % BM != 0;
+            if (ntaps == TMAX && !mpad)
+                kloop(std::true_type(), std::false_type());
+            else if (!mpad)
+                kloop(std::false_type(), std::false_type());
+            else
+                kloop(std::false_type(), std::true_type());
+        }
         __syncthreads();   // geometry table (and X window) written
 
         // ---- fixed-point scale per channel: the bound covers this pass plus everything
@@ -453,8 +649,12 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
             // both flags in one read: non-finite [BC], spikes [BC + 1]
             const int2 flags = *reinterpret_cast<const int2 *>(scl + BC);
             spikes = flags.y != 0;
-            bool nonfinite = flags.x != 0;
-            if (spikes) {
+            bool no_window = flags.x != 0;
+            if constexpr (DIM == 3) {
+                // 3D: a pass with spikes skips the window (the branch-light 3D path has no
+                // per-channel routing)
+                no_window = no_window || spikes;
+            } else if (spikes) {
                 // bound of the terms that stay in the window
 #pragma unroll
                 for (int v = 0; v < 4; ++v) th[v] = thr[mq + v];
@@ -467,11 +667,11 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     set_scale(bc);
                 }
                 __syncthreads();
-                nonfinite = scl[BC] != 0;
+                no_window = scl[BC] != 0;
             }
-            if (nonfinite) {
-                // not finite: what the window holds goes out at its scale, the pass goes to
-                // global float atomics (inf / nan propagate as in the reference)
+            if (no_window) {
+                // not finite (or 3D spikes): what the window holds goes out at its scale, the
+                // pass goes to global float atomics (inf / nan propagate as in the reference)
                 if (win_data) flush_window(true);
                 win_data = false;
                 spikes = false;
@@ -536,10 +736,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 float qv[DIM + 1];
                 bool done = false;
                 if constexpr (DIM == 3) {
-                    if (!SCATTER || (use_window && !lane_spike)) {
+                    if (!SCATTER || use_window) {
                         // 3D: one branch-light path for every lane (window margins of about one
-                        // cell: most waves hold a lane with a corner outside the window); lanes
-                        // holding a spike take the general path
+                        // cell: most waves hold a lane with a corner outside the window)
                         done = true;
                         const Corners3 cr(g, wt, tile, r, deformable);
                         if constexpr (COORD) {
@@ -783,14 +982,58 @@ weight_win_kernel(const T *__restrict__ w, float *__restrict__ out, int G, int M
     for (int e = threadIdx.x; e < n; e += blockDim.x) dst[e] = tile[e / (BM * BC)][(e / BM) % BC][e % BM];
 }
 
+// weight (M, Cg, Kn) -> split chunks [G][c_tiles][ms32][Kn][NP][4 q][16 c][8 e]: per (step, tap)
+// and piece, the 16x16x32 A-operand fragment of 16 channels x 32 GEMM-side channels (lane
+// q * 16 + c holds rows 8q .. 8q + 7 of channel c; zero past Mg / Cg). Block = (group, channel
+// slice, step, run of up to WL_TK taps), transposed through LDS.
+template <typename T, int NP>
+__global__ void __launch_bounds__(256)
+weight_split_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, int G, int Mg, int Cg, int Kn,
+                    int c_tiles, int ms32) {
+    __shared__ float tile[WL_TK][BC][33];   // [tap][c][m]
+    const int tchunks = (Kn + WL_TK - 1) / WL_TK;
+    int L = blockIdx.x;
+    const int tc = L % tchunks;
+    L /= tchunks;
+    const int st = L % ms32;
+    L /= ms32;
+    const int ct = L % c_tiles;
+    const int grp = L / c_tiles;
+    const int t0 = tc * WL_TK, nt = min(WL_TK, Kn - t0);
+    const int n = 32 * BC * nt;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        const int tt = e % nt, r = e / nt;   // (m, c, tap), taps fastest
+        const int ci = r % BC, mi = r / BC;
+        const int m = st * 32 + mi, c = ct * BC + ci;
+        float v = 0.f;
+        if (m < Mg && c < Cg) v = to_acc<float>(w[(((size_t)grp * Mg + m) * Cg + c) * Kn + t0 + tt]);
+        tile[tt][ci][mi] = v;
+    }
+    __syncthreads();
+    uint16_t *dst = out + ((((size_t)grp * c_tiles + ct) * ms32 + st) * Kn + t0) * (NP * 512);
+    bool bad = false;
+    for (int u = threadIdx.x; u < nt * 64; u += blockDim.x) {
+        const int tt = u >> 6, l = u & 63, q = l >> 4, c = l & 15;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = tile[tt][c][q * 8 + e];
+        uint4 o[NP];
+        bad = pack_pieces<T, NP>(v, o) || bad;
+#pragma unroll
+        for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + (size_t)tt * (NP * 512) + k * 512 + l * 8) = o[k];
+    }
+    if (NP == 3 && bad) atomicOr(flag, 1);
+}
+
 template <bool SCATTER, bool COORD> size_t lds_bytes(const WinTiles &t) {
     return ((size_t)FIXED_WORDS + (SCATTER ? (size_t)BC * fix_stride(t.cells) : 0) + (COORD ? (size_t)t.cells * XS : 0)) *
            sizeof(float);
 }
 
 template <int DIM, typename T, bool SCATTER, bool COORD>
-hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void *wchunks, const void *xcl,
-                    const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
+hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void *wchunks, const void *zs,
+                    const void *wsplit, const int *flag, const void *xcl, const void *offset, const void *mask,
+                    void *gx_cl, void *goff, void *gmask, hipStream_t s) {
     auto kern = bwd_data_win_kernel<DIM, T, SCATTER, COORD>;
     const size_t lds = lds_bytes<SCATTER, COORD>(tl);
     static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
@@ -798,7 +1041,8 @@ hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void 
         return e;
     const long long blocks = (long long)g.G * g.B * tl.ntile[0] * tl.ntile[1] * tl.ntile[2] * tl.c_tiles;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, tl, static_cast<const T *>(z),
-                       static_cast<const float *>(wchunks), static_cast<const float *>(xcl),
+                       static_cast<const float *>(wchunks), static_cast<const uint16_t *>(zs),
+                       static_cast<const uint16_t *>(wsplit), flag, static_cast<const float *>(xcl),
                        static_cast<const T *>(offset), static_cast<const T *>(mask), static_cast<float *>(gx_cl),
                        static_cast<float *>(goff), static_cast<float *>(gmask));
     return hipGetLastError();
@@ -806,24 +1050,48 @@ hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void 
 
 template <int DIM, typename T>
 hipError_t launch_f(const Geo &g, const WinTiles &tl, bool scatter, bool coord, const void *z, const void *wc,
-                    const void *xcl, const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask,
-                    hipStream_t s) {
-    if (scatter && coord) return launch_k<DIM, T, true, true>(g, tl, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
-    if (scatter) return launch_k<DIM, T, true, false>(g, tl, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
-    if (coord) return launch_k<DIM, T, false, true>(g, tl, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
+                    const void *zs, const void *wsp, const int *flag, const void *xcl, const void *offset,
+                    const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
+    if (scatter && coord)
+        return launch_k<DIM, T, true, true>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+    if (scatter)
+        return launch_k<DIM, T, true, false>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+    if (coord)
+        return launch_k<DIM, T, false, true>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
     return hipSuccess;
 }
 
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &tl, bool scatter, bool coord, const void *z,
-                    const void *wc, const void *xcl, const void *offset, const void *mask, void *gx_cl, void *goff,
-                    void *gmask, hipStream_t s) {
+                    const void *wc, const void *zs, const void *wsp, const int *flag, const void *xcl,
+                    const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
     switch (dim) {
-        case 1: return launch_f<1, T>(g, tl, scatter, coord, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
-        case 2: return launch_f<2, T>(g, tl, scatter, coord, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
-        case 3: return launch_f<3, T>(g, tl, scatter, coord, z, wc, xcl, offset, mask, gx_cl, goff, gmask, s);
+        case 1:
+            return launch_f<1, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+        case 2:
+            return launch_f<2, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+        case 3:
+            return launch_f<3, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
     }
     return hipErrorInvalidValue;
+}
+
+template <typename T>
+hipError_t launch_split(const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs, void *wsp, int *flag,
+                        hipStream_t s) {
+    constexpr int NP = npiece_of<T>();
+    const int pblocks = (g.Pn + 63) / 64;
+    const long long zblocks = (long long)g.B * g.G * t.ms32 * pblocks;
+    const long long wblocks = (long long)g.G * t.c_tiles * t.ms32 * ((g.Kn + WL_TK - 1) / WL_TK);
+    if (zblocks > INT_MAX || wblocks > INT_MAX) return hipErrorInvalidValue;
+    if (zblocks > 0)
+        hipLaunchKernelGGL((z_split_kernel<T, NP>), dim3((unsigned)zblocks), dim3(256), 0, s, static_cast<const T *>(z),
+                           static_cast<uint16_t *>(zs), flag, g.G, g.Mg, g.Pn, t.ms32, pblocks);
+    if (wblocks > 0)
+        hipLaunchKernelGGL((weight_split_kernel<T, NP>), dim3((unsigned)wblocks), dim3(256), 0, s,
+                           static_cast<const T *>(w), static_cast<uint16_t *>(wsp), flag, g.G, g.Mg, g.Cg, g.Kn,
+                           t.c_tiles, t.ms32);
+    return hipGetLastError();
 }
 
 int ilog2(int v) {
@@ -915,6 +1183,10 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
     const int npass = (g.Kn + WIN_TMAX - 1) / WIN_TMAX;
     t.tpp = (g.Kn + npass - 1) / npass;
     t.chunk_elems = (size_t)g.G * t.c_tiles * t.m_steps * g.Kn * BC * BM;
+    t.ms32 = (g.Mg + 31) / 32;
+    t.npiece = dtype == kF32 ? 3 : 1;
+    t.zs_elems = (size_t)g.B * g.G * t.ms32 * g.Pn * t.npiece * 32;
+    t.ws_elems = (size_t)g.G * t.c_tiles * t.ms32 * g.Kn * t.npiece * 512;
     t.ok = true;
     return t;
 }
@@ -937,15 +1209,30 @@ hipError_t launch_weight_win_layout(int dtype, const Geo &g, const WinTiles &t, 
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
-                               const void *z, const void *wchunks, const void *xcl, const void *offset,
-                               const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
+hipError_t launch_data_win_split(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w,
+                                 void *zs, void *wsplit, int *flag, hipStream_t s) {
     switch (dtype) {
-        case kF32: return launch_d<float>(dim, g, t, scatter, coord, z, wchunks, xcl, offset, mask, gx_cl, goff, gmask, s);
-        case kF16: return launch_d<__half>(dim, g, t, scatter, coord, z, wchunks, xcl, offset, mask, gx_cl, goff, gmask, s);
+        case kF32: return launch_split<float>(g, t, z, w, zs, wsplit, flag, s);
+        case kF16: return launch_split<__half>(g, t, z, w, zs, wsplit, flag, s);
+        case kBF16: return launch_split<__hip_bfloat16>(g, t, z, w, zs, wsplit, flag, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
+                               const void *z, const void *wchunks, const void *zs, const void *wsplit,
+                               const int *flag, const void *xcl, const void *offset, const void *mask, void *gx_cl,
+                               void *goff, void *gmask, hipStream_t s) {
+    switch (dtype) {
+        case kF32:
+            return launch_d<float>(dim, g, t, scatter, coord, z, wchunks, zs, wsplit, flag, xcl, offset, mask, gx_cl,
+                                   goff, gmask, s);
+        case kF16:
+            return launch_d<__half>(dim, g, t, scatter, coord, z, wchunks, zs, wsplit, flag, xcl, offset, mask, gx_cl,
+                                    goff, gmask, s);
         case kBF16:
-            return launch_d<__hip_bfloat16>(dim, g, t, scatter, coord, z, wchunks, xcl, offset, mask, gx_cl, goff, gmask,
-                                            s);
+            return launch_d<__hip_bfloat16>(dim, g, t, scatter, coord, z, wchunks, zs, wsplit, flag, xcl, offset, mask,
+                                            gx_cl, goff, gmask, s);
     }
     return hipErrorInvalidValue;
 }

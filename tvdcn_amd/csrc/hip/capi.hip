@@ -240,6 +240,7 @@ tvdcn_status batch_block(const tvdcn_conv_desc *d, int64_t &block, ImageElems *e
 // Workspace sub-buffers (byte offsets into the caller's workspace).
 struct Layout {
     size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, wpart = 0, goff_acc = 0, gmask_acc = 0, yacc = 0;
+    size_t zs = 0, wsplit = 0, flag = 0;   // the windowed data gradient's 16-bit MFMA operands
     size_t total = 0;
 };
 
@@ -262,6 +263,14 @@ Layout layout(const Plan &pl, bool backward) {
     };
     const size_t SENTINEL = (size_t)-1;
     L.xcl = L.wf = L.wd = L.cl_acc = L.wpart = L.goff_acc = L.gmask_acc = L.yacc = SENTINEL;
+    L.zs = L.wsplit = L.flag = SENTINEL;
+    // windowed data gradient (conv backward, transposed forward and backward): split operands
+    auto take_split = [&]() {
+        if (!pl.wn_s.ok) return;
+        L.zs = take(align_up(pl.wn_s.zs_elems * 2));
+        L.wsplit = take(align_up(pl.wn_s.ws_elems * 2));
+        L.flag = take(align_up(sizeof(int)));
+    };
     // fp32 output of a slice-split windowed forward when the output dtype is not fp32
     const bool split_acc = pl.fw.ok && pl.fw.ksplit > 1 && pl.dtype != kF32;
     const size_t yacc_bytes = align_up((size_t)g.B * g.M * g.Pn * sizeof(float));
@@ -273,10 +282,12 @@ Layout layout(const Plan &pl, bool backward) {
         } else {
             L.wd = take(wd_bytes);
             L.cl_acc = take(cl_bytes);
+            take_split();
         }
     } else {
         L.xcl = take(cl_bytes);
         L.wd = take(wd_bytes);
+        take_split();
         if (pl.transposed) {
             L.wf = take(wf_bytes);
             if (split_acc) L.yacc = take(yacc_bytes);
@@ -451,9 +462,14 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
         void *wd = at(workspace, L.wd), *ycl = at(workspace, L.cl_acc);
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
         if (pl.wn_s.ok) {
+            void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
+            int *flag = static_cast<int *>(at(workspace, L.flag));
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
-            TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, input, wd, nullptr,
-                                                                        offset, mask, ycl, nullptr, nullptr, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, flag, 1, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_split(dt, g, pl.wn_s, input, weight, zs, wsp, flag, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, input, wd, zs,
+                                                                        wsp, flag, nullptr, offset, mask, ycl, nullptr,
+                                                                        nullptr, s));
         } else {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, false, input, wd, nullptr, offset,
@@ -498,9 +514,13 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, X, xcl, (size_t)g.B * g.Sn * g.C, s));
         const bool coord = offset != nullptr || mask != nullptr;
-        if (pl.wn_s.ok)
+        void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
+        int *flag = static_cast<int *>(at(workspace, L.flag));
+        if (pl.wn_s.ok) {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
-        else
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, flag, 1, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_split(dt, g, pl.wn_s, Z, weight, zs, wsp, flag, s));
+        } else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
         if (!pl.transposed) {
             // channels-last grad_input of the accumulation type is accumulated in place
@@ -508,13 +528,15 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
             if (pl.wn_s.ok && coord && pl.data_split) {
                 // two launches, each with the larger window its LDS share allows
-                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, Z, wd, xcl, offset,
-                                                                            mask, gx_cl, nullptr, nullptr, s));
-                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_c, false, true, Z, wd, xcl, offset,
-                                                                            mask, nullptr, goff, gmask, s));
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, Z, wd, zs, wsp,
+                                                                            flag, xcl, offset, mask, gx_cl, nullptr, nullptr,
+                                                                            s));
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_c, false, true, Z, wd, zs, wsp,
+                                                                            flag, xcl, offset, mask, nullptr, goff, gmask, s));
             } else if (pl.wn_s.ok)
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, coord ? pl.wn_s : pl.wn_x, true, coord,
-                                                                            Z, wd, xcl, offset, mask, gx_cl, goff, gmask, s));
+                                                                            Z, wd, zs, wsp, flag, xcl, offset, mask, gx_cl,
+                                                                            goff, gmask, s));
             else
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask,
                                                                         gx_cl, goff, gmask, s));
@@ -544,8 +566,8 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
                              launch_fwd_gather_gemm(dt, pl.dim, g, pl.ft, xcl, wf, offset, mask, nullptr, grad_input, s));
             }
             if (coord && pl.wn_c.ok)
-                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_c, false, true, Z, wd, xcl, offset,
-                                                                            mask, nullptr, goff, gmask, s));
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_c, false, true, Z, wd, zs, wsp,
+                                                                            flag, xcl, offset, mask, nullptr, goff, gmask, s));
             else if (coord)
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, false, true, Z, wd, xcl, offset, mask,
                                                                         nullptr, goff, gmask, s));

@@ -60,6 +60,12 @@ struct WinTiles {
     int c_tiles, m_steps;
     int tpp;             // taps per pass (<= WIN_TMAX)
     size_t chunk_elems;  // floats of the re-laid-out weight
+    // 16-bit MFMA operands of the data gradient (16x16x32 MFMAs over 32 GEMM-side channels per
+    // step): fp32 tensors split into three bf16 pieces each, fp16 / bf16 tensors as they are
+    int ms32;            // 32-channel steps of the GEMM side (zero padded)
+    int npiece;          // 16-bit pieces per value: 3 (fp32), 1 (fp16 / bf16)
+    size_t zs_elems;     // 16-bit elements of the split Z: [B][G][ms32][Pn][npiece][32]
+    size_t ws_elems;     // 16-bit elements of the split weight: [G][c_tiles][ms32][Kn][npiece][512]
 };
 
 // Windowed weight-gradient kernel (bwd_weight_win.hip): workgroups own (group,
@@ -139,9 +145,15 @@ hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t,
                            void *gx_cl, void *goff, void *gmask, hipStream_t s);
 hipError_t launch_weight_win_layout(int dtype, const Geo &g, const WinTiles &t, const void *w, void *chunks,
                                     hipStream_t s);
+// Z (the GEMM-side tensor, (B, M, Pn)) and the weight as the data gradient's 16-bit MFMA operands
+// (zs, wsplit). For fp32 tensors, *flag (zeroed by the caller first) is set when a value is not
+// finite or would round past the bf16 range: the data gradient then runs its fp32 MFMA loop.
+hipError_t launch_data_win_split(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w,
+                                 void *zs, void *wsplit, int *flag, hipStream_t s);
 hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
-                               const void *z, const void *wchunks, const void *xcl, const void *offset,
-                               const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s);
+                               const void *z, const void *wchunks, const void *zs, const void *wsplit,
+                               const int *flag, const void *xcl, const void *offset, const void *mask, void *gx_cl,
+                               void *goff, void *gmask, hipStream_t s);
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
                                  void *gw, bool accumulate, hipStream_t s);
