@@ -412,3 +412,30 @@ def test_saved_input_version_check_by_default():
     xin.add_(1.0)
     with pytest.raises(RuntimeError, match="modified by an inplace operation"):
         y.sum().backward()
+
+
+@pytest.mark.parametrize("what", ["input", "mask", "grad_out"])
+def test_large_fp32_operands_take_the_fp32_loop(what):
+    """fp32 operands go into the 16-bit MFMA loops as three bf16 pieces only when the pieces cannot
+    overflow: an input at or above 2^96, a plain mask at or above 2^30 or a grad_out past the bf16
+    range sets the device flag, and the kernels run their fp32 MFMA loops. Results against the
+    float64 oracle at the fp32 tolerances (forward and every gradient)."""
+    case = make_case(2, False, batch=2, cin=32, cout=32, kernel=[3, 3], stride=[1, 1], padding=[1, 1],
+                     dilation=[1, 1], in_size=[14, 12], out_pad=[0, 0], seed=560)
+    g = torch.Generator().manual_seed(561)
+    gout = torch.randn(case["out_shape"], generator=g, dtype=torch.float64)
+    if what == "input":
+        case["input"] = case["input"] * 1e30
+    elif what == "mask":
+        case["mask"] = case["mask"] * 1e10
+    else:
+        # one value rounds past the largest bf16; the input is scaled down so that no gradient
+        # overflows fp32
+        case["input"] = case["input"] * 1e-3
+        gout[0, 0, 0, 0] = 3.3999e38
+    out, grads, _ = run_gpu(case, torch.float32, grad_out=gout)
+    ref_out, ref_grads = run_oracle(case, gout, torch.float32)
+    assert rel_err(out, ref_out) < TOL[torch.float32][0]
+    for name, gr, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
+        e = rel_err(gr, r)
+        assert e < TOL[torch.float32][1], f"grad_{name} rel err {e}"

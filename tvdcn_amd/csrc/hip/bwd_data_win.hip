@@ -119,77 +119,6 @@ __device__ __forceinline__ float row_sum4(float v) {
     return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
-// ---- 16-bit MFMA operands --------------------------------------------------------------
-// An fp32 value as three bf16 pieces, each rounded to nearest even from what the previous
-// ones leave: v = p0 + p1 + p2 + r, |r| <= 2^-27 |v| (each piece holds the next 8
-// significant bits; the residuals are exact in fp32). The products p_i * q_j with
-// i + j <= 2 are exact in the MFMA's fp32 accumulation; the three left out are below
-// 2^-25 |v w| together. `bad`: not finite, or rounds past the largest bf16.
-__device__ __forceinline__ uint32_t bf16_rne_bits(float v) {
-    const uint32_t u = __float_as_uint(v);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-__device__ __forceinline__ bool bf16_split_bad(float v) {
-    return (__float_as_uint(v) & 0x7FFFFFFFu) >= 0x7F7F8000u;
-}
-__device__ __forceinline__ void split3(float v, uint32_t (&p)[3]) {
-    float r = v;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        p[k] = bf16_rne_bits(r);
-        r -= __uint_as_float(p[k] << 16);
-    }
-}
-template <typename T> __device__ __forceinline__ uint32_t bits16(float v) {
-    if constexpr (std::is_same<T, __half>::value) return __half_as_ushort(__float2half(v));
-    else return bf16_rne_bits(v);   // bf16 storage: exact (v came from a bf16)
-}
-template <typename T> constexpr int npiece_of() { return std::is_same<T, float>::value ? 3 : 1; }
-
-// Eight 16-bit operand values of a lane (K = 8 * (lane / 16) .. + 7) from eight floats: piece k
-// of each value, packed two per dword (the lower K in the low half). Returns whether any value
-// is bad for the split.
-template <typename T, int NP>
-__device__ __forceinline__ bool pack_pieces(const float (&v)[8], uint4 (&out)[NP]) {
-    uint32_t w[NP][4];
-    bool bad = false;
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-        uint32_t lo[NP], hi[NP];
-        if constexpr (NP == 3) {
-            uint32_t a[3], b[3];
-            split3(v[e], a);
-            split3(v[e + 1], b);
-            bad = bad || bf16_split_bad(v[e]) || bf16_split_bad(v[e + 1]);
-#pragma unroll
-            for (int k = 0; k < 3; ++k) {
-                lo[k] = a[k];
-                hi[k] = b[k];
-            }
-        } else {
-            lo[0] = bits16<T>(v[e]);
-            hi[0] = bits16<T>(v[e + 1]);
-        }
-#pragma unroll
-        for (int k = 0; k < NP; ++k) w[k][e >> 1] = (lo[k] & 0xFFFFu) | (hi[k] << 16);
-    }
-#pragma unroll
-    for (int k = 0; k < NP; ++k) out[k] = uint4{w[k][0], w[k][1], w[k][2], w[k][3]};
-    return bad;
-}
-
-// D += A * B on one 16x16x32 MFMA: bf16 operands (fp32 pieces, bf16 tensors) or fp16
-template <typename T> __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
-    if constexpr (std::is_same<T, __half>::value) {
-        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
-    } else {
-        typedef __bf16 b8 __attribute__((ext_vector_type(8)));
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b), c, 0, 0,
-                                                        0);
-    }
-}
-
 // Z (B, G * Mg, Pn) -> zs [B][G][ms32][Pn][NP][32]: per pixel and 32-channel step, the NP pieces
 // of its 32 channels (zero past Mg), each as 4 lane groups of 8 (the 16x16x32 B-operand layout).
 // Block = 64 pixels of one (image, group, step), transposed through LDS.
@@ -218,10 +147,14 @@ z_split_kernel(const T *__restrict__ z, uint16_t *__restrict__ zs, int *flag, in
     const int pl = threadIdx.x >> 2, q = threadIdx.x & 3, p = p0 + pl;
     if (p >= Pn) return;
     float v[8];
+    bool bad = false;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = tile[q * 8 + e][pl];
+    for (int e = 0; e < 8; ++e) {
+        v[e] = tile[q * 8 + e][pl];
+        bad = bad || bf16_split_bad(v[e]);
+    }
     uint4 out[NP];
-    const bool bad = pack_pieces<T, NP>(v, out);
+    pack8_16<T, NP>(v, out);
     uint16_t *dst = zs + ((size_t)bgs * Pn + p) * (NP * 32) + q * 8;
 #pragma unroll
     for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + k * 32) = out[k];
@@ -502,17 +435,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                         ++ps;
                     }
 #pragma unroll
-                    for (int pb = 0; pb < PB; ++pb) {
-                        if constexpr (NP == 3) {
-                            // smallest products first: (2,0) (1,1) (0,2) (1,0) (0,1) (0,0)
-                            acc[tp][pb] = mfma16x16x32<T>(w0[2], zc[pb][0], acc[tp][pb]);
-                            acc[tp][pb] = mfma16x16x32<T>(w0[1], zc[pb][1], acc[tp][pb]);
-                            acc[tp][pb] = mfma16x16x32<T>(w0[0], zc[pb][2], acc[tp][pb]);
-                            acc[tp][pb] = mfma16x16x32<T>(w0[1], zc[pb][0], acc[tp][pb]);
-                            acc[tp][pb] = mfma16x16x32<T>(w0[0], zc[pb][1], acc[tp][pb]);
-                        }
-                        acc[tp][pb] = mfma16x16x32<T>(w0[0], zc[pb][0], acc[tp][pb]);
-                    }
+                    for (int pb = 0; pb < PB; ++pb) acc[tp][pb] = mfma16x16x32_np<T, NP>(w0, zc[pb], acc[tp][pb]);
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                     for (int k = 0; k < NP; ++k) w0[k] = w1[k];
@@ -1016,9 +939,12 @@ weight_split_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *fl
         const int tt = u >> 6, l = u & 63, q = l >> 4, c = l & 15;
         float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = tile[tt][c][q * 8 + e];
+        for (int e = 0; e < 8; ++e) {
+            v[e] = tile[tt][c][q * 8 + e];
+            bad = bad || bf16_split_bad(v[e]);
+        }
         uint4 o[NP];
-        bad = pack_pieces<T, NP>(v, o) || bad;
+        pack8_16<T, NP>(v, o);
 #pragma unroll
         for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + (size_t)tt * (NP * 512) + k * 512 + l * 8) = o[k];
     }

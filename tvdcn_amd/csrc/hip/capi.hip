@@ -6,6 +6,7 @@
 #include <string>
 #include <cstring>
 #include <climits>
+#include <cmath>
 #include <algorithm>
 #include <atomic>
 #include <mutex>
@@ -240,7 +241,9 @@ tvdcn_status batch_block(const tvdcn_conv_desc *d, int64_t &block, ImageElems *e
 // Workspace sub-buffers (byte offsets into the caller's workspace).
 struct Layout {
     size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, wpart = 0, goff_acc = 0, gmask_acc = 0, yacc = 0;
-    size_t zs = 0, wsplit = 0, flag = 0;   // the windowed data gradient's 16-bit MFMA operands
+    size_t zs = 0, wsplit = 0;   // the windowed data gradient's 16-bit MFMA operands
+    size_t w16 = 0;              // the windowed forward's 16-bit weight
+    size_t flag = 0;             // operand flag: some fp32 operand too large or not finite for them
     size_t total = 0;
 };
 
@@ -263,13 +266,17 @@ Layout layout(const Plan &pl, bool backward) {
     };
     const size_t SENTINEL = (size_t)-1;
     L.xcl = L.wf = L.wd = L.cl_acc = L.wpart = L.goff_acc = L.gmask_acc = L.yacc = SENTINEL;
-    L.zs = L.wsplit = L.flag = SENTINEL;
+    L.zs = L.wsplit = L.w16 = L.flag = SENTINEL;
+    L.flag = take(align_up(sizeof(int)));
     // windowed data gradient (conv backward, transposed forward and backward): split operands
     auto take_split = [&]() {
         if (!pl.wn_s.ok) return;
         L.zs = take(align_up(pl.wn_s.zs_elems * 2));
         L.wsplit = take(align_up(pl.wn_s.ws_elems * 2));
-        L.flag = take(align_up(sizeof(int)));
+    };
+    // windowed forward (conv forward, transposed backward's input gradient)
+    auto take_w16 = [&]() {
+        if (pl.fw.ok && pl.fw.w16_elems) L.w16 = take(align_up(pl.fw.w16_elems * 2));
     };
     // fp32 output of a slice-split windowed forward when the output dtype is not fp32
     const bool split_acc = pl.fw.ok && pl.fw.ksplit > 1 && pl.dtype != kF32;
@@ -278,6 +285,7 @@ Layout layout(const Plan &pl, bool backward) {
         if (!pl.transposed) {
             L.xcl = take(cl_bytes);
             L.wf = take(wf_bytes);
+            take_w16();
             if (split_acc) L.yacc = take(yacc_bytes);
         } else {
             L.wd = take(wd_bytes);
@@ -290,6 +298,7 @@ Layout layout(const Plan &pl, bool backward) {
         take_split();
         if (pl.transposed) {
             L.wf = take(wf_bytes);
+            take_w16();
             if (split_acc) L.yacc = take(yacc_bytes);
         } else
             L.cl_acc = take(cl_bytes);
@@ -423,6 +432,27 @@ tvdcn_status check_forward_pointers(const tvdcn_conv_desc *desc, const void *off
 // tvdcn_deform_conv_forward_noalloc (the per-device scratch array). Every workspace byte the
 // kernels read is written first in the same call (the zero-filled accumulator by a fill kernel),
 // so the workspace may hold anything on entry.
+// The sampled side of the 16-bit forward loop: mask * bilinear(X) in bf16 pieces (fp32) needs
+// |X| < SAMPLED_LIMIT and |mask| < MASK_LIMIT (checked on the device into *flag); a sigmoid mask
+// activation bounds the mask by its scale, a softmax by 1.
+bool sampled16_host_ok(const Plan &pl, const tvdcn_conv_desc *desc) {
+    if (pl.dtype != kF32) return true;
+    if (desc->flags & TVDCN_FLAG_MASK_SIGMOID) return std::fabs(desc->mask_scale) < (double)MASK_LIMIT;
+    return true;
+}
+hipError_t check_sampled(const Plan &pl, const tvdcn_conv_desc *desc, const void *x_in_place, const void *mask,
+                         int *flag, hipStream_t s) {
+    const Geo &g = pl.g;
+    if (pl.dtype != kF32) return hipSuccess;
+    if (x_in_place != nullptr) {
+        const hipError_t e = launch_check_range(x_in_place, (size_t)g.B * g.Sn * g.C, SAMPLED_LIMIT, flag, s);
+        if (e != hipSuccess) return e;
+    }
+    if (mask != nullptr && !(desc->flags & (TVDCN_FLAG_MASK_SIGMOID | TVDCN_FLAG_MASK_SOFTMAX)))
+        return launch_check_range(mask, (size_t)g.B * g.mg * g.Kn * g.Pn, MASK_LIMIT, flag, s);
+    return hipSuccess;
+}
+
 tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const void *input, const void *weight,
                              const void *offset, const void *mask, const void *bias, void *output, void *workspace,
                              void *stream) {
@@ -434,23 +464,32 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int dt = pl.dtype;
     g_last_error.clear();
+    int *flag = static_cast<int *>(at(workspace, L.flag));
+    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, flag, 1, s));
     if (!pl.transposed) {
         void *xcl = at(workspace, L.xcl), *wf = at(workspace, L.wf);
+        void *w16 = pl.fw.ok && sampled16_host_ok(pl, desc) ? at(workspace, L.w16) : nullptr;
+        const void *x_in_place = nullptr;
         if (!(desc->flags & TVDCN_FLAG_CHANNELS_LAST))
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s, flag));
         else if (acc_is_storage(dt))
-            xcl = const_cast<void *>(input);   // already the kernels' layout and type
+            x_in_place = xcl = const_cast<void *>(input);   // already the kernels' layout and type
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, input, xcl, (size_t)g.B * g.Sn * g.C, s));
         if (pl.fw.ok) {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
+            if (w16 != nullptr) {
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout16(dt, g, pl.fw, weight, w16, flag, s));
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
+            }
             void *y32 = nullptr;
             if (pl.fw.ksplit > 1) {
                 y32 = dt == kF32 ? output : at(workspace, L.yacc);
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, y32, (size_t)g.B * g.M * g.Pn, s));
             }
             TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
-                         launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, bias, output, y32, s));
+                         launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, w16, flag, offset, mask, bias, output,
+                                        y32, s));
             if (pl.fw.ksplit > 1 && dt != kF32)
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, y32, output, (size_t)g.B * g.M * g.Pn, s));
         } else {
@@ -463,9 +502,7 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
         if (pl.wn_s.ok) {
             void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
-            int *flag = static_cast<int *>(at(workspace, L.flag));
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, flag, 1, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_split(dt, g, pl.wn_s, input, weight, zs, wsp, flag, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, input, wd, zs,
                                                                         wsp, flag, nullptr, offset, mask, ycl, nullptr,
@@ -506,19 +543,20 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
     const void *X = pl.transposed ? grad_out : input;
     {
         void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
+        int *flag = static_cast<int *>(at(workspace, L.flag));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, flag, 1, s));
         const bool cl_in = (desc->flags & TVDCN_FLAG_CHANNELS_LAST) != 0;   // conv only
+        const void *x_in_place = nullptr;
         if (!cl_in)
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s, flag));
         else if (direct)
-            xcl = const_cast<void *>(X);   // already the kernels' layout and type
+            x_in_place = xcl = const_cast<void *>(X);   // already the kernels' layout and type
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, X, xcl, (size_t)g.B * g.Sn * g.C, s));
         const bool coord = offset != nullptr || mask != nullptr;
         void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
-        int *flag = static_cast<int *>(at(workspace, L.flag));
         if (pl.wn_s.ok) {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, flag, 1, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_split(dt, g, pl.wn_s, Z, weight, zs, wsp, flag, s));
         } else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
@@ -549,14 +587,20 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         } else {
             void *wf = at(workspace, L.wf);
             if (pl.fw.ok) {
+                void *w16 = sampled16_host_ok(pl, desc) ? at(workspace, L.w16) : nullptr;
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
+                if (w16 != nullptr) {
+                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout16(dt, g, pl.fw, weight, w16, flag, s));
+                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
+                }
                 void *y32 = nullptr;
                 if (pl.fw.ksplit > 1) {
                     y32 = dt == kF32 ? grad_input : at(workspace, L.yacc);
                     TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, y32, (size_t)g.B * g.M * g.Pn, s));
                 }
                 TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
-                             launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, offset, mask, nullptr, grad_input, y32, s));
+                             launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, w16, flag, offset, mask, nullptr,
+                                            grad_input, y32, s));
                 if (pl.fw.ksplit > 1 && dt != kF32)
                     TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
                                  launch_acc_to_storage(dt, y32, grad_input, (size_t)g.B * g.M * g.Pn, s));

@@ -43,8 +43,9 @@ constexpr int GEO_WORDS = TM * BPX * 4;
 template <int DIM, typename T, int MB>
 __global__ void __launch_bounds__(NT)
 fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__restrict__ xcl,
-               const float *__restrict__ wf, const T *__restrict__ offset, const T *__restrict__ mask,
-               const T *__restrict__ bias, T *__restrict__ y, float *__restrict__ y32) {
+               const float *__restrict__ wf, const uint16_t *__restrict__ w16, const int *flag,
+               const T *__restrict__ offset, const T *__restrict__ mask, const T *__restrict__ bias,
+               T *__restrict__ y, float *__restrict__ y32) {
     constexpr int NC = 1 << DIM;
     constexpr int BMR = MB * 16;
     constexpr int XQ = xq_of(MB);
@@ -67,6 +68,8 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     const int grp = L / n_sp;
     const bool deformable = offset != nullptr;
     const int slices = (g.Cg + BC - 1) / BC;
+    // the 16-bit loop (1D / 2D) when its weight was laid out and (fp32) no operand was flagged
+    const bool use16_flag = DIM < 3 && w16 != nullptr && (flag == nullptr || *flag == 0);
     const int cs_lo = ks * fw.slices_per, cs_hi = min(slices, cs_lo + fw.slices_per);
 
     Tile tile;
@@ -206,6 +209,86 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
         }
     };
 
+    // ---- 16-bit pass (1D / 2D): steps of (slice, tap pair) on 16x16x32 MFMAs. Lane (row
+    //      l % 16, K group q = l / 16) holds at e = 0..7 the value of channel 4q + e % 4 at tap
+    //      2j + e / 4 of the pair: its B fragment is the pair's two sampled quads (zero past the
+    //      pass), split into pieces for fp32 and rounded to T otherwise (the reference's columns
+    //      of a half-precision input are half). W16 holds the A fragments in the same K order.
+    //      Each row block's weight fragments are loaded one block ahead.
+    auto pass16 = [&](int t0, int ntaps) {
+        if constexpr (DIM < 3) {
+            constexpr int NP = npiece_of<T>();
+            const int npair = (ntaps + 1) >> 1;
+            const int nsteps = (cs_hi - cs_lo) * npair;
+            geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
+            const int nmb = fw.Mg_pad / 16;
+            const int pp0 = (t0 / wt.tpp) * fw.hp;
+            const uint16_t *wl = w16 + (size_t)mt * MB * (NP * 512) + lane * 8;
+            auto wptr16 = [&](int cs, int j) {
+                return wl + (((size_t)grp * slices + cs) * fw.pp + pp0 + j) * nmb * (NP * 512);
+            };
+            auto build_pair = [&](int cs, int j, uint4 (&bp)[PB][NP]) {
+                acc4 b0[PB], b1[PB];
+                build_b(cs, 2 * j, b0);
+                if (2 * j + 1 < ntaps) {
+                    build_b(cs, 2 * j + 1, b1);
+                } else {
+#pragma unroll
+                    for (int pb = 0; pb < PB; ++pb) b1[pb] = acc4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int pb = 0; pb < PB; ++pb) {
+                    const float v[8] = {b0[pb][0], b0[pb][1], b0[pb][2], b0[pb][3],
+                                        b1[pb][0], b1[pb][1], b1[pb][2], b1[pb][3]};
+                    pack8_16<T, NP>(v, bp[pb]);
+                }
+            };
+            auto load_w16 = [&](const uint16_t *p, uint4 (&f)[NP]) {
+#pragma unroll
+                for (int k = 0; k < NP; ++k) f[k] = *reinterpret_cast<const uint4 *>(p + k * 512);
+            };
+            // MFMAs of one step; block mb + 1's fragments (the next step's block 0 at the end)
+            // are loaded before block mb's MFMAs
+            auto mfma_pair = [&](const uint4 (&bv)[PB][NP], uint4 (&wa)[2][NP], const uint16_t *pcur,
+                                 const uint16_t *pnext) {
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    load_w16(mb + 1 < MB ? pcur + (size_t)(mb + 1) * (NP * 512) : pnext, wa[(mb + 1) & 1]);
+#pragma unroll
+                    for (int pb = 0; pb < PB; ++pb)
+                        acc[mb][pb] = mfma16x16x32_np<T, NP>(wa[mb & 1], bv[pb], acc[mb][pb]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            };
+            static_assert(MB % 2 == 0, "row blocks in pairs: the next step's block 0 lands in slot 0");
+            // step k: its B fragments are built, then its MFMAs run (the LDS latency of the
+            // sampling is covered by the other wave of the SIMD)
+            uint4 wa[2][NP], bv[PB][NP];
+            prefetch_x(cs_lo);
+            load_w16(wptr16(cs_lo, 0), wa[0]);
+            __syncthreads();   // previous pass done with the tables
+            open_slice(cs_lo, t0, ntaps);
+            __syncthreads();
+            // the next slice's X window is requested two pair steps before it is needed
+            const int pf_j = max(npair - 2, 0);
+            for (int k = 0; k < nsteps; ++k) {
+                const bool more = k + 1 < nsteps;
+                const int kn = k + 1, csn_r = kn / npair, jn = kn - csn_r * npair;
+                const int cs_r = k / npair, j = k - cs_r * npair;
+                const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
+                if (j == pf_j && cs + 1 < cs_hi) prefetch_x(cs + 1);
+                build_pair(cs, j, bv);
+                const uint16_t *pcur = wptr16(cs, j);
+                mfma_pair(bv, wa, pcur, more ? wptr16(csn, jn) : pcur);
+                if (more && jn == 0) {
+                    __syncthreads();   // every wave done reading the current window
+                    open_slice(csn, t0, ntaps);
+                    __syncthreads();
+                }
+            }
+        }
+    };
+
     if constexpr (DIM == 3) {
         // 3D: taps in groups of four, lane row q sampling tap 4 * group + q at its pixel for
         // all 16 channels of the slice (the corner geometry formed once per (pixel, tap)
@@ -272,6 +355,8 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 }
             }
         }
+    } else if (use16_flag) {
+        for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) pass16(t0, min(wt.tpp, g.Kn - t0));
     } else {
         for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
             const int ntaps = min(wt.tpp, g.Kn - t0);
@@ -358,9 +443,48 @@ __global__ void fwd_win_weight_kernel(const T *__restrict__ w, float *__restrict
     }
 }
 
+// weight (M, Cg, Kn) -> W16[G][slices][pp][Mg_pad / 16][NP][64 lanes][8]: per (slice, tap pair j
+// of pass p, 16-row block) the 16x16x32 A fragments: lane l = m % 16 + 16 q holds at e = 0..7
+// W[m][slice * 16 + 4 q + e % 4] at tap p * tpp + 2 j + e / 4 (zero past the pass, Mg, Cg); fp32
+// as three bf16 pieces (*flag set for a value bad for the split), fp16 / bf16 as they are
+template <typename T, int NP>
+__global__ void __launch_bounds__(256)
+fwd_w16_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, int G, int Mg, int Cg, int Kn, int slices,
+               int nmb, int tpp, int hp, int pp) {
+    const size_t total = (size_t)G * slices * pp * nmb * 64;
+    bool bad = false;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int l = (int)(i & 63);
+        size_t r = i >> 6;
+        const int mb = (int)(r % nmb);
+        r /= nmb;
+        const int pq = (int)(r % pp);
+        r /= pp;
+        const int cs = (int)(r % slices);
+        const int grp = (int)(r / slices);
+        const int pass = pq / hp, j = pq - pass * hp;
+        const int tf = pass * tpp, ntp = min(tpp, Kn - tf);
+        const int m = mb * 16 + (l & 15), q = l >> 4;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int tl = 2 * j + (e >> 2), c = cs * BC + 4 * q + (e & 3);
+            v[e] = (tl < ntp && m < Mg && c < Cg) ? to_acc<float>(w[(((size_t)grp * Mg + m) * Cg + c) * Kn + tf + tl]) : 0.f;
+            bad = bad || bf16_split_bad(v[e]);
+        }
+        uint4 o[NP];
+        pack8_16<T, NP>(v, o);
+        uint16_t *dst = out + ((((size_t)grp * slices + cs) * pp + pq) * nmb + mb) * (NP * 512) + l * 8;
+#pragma unroll
+        for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + k * 512) = o[k];
+    }
+    if (NP == 3 && bad) atomicOr(flag, 1);
+}
+
 template <int DIM, typename T, int MB>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
-                    const void *offset, const void *mask, const void *bias, void *y, void *y32, hipStream_t s) {
+                    const void *w16, const int *flag, const void *offset, const void *mask, const void *bias, void *y,
+                    void *y32, hipStream_t s) {
     auto kern = fwd_win_kernel<DIM, T, MB>;
     const size_t lds = ((size_t)GEO_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
     static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
@@ -368,29 +492,32 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const vo
         return e;
     const long long blocks = (long long)g.G * g.B * wt.ntile[0] * wt.ntile[1] * wt.ntile[2] * fw.m_tiles * fw.ksplit;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, wt, fw, static_cast<const float *>(xcl),
-                       static_cast<const float *>(wf), static_cast<const T *>(offset), static_cast<const T *>(mask),
+                       static_cast<const float *>(wf), static_cast<const uint16_t *>(w16), flag,
+                       static_cast<const T *>(offset), static_cast<const T *>(mask),
                        static_cast<const T *>(bias), static_cast<T *>(y), static_cast<float *>(y32));
     return hipGetLastError();
 }
 
 template <int DIM, typename T>
 hipError_t launch_m(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
-                    const void *offset, const void *mask, const void *bias, void *y, void *y32, hipStream_t s) {
+                    const void *w16, const int *flag, const void *offset, const void *mask, const void *bias, void *y,
+                    void *y32, hipStream_t s) {
     // 3D: 64-row tiles only (the trilinear sampler needs the registers)
     if constexpr (DIM < 3) {
-        if (fw.mb == 8) return launch_k<DIM, T, 8>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
+        if (fw.mb == 8) return launch_k<DIM, T, 8>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
     }
-    if (fw.mb == 4) return launch_k<DIM, T, 4>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
+    if (fw.mb == 4) return launch_k<DIM, T, 4>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
     return hipErrorInvalidValue;
 }
 
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
-                    const void *offset, const void *mask, const void *bias, void *y, void *y32, hipStream_t s) {
+                    const void *w16, const int *flag, const void *offset, const void *mask, const void *bias, void *y,
+                    void *y32, hipStream_t s) {
     switch (dim) {
-        case 1: return launch_m<1, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
-        case 2: return launch_m<2, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
-        case 3: return launch_m<3, T>(g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
+        case 1: return launch_m<1, T>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
+        case 2: return launch_m<2, T>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
+        case 3: return launch_m<3, T>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
     }
     return hipErrorInvalidValue;
 }
@@ -426,6 +553,12 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     // 3D samples taps in groups of four: passes of eight taps fill their groups (27 taps:
     // 8, 8, 8, 3 = seven groups, where passes of nine would take nine)
     if (dim == 3 && g.Kn > WIN_TMAX) wt.tpp = 8;
+    // 16-bit weight fragments (1D / 2D)
+    f.npiece = base.npiece;
+    f.tpp = wt.tpp;
+    f.hp = (wt.tpp + 1) / 2;
+    f.pp = (g.Kn + wt.tpp - 1) / wt.tpp * f.hp;
+    f.w16_elems = dim < 3 ? (size_t)g.G * slices * f.pp * (f.Mg_pad / 16) * f.npiece * 512 : 0;
     f.ok = true;
     return f;
 }
@@ -449,14 +582,37 @@ hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, cons
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_fwd_win_layout16(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *w16, int *flag,
+                                   hipStream_t s) {
+    if (fw.w16_elems == 0) return hipSuccess;
+    const int slices = fw.Cg_pad / BC;
+    const size_t n = fw.w16_elems / (fw.npiece * 8);   // threads: one per lane fragment
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+#define TVDCN_FW16(T, NP)                                                                                              \
+    hipLaunchKernelGGL((fwd_w16_kernel<T, NP>), dim3((unsigned)blocks), dim3(256), 0, s, static_cast<const T *>(w),    \
+                       static_cast<uint16_t *>(w16), flag, g.G, g.Mg, g.Cg, g.Kn, slices, fw.Mg_pad / 16, fw.tpp,    \
+                       fw.hp, fw.pp);                                                                                  \
+    return hipGetLastError();
+    switch (dtype) {
+        case kF32: { TVDCN_FW16(float, 3) }
+        case kF16: { TVDCN_FW16(__half, 1) }
+        case kBF16: { TVDCN_FW16(__hip_bfloat16, 1) }
+    }
+#undef TVDCN_FW16
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,
-                          const void *wf, const void *offset, const void *mask, const void *bias, void *y, void *y32,
-                          hipStream_t s) {
+                          const void *wf, const void *w16, const int *flag, const void *offset, const void *mask,
+                          const void *bias, void *y, void *y32, hipStream_t s) {
     if (fw.ksplit != 1 && y32 == nullptr) return hipErrorInvalidValue;
     switch (dtype) {
-        case kF32: return launch_d<float>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
-        case kF16: return launch_d<__half>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
-        case kBF16: return launch_d<__hip_bfloat16>(dim, g, wt, fw, xcl, wf, offset, mask, bias, y, y32, s);
+        case kF32: return launch_d<float>(dim, g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
+        case kF16: return launch_d<__half>(dim, g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
+        case kBF16:
+            return launch_d<__hip_bfloat16>(dim, g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
     }
     return hipErrorInvalidValue;
 }

@@ -93,6 +93,10 @@ struct FwdWin {
                          // partials are added onto a zeroed fp32 output (y32)
     int slices_per;      // 16-channel slices per share
     int Mg_pad, Cg_pad;  // padded weight layout Wf[G][Kn][Mg_pad][Cg_pad]
+    // 16x16x32 MFMAs over (tap pair, 16 channels) steps (1D / 2D): the weight as
+    // W16[G][slices][pp][Mg_pad / 16][npiece][512] 16-bit values, pp = passes x hp tap pairs
+    int tpp, hp, pp, npiece;   // taps per pass, tap pairs per pass, pairs, pieces per value
+    size_t w16_elems;    // 0: no 16-bit path
 };
 
 FwdTiles plan_fwd(const Geo &g, int dtype);
@@ -112,7 +116,16 @@ DataTiles plan_data(const Geo &g, int dtype);
 WeightTiles plan_weight(const Geo &g, int dtype);
 
 // layout / elementwise helpers (prep.hip)
-hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s);
+// (flag: when not null, fp32 values not below SAMPLED_LIMIT in magnitude set *flag)
+hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s,
+                                   int *flag = nullptr);
+// 16-bit MFMA operands of the sampled side (forward, weight gradient): the sampled values are
+// mask * bilinear(X), below 2^126 (and so within bf16's range) when |X| < SAMPLED_LIMIT and
+// |mask| < MASK_LIMIT; larger or non-finite values send the launch to its fp32 MFMA loop.
+constexpr float SAMPLED_LIMIT = 0x1p96f;
+constexpr float MASK_LIMIT = 0x1p30f;
+// *flag |= some fp32 value of v[0 .. n) is not below limit in magnitude (or is nan)
+hipError_t launch_check_range(const void *v, size_t n, float limit, int *flag, hipStream_t s);
 hipError_t launch_from_channels_last(int dtype, const void *xcl, void *x, const void *bias, int B, int C, int Sn,
                                      hipStream_t s);
 hipError_t launch_weight_fwd_layout(int dtype, const Geo &g, const void *w, void *wf, int Mg_pad, int Cg_pad,
@@ -137,9 +150,13 @@ hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTil
                                   hipStream_t s);
 // weight -> the windowed forward's fragment-major layout (fwd_win.hip)
 hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *wp, hipStream_t s);
+// the weight as W16 (fp32: three bf16 pieces; *flag set for a value bad for the split)
+hipError_t launch_fwd_win_layout16(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *w16, int *flag,
+                                   hipStream_t s);
+// w16 / flag: the 16-bit weight and the operand flag (w16 null, or *flag set: the fp32 loop)
 hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,
-                          const void *wf, const void *offset, const void *mask, const void *bias, void *y, void *y32,
-                          hipStream_t s);
+                          const void *wf, const void *w16, const int *flag, const void *offset, const void *mask,
+                          const void *bias, void *y, void *y32, hipStream_t s);
 hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t, bool scatter, bool coord,
                            const void *z, const void *wd, const void *xcl, const void *offset, const void *mask,
                            void *gx_cl, void *goff, void *gmask, hipStream_t s);

@@ -15,17 +15,22 @@ constexpr int TT = 64;   // transpose tile
 
 // x [B][C][S] (T) -> xcl [B][S][C] (A); 64 x 64 tile through LDS, 256 threads
 template <typename T, typename A>
-__global__ void __launch_bounds__(256) to_cl_kernel(const T *__restrict__ x, A *__restrict__ xcl, int C, int S) {
+__global__ void __launch_bounds__(256) to_cl_kernel(const T *__restrict__ x, A *__restrict__ xcl, int C, int S,
+                                                    int *flag) {
     __shared__ A tile[TT][TT + 1];
     const int b = blockIdx.z;
     const int s0 = blockIdx.x * TT, c0 = blockIdx.y * TT;
     const T *xb = x + (size_t)b * C * S;
     A *ob = xcl + (size_t)b * C * S;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    bool big = false;
     for (int r = ty; r < TT; r += 4) {
         const int c = c0 + r, s = s0 + tx;
-        tile[r][tx] = (c < C && s < S) ? to_acc<A>(xb[(size_t)c * S + s]) : A(0);
+        const A v = (c < C && s < S) ? to_acc<A>(xb[(size_t)c * S + s]) : A(0);
+        if constexpr (std::is_same<A, float>::value) big = big || !(fabsf(v) < SAMPLED_LIMIT);
+        tile[r][tx] = v;
     }
+    if (flag != nullptr && big) atomicOr(flag, 1);
     __syncthreads();
     for (int r = ty; r < TT; r += 4) {
         const int s = s0 + r, c = c0 + tx;
@@ -178,13 +183,14 @@ hipError_t by_dtype(int dtype, F &&f) {
 
 }  // namespace
 
-hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s) {
+hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s,
+                                   int *flag) {
     return by_dtype(dtype, [&](auto tv, auto av) {
         using T = decltype(tv);
         using A = decltype(av);
         dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B);
         hipLaunchKernelGGL((to_cl_kernel<T, A>), grid, dim3(256), 0, s, static_cast<const T *>(x),
-                           static_cast<A *>(xcl), C, Sn);
+                           static_cast<A *>(xcl), C, Sn, flag);
         return hipGetLastError();
     });
 }
@@ -276,6 +282,22 @@ hipError_t launch_mask_sigmoid_grad(int dtype, const void *logits, void *gmask_a
                            static_cast<const T *>(logits), static_cast<A *>(gmask_acc), scale, n);
         return hipGetLastError();
     });
+}
+
+// *flag |= any of v[0 .. n) is not below `limit` in magnitude (nan included)
+__global__ void __launch_bounds__(256) check_range_kernel(const float *__restrict__ v, size_t n, float limit,
+                                                          int *flag) {
+    bool big = false;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        big = big || !(fabsf(v[i]) < limit);
+    if (big) atomicOr(flag, 1);
+}
+
+hipError_t launch_check_range(const void *v, size_t n, float limit, int *flag, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(check_range_kernel, dim3(grid_for(n)), dim3(256), 0, s, static_cast<const float *>(v), n, limit,
+                       flag);
+    return hipGetLastError();
 }
 
 hipError_t launch_storage_to_acc(int dtype, const void *x, void *acc, size_t n, hipStream_t s) {

@@ -525,5 +525,93 @@ __device__ __forceinline__ AxisW<DIM, float> record_weights(const Geo &g, const 
     return axis_weights<DIM, float>(g, pt, deformable);
 }
 
+
+// ---------------------------------------------------------------------------
+// 16-bit MFMA operands. v_mfma_f32_16x16x32_bf16 / _f16: lane l supplies K = 8 (l / 16) ..
+// + 7 of row (A) / column (B) l % 16 as eight 16-bit values in four dwords (the lower K in
+// the low half); the 16x16 result has the layout of the 16x16x4 fp32 MFMA. fp32 operands
+// go in as three bf16 pieces each: p0 = bf16(v), p1 = bf16(v - p0), p2 = bf16(v - p0 - p1)
+// (nearest, ties to even; the residuals are exact in fp32), so v = p0 + p1 + p2 + r with
+// |r| <= 2^-27 |v|. Of the nine cross products p_i q_j, the six with i + j <= 2 are summed;
+// the three left out and both residuals are below 2^-25 |v w| together, under fp32's own
+// rounding of one multiply-add. An fp32 value is bad for this when it is not finite or
+// rounds past the largest bf16; fp16 / bf16 operands go in as they are.
+// ---------------------------------------------------------------------------
+template <typename T> constexpr int npiece_of() { return std::is_same<T, float>::value ? 3 : 1; }
+
+__device__ __forceinline__ bool bf16_split_bad(float v) {
+    return (__float_as_uint(v) & 0x7FFFFFFFu) >= 0x7F7F8000u;
+}
+
+// the pieces of two values, packed two per dword (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ void split3_pk(float a, float b, uint32_t (&w)[3]) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const b2 h = {(__bf16)a, (__bf16)b};
+        w[k] = __builtin_bit_cast(uint32_t, h);
+        a -= (float)h[0];
+        b -= (float)h[1];
+    }
+}
+
+// two values rounded to the 16-bit type T (fp16 or bf16), packed
+template <typename T> __device__ __forceinline__ uint32_t pack2_16(float a, float b) {
+    if constexpr (std::is_same<T, __half>::value) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 h = {(_Float16)a, (_Float16)b};
+        return __builtin_bit_cast(uint32_t, h);
+    } else {
+        typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+        const b2 h = {(__bf16)a, (__bf16)b};
+        return __builtin_bit_cast(uint32_t, h);
+    }
+}
+
+// eight values of a lane as NP 16-bit operand fragments (pieces for fp32, T's values otherwise)
+template <typename T, int NP>
+__device__ __forceinline__ void pack8_16(const float (&v)[8], uint4 (&out)[NP]) {
+    uint32_t w[NP][4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        if constexpr (NP == 3) {
+            uint32_t p[3];
+            split3_pk(v[e], v[e + 1], p);
+#pragma unroll
+            for (int k = 0; k < 3; ++k) w[k][e >> 1] = p[k];
+        } else {
+            w[0][e >> 1] = pack2_16<T>(v[e], v[e + 1]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NP; ++k) out[k] = uint4{w[k][0], w[k][1], w[k][2], w[k][3]};
+}
+
+// D += A * B on one 16x16x32 MFMA: fp16 operands for T = fp16, bf16 otherwise
+template <typename T> __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
+    if constexpr (std::is_same<T, __half>::value) {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+    } else {
+        typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b), c, 0, 0,
+                                                        0);
+    }
+}
+
+// acc += the split product of A and B fragments (NP pieces each): the six products with
+// i + j <= 2, smallest first, for fp32; the one product otherwise
+template <typename T, int NP>
+__device__ __forceinline__ f32x4 mfma16x16x32_np(const uint4 (&a)[NP], const uint4 (&b)[NP], f32x4 c) {
+    if constexpr (NP == 3) {
+        c = mfma16x16x32<T>(a[2], b[0], c);
+        c = mfma16x16x32<T>(a[1], b[1], c);
+        c = mfma16x16x32<T>(a[0], b[2], c);
+        c = mfma16x16x32<T>(a[1], b[0], c);
+        c = mfma16x16x32<T>(a[0], b[1], c);
+    }
+    return mfma16x16x32<T>(a[0], b[0], c);
+}
+
 }  // namespace win
 }  // namespace tvdcn_hip
