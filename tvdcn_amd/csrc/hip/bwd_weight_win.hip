@@ -58,12 +58,15 @@ size_t fixed_words(const Geo &g, int tpp) {
                                : WShape<WIN_TMAX, 32>::GEO_WORDS + WShape<WIN_TMAX, 32>::SBUF_WORDS;
 }
 
-// FULL: every pass uses all TM tap slots (no per-tap guards)
-template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
+// FULL: every pass uses all TM tap slots (no per-tap guards). USE16: the instantiation with the
+// 16x16x32 MFMA chunks (1D / 2D); it runs when the operand flag is clear and the fp32 one when it
+// is set (both are launched; each returns at once when the flag selects the other), so that
+// neither loop's registers weigh on the other's.
+template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV, bool USE16>
 __global__ void __launch_bounds__(NT)
 bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const T *__restrict__ z,
                       const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
-                      float *__restrict__ part) {
+                      float *__restrict__ part, const int *flag) {
     using SH = WShape<TMV, KPV>;
     constexpr int TM = SH::TM, KP = SH::KP, NCH = SH::NCH, NH = SH::NH, SS = SH::SS;
     constexpr int GEO_WORDS = SH::GEO_WORDS, SBUF_WORDS = SH::SBUF_WORDS;
@@ -93,6 +96,8 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     const bool deformable = offset != nullptr;
     const int tg = wave / (NW / TG);                     // this wave's tap group
     const int mrow = mt * BMW + (wave % (NW / TG)) * (MB * 16);   // first row of this wave
+    constexpr bool use16 = USE16 && DIM < 3;
+    if (flag != nullptr && (*flag == 0) != use16) return;   // the other instantiation's launch
 
     if constexpr (DIM == 3) {
         if (tid < XS) xwin[wt.cells * XS + tid] = 0.f;   // zero cell of the 3D corner reads
@@ -125,6 +130,40 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
             fill_xwin(g, wt, tile, xb, xwin, tid, NT);
             __syncthreads();
 
+            // mask * sampled value of channels 4 sq .. + 3 at (tap tl, tile pixel i) (1D / 2D)
+            auto sample_quad = [&](int tl, int i) -> acc4 {
+                const acc4 r = geo[tl * BPX + i];
+                const int fc = fast_cell<DIM>(r);
+                const float mk = rec_mask<DIM>(r);
+                acc4 sv;
+                if (fc >= 0) {
+                    // every corner cell is in the window (zeros outside the grid)
+                    sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * sq, r, mk);
+                } else {
+                    const AxisW<DIM, float> aw = record_weights<DIM>(g, r, deformable);
+                    sv = acc4{0.f, 0.f, 0.f, 0.f};
+                    if (aw.inside) {
+#pragma unroll
+                        for (int kk = 0; kk < NC; ++kk) {
+                            int idx;
+                            bool v;
+                            corner_at<DIM, float>(g, aw, kk, idx, v);
+                            if (!v) continue;
+                            const int cell = tile.corner_cell<DIM>(wt, aw, kk);
+                            // LDS read unconditional (clamped), global read in its own branch:
+                            // the two address spaces are never merged into one pointer
+                            acc4 x = *reinterpret_cast<const acc4 *>(xwin + max(cell, 0) * XS + 4 * sq);
+                            if (cell < 0) {
+                                x = acc4{0.f, 0.f, 0.f, 0.f};
+                                if (cq_ok) x = *reinterpret_cast<const acc4 *>(xb + (size_t)idx * g.C + 4 * sq);
+                            }
+                            sv += corner_weight<DIM, float>(aw, kk) * x;
+                        }
+                    }
+                    sv *= mk;
+                }
+                return sv;
+            };
             // S[tap][c][px] of chunk k into buffer bf
             auto build_s = [&](int k, int bf) {
                 float *dst = sbuf + bf * (TM * BC * SS);
@@ -149,36 +188,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                     return;
                 }
                 for (int tl = st0; tl < ntaps; tl += SSTEP) {
-                    const acc4 r = geo[tl * BPX + i];
-                    const int fc = fast_cell<DIM>(r);
-                    const float mk = rec_mask<DIM>(r);
-                    acc4 sv;
-                    if (fc >= 0) {
-                        // every corner cell is in the window (zeros outside the grid)
-                        sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * sq, r, mk);
-                    } else {
-                        const AxisW<DIM, float> aw = record_weights<DIM>(g, r, deformable);
-                        sv = acc4{0.f, 0.f, 0.f, 0.f};
-                        if (aw.inside) {
-#pragma unroll
-                            for (int kk = 0; kk < NC; ++kk) {
-                                int idx;
-                                bool v;
-                                corner_at<DIM, float>(g, aw, kk, idx, v);
-                                if (!v) continue;
-                                const int cell = tile.corner_cell<DIM>(wt, aw, kk);
-                                // LDS read unconditional (clamped), global read in its own branch:
-                                // the two address spaces are never merged into one pointer
-                                acc4 x = *reinterpret_cast<const acc4 *>(xwin + max(cell, 0) * XS + 4 * sq);
-                                if (cell < 0) {
-                                    x = acc4{0.f, 0.f, 0.f, 0.f};
-                                    if (cq_ok) x = *reinterpret_cast<const acc4 *>(xb + (size_t)idx * g.C + 4 * sq);
-                                }
-                                sv += corner_weight<DIM, float>(aw, kk) * x;
-                            }
-                        }
-                        sv *= mk;
-                    }
+                    const acc4 sv = sample_quad(tl, i);
                     float *row = dst + (tl * BC + 4 * sq) * SS + sj;
 #pragma unroll
                     for (int v = 0; v < 4; ++v) row[v * SS] = sv[v];
@@ -238,7 +248,105 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                 }
             };
 
-            {
+            if (use16) {
+                // ---- 16-bit chunks: S16 [NP][TM * BC][SS16] (16-bit, single buffer) built from
+                //      the window, its values split into pieces once per value (fp32) or rounded
+                //      to T (the reference's columns of a half-precision input are half); per
+                //      32-pixel K block, A = Z[m][8 consecutive pixels of lane group q] (pieces
+                //      formed in registers), B = S16[tap][c][the same pixels]
+                constexpr int NP = npiece_of<T>();
+                constexpr int SS16 = KP + 8;
+                constexpr int KB = KP / 32;
+                static_assert(NP * TM * BC * SS16 * 2 <= SBUF_WORDS * 4, "the S16 tile fits the fp32 S buffers");
+                uint16_t *s16 = reinterpret_cast<uint16_t *>(sbuf);
+                auto build_s16 = [&](int k) {
+                    const int i = k * KP + sj;
+                    for (int tl = st0; tl < ntaps; tl += SSTEP) {
+                        const acc4 sv = sample_quad(tl, i);
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            uint16_t pc[NP];
+                            split_one16<T, NP>(sv[v], pc);
+#pragma unroll
+                            for (int kk = 0; kk < NP; ++kk)
+                                s16[((size_t)kk * TM * BC + tl * BC + 4 * sq + v) * SS16 + sj] = pc[kk];
+                        }
+                    }
+                };
+                // Z of K block kb of chunk k: pixels k * KP + 32 kb + 8 q .. + 7 (zero outside the grid)
+                auto load_a8 = [&](int k, int kb, float (&za)[MB][8]) {
+                    const int i0 = k * KP + 32 * kb + 8 * q;
+                    if (quad) {
+                        // the 8 pixels lie in one row of the box (box_x >= 16, 8-aligned), each
+                        // half of 4 wholly inside or outside the grid (P_x % 4 == 0)
+                        const int iz = i0 >> wt.lbxy, iy = (i0 >> wt.lbx) & (wt.box[1] - 1), ix = i0 & (wt.box[2] - 1);
+                        const int pz = tile.p0[0] + iz, py = tile.p0[1] + iy, px = tile.p0[2] + ix;
+                        const int p = (pz * g.P[1] + py) * g.P[2] + px;
+                        const bool row_ok = pz < g.P[0] && py < g.P[1];
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const bool ok = full || (row_ok && px + 4 * h < g.P[2]);
+#pragma unroll
+                            for (int mb = 0; mb < MB; ++mb) {
+                                Vec4<float> v{0.f, 0.f, 0.f, 0.f};
+                                if (ok) v = load4_t<float, T>(zrow[mb] + p + 4 * h);
+                                za[mb][4 * h] = v.x;
+                                za[mb][4 * h + 1] = v.y;
+                                za[mb][4 * h + 2] = v.z;
+                                za[mb][4 * h + 3] = v.w;
+                            }
+                        }
+                    } else {
+                        int pu[8];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) pu[u] = tile.pixel(g, wt, i0 + u);
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                            for (int u = 0; u < 8; ++u) za[mb][u] = pu[u] >= 0 ? to_acc<float>(zrow[mb][pu[u]]) : 0.f;
+                    }
+                };
+                float zc[KB][MB][8], zn[KB][MB][8];
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) load_a8(0, kb, zc[kb]);
+                for (int k = 0; k < NCH; ++k) {
+                    __syncthreads();   // every wave done with the previous chunk's S16 tile
+                    build_s16(k);
+                    const bool more = k + 1 < NCH;
+                    if (more) {
+#pragma unroll
+                        for (int kb = 0; kb < KB; ++kb) load_a8(k + 1, kb, zn[kb]);
+                    }
+                    __syncthreads();
+                    const uint16_t *sb = s16 + (size_t)(lane & 15) * SS16 + 8 * q;
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb) {
+                        uint4 za16[MB][NP];
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb) pack8_16<T, NP>(zc[kb][mb], za16[mb]);
+#pragma unroll
+                        for (int tp = 0; tp < TM; ++tp) {
+                            if ((FULL || tp < ntaps) && (TG == 1 || tp % TG == tg)) {
+                                uint4 bf[NP];
+#pragma unroll
+                                for (int kk = 0; kk < NP; ++kk)
+                                    bf[kk] = *reinterpret_cast<const uint4 *>(sb + ((size_t)kk * TM * BC + tp * BC) * SS16 + 32 * kb);
+#pragma unroll
+                                for (int mb = 0; mb < MB; ++mb)
+                                    acc[mb][tp] = mfma16x16x32_np<T, NP>(za16[mb], bf, acc[mb][tp]);
+                            }
+                        }
+                    }
+                    if (more) {
+#pragma unroll
+                        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) zc[kb][mb][e] = zn[kb][mb][e];
+                    }
+                }
+            } else {
                 acc4 za[NH][MB], zn[NH][MB];
 #pragma unroll
                 for (int h = 0; h < NH; ++h) load_a(0, h, za[h]);
@@ -295,12 +403,11 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     }
 }
 
-template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
-hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
-                    const void *offset, const void *mask, void *part, hipStream_t s) {
+template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV, bool USE16>
+hipError_t launch_k1(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
+                     const void *offset, const void *mask, void *part, const int *flag, hipStream_t s) {
     using SH = WShape<TMV, KPV>;
-    if (wt.tpp > TMV) return hipErrorInvalidValue;   // a pass must fit the tap slots
-    auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG, TMV, KPV>;
+    auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG, TMV, KPV, USE16>;
     const size_t lds =
         ((size_t)SH::GEO_WORDS + SH::SBUF_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
     static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
@@ -309,25 +416,42 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const
     const long long blocks = (long long)g.G * ww.n_split * ww.m_tiles * wt.c_tiles;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, wt, ww, static_cast<const T *>(z),
                        static_cast<const float *>(xcl), static_cast<const T *>(offset), static_cast<const T *>(mask),
-                       static_cast<float *>(part));
+                       static_cast<float *>(part), flag);
     return hipGetLastError();
+}
+
+// the fp32 instantiation, and (1D / 2D, with an operand flag) the 16-bit one beside it
+template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
+hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
+                    const void *offset, const void *mask, void *part, const int *flag, hipStream_t s) {
+    if (wt.tpp > TMV) return hipErrorInvalidValue;   // a pass must fit the tap slots
+    if constexpr (DIM < 3) {
+        if (flag != nullptr) {
+            const hipError_t e = launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, true>(g, wt, ww, z, xcl, offset, mask, part,
+                                                                                  flag, s);
+            if (e != hipSuccess) return e;
+        }
+    }
+    // (3D has no 16-bit instantiation: its fp32 one runs whatever the flag)
+    return launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, false>(g, wt, ww, z, xcl, offset, mask, part,
+                                                             DIM < 3 ? flag : nullptr, s);
 }
 
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
-                    const void *offset, const void *mask, void *part, hipStream_t s) {
+                    const void *offset, const void *mask, void *part, const int *flag, hipStream_t s) {
     const bool small = small_shape(g, wt.tpp);
     const int tm = small ? SMALL_TM : WIN_TMAX;
     const bool full = wt.tpp == tm && g.Kn % tm == 0;
     auto pick = [&](auto dim_tag) -> hipError_t {
         constexpr int D = decltype(dim_tag)::value;
-        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, s)
-                                    : launch_k<D, T, false, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, s);
+        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, s)
+                                    : launch_k<D, T, false, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, s);
         if (small)
-            return full ? launch_k<D, T, true, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, s)
-                        : launch_k<D, T, false, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, s);
-        return full ? launch_k<D, T, true, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, s)
-                    : launch_k<D, T, false, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, s);
+            return full ? launch_k<D, T, true, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, flag, s)
+                        : launch_k<D, T, false, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, flag, s);
+        return full ? launch_k<D, T, true, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, s)
+                    : launch_k<D, T, false, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, s);
     };
     switch (dim) {
         case 1: return pick(std::integral_constant<int, 1>());
@@ -372,12 +496,12 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
 
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
-                                 void *gw, bool accumulate, hipStream_t s) {
+                                 void *gw, bool accumulate, const int *flag, hipStream_t s) {
     hipError_t e = hipErrorInvalidValue;
     switch (dtype) {
-        case kF32: e = launch_d<float>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
-        case kF16: e = launch_d<__half>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
-        case kBF16: e = launch_d<__hip_bfloat16>(dim, g, wt, ww, z, xcl, offset, mask, part, s); break;
+        case kF32: e = launch_d<float>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, s); break;
+        case kF16: e = launch_d<__half>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, s); break;
+        case kBF16: e = launch_d<__hip_bfloat16>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, s); break;
     }
     if (e != hipSuccess) return e;
     return launch_weight_reduce(dtype, g, ww.n_split, part, gw, accumulate, s, ww.units_per_split, ww.n_spatial,

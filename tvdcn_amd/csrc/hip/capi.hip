@@ -554,6 +554,9 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, X, xcl, (size_t)g.B * g.Sn * g.C, s));
         const bool coord = offset != nullptr || mask != nullptr;
+        // the 16-bit loops of the sampled side (weight gradient; transposed: input gradient)
+        const bool sampled16 = sampled16_host_ok(pl, desc) && (pl.ww.ok || (pl.transposed && pl.fw.ok));
+        if (sampled16) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
         void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
         if (pl.wn_s.ok) {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
@@ -587,12 +590,10 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         } else {
             void *wf = at(workspace, L.wf);
             if (pl.fw.ok) {
-                void *w16 = sampled16_host_ok(pl, desc) ? at(workspace, L.w16) : nullptr;
+                void *w16 = sampled16 ? at(workspace, L.w16) : nullptr;
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
-                if (w16 != nullptr) {
+                if (w16 != nullptr)
                     TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout16(dt, g, pl.fw, weight, w16, flag, s));
-                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
-                }
                 void *y32 = nullptr;
                 if (pl.fw.ksplit > 1) {
                     y32 = dt == kF32 ? grad_input : at(workspace, L.yacc);
@@ -619,7 +620,7 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         if (pl.ww.ok)
             TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight_win(dt, pl.dim, g, pl.wn_w, pl.ww, Z, xcl, offset,
                                                                             mask, at(workspace, L.wpart), grad_weight,
-                                                                            accumulate_weight, s));
+                                                                            accumulate_weight, sampled16 ? flag : nullptr, s));
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,
                                                                         at(workspace, L.wpart), grad_weight,

@@ -171,9 +171,10 @@ hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles 
                                const void *z, const void *wchunks, const void *zs, const void *wsplit,
                                const int *flag, const void *xcl, const void *offset, const void *mask, void *gx_cl,
                                void *goff, void *gmask, hipStream_t s);
+// flag: the operand flag (null: the fp32 MFMA loop; set: the same)
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
-                                 void *gw, bool accumulate, hipStream_t s);
+                                 void *gw, bool accumulate, const int *flag, hipStream_t s);
 // gw (storage type, layout (M, Cg, Kn)) = sum over k_splits of part[ks][G][Kn][Mg][Cg]
 // dW = sum over splits of the partials; with units_per_split > 0 (windowed kernel) tap t sums only
 // the splits whose unit range meets its pass (t / tpp) over n_spatial tiles

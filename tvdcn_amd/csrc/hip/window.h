@@ -568,6 +568,23 @@ template <typename T> __device__ __forceinline__ uint32_t pack2_16(float a, floa
     }
 }
 
+// one value as its NP 16-bit pieces (fp32) or as T (fp16 / bf16)
+template <typename T, int NP>
+__device__ __forceinline__ void split_one16(float v, uint16_t (&p)[NP]) {
+    if constexpr (NP == 3) {
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const __bf16 h = (__bf16)v;
+            p[k] = __builtin_bit_cast(uint16_t, h);
+            v -= (float)h;
+        }
+    } else if constexpr (std::is_same<T, __half>::value) {
+        p[0] = __builtin_bit_cast(uint16_t, (_Float16)v);
+    } else {
+        p[0] = __builtin_bit_cast(uint16_t, (__bf16)v);
+    }
+}
+
 // eight values of a lane as NP 16-bit operand fragments (pieces for fp32, T's values otherwise)
 template <typename T, int NP>
 __device__ __forceinline__ void pack8_16(const float (&v)[8], uint4 (&out)[NP]) {
