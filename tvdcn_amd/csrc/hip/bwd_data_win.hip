@@ -205,8 +205,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     float *thr = reinterpret_cast<float *>(shift);
     int *bmax = shift + BC;                                    // [BC] largest |G * mask| (float bits, >= 0)
     unsigned *bexp = reinterpret_cast<unsigned *>(bmax + BC);  // [BC] exponent sums + (counts << 20)
+    // (xg: the offset / mask gradients read X from global memory; no X window)
+    const bool xg = COORD && wt.xglobal != 0;
     float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X window (COORD)
-    int *iwin = reinterpret_cast<int *>(xwin + (COORD ? wt.cells * XS : 0));   // [BC][cst] fixed point
+    int *iwin = reinterpret_cast<int *>(xwin + (COORD && !xg ? wt.cells * XS : 0));   // [BC][cst] fixed point
     const int cst = fix_stride(wt.cells);
 
     const int tid = threadIdx.x;
@@ -231,7 +233,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 
     // ---- per-tile LDS state: X window (read by the offset/mask gradients), zeroed
     //      fixed-point window (scatter)
-    if constexpr (COORD) fill_xwin(g, wt, tile, xb, xwin, tid, NT);
+    if constexpr (COORD) {
+        if (!xg) fill_xwin(g, wt, tile, xb, xwin, tid, NT);
+    }
     if constexpr (SCATTER) {
         for (int i = tid; i < BC * cst; i += NT) iwin[i] = 0;
         if (tid < BC) {
@@ -670,7 +674,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 #pragma unroll
                             for (int k = 0; k < 8; ++k) {
                                 if (k > 0 && !deformable) break;
-                                const acc4 x = corner_x3(g, wt, cr, k, xwin, mq, xb + mq, cq_ok);
+                                const acc4 x = corner_x3(g, wt, cr, k, xwin, mq, xb + mq, cq_ok, xg);
                                 const float gk = gv[0] * x[0] + gv[1] * x[1] + gv[2] * x[2] + gv[3] * x[3];
                                 const int bz = k >> 2, by = (k >> 1) & 1, bx = k & 1;
                                 const float wz = bz ? cr.fh[0] : 1.f - cr.fh[0];
@@ -798,7 +802,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                         for (int k = 0; k < NC; ++k) {
                             // LDS read unconditional (clamped), global read in its own branch
                             xv[k] = *reinterpret_cast<const acc4 *>(xwin + max(loc[k], 0) * XS + mq);
-                            if (loc[k] < 0) {
+                            if (loc[k] < 0 || xg) {
                                 xv[k] = acc4{0.f, 0.f, 0.f, 0.f};
                                 if (gidx[k] >= 0 && cq_ok)
                                     xv[k] = *reinterpret_cast<const acc4 *>(xb + (size_t)gidx[k] * g.C + mq);
@@ -952,7 +956,8 @@ weight_split_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *fl
 }
 
 template <bool SCATTER, bool COORD> size_t lds_bytes(const WinTiles &t) {
-    return ((size_t)FIXED_WORDS + (SCATTER ? (size_t)BC * fix_stride(t.cells) : 0) + (COORD ? (size_t)t.cells * XS : 0)) *
+    return ((size_t)FIXED_WORDS + (SCATTER ? (size_t)BC * fix_stride(t.cells) : 0) +
+            (COORD && !t.xglobal ? (size_t)t.cells * XS : 0)) *
            sizeof(float);
 }
 

@@ -69,6 +69,7 @@ struct Plan {
     WinTiles wn_s;   // windowed data-gradient plan, scatter + offset/mask gradients (conv backward)
     WinTiles wn_x;   // the same tiling, scatter only (transposed forward): a larger window
     WinTiles wn_c;   // the same tiling, offset/mask gradients only (transposed backward)
+    WinTiles wn_xg;  // 3D conv backward: one launch on the scatter window, X read from global memory
     bool data_split; // conv backward: scatter (wn_x) and offset/mask gradients (wn_c) as two
                      // launches, when the shared window of wn_s would be too small
     WeightTiles wt;
@@ -178,6 +179,8 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl, int64_t batch) {
     // (3D: the window grows with the cube of its extent); two launches recompute the
     // grad-columns contraction but each gets about twice the window
     pl.data_split = pl.wn_s.ok && pl.wn_s.R[2] < 2 && pl.wn_x.R[2] > pl.wn_s.R[2] && pl.wn_c.R[2] > pl.wn_s.R[2];
+    pl.wn_xg = pl.wn_x;
+    pl.wn_xg.xglobal = 1;
     pl.wt = plan_weight(g, pl.dtype);
     pl.wn_w = win_resize(pl.wn_s, g, pl.dim, weight_win_fixed_bytes(g, pl.dim, pl.wn_s.tpp), x_window_cell_bytes());
     pl.ww = plan_weight_win(g, pl.wn_w, pl.dim);
@@ -567,7 +570,12 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
             // channels-last grad_input of the accumulation type is accumulated in place
             void *gx_cl = cl_in && direct ? grad_input : at(workspace, L.cl_acc);
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
-            if (pl.wn_s.ok && coord && pl.data_split) {
+            if (pl.wn_s.ok && coord && pl.data_split && pl.dim == 3) {
+                // 3D: one launch on the scatter window, the offset / mask gradients reading X
+                // from global memory (cached), instead of two that each recompute the contraction
+                TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_xg, true, true, Z, wd, zs, wsp,
+                                                                            flag, xcl, offset, mask, gx_cl, goff, gmask, s));
+            } else if (pl.wn_s.ok && coord && pl.data_split) {
                 // two launches, each with the larger window its LDS share allows
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, Z, wd, zs, wsp,
                                                                             flag, xcl, offset, mask, gx_cl, nullptr, nullptr,

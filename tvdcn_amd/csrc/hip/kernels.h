@@ -62,6 +62,7 @@ struct WinTiles {
     size_t chunk_elems;  // floats of the re-laid-out weight
     // 16-bit MFMA operands of the data gradient (16x16x32 MFMAs over 32 GEMM-side channels per
     // step): fp32 tensors split into three bf16 pieces each, fp16 / bf16 tensors as they are
+    int xglobal;         // 3D only: offset / mask gradients read X from global memory, no X window
     int ms32;            // 32-channel steps of the GEMM side (zero padded)
     int npiece;          // 16-bit pieces per value: 3 (fp32), 1 (fp16 / bf16)
     size_t zs_elems;     // 16-bit elements of the split Z: [B][G][ms32][Pn][npiece][32]

@@ -203,8 +203,8 @@ struct Corners3 {
 // unconditional (clamped) and the global read sits in its own branch: the two address
 // spaces are never merged into one pointer.
 __device__ __forceinline__ acc4 corner_x3(const Geo &g, const WinTiles &wt, const Corners3 &cr, int k, const float *xwin,
-                                          int xq, const float *__restrict__ xgq, bool q_ok) {
-    const bool iw = cr.in_win(k);
+                                          int xq, const float *__restrict__ xgq, bool q_ok, bool xglobal = false) {
+    const bool iw = !xglobal && cr.in_win(k);
     acc4 x = *reinterpret_cast<const acc4 *>(xwin + (iw ? cr.cell(wt, k) : 0) * XS + xq);
     if (!iw) {
         x = acc4{0.f, 0.f, 0.f, 0.f};
