@@ -34,6 +34,20 @@ sys.path.insert(0, ROOT)
 METRIC = "deform_conv2d fwd+bwd ms and % HBM/MFMA roofline, B8 C256 64x64 k3 fp32"
 PEAK_FP32_MFMA = 157.3e12      # MI355X dense fp32 matrix, FLOP/s
 PEAK_HBM = 8.0e12              # MI355X HBM3E, B/s
+PEAK_16BIT_MFMA = 2.5e15       # MI355X dense fp16 / bf16 matrix, FLOP/s
+
+
+def mfma_path(family, dtype=torch.float32, dim=2):
+    """(MFMA instruction, MFMA products per algorithmic product, its dense peak) of a kernel family's
+    K loop: 16x16x32 MFMAs in the 1D/2D kernels and the data gradient, fp32 operands as three bf16
+    pieces of which six cross products are summed (fp32-accurate), fp16/bf16 operands as they are;
+    the 3D forward and weight gradient run fp32 16x16x4 MFMAs (operands widened). A launch whose fp32
+    operands were flagged (not finite, or too large for the pieces) runs the fp32 loop instead."""
+    if dim == 3 and family in ("gather_gemm", "weight_grad"):
+        return "v_mfma_f32_16x16x4_f32", 1, PEAK_FP32_MFMA
+    if dtype == torch.float32:
+        return "v_mfma_f32_16x16x32_bf16 (3 bf16 pieces per fp32 value, 6 products)", 6, PEAK_16BIT_MFMA
+    return f"v_mfma_f32_16x16x32_{'f16' if dtype == torch.float16 else 'bf16'}", 1, PEAK_16BIT_MFMA
 FAMILIES = ["layout", "gather_gemm", "data_grad", "weight_grad", "bias_grad", "mask_softmax"]
 
 
@@ -128,11 +142,13 @@ def gpu_bench(inp, steps, warmup):
     return time_path(params, fwd, gout, steps, warmup)
 
 
-def family_rooflines(kern, contraction_flops, grad_out_bytes, mask_bytes=0):
+def family_rooflines(kern, contraction_flops, grad_out_bytes, mask_bytes=0, dtype=torch.float32, dim=2):
     """Algorithmic work per launch of each kernel family against the bound that applies: each of
-    the three MFMA families performs one contraction of `contraction_flops` per launch; the bias
-    gradient reads grad_out once; mask_softmax reads + writes the mask (forward) or reads two
-    tensors and writes one (backward): 2.5 passes over `mask_bytes` on average."""
+    the three MFMA families performs one contraction of `contraction_flops` per launch (its fraction
+    taken of the fp32 MFMA peak, the arithmetic the path delivers; `mfma` names the instruction its
+    K loop runs on and `hw_frac` that instruction's use of its own dense peak); the bias gradient
+    reads grad_out once; mask_softmax reads + writes the mask (forward) or reads two tensors and
+    writes one (backward): 2.5 passes over `mask_bytes` on average."""
     work = {
         "gather_gemm": ("mfma", contraction_flops, PEAK_FP32_MFMA, "TFLOP/s"),
         "data_grad": ("mfma", contraction_flops, PEAK_FP32_MFMA, "TFLOP/s"),
@@ -149,6 +165,9 @@ def family_rooflines(kern, contraction_flops, grad_out_bytes, mask_bytes=0):
             out[name] = dict(avg_ms=round(k["avg_ms"], 4), launches=k["launches"], bound=bound,
                              achieved=round(achieved / scale, 2), peak=round(peak / scale, 1), unit=unit,
                              frac=round(achieved / peak, 4))
+            if bound == "mfma":
+                instr, products, hw_peak = mfma_path(name, dtype, dim)
+                out[name].update(mfma=instr, hw_frac=round(products * achieved / hw_peak, 4))
         else:
             # layout family: several small launches (channels-last copies, weight re-layouts, zero fills)
             out[name] = dict(avg_ms=round(k["avg_ms"], 4), launches=k["launches"], total_ms=round(k["total_ms"], 4))
@@ -249,9 +268,12 @@ def run_suite_case(n, dtype, steps, warmup, cpu=False):
     nb = 3 if c["tr"] else 2
     es = torch.finfo(dtype).bits // 8
     mask_bytes = es * (logits.numel() if logits is not None else 0)
-    roof = family_rooflines(kern, F, es * gout.numel(), mask_bytes)
+    roof = family_rooflines(kern, F, es * gout.numel(), mask_bytes, dtype=dtype, dim=dim)
     row = {
-        "case": c["name"], "dtype": str(dtype).replace("torch.", ""), "compute": "f32 (fp32 MFMA, fp32 accumulate)",
+        "case": c["name"], "dtype": str(dtype).replace("torch.", ""),
+        "compute": ("fp32-accurate: bf16 pieces on 16x16x32 MFMAs, fp32 accumulate" if dtype == torch.float32 else
+                    f"{str(dtype).replace('torch.', '')} operands on 16x16x32 MFMAs, fp32 accumulate") +
+                   ("; 3D forward and weight gradient: fp32 16x16x4 MFMAs" if dim == 3 else ""),
         "mask": "softmax of logits in the mask load" if logits is not None else "given",
         "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(step_ms - fwd_ms, 4), "fwd_bwd_ms": round(step_ms, 4),
         "gflop_fwd": round(F / 1e9, 3), "gflop_bwd": round(nb * F / 1e9, 3),
@@ -275,7 +297,7 @@ SUITE = [(2, torch.float32), (3, torch.float32), (4, torch.float32), (5, torch.f
 
 TRAFFIC_KERNELS = {"gather_gemm": "fwd_win_kernel<2, float, 8>",
                    "data_grad": "bwd_data_win_kernel<2, float, true, true>",
-                   "weight_grad": "bwd_weight_win_kernel<2, float, true, 2, 1>"}
+                   "weight_grad": "bwd_weight_win_kernel<2, float, true, 2, 1, 9, 32, true>"}
 
 
 def load_traffic(family):
@@ -409,7 +431,7 @@ def main():
     dom = max(mfma, key=lambda k: kern[k]["total_ms"])
     d = roof[dom]
     roofline = dict(kernel=dom, bound=d["bound"], achieved=d["achieved"], peak=d["peak"], unit=d["unit"],
-                    frac=d["frac"], traffic=load_traffic(dom))
+                    frac=d["frac"], traffic=load_traffic(dom), mfma=d.get("mfma"), hw_frac=d.get("hw_frac"))
 
     cpu = None
     if not args.no_cpu_baseline:
