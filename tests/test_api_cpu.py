@@ -6,7 +6,8 @@
 * shape inference and validation run on meta tensors, with the reference's error
   texts (checked side by side with the reference build when oracle/_ref exists);
 * autograd and double-backward behaviour, on meta tensors;
-* CPU tensors are refused loudly (no CPU fallback);
+* CPU tensors go to the CPU dispatch key (host kernels; tests/test_cpu_kernels.py checks their
+  numbers), GPU tensors never do;
 * the nn.Module wrappers and mask activations keep the reference's API and errors.
 """
 import ctypes
@@ -247,11 +248,20 @@ def test_dtype_mismatch_error():
                                           [0, 0], [1, 1], 1)
 
 
-def test_cpu_tensors_are_refused():
-    with pytest.raises(NotImplementedError, match="CPU"):
-        tvdcn.deform_conv2d(torch.rand(1, 2, 5, 5), torch.rand(2, 2, 3, 3), torch.rand(1, 18, 3, 3))
-    with pytest.raises(NotImplementedError, match="CPU"):
-        tvdcn.mask_softmax2d(torch.rand(1, 9, 3, 3), (3, 3))
+def test_cpu_key_registered_for_every_op():
+    """every schema has a CPU kernel (the reference registers CPU twins of its CUDA drivers,
+    ops/cpu/deform_conv2d_kernel.cpp:645) besides the CUDA (HIP) one"""
+    ops = ["deform_conv1d", "deform_conv2d", "deform_conv3d", "deform_conv_transpose1d", "deform_conv_transpose2d",
+           "deform_conv_transpose3d"]
+    names = ops + [f"_{o}_backward" for o in ops] + ["mask_softmax", "_mask_softmax_backward",
+                                                      "deform_conv_mask_activation",
+                                                      "_deform_conv_mask_activation_backward"]
+    for n in names:
+        for key in ("CPU", "CUDA", "Meta"):
+            assert torch._C._dispatch_has_kernel_for_dispatch_key(f"tvdcn::{n}", key), (n, key)
+    y = tvdcn.deform_conv2d(torch.rand(1, 2, 5, 5), torch.rand(2, 2, 3, 3), torch.rand(1, 18, 3, 3))
+    assert y.device.type == "cpu" and y.shape == (1, 2, 3, 3)
+    assert tvdcn.mask_softmax2d(torch.rand(1, 9, 3, 3), (3, 3)).device.type == "cpu"
 
 
 def test_meta_autograd_and_double_backward():

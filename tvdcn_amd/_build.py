@@ -5,7 +5,8 @@ Two shared objects are produced next to this file:
 * ``libtvdcn_hip.so`` -- the gfx950 HIP kernels behind the C ABI declared in
   ``include/tvdcn_hip.h`` (hipcc, one object per ``csrc/hip/*.hip``).
 * ``_C.so`` -- the PyTorch operator layer (``csrc/torch/ops.cpp``) that registers
-  the ``tvdcn_amd`` ops and calls the C ABI; links against ``libtvdcn_hip.so``.
+  the ``tvdcn`` ops and calls the C ABI (links against ``libtvdcn_hip.so``), with the
+  host-tensor (CPU key) kernels of ``csrc/torch/cpu_kernels.cpp``.
 
 Run ``python -m tvdcn_amd._build`` (or ``__graft_entry__.build()``). Objects go to
 ``tvdcn_amd/_build/`` and are rebuilt when their sources (or shared headers) change.
@@ -20,6 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 HIP_DIR = os.path.join(HERE, "csrc", "hip")
 TORCH_SRC = os.path.join(HERE, "csrc", "torch", "ops.cpp")
+CPU_SRC = os.path.join(HERE, "csrc", "torch", "cpu_kernels.cpp")
 INCLUDE = os.path.join(ROOT, "include")
 OBJ_DIR = os.path.join(HERE, "_build")
 HIP_LIB = os.path.join(HERE, "libtvdcn_hip.so")
@@ -44,6 +46,11 @@ def _hip_sources():
 def _headers():
     return [os.path.join(HIP_DIR, f) for f in os.listdir(HIP_DIR) if f.endswith(".h")] + \
         [os.path.join(INCLUDE, f) for f in os.listdir(INCLUDE) if f.endswith(".h")]
+
+
+def _torch_headers():
+    d = os.path.join(HERE, "csrc", "torch")
+    return [os.path.join(d, f) for f in os.listdir(d) if f.endswith(".h")]
 
 
 def _stale(target, deps):
@@ -94,23 +101,27 @@ def _torch_paths():
 def build_torch(force=False, verbose=False):
     import torch
     tdir, incs = _torch_paths()
-    obj = os.path.join(OBJ_DIR, "ops_torch.o")
     os.makedirs(OBJ_DIR, exist_ok=True)
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    if force or _stale(obj, [TORCH_SRC] + _headers()):
-        cmd = ["g++", "-O2", "-std=c++17", "-fPIC", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
-               "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-Wno-deprecated-declarations",
-               "-I", INCLUDE, "-I", os.path.join(ROCM, "include")]
-        for i in incs:
-            cmd += ["-isystem", i]
-        cmd += ["-c", TORCH_SRC, "-o", obj]
-        _run(cmd)
-        if verbose:
-            print("compiled", os.path.relpath(TORCH_SRC, ROOT), flush=True)
-    if force or _stale(TORCH_LIB, [obj, HIP_LIB]):
+    objs = []
+    for src, extra in ((TORCH_SRC, []), (CPU_SRC, ["-O3", "-fopenmp"])):
+        obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + "_torch.o")
+        objs.append(obj)
+        if force or _stale(obj, [src] + _headers() + _torch_headers()):
+            cmd = ["g++", "-O2", "-std=c++17", "-fPIC", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+                   "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-Wno-deprecated-declarations",
+                   "-I", INCLUDE, "-I", os.path.join(ROCM, "include")] + extra
+            for i in incs:
+                cmd += ["-isystem", i]
+            cmd += ["-c", src, "-o", obj]
+            _run(cmd)
+            if verbose:
+                print("compiled", os.path.relpath(src, ROOT), flush=True)
+    if force or _stale(TORCH_LIB, objs + [HIP_LIB]):
         libdir = os.path.join(tdir, "lib")
-        _run(["g++", "-shared", "-o", TORCH_LIB, obj, "-L", libdir, "-lc10", "-lc10_hip", "-ltorch",
-              "-ltorch_cpu", "-ltorch_hip", "-L", HERE, "-ltvdcn_hip",
+        # OpenMP from torch's own libgomp (the runtime ATen's parallel_for already uses)
+        _run(["g++", "-shared", "-o", TORCH_LIB] + objs + ["-L", libdir, "-lc10", "-lc10_hip", "-ltorch",
+              "-ltorch_cpu", "-ltorch_hip", "-lgomp", "-L", HERE, "-ltvdcn_hip",
               "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}"])
     return TORCH_LIB
 

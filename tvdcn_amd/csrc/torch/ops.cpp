@@ -1,9 +1,10 @@
 // PyTorch-ROCm operator layer of tvdcn_amd: the reference's twelve operator
 // schemas (plus mask_softmax), registered under the reference's `tvdcn` namespace with
-// CUDA (= HIP on ROCm), Meta, Autograd and Autocast kernels. The CUDA kernels
+// CUDA (= HIP on ROCm), CPU, Meta, Autograd and Autocast kernels. The CUDA kernels
 // validate, allocate outputs and workspace from the caching allocator, and call
-// the C ABI of libtvdcn_hip.so on the current HIP stream. There is no CPU
-// kernel: CPU tensors fail in the dispatcher, loudly.
+// the C ABI of libtvdcn_hip.so on the current HIP stream. The CPU kernels
+// (host tensors only; cpu_kernels.cpp) run the same validation and compute on the
+// host, as the reference's CPU key does (ops/cpu/deform_conv2d_kernel.cpp:645).
 //
 // Reference interface mirrored (paths relative to tvdcn/csrc/):
 //   schemas        ops/deform_conv{1,2,3}d.cpp, ops/deform_conv_transpose{1,2,3}d.cpp
@@ -29,6 +30,7 @@
 #include <string>
 #include <vector>
 
+#include "cpu_kernels.h"
 #include "tvdcn_hip.h"
 
 namespace tvdcn_amd {
@@ -401,6 +403,57 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_meta(
 }
 
 // ---------------------------------------------------------------------------
+// CPU key: same validation, host kernels (cpu_kernels.cpp); channels-last host inputs are
+// made NC<spatial>-contiguous first, as the reference does (cpu/deform_conv2d_kernel.cpp:114)
+// ---------------------------------------------------------------------------
+cpu::Operands cpu_operands(Problem &pr) {
+    dtype_code(pr.input.scalar_type());
+    if (pr.channels_last) {
+        pr.input = pr.input.contiguous();
+        pr.channels_last = false;
+        pr.desc.flags &= ~TVDCN_FLAG_CHANNELS_LAST;
+    }
+    return cpu::Operands{pr.desc, pr.out_size, pr.input, pr.weight, pr.offset, pr.mask, pr.bias};
+}
+
+Tensor forward_cpu(int dim, bool transposed, const Tensor &input, const Tensor &weight,
+                   const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
+                   at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding,
+                   at::IntArrayRef dilation, int64_t groups, const char *name, int64_t activation = 0,
+                   double mask_scale = 0.0) {
+    TORCH_CHECK(input.device().is_cpu(), name, ": expected a CPU tensor");
+    Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
+                              dilation, groups, name);
+    set_mask_activation(pr, activation, mask_scale);
+    Tensor output = cpu::forward(cpu_operands(pr));
+    if (pr.unbatched) output = output.squeeze(0);
+    return output;
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_cpu(
+    int dim, bool transposed, const Tensor &grad, const Tensor &input, const Tensor &weight,
+    const optional<Tensor> &offset, const optional<Tensor> &mask, const optional<Tensor> &bias,
+    at::IntArrayRef stride, at::IntArrayRef padding, at::IntArrayRef output_padding, at::IntArrayRef dilation,
+    int64_t groups, const char *name, int64_t activation = 0, double mask_scale = 0.0) {
+    TORCH_CHECK(input.device().is_cpu(), name, ": expected a CPU tensor");
+    Problem pr = make_problem(dim, transposed, input, weight, offset, mask, bias, stride, padding, output_padding,
+                              dilation, groups, name);
+    set_mask_activation(pr, activation, mask_scale);
+    Tensor g = grad.contiguous();
+    if (pr.unbatched) g = g.unsqueeze(0);
+    TORCH_CHECK(g.sizes() == at::IntArrayRef(out_shape(pr)), name, ": grad has shape ", g.sizes(), ", expected ",
+                at::IntArrayRef(out_shape(pr)));
+    TORCH_CHECK(g.scalar_type() == pr.input.scalar_type(), name, ": grad dtype must match input dtype");
+    auto r = cpu::backward(cpu_operands(pr), g);
+    if (pr.unbatched) {
+        std::get<0>(r) = std::get<0>(r).squeeze(0);
+        if (std::get<2>(r).defined()) std::get<2>(r) = std::get<2>(r).squeeze(0);
+        if (std::get<3>(r).defined()) std::get<3>(r) = std::get<3>(r).squeeze(0);
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------------------
 // autograd (ops/autograd/deform_conv2d_kernel.cpp:9-203): save the five tensors,
 // backward calls the `_..._backward` op, which itself refuses double backward.
 // ---------------------------------------------------------------------------
@@ -649,7 +702,27 @@ struct Kernels {
                              at::IntArrayRef d, int64_t g) {
         return forward_meta(DIM, TR, i, w, o, m, b, s, p, op, d, g, Names<DIM, TR>::short_name);
     }
+    static Tensor fwd_cpu_c(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                            const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef d,
+                            int64_t g) {
+        return forward_cpu(DIM, TR, i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g, Names<DIM, TR>::short_name);
+    }
+    static Tensor fwd_cpu_t(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const optional<Tensor> &m,
+                            const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                            at::IntArrayRef d, int64_t g) {
+        return forward_cpu(DIM, TR, i, w, o, m, b, s, p, op, d, g, Names<DIM, TR>::short_name);
+    }
     using G5 = std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor>;
+    static G5 bwd_cpu_c(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
+                        const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
+                        at::IntArrayRef d, int64_t g) {
+        return backward_cpu(DIM, TR, gr, i, w, o, m, b, s, p, at::IntArrayRef({0}), d, g, Names<DIM, TR>::short_name);
+    }
+    static G5 bwd_cpu_t(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
+                        const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
+                        at::IntArrayRef op, at::IntArrayRef d, int64_t g) {
+        return backward_cpu(DIM, TR, gr, i, w, o, m, b, s, p, op, d, g, Names<DIM, TR>::short_name);
+    }
     static G5 bwd_hip_c(const Tensor &gr, const Tensor &i, const Tensor &w, const optional<Tensor> &o,
                         const optional<Tensor> &m, const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p,
                         at::IntArrayRef d, int64_t g) {
@@ -745,6 +818,23 @@ Tensor mask_softmax_backward_hip(const Tensor &grad, const Tensor &y, int64_t K)
     return gx;
 }
 
+Tensor mask_softmax_cpu(const Tensor &x, int64_t K) {
+    TORCH_CHECK(x.device().is_cpu(), "mask_softmax: expected a CPU tensor");
+    int64_t B, G, S;
+    softmax_dims(x, K, B, G, S);
+    dtype_code(x.scalar_type());
+    return cpu::mask_softmax(x, B, G, K, S);
+}
+
+Tensor mask_softmax_backward_cpu(const Tensor &grad, const Tensor &y, int64_t K) {
+    TORCH_CHECK(y.device().is_cpu(), "mask_softmax: expected a CPU tensor");
+    int64_t B, G, S;
+    softmax_dims(y, K, B, G, S);
+    TORCH_CHECK(grad.sizes() == y.sizes() && grad.scalar_type() == y.scalar_type(),
+                "mask_softmax backward: grad must match the output");
+    return cpu::mask_softmax_backward(grad, y, B, G, K, S);
+}
+
 Tensor mask_softmax_meta(const Tensor &x, int64_t K) {
     int64_t B, G, S;
     softmax_dims(x, K, B, G, S);
@@ -819,6 +909,23 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> act_bwd_hip(const Tensor &gr,
                                                                double scale) {
     check_activation(act, scale);
     return backward_hip(act_dim(s), tr, gr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, kActName, act, scale);
+}
+
+Tensor act_fwd_cpu(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
+                   const optional<Tensor> &b, at::IntArrayRef s, at::IntArrayRef p, at::IntArrayRef op,
+                   at::IntArrayRef d, int64_t g, bool tr, int64_t act, double scale) {
+    check_activation(act, scale);
+    return forward_cpu(act_dim(s), tr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, kActName, act, scale);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> act_bwd_cpu(const Tensor &gr, const Tensor &i, const Tensor &w,
+                                                               const optional<Tensor> &o, const Tensor &m,
+                                                               const optional<Tensor> &b, at::IntArrayRef s,
+                                                               at::IntArrayRef p, at::IntArrayRef op,
+                                                               at::IntArrayRef d, int64_t g, bool tr, int64_t act,
+                                                               double scale) {
+    check_activation(act, scale);
+    return backward_cpu(act_dim(s), tr, gr, i, w, o, optional<Tensor>(m), b, s, p, op, d, g, kActName, act, scale);
 }
 
 Tensor act_fwd_meta(const Tensor &i, const Tensor &w, const optional<Tensor> &o, const Tensor &m,
@@ -1034,6 +1141,16 @@ TORCH_LIBRARY_IMPL(tvdcn, CUDA, m) {
     m.impl("_deform_conv_mask_activation_backward", TORCH_FN(tvdcn_amd::act_bwd_hip));
     m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_hip));
     m.impl("_mask_softmax_backward", TORCH_FN(tvdcn_amd::mask_softmax_backward_hip));
+}
+
+TORCH_LIBRARY_IMPL(tvdcn, CPU, m) {
+    TVDCN_IMPL_CONV(1, fwd_cpu, bwd_cpu)
+    TVDCN_IMPL_CONV(2, fwd_cpu, bwd_cpu)
+    TVDCN_IMPL_CONV(3, fwd_cpu, bwd_cpu)
+    m.impl("deform_conv_mask_activation", TORCH_FN(tvdcn_amd::act_fwd_cpu));
+    m.impl("_deform_conv_mask_activation_backward", TORCH_FN(tvdcn_amd::act_bwd_cpu));
+    m.impl("mask_softmax", TORCH_FN(tvdcn_amd::mask_softmax_cpu));
+    m.impl("_mask_softmax_backward", TORCH_FN(tvdcn_amd::mask_softmax_backward_cpu));
 }
 
 TORCH_LIBRARY_IMPL(tvdcn, Meta, m) {
