@@ -179,6 +179,28 @@ def test_mask_softmax_matches_torch_softmax():
         assert rel_err(x.grad, xr.grad) < 1e-12
 
 
+@pytest.mark.parametrize("K,shape", [(3, (2, 6, 37)), (4, (3, 8, 130)), (7, (2, 14, 65)), (9, (1, 18, 4097)),
+                                     (25, (2, 50, 99)), (9, (4, 36, 20000)), (16, (2, 32, 70001)),
+                                     (9, (70000, 9, 1)), (40, (2, 80, 33))])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_mask_softmax_tap_counts_and_ragged_columns(K, shape, dtype):
+    """every tap-count instantiation of the softmax kernels (3, 4, 9, 25 compiled in, 7 and 40 at
+    run time, 40 on the re-reading kernel), one and four columns per thread, column counts that
+    are not multiples of the 64-lane wavefront, and more (batch, group) rows than one grid axis
+    holds: against torch.softmax on the same view, forward and backward"""
+    g = torch.Generator().manual_seed(K + shape[-1])
+    x = torch.randn(*shape, generator=g).to(DEV, dtype).requires_grad_(True)
+    y = torch.ops.tvdcn.mask_softmax(x, K)
+    xr = x.detach().double().requires_grad_(True)
+    yr = torch.softmax(xr.view(shape[0], shape[1] // K, K, -1), dim=2).view(shape)
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    assert rel_err(y, yr) < tol
+    gy = torch.randn(*shape, generator=g).to(DEV, dtype)
+    y.backward(gy)
+    yr.backward(gy.double())
+    assert rel_err(x.grad, xr.grad) < (1e-5 if dtype == torch.float32 else 2e-2)
+
+
 @pytest.mark.parametrize("dim,transposed", [(2, False), (2, True), (1, False), (3, False)])
 def test_autocast_runs_in_float32_and_casts_back(dim, transposed):
     """Under torch.autocast("cuda"), float16 inputs run in float32 and the result is cast back to the

@@ -19,7 +19,7 @@
 //     run): wave w computes Gt[c][px] for its 32 pixels, so each lane holds four
 //     consecutive channels of one pixel per (tap, 16-pixel block). It runs on
 //     16x16x32 MFMAs, 32 channels per step, from 16-bit operands laid out by
-//     z_split_kernel / weight_split_kernel: fp16 and bf16 tensors as they are, fp32
+//     data_prep_kernel (Z and weight splits, one launch): fp16 and bf16 tensors as they are, fp32
 //     tensors as three bf16 pieces each, of whose nine cross products the six with
 //     i + j <= 2 are summed (the rest are below 2^-25 of the product, under fp32's own
 //     rounding; 6 MFMAs at 16 cycles against 8 fp32 16x16x4 MFMAs at 32 cycles per 32
@@ -123,11 +123,10 @@ __device__ __forceinline__ float row_sum4(float v) {
 // of its 32 channels (zero past Mg), each as 4 lane groups of 8 (the 16x16x32 B-operand layout).
 // Block = 64 pixels of one (image, group, step), transposed through LDS.
 template <typename T, int NP>
-__global__ void __launch_bounds__(256)
-z_split_kernel(const T *__restrict__ z, uint16_t *__restrict__ zs, int *flag, int G, int Mg, int Pn, int ms32,
-               int pblocks) {
-    __shared__ float tile[32][65];
-    const long long bid = blockIdx.x;
+__device__ __forceinline__ void z_split_block(long long bid, float *smem, const T *__restrict__ z,
+                                              uint16_t *__restrict__ zs, int *flag, int G, int Mg, int Pn, int ms32,
+                                              int pblocks) {
+    float(*tile)[65] = reinterpret_cast<float(*)[65]>(smem);   // [32][65]
     const int pb = (int)(bid % pblocks);
     const long long bgs = bid / pblocks;   // (b * G + grp) * ms32 + step
     const int st = (int)(bgs % ms32);
@@ -882,12 +881,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 // LDS, writes its 256 * taps contiguous output floats.
 constexpr int WL_TK = 16;
 template <typename T>
-__global__ void __launch_bounds__(256)
-weight_win_kernel(const T *__restrict__ w, float *__restrict__ out, int G, int Mg, int Cg, int Kn, int c_tiles,
-                  int m_steps) {
-    __shared__ float tile[WL_TK][BC][BM + 1];   // [tap][c][m]
+__device__ __forceinline__ void weight_win_block(int L, float *smem, const T *__restrict__ w, float *__restrict__ out,
+                                                 int G, int Mg, int Cg, int Kn, int c_tiles, int m_steps) {
+    float(*tile)[BC][BM + 1] = reinterpret_cast<float(*)[BC][BM + 1]>(smem);   // [tap][c][m]
     const int tchunks = (Kn + WL_TK - 1) / WL_TK;
-    int L = blockIdx.x;
     const int tc = L % tchunks;
     L /= tchunks;
     const int ms = L % m_steps;
@@ -914,12 +911,11 @@ weight_win_kernel(const T *__restrict__ w, float *__restrict__ out, int G, int M
 // q * 16 + c holds rows 8q .. 8q + 7 of channel c; zero past Mg / Cg). Block = (group, channel
 // slice, step, run of up to WL_TK taps), transposed through LDS.
 template <typename T, int NP>
-__global__ void __launch_bounds__(256)
-weight_split_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, int G, int Mg, int Cg, int Kn,
-                    int c_tiles, int ms32) {
-    __shared__ float tile[WL_TK][BC][33];   // [tap][c][m]
+__device__ __forceinline__ void weight_split_block(int L, float *smem, const T *__restrict__ w,
+                                                   uint16_t *__restrict__ out, int *flag, int G, int Mg, int Cg,
+                                                   int Kn, int c_tiles, int ms32) {
+    float(*tile)[BC][33] = reinterpret_cast<float(*)[BC][33]>(smem);   // [tap][c][m]
     const int tchunks = (Kn + WL_TK - 1) / WL_TK;
-    int L = blockIdx.x;
     const int tc = L % tchunks;
     L /= tchunks;
     const int st = L % ms32;
@@ -953,6 +949,28 @@ weight_split_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *fl
         for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + (size_t)tt * (NP * 512) + k * 512 + l * 8) = o[k];
     }
     if (NP == 3 && bad) atomicOr(flag, 1);
+}
+
+// The data gradient's operand layouts in one launch: blocks [0, nz) split Z (z_split_block),
+// the next nws split the weight (weight_split_block), the last nww lay the weight out for the
+// fp32 loop (weight_win_block); each block's branch is uniform, so its barriers are too.
+template <typename T, int NP>
+__global__ void __launch_bounds__(256)
+data_prep_kernel(const T *__restrict__ z, uint16_t *__restrict__ zs, const T *__restrict__ w, uint16_t *__restrict__ wsp,
+                 float *__restrict__ wd, int *flag, int G, int Mg, int Cg, int Pn, int Kn, int c_tiles, int ms32,
+                 int m_steps, int pblocks, long long nz, int nws) {
+    __shared__ float smem[WL_TK * BC * 33];
+    long long L = blockIdx.x;
+    if (L < nz) {
+        z_split_block<T, NP>(L, smem, z, zs, flag, G, Mg, Pn, ms32, pblocks);
+        return;
+    }
+    L -= nz;
+    if (L < nws) {
+        weight_split_block<T, NP>((int)L, smem, w, wsp, flag, G, Mg, Cg, Kn, c_tiles, ms32);
+        return;
+    }
+    weight_win_block<T>((int)(L - nws), smem, w, wd, G, Mg, Cg, Kn, c_tiles, m_steps);
 }
 
 template <bool SCATTER, bool COORD> size_t lds_bytes(const WinTiles &t) {
@@ -1008,20 +1026,21 @@ hipError_t launch_d(int dim, const Geo &g, const WinTiles &tl, bool scatter, boo
 }
 
 template <typename T>
-hipError_t launch_split(const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs, void *wsp, int *flag,
-                        hipStream_t s) {
+hipError_t launch_prep(const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs, void *wsp, void *wd,
+                       int *flag, hipStream_t s) {
     constexpr int NP = npiece_of<T>();
     const int pblocks = (g.Pn + 63) / 64;
-    const long long zblocks = (long long)g.B * g.G * t.ms32 * pblocks;
-    const long long wblocks = (long long)g.G * t.c_tiles * t.ms32 * ((g.Kn + WL_TK - 1) / WL_TK);
-    if (zblocks > INT_MAX || wblocks > INT_MAX) return hipErrorInvalidValue;
-    if (zblocks > 0)
-        hipLaunchKernelGGL((z_split_kernel<T, NP>), dim3((unsigned)zblocks), dim3(256), 0, s, static_cast<const T *>(z),
-                           static_cast<uint16_t *>(zs), flag, g.G, g.Mg, g.Pn, t.ms32, pblocks);
-    if (wblocks > 0)
-        hipLaunchKernelGGL((weight_split_kernel<T, NP>), dim3((unsigned)wblocks), dim3(256), 0, s,
-                           static_cast<const T *>(w), static_cast<uint16_t *>(wsp), flag, g.G, g.Mg, g.Cg, g.Kn,
-                           t.c_tiles, t.ms32);
+    const int tchunks = (g.Kn + WL_TK - 1) / WL_TK;
+    const long long zblocks = z != nullptr ? (long long)g.B * g.G * t.ms32 * pblocks : 0;
+    const long long wblocks = (long long)g.G * t.c_tiles * t.ms32 * tchunks;
+    const long long dblocks = wd != nullptr ? (long long)g.G * t.c_tiles * t.m_steps * tchunks : 0;
+    const long long total = zblocks + wblocks + dblocks;
+    if (wblocks > INT_MAX || dblocks > INT_MAX || total > INT_MAX) return hipErrorInvalidValue;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL((data_prep_kernel<T, NP>), dim3((unsigned)total), dim3(256), 0, s, static_cast<const T *>(z),
+                       static_cast<uint16_t *>(zs), static_cast<const T *>(w), static_cast<uint16_t *>(wsp),
+                       static_cast<float *>(wd), flag, g.G, g.Mg, g.Cg, g.Pn, g.Kn, t.c_tiles, t.ms32, t.m_steps,
+                       pblocks, zblocks, (int)wblocks);
     return hipGetLastError();
 }
 
@@ -1122,30 +1141,12 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
     return t;
 }
 
-hipError_t launch_weight_win_layout(int dtype, const Geo &g, const WinTiles &t, const void *w, void *chunks,
-                                    hipStream_t s) {
-    const long long blocks = (long long)g.G * t.c_tiles * t.m_steps * ((g.Kn + WL_TK - 1) / WL_TK);
-    if (blocks <= 0) return hipSuccess;
-    if (blocks > INT_MAX) return hipErrorInvalidValue;
-#define TVDCN_WW(T)                                                                                             \
-    hipLaunchKernelGGL((weight_win_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, s, static_cast<const T *>(w), \
-                       static_cast<float *>(chunks), g.G, g.Mg, g.Cg, g.Kn, t.c_tiles, t.m_steps);               \
-    return hipGetLastError();
+hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs,
+                                void *wsplit, void *wd, int *flag, hipStream_t s) {
     switch (dtype) {
-        case kF32: { TVDCN_WW(float) }
-        case kF16: { TVDCN_WW(__half) }
-        case kBF16: { TVDCN_WW(__hip_bfloat16) }
-    }
-#undef TVDCN_WW
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_data_win_split(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w,
-                                 void *zs, void *wsplit, int *flag, hipStream_t s) {
-    switch (dtype) {
-        case kF32: return launch_split<float>(g, t, z, w, zs, wsplit, flag, s);
-        case kF16: return launch_split<__half>(g, t, z, w, zs, wsplit, flag, s);
-        case kBF16: return launch_split<__hip_bfloat16>(g, t, z, w, zs, wsplit, flag, s);
+        case kF32: return launch_prep<float>(g, t, z, w, zs, wsplit, wd, flag, s);
+        case kF16: return launch_prep<__half>(g, t, z, w, zs, wsplit, wd, flag, s);
+        case kBF16: return launch_prep<__hip_bfloat16>(g, t, z, w, zs, wsplit, wd, flag, s);
     }
     return hipErrorInvalidValue;
 }

@@ -443,6 +443,14 @@ bool sampled16_host_ok(const Plan &pl, const tvdcn_conv_desc *desc) {
     if (desc->flags & TVDCN_FLAG_MASK_SIGMOID) return std::fabs(desc->mask_scale) < (double)MASK_LIMIT;
     return true;
 }
+// the mask when its values feed the 16-bit loops unbounded (fp32, no activation), else null
+const void *mask_to_check(const Plan &pl, const tvdcn_conv_desc *desc, const void *mask) {
+    if (pl.dtype != kF32 || mask == nullptr || (desc->flags & (TVDCN_FLAG_MASK_SIGMOID | TVDCN_FLAG_MASK_SOFTMAX)))
+        return nullptr;
+    return mask;
+}
+size_t mask_numel(const Geo &g) { return (size_t)g.B * g.mg * g.Kn * g.Pn; }
+
 hipError_t check_sampled(const Plan &pl, const tvdcn_conv_desc *desc, const void *x_in_place, const void *mask,
                          int *flag, hipStream_t s) {
     const Geo &g = pl.g;
@@ -468,27 +476,31 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
     const int dt = pl.dtype;
     g_last_error.clear();
     int *flag = static_cast<int *>(at(workspace, L.flag));
-    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, flag, 1, s));
     if (!pl.transposed) {
         void *xcl = at(workspace, L.xcl), *wf = at(workspace, L.wf);
         void *w16 = pl.fw.ok && sampled16_host_ok(pl, desc) ? at(workspace, L.w16) : nullptr;
+        // the flag and (split channel slices) the fp32 accumulator zeroed by one launch
+        void *y32 = pl.fw.ok && pl.fw.ksplit > 1 ? (dt == kF32 ? output : at(workspace, L.yacc)) : nullptr;
+        const FillItem fills[2] = {{flag, 4}, {y32, y32 ? (size_t)g.B * g.M * g.Pn * 4 : 0}};
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero_multi(fills, 2, s));
         const void *x_in_place = nullptr;
+        // the 16-bit loop's mask range check rides on the input's layout copy when there is one
+        const void *mchk = w16 != nullptr ? mask_to_check(pl, desc, mask) : nullptr;
         if (!(desc->flags & TVDCN_FLAG_CHANNELS_LAST))
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s, flag));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s, flag, mchk,
+                                                                         mask_numel(g), MASK_LIMIT));
         else if (acc_is_storage(dt))
             x_in_place = xcl = const_cast<void *>(input);   // already the kernels' layout and type
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, input, xcl, (size_t)g.B * g.Sn * g.C, s));
         if (pl.fw.ok) {
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
             if (w16 != nullptr) {
-                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout16(dt, g, pl.fw, weight, w16, flag, s));
-                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
-            }
-            void *y32 = nullptr;
-            if (pl.fw.ksplit > 1) {
-                y32 = dt == kF32 ? output : at(workspace, L.yacc);
-                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, y32, (size_t)g.B * g.M * g.Pn, s));
+                // both weight layouts (16-bit pieces and the fp32 loop's) in one launch
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout16(dt, g, pl.fw, weight, w16, flag, s, wf));
+                if (desc->flags & TVDCN_FLAG_CHANNELS_LAST)
+                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
+            } else {
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
             }
             TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
                          launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, w16, flag, offset, mask, bias, output,
@@ -502,11 +514,11 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
         }
     } else {
         void *wd = at(workspace, L.wd), *ycl = at(workspace, L.cl_acc);
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero((int)acc_size(dt), ycl, (size_t)g.B * g.Sn * g.C, s));
+        const FillItem fills[2] = {{flag, 4}, {ycl, (size_t)g.B * g.Sn * g.C * acc_size(dt)}};
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero_multi(fills, 2, s));
         if (pl.wn_s.ok) {
             void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_split(dt, g, pl.wn_s, input, weight, zs, wsp, flag, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_prep(dt, g, pl.wn_s, input, weight, zs, wsp, wd, flag, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, input, wd, zs,
                                                                         wsp, flag, nullptr, offset, mask, ycl, nullptr,
                                                                         nullptr, s));
@@ -537,8 +549,6 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
     const size_t n_gmask = g.mg ? (size_t)g.B * g.mg * g.Kn * g.Pn : 0;
     void *goff = direct ? grad_offset : at(workspace, L.goff_acc);
     void *gmask = direct ? grad_mask : at(workspace, L.gmask_acc);
-    if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, goff, n_goff, s));
-    if (gmask) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gmask, n_gmask, s));
 
     // Z: the GEMM-side tensor (conv: grad_out; transposed: input)
     // X: the sampled tensor (conv: input; transposed: grad_out)
@@ -547,29 +557,37 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
     {
         void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
         int *flag = static_cast<int *>(at(workspace, L.flag));
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, flag, 1, s));
         const bool cl_in = (desc->flags & TVDCN_FLAG_CHANNELS_LAST) != 0;   // conv only
-        const void *x_in_place = nullptr;
-        if (!cl_in)
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s, flag));
-        else if (direct)
-            x_in_place = xcl = const_cast<void *>(X);   // already the kernels' layout and type
-        else
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, X, xcl, (size_t)g.B * g.Sn * g.C, s));
+        // conv: the channels-last grad_input of the accumulation type, accumulated in place
+        void *gx_cl = pl.transposed ? nullptr : cl_in && direct ? grad_input : at(workspace, L.cl_acc);
+        // the offset / mask gradient accumulators, the operand flag and grad_input zeroed by one launch
+        const FillItem fills[4] = {{goff, goff ? n_goff * ab : 0},
+                                   {gmask, gmask ? n_gmask * ab : 0},
+                                   {flag, 4},
+                                   {gx_cl, gx_cl ? (size_t)g.B * g.Sn * g.C * ab : 0}};
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero_multi(fills, 4, s));
         const bool coord = offset != nullptr || mask != nullptr;
         // the 16-bit loops of the sampled side (weight gradient; transposed: input gradient)
         const bool sampled16 = sampled16_host_ok(pl, desc) && (pl.ww.ok || (pl.transposed && pl.fw.ok));
-        if (sampled16) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
+        const void *x_in_place = nullptr;
+        if (!cl_in) {
+            // the mask's range check rides on the layout copy
+            const void *mchk = sampled16 ? mask_to_check(pl, desc, mask) : nullptr;
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s, flag, mchk,
+                                                                         mask_numel(g), MASK_LIMIT));
+        } else {
+            if (direct)
+                x_in_place = xcl = const_cast<void *>(X);   // already the kernels' layout and type
+            else
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, X, xcl, (size_t)g.B * g.Sn * g.C, s));
+            if (sampled16) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
+        }
         void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
-        if (pl.wn_s.ok) {
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_win_layout(dt, g, pl.wn_s, weight, wd, s));
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_split(dt, g, pl.wn_s, Z, weight, zs, wsp, flag, s));
-        } else
+        if (pl.wn_s.ok)
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_prep(dt, g, pl.wn_s, Z, weight, zs, wsp, wd, flag, s));
+        else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
         if (!pl.transposed) {
-            // channels-last grad_input of the accumulation type is accumulated in place
-            void *gx_cl = cl_in && direct ? grad_input : at(workspace, L.cl_acc);
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(ab, gx_cl, (size_t)g.B * g.Sn * g.C, s));
             if (pl.wn_s.ok && coord && pl.data_split && pl.dim == 3) {
                 // 3D: one launch on the scatter window, the offset / mask gradients reading X
                 // from global memory (cached), instead of two that each recompute the contraction
@@ -599,9 +617,10 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
             void *wf = at(workspace, L.wf);
             if (pl.fw.ok) {
                 void *w16 = sampled16 ? at(workspace, L.w16) : nullptr;
-                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
                 if (w16 != nullptr)
-                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout16(dt, g, pl.fw, weight, w16, flag, s));
+                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout16(dt, g, pl.fw, weight, w16, flag, s, wf));
+                else
+                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
                 void *y32 = nullptr;
                 if (pl.fw.ksplit > 1) {
                     y32 = dt == kF32 ? grad_input : at(workspace, L.yacc);

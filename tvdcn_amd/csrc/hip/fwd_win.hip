@@ -422,10 +422,11 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     }
 }
 
-// weight (M, Cg, Kn) -> Wp[G][slices][Kn][Mg_pad / 16][16 m][16 c], zero padded
+// weight (M, Cg, Kn) -> Wp[G][slices][Kn][Mg_pad / 16][16 m][16 c], zero padded (grid-stride loop
+// over the calling grid)
 template <typename T>
-__global__ void fwd_win_weight_kernel(const T *__restrict__ w, float *__restrict__ wp, int G, int Mg, int Cg, int Kn,
-                                      int slices, int Mg_pad) {
+__device__ __forceinline__ void fwd_weight_f32(const T *__restrict__ w, float *__restrict__ wp, int G, int Mg, int Cg,
+                                               int Kn, int slices, int Mg_pad) {
     const size_t total = (size_t)G * slices * Kn * Mg_pad * BC;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
         const int ci = (int)(i % BC);
@@ -443,14 +444,22 @@ __global__ void fwd_win_weight_kernel(const T *__restrict__ w, float *__restrict
     }
 }
 
+template <typename T>
+__global__ void fwd_win_weight_kernel(const T *__restrict__ w, float *__restrict__ wp, int G, int Mg, int Cg, int Kn,
+                                      int slices, int Mg_pad) {
+    fwd_weight_f32<T>(w, wp, G, Mg, Cg, Kn, slices, Mg_pad);
+}
+
 // weight (M, Cg, Kn) -> W16[G][slices][pp][Mg_pad / 16][NP][64 lanes][8]: per (slice, tap pair j
 // of pass p, 16-row block) the 16x16x32 A fragments: lane l = m % 16 + 16 q holds at e = 0..7
 // W[m][slice * 16 + 4 q + e % 4] at tap p * tpp + 2 j + e / 4 (zero past the pass, Mg, Cg); fp32
 // as three bf16 pieces (*flag set for a value bad for the split), fp16 / bf16 as they are
+// (wp: when not null, the fp32 layout of fwd_win_weight_kernel is written by the same launch)
 template <typename T, int NP>
 __global__ void __launch_bounds__(256)
 fwd_w16_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, int G, int Mg, int Cg, int Kn, int slices,
-               int nmb, int tpp, int hp, int pp) {
+               int nmb, int tpp, int hp, int pp, float *__restrict__ wp) {
+    if (wp != nullptr) fwd_weight_f32<T>(w, wp, G, Mg, Cg, Kn, slices, nmb * 16);
     const size_t total = (size_t)G * slices * pp * nmb * 64;
     bool bad = false;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
@@ -583,17 +592,18 @@ hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, cons
 }
 
 hipError_t launch_fwd_win_layout16(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *w16, int *flag,
-                                   hipStream_t s) {
-    if (fw.w16_elems == 0) return hipSuccess;
+                                   hipStream_t s, void *wp) {
+    if (fw.w16_elems == 0) return wp != nullptr ? launch_fwd_win_layout(dtype, g, fw, w, wp, s) : hipSuccess;
     const int slices = fw.Cg_pad / BC;
-    const size_t n = fw.w16_elems / (fw.npiece * 8);   // threads: one per lane fragment
+    size_t n = fw.w16_elems / (fw.npiece * 8);   // threads: one per lane fragment
+    if (wp != nullptr) n = std::max(n, (size_t)g.G * slices * g.Kn * fw.Mg_pad * BC);
     size_t blocks = (n + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     if (blocks < 1) blocks = 1;
 #define TVDCN_FW16(T, NP)                                                                                              \
     hipLaunchKernelGGL((fwd_w16_kernel<T, NP>), dim3((unsigned)blocks), dim3(256), 0, s, static_cast<const T *>(w),    \
                        static_cast<uint16_t *>(w16), flag, g.G, g.Mg, g.Cg, g.Kn, slices, fw.Mg_pad / 16, fw.tpp,    \
-                       fw.hp, fw.pp);                                                                                  \
+                       fw.hp, fw.pp, static_cast<float *>(wp));                                                        \
     return hipGetLastError();
     switch (dtype) {
         case kF32: { TVDCN_FW16(float, 3) }

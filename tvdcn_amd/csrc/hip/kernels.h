@@ -117,9 +117,12 @@ DataTiles plan_data(const Geo &g, int dtype);
 WeightTiles plan_weight(const Geo &g, int dtype);
 
 // layout / elementwise helpers (prep.hip)
-// (flag: when not null, fp32 values not below SAMPLED_LIMIT in magnitude set *flag)
+// (flag: when not null, fp32 values not below SAMPLED_LIMIT in magnitude set *flag; chk: when not
+// null, an fp32 tensor of chk_n values range-checked against chk_limit into *flag by the same
+// launch, as launch_check_range does)
 hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s,
-                                   int *flag = nullptr);
+                                   int *flag = nullptr, const void *chk = nullptr, size_t chk_n = 0,
+                                   float chk_limit = 0.f);
 // 16-bit MFMA operands of the sampled side (forward, weight gradient): the sampled values are
 // mask * bilinear(X), below 2^126 (and so within bf16's range) when |X| < SAMPLED_LIMIT and
 // |mask| < MASK_LIMIT; larger or non-finite values send the launch to its fp32 MFMA loop.
@@ -134,6 +137,14 @@ hipError_t launch_weight_fwd_layout(int dtype, const Geo &g, const void *w, void
 hipError_t launch_weight_data_layout(int dtype, const Geo &g, const void *w, void *wd, int Mg_pad, int Cg_pad,
                                      hipStream_t s);
 hipError_t launch_fill_zero(int elem_bytes, void *p, size_t n, hipStream_t s);   // elem_bytes 2, 4 or 8
+// Zeroes up to kFillMax buffers in one launch (entries with p == nullptr or bytes == 0 are
+// skipped); every buffer 2-byte aligned with an even byte count.
+constexpr int kFillMax = 4;
+struct FillItem {
+    void *p;
+    size_t bytes;
+};
+hipError_t launch_fill_zero_multi(const FillItem *items, int n, hipStream_t s);
 hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n, hipStream_t s);
 hipError_t launch_storage_to_acc(int dtype, const void *x, void *acc, size_t n, hipStream_t s);   // elementwise widening
 // gmask_acc (accumulation type) *= d(scale * sigmoid(logit)) / d(logit), elementwise
@@ -152,8 +163,9 @@ hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTil
 // weight -> the windowed forward's fragment-major layout (fwd_win.hip)
 hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *wp, hipStream_t s);
 // the weight as W16 (fp32: three bf16 pieces; *flag set for a value bad for the split)
+// (wp: when not null, also the fp32 layout of launch_fwd_win_layout, in the same launch)
 hipError_t launch_fwd_win_layout16(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *w16, int *flag,
-                                   hipStream_t s);
+                                   hipStream_t s, void *wp = nullptr);
 // w16 / flag: the 16-bit weight and the operand flag (w16 null, or *flag set: the fp32 loop)
 hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl,
                           const void *wf, const void *w16, const int *flag, const void *offset, const void *mask,
@@ -161,13 +173,13 @@ hipError_t launch_fwd_win(int dtype, int dim, const Geo &g, const WinTiles &wt, 
 hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t, bool scatter, bool coord,
                            const void *z, const void *wd, const void *xcl, const void *offset, const void *mask,
                            void *gx_cl, void *goff, void *gmask, hipStream_t s);
-hipError_t launch_weight_win_layout(int dtype, const Geo &g, const WinTiles &t, const void *w, void *chunks,
-                                    hipStream_t s);
 // Z (the GEMM-side tensor, (B, M, Pn)) and the weight as the data gradient's 16-bit MFMA operands
-// (zs, wsplit). For fp32 tensors, *flag (zeroed by the caller first) is set when a value is not
-// finite or would round past the bf16 range: the data gradient then runs its fp32 MFMA loop.
-hipError_t launch_data_win_split(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w,
-                                 void *zs, void *wsplit, int *flag, hipStream_t s);
+// (zs, wsplit), and the weight's fp32-loop chunks (wd: [G][c_tiles][m_steps][Kn][16 c][16 m]; skipped
+// when null), in one launch. For fp32 tensors, *flag (zeroed by the caller first) is set
+// when a value is not finite or would round past the bf16 range: the data gradient then runs its
+// fp32 MFMA loop.
+hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs,
+                                void *wsplit, void *wd, int *flag, hipStream_t s);
 hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
                                const void *z, const void *wchunks, const void *zs, const void *wsplit,
                                const int *flag, const void *xcl, const void *offset, const void *mask, void *gx_cl,

@@ -13,12 +13,24 @@ namespace {
 
 constexpr int TT = 64;   // transpose tile
 
-// x [B][C][S] (T) -> xcl [B][S][C] (A); 64 x 64 tile through LDS, 256 threads
+// x [B][C][S] (T) -> xcl [B][S][C] (A); 64 x 64 tile through LDS, 256 threads. With chk, the
+// grid holds one more z slice whose blocks range-check chk[0 .. chk_n) into *flag instead (one
+// launch for the copy and the check of another operand, e.g. the mask).
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) to_cl_kernel(const T *__restrict__ x, A *__restrict__ xcl, int C, int S,
-                                                    int *flag) {
+                                                    int *flag, const float *__restrict__ chk, size_t chk_n,
+                                                    float chk_limit) {
     __shared__ A tile[TT][TT + 1];
     const int b = blockIdx.z;
+    if (chk != nullptr && b == (int)gridDim.z - 1) {
+        bool bad = false;
+        const size_t nb = (size_t)gridDim.x * gridDim.y;
+        for (size_t i = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < chk_n;
+             i += nb * blockDim.x)
+            bad = bad || !(fabsf(chk[i]) < chk_limit);
+        if (bad) atomicOr(flag, 1);
+        return;
+    }
     const int s0 = blockIdx.x * TT, c0 = blockIdx.y * TT;
     const T *xb = x + (size_t)b * C * S;
     A *ob = xcl + (size_t)b * C * S;
@@ -99,6 +111,29 @@ template <typename A>
 __global__ void fill_zero_kernel(A *__restrict__ p, size_t n) {
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         p[i] = A{};
+}
+
+// Several buffers zeroed by one launch: the 16-byte-aligned body of each with vector stores
+// (one flat index space over the bodies), the unaligned head and tail (under 16 bytes each)
+// with 2-byte stores by block 0.
+struct FillSet {
+    uint4 *body[kFillMax];
+    size_t start[kFillMax + 1];      // prefix sums of the body word counts
+    uint16_t *edge[2 * kFillMax];    // head and tail of each buffer
+    int edge_n[2 * kFillMax];        // 2-byte units, < 8
+    int n;
+};
+__global__ void __launch_bounds__(256) fill_zero_multi_kernel(const FillSet f) {
+    const size_t total = f.start[f.n];
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        int k = 0;
+        while (k + 1 < f.n && i >= f.start[k + 1]) ++k;
+        f.body[k][i - f.start[k]] = uint4{0u, 0u, 0u, 0u};
+    }
+    if (blockIdx.x == 0 && threadIdx.x < 2 * kFillMax * 8) {
+        const int e = threadIdx.x >> 3, j = threadIdx.x & 7;
+        if (e < 2 * f.n && j < f.edge_n[e]) f.edge[e][j] = 0;
+    }
 }
 
 template <typename T, typename A>
@@ -184,15 +219,44 @@ hipError_t by_dtype(int dtype, F &&f) {
 }  // namespace
 
 hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s,
-                                   int *flag) {
+                                   int *flag, const void *chk, size_t chk_n, float chk_limit) {
+    if (chk != nullptr && (flag == nullptr || chk_n == 0)) chk = nullptr;
     return by_dtype(dtype, [&](auto tv, auto av) {
         using T = decltype(tv);
         using A = decltype(av);
-        dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B);
+        dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B + (chk != nullptr ? 1 : 0));
         hipLaunchKernelGGL((to_cl_kernel<T, A>), grid, dim3(256), 0, s, static_cast<const T *>(x),
-                           static_cast<A *>(xcl), C, Sn, flag);
+                           static_cast<A *>(xcl), C, Sn, flag, static_cast<const float *>(chk), chk_n, chk_limit);
         return hipGetLastError();
     });
+}
+
+hipError_t launch_fill_zero_multi(const FillItem *items, int n, hipStream_t s) {
+    FillSet f{};
+    size_t total = 0;
+    for (int i = 0; i < n; ++i) {
+        if (items[i].p == nullptr || items[i].bytes == 0) continue;
+        if (f.n == kFillMax) return hipErrorInvalidValue;
+        char *p = static_cast<char *>(items[i].p);
+        const size_t bytes = items[i].bytes;
+        if (reinterpret_cast<uintptr_t>(p) % 2 != 0 || bytes % 2 != 0) return hipErrorInvalidValue;
+        size_t head = (16 - reinterpret_cast<uintptr_t>(p) % 16) % 16;
+        if (head > bytes) head = bytes;
+        const size_t words = (bytes - head) / 16;
+        const size_t tail = bytes - head - words * 16;
+        const int k = f.n++;
+        f.body[k] = reinterpret_cast<uint4 *>(p + head);
+        f.start[k] = total;
+        total += words;
+        f.edge[2 * k] = reinterpret_cast<uint16_t *>(p);
+        f.edge_n[2 * k] = (int)(head / 2);
+        f.edge[2 * k + 1] = reinterpret_cast<uint16_t *>(p + head + words * 16);
+        f.edge_n[2 * k + 1] = (int)(tail / 2);
+    }
+    if (f.n == 0) return hipSuccess;
+    f.start[f.n] = total;
+    hipLaunchKernelGGL(fill_zero_multi_kernel, dim3(grid_for(total > 0 ? total : 1)), dim3(256), 0, s, f);
+    return hipGetLastError();
 }
 
 hipError_t launch_from_channels_last(int dtype, const void *xcl, void *x, const void *bias, int B, int C, int Sn,
