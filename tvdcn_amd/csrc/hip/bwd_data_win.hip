@@ -395,7 +395,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
         };
         // ---- 16-bit K loop: 16x16x32 MFMAs over 32 channels per step, operands straight
         //      from the split layouts into registers; Z of the next step and the weight
-        //      fragment one tap ahead (of the (step, tap) sequence) in flight
+        //      fragments of the next two taps (of the (step, tap) sequence) in flight, in a
+        //      ring of three that the unrolled tap loop indexes statically (a load one tap
+        //      ahead left the MFMAs waiting on it: 5% of the kernel at cfg2)
         auto kloop16 = [&]() {
             constexpr int NP = npiece_of<T>();
             const int ms32 = wt.ms32;
@@ -417,31 +419,45 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     for (int k = 0; k < NP; ++k)
                         f[pb][k] = *reinterpret_cast<const uint4 *>(zl[pb] + (size_t)st * zstep + k * 32);
             };
-            uint4 zc[PB][NP], zn[PB][NP], w0[NP], w1[NP];
+            uint4 zc[PB][NP], zn[PB][NP], wr[3][NP];
             zfrag(0, zc);
-            wfrag(0, 0, w0);
-            // (ps, pt): the next weight fragment of the (step, tap) sequence to load
-            int ps = 0, pt = 1;
-            if (pt == ntaps) {
-                pt = 0;
-                ++ps;
-            }
+            // (ps, pt): the next weight fragment of the (step, tap) sequence to load; two in flight
+            int ps = 0, pt = 0;
+            auto advance = [&]() {
+                if (++pt == ntaps) {
+                    pt = 0;
+                    ++ps;
+                }
+            };
+            wfrag(ps, pt, wr[0]);
+            advance();
+            wfrag(ps, pt, wr[1]);
+            advance();
             for (int st = 0; st < ms32; ++st) {
                 zfrag(min(st + 1, ms32 - 1), zn);
                 issue_fence();
 #pragma unroll
                 for (int tp = 0; tp < TMAX; ++tp) {
                     if (tp >= ntaps) break;
-                    wfrag(ps, pt, w1);
-                    if (++pt == ntaps) {
-                        pt = 0;
-                        ++ps;
-                    }
+                    wfrag(ps, pt, wr[(tp + 2) % 3]);
+                    advance();
 #pragma unroll
-                    for (int pb = 0; pb < PB; ++pb) acc[tp][pb] = mfma16x16x32_np<T, NP>(w0, zc[pb], acc[tp][pb]);
+                    for (int pb = 0; pb < PB; ++pb)
+                        acc[tp][pb] = mfma16x16x32_np<T, NP>(wr[tp % 3], zc[pb], acc[tp][pb]);
                     __builtin_amdgcn_sched_barrier(0);
+                }
+                if (ntaps % 3 != 0) {
+                    // keep the ring aligned with tap 0 of the next step
+                    uint4 t[3][NP];
 #pragma unroll
-                    for (int k = 0; k < NP; ++k) w0[k] = w1[k];
+                    for (int i = 0; i < 3; ++i)
+#pragma unroll
+                        for (int k = 0; k < NP; ++k) t[i][k] = wr[i][k];
+                    const int r = ntaps % 3;
+#pragma unroll
+                    for (int i = 0; i < 3; ++i)
+#pragma unroll
+                        for (int k = 0; k < NP; ++k) wr[i][k] = r == 1 ? t[(i + 1) % 3][k] : t[(i + 2) % 3][k];
                 }
 #pragma unroll
                 for (int pb = 0; pb < PB; ++pb)
