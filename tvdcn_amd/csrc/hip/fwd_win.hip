@@ -40,7 +40,8 @@ static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
 
 constexpr int GEO_WORDS = TM * BPX * 4;
 
-template <int DIM, typename T, int MB>
+// STAGE: the 16-bit loop's weight blocks are staged in LDS (1D / 2D, fw.stage_bytes > 0)
+template <int DIM, typename T, int MB, bool STAGE>
 __global__ void __launch_bounds__(NT)
 fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__restrict__ xcl,
                const float *__restrict__ wf, const uint16_t *__restrict__ w16, const int *flag,
@@ -214,7 +215,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     //      2j + e / 4 of the pair: its B fragment is the pair's two sampled quads (zero past the
     //      pass), split into pieces for fp32 and rounded to T otherwise (the reference's columns
     //      of a half-precision input are half). W16 holds the A fragments in the same K order.
-    //      Each row block's weight fragments are loaded one block ahead.
+    //      The weight blocks are staged in LDS (below).
     auto pass16 = [&](int t0, int ntaps) {
         if constexpr (DIM < 3) {
             constexpr int NP = npiece_of<T>();
@@ -223,7 +224,8 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
             geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
             const int nmb = fw.Mg_pad / 16;
             const int pp0 = (t0 / wt.tpp) * fw.hp;
-            const uint16_t *wl = w16 + (size_t)mt * MB * (NP * 512) + lane * 8;
+            // (the step's block: wave-uniform; lanes add their offsets when they load)
+            const uint16_t *wl = w16 + (size_t)mt * MB * (NP * 512);
             auto wptr16 = [&](int cs, int j) {
                 return wl + (((size_t)grp * slices + cs) * fw.pp + pp0 + j) * nmb * (NP * 512);
             };
@@ -243,47 +245,125 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                     pack8_16<T, NP>(v, bp[pb]);
                 }
             };
-            auto load_w16 = [&](const uint16_t *p, uint4 (&f)[NP]) {
+            if constexpr (STAGE) {
+                // The weight blocks (per step MB row blocks x NP pieces, 1 KB each, contiguous in W16)
+                // are staged in LDS, double-buffered, in units of U = 8 / MB steps (64-row tiles take
+                // two steps per unit, so that a unit's MFMAs cover the loads of the next): the
+                // global-to-LDS loads of unit u + 1 are issued at the top of unit u (one 1 KB wave
+                // instruction per piece, spread over the waves), and every wave reads its A fragments
+                // from LDS. Loaded straight from global memory each wave fetched the same blocks:
+                // eight times the bytes through the vector memory path, which then bounded the MFMAs.
+                constexpr int U = 8 / MB;            // steps per staging unit
+                constexpr int NI = MB * NP;          // 1 KB pieces per step
+                constexpr int WBLK = NI * 512;       // 16-bit values per step
+                uint16_t *wst = reinterpret_cast<uint16_t *>(xwin + (size_t)wt.cells * XS);   // [2][U][WBLK]
+                auto step_cs = [&](int k) { return cs_lo + k / npair; };
+                auto step_j = [&](int k) { return k - (k / npair) * npair; };
+                auto stage_unit = [&](int u, int buf) {
 #pragma unroll
-                for (int k = 0; k < NP; ++k) f[k] = *reinterpret_cast<const uint4 *>(p + k * 512);
-            };
-            // MFMAs of one step; block mb + 1's fragments (the next step's block 0 at the end)
-            // are loaded before block mb's MFMAs
-            auto mfma_pair = [&](const uint4 (&bv)[PB][NP], uint4 (&wa)[2][NP], const uint16_t *pcur,
-                                 const uint16_t *pnext) {
+                    for (int su = 0; su < U; ++su) {
+                        const int k = u * U + su;
+                        if (k >= nsteps) break;
+                        const uint16_t *blk = wptr16(step_cs(k), step_j(k));
+                        uint16_t *dst = wst + (buf * U + su) * WBLK;
+                        for (int i = wave; i < NI; i += NW)
+                            __builtin_amdgcn_global_load_lds(blk + i * 512 + lane * 8, dst + i * 512, 16, 0, 0);
+                    }
+                };
+                auto load_w16 = [&](const uint16_t *blk, int mb, uint4 (&f)[NP]) {
+                    const uint16_t *p = blk + mb * (NP * 512) + lane * 8;
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    load_w16(mb + 1 < MB ? pcur + (size_t)(mb + 1) * (NP * 512) : pnext, wa[(mb + 1) & 1]);
+                    for (int k = 0; k < NP; ++k) f[k] = *reinterpret_cast<const uint4 *>(p + k * 512);
+                };
+                // MFMAs of one step on its staged block; block mb + 1's fragments are read before
+                // block mb's MFMAs
+                auto mfma_pair = [&](const uint4 (&bv)[PB][NP], uint4 (&wa)[2][NP], const uint16_t *blk) {
+                    load_w16(blk, 0, wa[0]);
 #pragma unroll
-                    for (int pb = 0; pb < PB; ++pb)
-                        acc[mb][pb] = mfma16x16x32_np<T, NP>(wa[mb & 1], bv[pb], acc[mb][pb]);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            };
-            static_assert(MB % 2 == 0, "row blocks in pairs: the next step's block 0 lands in slot 0");
-            // step k: its B fragments are built, then its MFMAs run (the LDS latency of the
-            // sampling is covered by the other wave of the SIMD)
-            uint4 wa[2][NP], bv[PB][NP];
-            prefetch_x(cs_lo);
-            load_w16(wptr16(cs_lo, 0), wa[0]);
-            __syncthreads();   // previous pass done with the tables
-            open_slice(cs_lo, t0, ntaps);
-            __syncthreads();
-            // the next slice's X window is requested two pair steps before it is needed
-            const int pf_j = max(npair - 2, 0);
-            for (int k = 0; k < nsteps; ++k) {
-                const bool more = k + 1 < nsteps;
-                const int kn = k + 1, csn_r = kn / npair, jn = kn - csn_r * npair;
-                const int cs_r = k / npair, j = k - cs_r * npair;
-                const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
-                if (j == pf_j && cs + 1 < cs_hi) prefetch_x(cs + 1);
-                build_pair(cs, j, bv);
-                const uint16_t *pcur = wptr16(cs, j);
-                mfma_pair(bv, wa, pcur, more ? wptr16(csn, jn) : pcur);
-                if (more && jn == 0) {
-                    __syncthreads();   // every wave done reading the current window
-                    open_slice(csn, t0, ntaps);
+                    for (int mb = 0; mb < MB; ++mb) {
+                        if (mb + 1 < MB) load_w16(blk, mb + 1, wa[(mb + 1) & 1]);
+#pragma unroll
+                        for (int pb = 0; pb < PB; ++pb)
+                            acc[mb][pb] = mfma16x16x32_np<T, NP>(wa[mb & 1], bv[pb], acc[mb][pb]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                };
+                // the staged unit's loads done, then the workgroup barrier that publishes it
+                auto publish = [&]() {
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                     __syncthreads();
+                };
+                // step k: its B fragments are built, then its MFMAs run (the LDS latency of the
+                // sampling is covered by the other wave of the SIMD)
+                uint4 wa[2][NP], bv[PB][NP];
+                prefetch_x(cs_lo);
+                __syncthreads();   // previous pass done with the tables and the staging buffers
+                stage_unit(0, 0);
+                open_slice(cs_lo, t0, ntaps);
+                publish();
+                // the next slice's X window is requested two pair steps before it is needed
+                const int pf_j = max(npair - 2, 0);
+                for (int k = 0; k < nsteps; ++k) {
+                    const bool more = k + 1 < nsteps;
+                    const int u = k / U, su = k - u * U;
+                    const int cs = step_cs(k), j = step_j(k);
+                    const int jn = more ? step_j(k + 1) : 0;
+                    if (su == 0 && (u + 1) * U < nsteps) stage_unit(u + 1, (u + 1) & 1);
+                    if (j == pf_j && cs + 1 < cs_hi) prefetch_x(cs + 1);
+                    build_pair(cs, j, bv);
+                    mfma_pair(bv, wa, wst + ((u & 1) * U + su) * WBLK);
+                    // the unit's end: every wave done with its buffer (and, at a slice change, with
+                    // the window), the next unit's blocks visible
+                    const bool unit_end = su == U - 1 || !more;
+                    if (unit_end) publish();
+                    if (more && jn == 0) {
+                        if (!unit_end) __syncthreads();   // every wave done reading the window
+                        open_slice(step_cs(k + 1), t0, ntaps);
+                        __syncthreads();
+                    }
+                }
+            } else {
+                // (the weight's staging would cost the window its margin: fragments straight from
+                // global memory, each row block's loaded one block ahead)
+                auto load_w16g = [&](const uint16_t *p, uint4 (&f)[NP]) {
+#pragma unroll
+                    for (int k = 0; k < NP; ++k) f[k] = *reinterpret_cast<const uint4 *>(p + lane * 8 + k * 512);
+                };
+                // MFMAs of one step; block mb + 1's fragments (the next step's block 0 at the end)
+                // are loaded before block mb's MFMAs
+                auto mfma_pair_g = [&](const uint4 (&bv)[PB][NP], uint4 (&wa)[2][NP], const uint16_t *pcur,
+                                       const uint16_t *pnext) {
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) {
+                        load_w16g(mb + 1 < MB ? pcur + (size_t)(mb + 1) * (NP * 512) : pnext, wa[(mb + 1) & 1]);
+#pragma unroll
+                        for (int pb = 0; pb < PB; ++pb)
+                            acc[mb][pb] = mfma16x16x32_np<T, NP>(wa[mb & 1], bv[pb], acc[mb][pb]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                };
+                static_assert(MB % 2 == 0, "row blocks in pairs: the next step's block 0 lands in slot 0");
+                uint4 wa[2][NP], bv[PB][NP];
+                prefetch_x(cs_lo);
+                load_w16g(wptr16(cs_lo, 0), wa[0]);
+                __syncthreads();   // previous pass done with the tables
+                open_slice(cs_lo, t0, ntaps);
+                __syncthreads();
+                const int pf_j = max(npair - 2, 0);
+                for (int k = 0; k < nsteps; ++k) {
+                    const bool more = k + 1 < nsteps;
+                    const int kn = k + 1, csn_r = kn / npair, jn = kn - csn_r * npair;
+                    const int cs_r = k / npair, j = k - cs_r * npair;
+                    const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
+                    if (j == pf_j && cs + 1 < cs_hi) prefetch_x(cs + 1);
+                    build_pair(cs, j, bv);
+                    const uint16_t *pcur = wptr16(cs, j);
+                    mfma_pair_g(bv, wa, pcur, more ? wptr16(csn, jn) : pcur);
+                    if (more && jn == 0) {
+                        __syncthreads();   // every wave done reading the current window
+                        open_slice(csn, t0, ntaps);
+                        __syncthreads();
+                    }
                 }
             }
         }
@@ -490,12 +570,12 @@ fwd_w16_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, i
     if (NP == 3 && bad) atomicOr(flag, 1);
 }
 
-template <int DIM, typename T, int MB>
+template <int DIM, typename T, int MB, bool STAGE>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
                     const void *w16, const int *flag, const void *offset, const void *mask, const void *bias, void *y,
                     void *y32, hipStream_t s) {
-    auto kern = fwd_win_kernel<DIM, T, MB>;
-    const size_t lds = ((size_t)GEO_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
+    auto kern = fwd_win_kernel<DIM, T, MB, STAGE>;
+    const size_t lds = ((size_t)GEO_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float) + fw.stage_bytes;
     static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
     if (const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kern), lds_raised); e != hipSuccess)
         return e;
@@ -511,11 +591,16 @@ template <int DIM, typename T>
 hipError_t launch_m(const Geo &g, const WinTiles &wt, const FwdWin &fw, const void *xcl, const void *wf,
                     const void *w16, const int *flag, const void *offset, const void *mask, const void *bias, void *y,
                     void *y32, hipStream_t s) {
-    // 3D: 64-row tiles only (the trilinear sampler needs the registers)
+    // 3D: 64-row tiles only (the trilinear sampler needs the registers), no weight staging
     if constexpr (DIM < 3) {
-        if (fw.mb == 8) return launch_k<DIM, T, 8>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
+        if (fw.stage_bytes > 0) {
+            if (fw.mb == 8) return launch_k<DIM, T, 8, true>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
+            if (fw.mb == 4) return launch_k<DIM, T, 4, true>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
+            return hipErrorInvalidValue;
+        }
+        if (fw.mb == 8) return launch_k<DIM, T, 8, false>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
     }
-    if (fw.mb == 4) return launch_k<DIM, T, 4>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
+    if (fw.mb == 4) return launch_k<DIM, T, 4, false>(g, wt, fw, xcl, wf, w16, flag, offset, mask, bias, y, y32, s);
     return hipErrorInvalidValue;
 }
 
@@ -549,7 +634,22 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     // (3D: one more cell, the zero cell)
     const int zc = dim == 3 ? 1 : 0;
     wt = win_resize(base, g, dim, (size_t)(GEO_WORDS + zc * XS) * sizeof(float), XS * sizeof(float), max_cells - zc);
-    const size_t lds = ((size_t)GEO_WORDS + (size_t)(wt.cells + zc) * XS) * sizeof(float);
+    // 1D / 2D: two staging buffers of the 16-bit loop's weight blocks (8 row blocks x npiece KB
+    // each: one step of 128-row tiles or two of 64-row tiles) when the window keeps a margin of
+    // min(R, 4) cells beside them (a smaller window sends samples to global memory)
+    f.stage_bytes = 0;
+    if (dim < 3) {
+        const int stage = 2 * 8 * base.npiece * 1024;
+        const WinTiles ws =
+            win_resize(base, g, dim, (size_t)(GEO_WORDS + zc * XS) * sizeof(float) + stage, XS * sizeof(float),
+                       max_cells - zc);
+        const int e = 2;   // the last axis: used in every rank
+        if (ws.cells > 0 && ws.R[e] >= std::min(wt.R[e], 4)) {
+            wt = ws;
+            f.stage_bytes = stage;
+        }
+    }
+    const size_t lds = ((size_t)GEO_WORDS + (size_t)(wt.cells + zc) * XS) * sizeof(float) + f.stage_bytes;
     if (lds > WIN_LDS_TARGET || wt.cells > max_cells) return f;
     f.m_tiles = (g.Mg + rows - 1) / rows;
     f.Mg_pad = f.m_tiles * rows;

@@ -98,6 +98,7 @@ struct FwdWin {
     // W16[G][slices][pp][Mg_pad / 16][npiece][512] 16-bit values, pp = passes x hp tap pairs
     int tpp, hp, pp, npiece;   // taps per pass, tap pairs per pass, pairs, pieces per value
     size_t w16_elems;    // 0: no 16-bit path
+    int stage_bytes;     // LDS past the X window: the 16-bit loop's two weight staging buffers
 };
 
 FwdTiles plan_fwd(const Geo &g, int dtype);
