@@ -295,7 +295,7 @@ SUITE = [(2, torch.float32), (3, torch.float32), (4, torch.float32), (5, torch.f
          (5, torch.bfloat16)]
 
 
-TRAFFIC_KERNELS = {"gather_gemm": "fwd_win_kernel<2, float, 8>",
+TRAFFIC_KERNELS = {"gather_gemm": "fwd_win_kernel<2, float, 8, true>",
                    "data_grad": "bwd_data_win_kernel<2, float, true, true>",
                    "weight_grad": "bwd_weight_win_kernel<2, float, true, 2, 1, 9, 32, true>"}
 

@@ -139,6 +139,52 @@ __global__ void __launch_bounds__(SB) softmax_bwd_loop_kernel(const T *__restric
 // Gradient with respect to the logits of a mask the convolution kernels softmax-activated in
 // their mask load: g (accumulation type, in place) holds d(loss)/d(y) summed over channels;
 // y is recomputed from the logits x as in the forward, then g <- y * (g - sum_k g_k * y_k).
+// Register version (K <= KMAX_REG, 32-bit indices): one read of x and g, one write of g.
+template <typename T, typename A, int KC, int CPT>
+__global__ void __launch_bounds__(SB) softmax_logit_grad_reg_kernel(const T *__restrict__ x, A *__restrict__ g, int BG,
+                                                                    int K, int S) {
+    constexpr int KS = tap_slots<KC>();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int s0 = (blockIdx.x * (SB / 64) + wave) * (64 * CPT) + lane;
+    for (int bg = blockIdx.y; bg < BG; bg += gridDim.y) {
+        const size_t o = (size_t)bg * K * S;
+        A xv[CPT][KS], gv[CPT][KS];
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int sc = min(s0 + c * 64, S - 1);
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                if (tap_on<KC>(k, K)) {
+                    xv[c][k] = to_acc<A>(x[o + k * S + sc]);
+                    gv[c][k] = g[o + k * S + sc];
+                }
+        }
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            A mx = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                if (tap_on<KC>(k, K)) mx = xv[c][k] > mx ? xv[c][k] : mx;
+            A sum = A(0), dot = A(0);
+#pragma unroll
+            for (int k = 0; k < KS; ++k)
+                if (tap_on<KC>(k, K)) {
+                    xv[c][k] = exp(xv[c][k] - mx);
+                    sum += xv[c][k];
+                    dot += xv[c][k] * gv[c][k];
+                }
+            const A inv = A(1) / sum;
+            dot *= inv;
+            const int sc = s0 + c * 64;
+            if (sc < S) {
+#pragma unroll
+                for (int k = 0; k < KS; ++k)
+                    if (tap_on<KC>(k, K)) g[o + k * S + sc] = xv[c][k] * inv * (gv[c][k] - dot);
+            }
+        }
+    }
+}
+
 template <typename T, typename A>
 __global__ void __launch_bounds__(SB) softmax_logit_grad_kernel(const T *__restrict__ x, A *__restrict__ g,
                                                                 int64_t BG, int K, int64_t S) {
@@ -262,9 +308,21 @@ hipError_t launch_mask_softmax_logit_grad(int dtype, const void *logits, void *g
     return by_dtype(dtype, [&](auto tv, auto av) {
         using T = decltype(tv);
         using A = decltype(av);
-        hipLaunchKernelGGL((softmax_logit_grad_kernel<T, A>), dim3((unsigned)((n + SB - 1) / SB)), dim3(SB), 0, s,
-                           static_cast<const T *>(logits), static_cast<A *>(gmask_acc), BG, K, S);
-        return hipGetLastError();
+        if (!reg_path(BG, K, S)) {
+            hipLaunchKernelGGL((softmax_logit_grad_kernel<T, A>), dim3((unsigned)((n + SB - 1) / SB)), dim3(SB), 0, s,
+                               static_cast<const T *>(logits), static_cast<A *>(gmask_acc), BG, K, S);
+            return hipGetLastError();
+        }
+        return by_taps(K, [&](auto kc) {
+            constexpr int KC = decltype(kc)::value;
+            if (four_columns(KC, BG, S))
+                hipLaunchKernelGGL((softmax_logit_grad_reg_kernel<T, A, KC, 4>), grid_of(BG, S, 4), dim3(SB), 0, s,
+                                   static_cast<const T *>(logits), static_cast<A *>(gmask_acc), (int)BG, K, (int)S);
+            else
+                hipLaunchKernelGGL((softmax_logit_grad_reg_kernel<T, A, KC, 1>), grid_of(BG, S, 1), dim3(SB), 0, s,
+                                   static_cast<const T *>(logits), static_cast<A *>(gmask_acc), (int)BG, K, (int)S);
+            return hipGetLastError();
+        });
     });
 }
 
