@@ -895,7 +895,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 // Block = (group, channel slice, row step, run of up to WL_TK taps): reads 16 rows of
 // 16 channels x the run's taps (contiguous runs of taps per channel), transposes through
 // LDS, writes its 256 * taps contiguous output floats.
-constexpr int WL_TK = 16;
+constexpr int WL_TK = 8;   // (LDS of the merged layout kernel: 17 KB per block)
 template <typename T>
 __device__ __forceinline__ void weight_win_block(int L, float *smem, const T *__restrict__ w, float *__restrict__ out,
                                                  int G, int Mg, int Cg, int Kn, int c_tiles, int m_steps) {

@@ -50,6 +50,83 @@ __global__ void __launch_bounds__(256) to_cl_kernel(const T *__restrict__ x, A *
     }
 }
 
+// float32 x [B][C][S] -> xcl [B][S][C] with 16-byte accesses on both sides (C % 4 == 0 and
+// S % 4 == 0: a quad is wholly inside or outside the tensor): 64 x 64 tile through LDS, 256
+// threads; a load quad runs along s, a store quad along c. Same chk / flag jobs as to_cl_kernel.
+__global__ void __launch_bounds__(256) to_cl4_kernel(const float *__restrict__ x, float *__restrict__ xcl, int C,
+                                                     int S, int *flag, const float *__restrict__ chk, size_t chk_n,
+                                                     float chk_limit) {
+    __shared__ float tile[TT][TT + 1];   // [c][s]
+    const int b = blockIdx.z;
+    if (chk != nullptr && b == (int)gridDim.z - 1) {
+        bool bad = false;
+        const size_t nb = (size_t)gridDim.x * gridDim.y;
+        for (size_t i = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < chk_n;
+             i += nb * blockDim.x)
+            bad = bad || !(fabsf(chk[i]) < chk_limit);
+        if (bad) atomicOr(flag, 1);
+        return;
+    }
+    const int s0 = blockIdx.x * TT, c0 = blockIdx.y * TT;
+    const float *xb = x + (size_t)b * C * S;
+    float *ob = xcl + (size_t)b * C * S;
+    const int u = threadIdx.x & 15, r0 = threadIdx.x >> 4;
+    bool big = false;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int cl = r0 + 16 * k, c = c0 + cl, s = s0 + 4 * u;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < C && s < S) v = *reinterpret_cast<const float4 *>(xb + (size_t)c * S + s);
+        big = big || !(fabsf(v.x) < SAMPLED_LIMIT) || !(fabsf(v.y) < SAMPLED_LIMIT) ||
+              !(fabsf(v.z) < SAMPLED_LIMIT) || !(fabsf(v.w) < SAMPLED_LIMIT);
+        tile[cl][4 * u] = v.x;
+        tile[cl][4 * u + 1] = v.y;
+        tile[cl][4 * u + 2] = v.z;
+        tile[cl][4 * u + 3] = v.w;
+    }
+    if (flag != nullptr && big) atomicOr(flag, 1);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int sl = r0 + 16 * k, s = s0 + sl, c = c0 + 4 * u;
+        if (s < S && c < C)
+            *reinterpret_cast<float4 *>(ob + (size_t)s * C + c) =
+                make_float4(tile[4 * u][sl], tile[4 * u + 1][sl], tile[4 * u + 2][sl], tile[4 * u + 3][sl]);
+    }
+}
+
+// float32 xcl [B][S][C] -> x [B][C][S] (+ bias[c]) with 16-byte accesses (C % 4 == 0, S % 4 == 0)
+__global__ void __launch_bounds__(256) from_cl4_kernel(const float *__restrict__ xcl, float *__restrict__ x,
+                                                       const float *__restrict__ bias, int C, int S) {
+    __shared__ float tile[TT][TT + 1];   // [s][c]
+    const int b = blockIdx.z;
+    const int s0 = blockIdx.x * TT, c0 = blockIdx.y * TT;
+    const float *ib = xcl + (size_t)b * C * S;
+    float *ob = x + (size_t)b * C * S;
+    const int u = threadIdx.x & 15, r0 = threadIdx.x >> 4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int sl = r0 + 16 * k, s = s0 + sl, c = c0 + 4 * u;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (s < S && c < C) v = *reinterpret_cast<const float4 *>(ib + (size_t)s * C + c);
+        tile[sl][4 * u] = v.x;
+        tile[sl][4 * u + 1] = v.y;
+        tile[sl][4 * u + 2] = v.z;
+        tile[sl][4 * u + 3] = v.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int cl = r0 + 16 * k, c = c0 + cl, s = s0 + 4 * u;
+        if (c < C && s < S) {
+            const float bv = bias != nullptr ? bias[c] : 0.f;
+            *reinterpret_cast<float4 *>(ob + (size_t)c * S + s) =
+                make_float4(tile[4 * u][cl] + bv, tile[4 * u + 1][cl] + bv, tile[4 * u + 2][cl] + bv,
+                            tile[4 * u + 3][cl] + bv);
+        }
+    }
+}
+
 // xcl [B][S][C] (A) -> x [B][C][S] (T), plus bias[c]
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) from_cl_kernel(const A *__restrict__ xcl, T *__restrict__ x,
@@ -198,6 +275,8 @@ __global__ void __launch_bounds__(1024) bias_grad_kernel(const T *__restrict__ g
     }
 }
 
+bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 unsigned grid_for(size_t n) {
     size_t b = (n + 255) / 256;
     if (b > 65536) b = 65536;
@@ -221,6 +300,12 @@ hipError_t by_dtype(int dtype, F &&f) {
 hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s,
                                    int *flag, const void *chk, size_t chk_n, float chk_limit) {
     if (chk != nullptr && (flag == nullptr || chk_n == 0)) chk = nullptr;
+    if (dtype == kF32 && C % 4 == 0 && Sn % 4 == 0 && al16(x) && al16(xcl)) {
+        dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B + (chk != nullptr ? 1 : 0));
+        hipLaunchKernelGGL(to_cl4_kernel, grid, dim3(256), 0, s, static_cast<const float *>(x), static_cast<float *>(xcl),
+                           C, Sn, flag, static_cast<const float *>(chk), chk_n, chk_limit);
+        return hipGetLastError();
+    }
     return by_dtype(dtype, [&](auto tv, auto av) {
         using T = decltype(tv);
         using A = decltype(av);
@@ -261,6 +346,12 @@ hipError_t launch_fill_zero_multi(const FillItem *items, int n, hipStream_t s) {
 
 hipError_t launch_from_channels_last(int dtype, const void *xcl, void *x, const void *bias, int B, int C, int Sn,
                                      hipStream_t s) {
+    if (dtype == kF32 && C % 4 == 0 && Sn % 4 == 0 && al16(x) && al16(xcl)) {
+        dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B);
+        hipLaunchKernelGGL(from_cl4_kernel, grid, dim3(256), 0, s, static_cast<const float *>(xcl),
+                           static_cast<float *>(x), static_cast<const float *>(bias), C, Sn);
+        return hipGetLastError();
+    }
     return by_dtype(dtype, [&](auto tv, auto av) {
         using T = decltype(tv);
         using A = decltype(av);
