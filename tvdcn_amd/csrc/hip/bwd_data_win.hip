@@ -122,10 +122,11 @@ __device__ __forceinline__ float row_sum4(float v) {
 // Z (B, G * Mg, Pn) -> zs [B][G][ms32][Pn][NP][32]: per pixel and 32-channel step, the NP pieces
 // of its 32 channels (zero past Mg), each as 4 lane groups of 8 (the 16x16x32 B-operand layout).
 // Block = 64 pixels of one (image, group, step), transposed through LDS.
+// (zvec: Pn % 4 == 0 and z aligned to 4 elements: the tile is read in 4-pixel vectors)
 template <typename T, int NP>
 __device__ __forceinline__ void z_split_block(long long bid, float *smem, const T *__restrict__ z,
                                               uint16_t *__restrict__ zs, int *flag, int G, int Mg, int Pn, int ms32,
-                                              int pblocks) {
+                                              int pblocks, bool zvec) {
     float(*tile)[65] = reinterpret_cast<float(*)[65]>(smem);   // [32][65]
     const int pb = (int)(bid % pblocks);
     const long long bgs = bid / pblocks;   // (b * G + grp) * ms32 + step
@@ -135,12 +136,25 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
     const long long b = bg / G;
     const int p0 = pb * 64;
     const T *src = z + ((size_t)b * G + grp) * (size_t)Mg * Pn;
-    for (int i = threadIdx.x; i < 32 * 64; i += 256) {
-        const int ml = i >> 6, pl = i & 63;
-        const int m = st * 32 + ml, p = p0 + pl;
-        float v = 0.f;
-        if (m < Mg && p < Pn) v = to_acc<float>(src[(size_t)m * Pn + p]);
-        tile[ml][pl] = v;
+    if (zvec) {
+        for (int i = threadIdx.x; i < 32 * 16; i += 256) {
+            const int ml = i >> 4, pl = 4 * (i & 15);
+            const int m = st * 32 + ml, p = p0 + pl;
+            Vec4<float> v{0.f, 0.f, 0.f, 0.f};
+            if (m < Mg && p < Pn) v = load4_t<float, T>(src + (size_t)m * Pn + p);   // all four inside
+            tile[ml][pl] = v.x;
+            tile[ml][pl + 1] = v.y;
+            tile[ml][pl + 2] = v.z;
+            tile[ml][pl + 3] = v.w;
+        }
+    } else {
+        for (int i = threadIdx.x; i < 32 * 64; i += 256) {
+            const int ml = i >> 6, pl = i & 63;
+            const int m = st * 32 + ml, p = p0 + pl;
+            float v = 0.f;
+            if (m < Mg && p < Pn) v = to_acc<float>(src[(size_t)m * Pn + p]);
+            tile[ml][pl] = v;
+        }
     }
     __syncthreads();
     const int pl = threadIdx.x >> 2, q = threadIdx.x & 3, p = p0 + pl;
@@ -974,11 +988,11 @@ template <typename T, int NP>
 __global__ void __launch_bounds__(256)
 data_prep_kernel(const T *__restrict__ z, uint16_t *__restrict__ zs, const T *__restrict__ w, uint16_t *__restrict__ wsp,
                  float *__restrict__ wd, int *flag, int G, int Mg, int Cg, int Pn, int Kn, int c_tiles, int ms32,
-                 int m_steps, int pblocks, long long nz, int nws) {
+                 int m_steps, int pblocks, long long nz, int nws, bool zvec) {
     __shared__ float smem[WL_TK * BC * 33];
     long long L = blockIdx.x;
     if (L < nz) {
-        z_split_block<T, NP>(L, smem, z, zs, flag, G, Mg, Pn, ms32, pblocks);
+        z_split_block<T, NP>(L, smem, z, zs, flag, G, Mg, Pn, ms32, pblocks, zvec);
         return;
     }
     L -= nz;
@@ -1056,7 +1070,8 @@ hipError_t launch_prep(const Geo &g, const WinTiles &t, const void *z, const voi
     hipLaunchKernelGGL((data_prep_kernel<T, NP>), dim3((unsigned)total), dim3(256), 0, s, static_cast<const T *>(z),
                        static_cast<uint16_t *>(zs), static_cast<const T *>(w), static_cast<uint16_t *>(wsp),
                        static_cast<float *>(wd), flag, g.G, g.Mg, g.Cg, g.Pn, g.Kn, t.c_tiles, t.ms32, t.m_steps,
-                       pblocks, zblocks, (int)wblocks);
+                       pblocks, zblocks, (int)wblocks,
+                       g.Pn % 4 == 0 && reinterpret_cast<uintptr_t>(z) % (4 * sizeof(T)) == 0);
     return hipGetLastError();
 }
 
