@@ -1085,9 +1085,9 @@ int ilog2(int v) {
 
 WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_bytes, size_t cell_bytes,
                     long long cell_cap) {
-    // window = undeformed footprint of the box (low and high corners) plus a margin R per
-    // used axis, the largest R (up to 8, 32 in 1D) whose LDS fits beside fixed_bytes and
-    // whose cell count stays within cell_cap (0: no cap)
+    // window = undeformed footprint of the box (low and high corners) plus a margin R[e] per
+    // used axis: first the largest common R (up to 8, 32 in 1D) whose LDS fits beside
+    // fixed_bytes and whose cell count stays within cell_cap (0: no cap)
     WinTiles t = base;
     int need[3] = {1, 1, 1};
     for (int e = 3 - dim; e < 3; ++e) need[e] = (t.box[e] - 1) * g.st[e] + (g.K[e] - 1) * g.dil[e] + 2;
@@ -1112,10 +1112,28 @@ WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_by
             }
         }
     }
+    // then, while the margins are thin (under 3 cells), one more cell on the axis of the
+    // smallest window extent that still fits: a short axis (3D boxes are 4 deep) sends the
+    // most samples past its faces
+    int Re[3] = {R, R, R};
+    if (t.cells > 0) {
+        for (;;) {
+            int best = -1;
+            for (int e = 3 - dim; e < 3; ++e) {
+                const int ext = need[e] + 2 * Re[e];
+                if (Re[e] >= 3 || (long long)t.cells / ext * (ext + 2) > max_cells) continue;
+                if (best < 0 || ext < need[best] + 2 * Re[best]) best = e;
+            }
+            if (best < 0) break;
+            const int ext = need[best] + 2 * Re[best];
+            t.cells = t.cells / ext * (ext + 2);
+            ++Re[best];
+        }
+    }
     for (int e = 0; e < 3; ++e) {
         const bool used = e >= 3 - dim;
-        t.R[e] = (used && t.cells) ? R : 0;
-        t.WE[e] = (used && t.cells) ? need[e] + 2 * R : 1;
+        t.R[e] = (used && t.cells) ? Re[e] : 0;
+        t.WE[e] = (used && t.cells) ? need[e] + 2 * Re[e] : 1;
     }
     return t;
 }
