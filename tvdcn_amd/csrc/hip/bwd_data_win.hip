@@ -223,6 +223,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     float *xwin = smem + FIXED_WORDS;                          // [cells][XS] X window (COORD)
     int *iwin = reinterpret_cast<int *>(xwin + (COORD && !xg ? wt.cells * XS : 0));   // [BC][cst] fixed point
     const int cst = fix_stride(wt.cells);
+    // [2][tpp][npiece][512] staged weight blocks of the 16-bit K loop (wt.wstage > 0)
+    uint16_t *wst = reinterpret_cast<uint16_t *>(iwin + (SCATTER ? BC * cst : 0));
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -479,12 +481,83 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     for (int k = 0; k < NP; ++k) zc[pb][k] = zn[pb][k];
             }
         };
+        // ---- 16-bit K loop with the weight blocks staged in LDS: a step's block (the pass's
+        //      taps x NP pieces, 1 KB each, contiguous in the split layout) is the same for all
+        //      eight waves; read straight from global memory it went eight times through the
+        //      vector memory path. The next step's block is copied global -> LDS (one 1 KB wave
+        //      instruction per piece, spread over the waves) while this step's MFMAs run, into
+        //      the other half of a double buffer; one barrier per step publishes it.
+        auto kloop16s = [&]() {
+            constexpr int NP = npiece_of<T>();
+            const int ms32 = wt.ms32;
+            const size_t zstep = (size_t)g.Pn * (NP * 32);
+            const uint16_t *zl[PB];
+#pragma unroll
+            for (int pb = 0; pb < PB; ++pb)
+                zl[pb] = zs + ((size_t)(b * g.G + grp) * ms32 * g.Pn + (zp[pb] < 0 ? 0 : zp[pb])) * (NP * 32) + q * 8;
+            auto zfrag = [&](int st, uint4 (&f)[PB][NP]) {
+#pragma unroll
+                for (int pb = 0; pb < PB; ++pb)
+#pragma unroll
+                    for (int k = 0; k < NP; ++k)
+                        f[pb][k] = *reinterpret_cast<const uint4 *>(zl[pb] + (size_t)st * zstep + k * 32);
+            };
+            const uint16_t *wblk = wsplit + ((size_t)(grp * wt.c_tiles + ct) * ms32 * g.Kn + t0) * (NP * 512);
+            const int blk = wt.tpp * (NP * 512);   // buffer stride (16-bit values)
+            const int npc = ntaps * NP;            // 1 KB pieces per step
+            auto stage = [&](int st, int buf) {
+                const uint16_t *src = wblk + (size_t)st * g.Kn * (NP * 512);
+                uint16_t *dst = wst + buf * blk;
+                for (int i = wave; i < npc; i += NW)
+                    __builtin_amdgcn_global_load_lds(src + i * 512 + lane * 8, dst + i * 512, 16, 0, 0);
+            };
+            auto wread = [&](const uint16_t *bb, int tl, uint4 (&f)[NP]) {
+                const uint16_t *p = bb + tl * (NP * 512) + lane * 8;
+#pragma unroll
+                for (int k = 0; k < NP; ++k) f[k] = *reinterpret_cast<const uint4 *>(p + k * 512);
+            };
+            // the staged block's loads done, then the workgroup barrier that publishes it
+            auto publish = [&]() {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+            };
+            uint4 zc[PB][NP], zn[PB][NP], wa[2][NP];
+            stage(0, 0);
+            zfrag(0, zc);
+            publish();
+            for (int st = 0; st < ms32; ++st) {
+                if (st + 1 < ms32) stage(st + 1, (st + 1) & 1);
+                zfrag(min(st + 1, ms32 - 1), zn);
+                issue_fence();
+                const uint16_t *bb = wst + (st & 1) * blk;
+                wread(bb, 0, wa[0]);
+#pragma unroll
+                for (int tp = 0; tp < TMAX; ++tp) {
+                    if (tp >= ntaps) break;
+                    // tap tp + 1's fragments read from LDS before tap tp's MFMAs
+                    if (tp + 1 < ntaps) wread(bb, tp + 1, wa[(tp + 1) & 1]);
+#pragma unroll
+                    for (int pb = 0; pb < PB; ++pb)
+                        acc[tp][pb] = mfma16x16x32_np<T, NP>(wa[tp & 1], zc[pb], acc[tp][pb]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // the next block landed, every wave done with this one
+                publish();
+#pragma unroll
+                for (int pb = 0; pb < PB; ++pb)
+#pragma unroll
+                    for (int k = 0; k < NP; ++k) zc[pb][k] = zn[pb][k];
+            }
+        };
         // (opaque to the optimiser: the choice is made per pass rather than by two copies of
         // the whole pass loop)
         int use16 = __builtin_amdgcn_readfirstlane(use16_flag);
         asm volatile("" : "+s"(use16));
         if (use16) {
-            kloop16();
+            if (wt.wstage > 0)
+                kloop16s();
+            else
+                kloop16();
         } else {
             const bool mpad = g.Mg % BM != 0;
             if (ntaps == TMAX && !mpad)
@@ -1006,7 +1079,8 @@ data_prep_kernel(const T *__restrict__ z, uint16_t *__restrict__ zs, const T *__
 template <bool SCATTER, bool COORD> size_t lds_bytes(const WinTiles &t) {
     return ((size_t)FIXED_WORDS + (SCATTER ? (size_t)BC * fix_stride(t.cells) : 0) +
             (COORD && !t.xglobal ? (size_t)t.cells * XS : 0)) *
-           sizeof(float);
+               sizeof(float) +
+           (size_t)t.wstage;
 }
 
 template <int DIM, typename T, bool SCATTER, bool COORD>
@@ -1177,13 +1251,32 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
     // per window cell: the fixed-point accumulators (scatter) and / or the X values
     // (offset/mask gradients), as the launches this plan serves need them
     // (+ BC * 16 words: the fixed-point window's stride rounding)
-    t = win_resize(t, g, dim, (FIXED_WORDS + (scatter ? BC * 16 : 0)) * sizeof(float),
-                   ((scatter ? BC : 0) + (coord ? XS : 0)) * sizeof(float));
+    const size_t fixed = (FIXED_WORDS + (scatter ? BC * 16 : 0)) * sizeof(float);
+    const size_t cell = ((scatter ? BC : 0) + (coord ? XS : 0)) * sizeof(float);
+    const WinTiles base = t;
+    t = win_resize(base, g, dim, fixed, cell);
     const int npass = (g.Kn + WIN_TMAX - 1) / WIN_TMAX;
     t.tpp = (g.Kn + npass - 1) / npass;
+    t.npiece = dtype == kF32 ? 3 : 1;
+    // 1D / 2D passes of nine taps: the K loop's weight blocks staged in LDS when the window
+    // keeps a margin of min(R, 4) cells beside the buffers (3D: short K loops, and the window
+    // needs the room; passes of fewer taps: measured slower, a step's MFMAs then cover too
+    // little of the next block's load and barrier)
+    t.wstage = 0;
+    if (dim < 3 && t.cells > 0 && t.tpp == WIN_TMAX) {
+        const int stage = 2 * t.tpp * t.npiece * 1024;
+        WinTiles ws = win_resize(base, g, dim, fixed + stage, cell);
+        bool keep = ws.cells > 0;
+        for (int e = 3 - dim; e < 3; ++e) keep = keep && ws.R[e] >= std::min(t.R[e], 4);
+        if (keep) {
+            ws.tpp = t.tpp;
+            ws.npiece = t.npiece;
+            ws.wstage = stage;
+            t = ws;
+        }
+    }
     t.chunk_elems = (size_t)g.G * t.c_tiles * t.m_steps * g.Kn * BC * BM;
     t.ms32 = (g.Mg + 31) / 32;
-    t.npiece = dtype == kF32 ? 3 : 1;
     t.zs_elems = (size_t)g.B * g.G * t.ms32 * g.Pn * t.npiece * 32;
     t.ws_elems = (size_t)g.G * t.c_tiles * t.ms32 * g.Kn * t.npiece * 512;
     t.ok = true;
