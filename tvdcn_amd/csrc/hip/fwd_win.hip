@@ -257,14 +257,18 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 constexpr int NI = MB * NP;          // 1 KB pieces per step
                 constexpr int WBLK = NI * 512;       // 16-bit values per step
                 uint16_t *wst = reinterpret_cast<uint16_t *>(xwin + (size_t)wt.cells * XS);   // [2][U][WBLK]
-                auto step_cs = [&](int k) { return cs_lo + k / npair; };
-                auto step_j = [&](int k) { return k - (k / npair) * npair; };
+                // (slice, pair) of the next step to stage, advanced step by step (no divisions)
+                int s_cs = cs_lo, s_j = 0;
                 auto stage_unit = [&](int u, int buf) {
 #pragma unroll
                     for (int su = 0; su < U; ++su) {
                         const int k = u * U + su;
                         if (k >= nsteps) break;
-                        const uint16_t *blk = wptr16(step_cs(k), step_j(k));
+                        const uint16_t *blk = wptr16(s_cs, s_j);
+                        if (++s_j == npair) {
+                            s_j = 0;
+                            ++s_cs;
+                        }
                         uint16_t *dst = wst + (buf * U + su) * WBLK;
                         for (int i = wave; i < NI; i += NW)
                             __builtin_amdgcn_global_load_lds(blk + i * 512 + lane * 8, dst + i * 512, 16, 0, 0);
@@ -303,11 +307,12 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 publish();
                 // the next slice's X window is requested two pair steps before it is needed
                 const int pf_j = max(npair - 2, 0);
+                // (slice, pair) of step k, advanced step by step
+                int cs = cs_lo, j = 0;
                 for (int k = 0; k < nsteps; ++k) {
                     const bool more = k + 1 < nsteps;
                     const int u = k / U, su = k - u * U;
-                    const int cs = step_cs(k), j = step_j(k);
-                    const int jn = more ? step_j(k + 1) : 0;
+                    const int jn = j + 1 == npair ? 0 : j + 1;
                     if (su == 0 && (u + 1) * U < nsteps) stage_unit(u + 1, (u + 1) & 1);
                     if (j == pf_j && cs + 1 < cs_hi) prefetch_x(cs + 1);
                     build_pair(cs, j, bv);
@@ -318,9 +323,11 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                     if (unit_end) publish();
                     if (more && jn == 0) {
                         if (!unit_end) __syncthreads();   // every wave done reading the window
-                        open_slice(step_cs(k + 1), t0, ntaps);
+                        open_slice(cs + 1, t0, ntaps);
                         __syncthreads();
                     }
+                    j = jn;
+                    if (jn == 0) ++cs;
                 }
             } else {
                 // (the weight's staging would cost the window its margin: fragments straight from
@@ -350,11 +357,11 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 open_slice(cs_lo, t0, ntaps);
                 __syncthreads();
                 const int pf_j = max(npair - 2, 0);
+                int cs = cs_lo, j = 0;   // step k's (slice, pair), advanced step by step
                 for (int k = 0; k < nsteps; ++k) {
                     const bool more = k + 1 < nsteps;
-                    const int kn = k + 1, csn_r = kn / npair, jn = kn - csn_r * npair;
-                    const int cs_r = k / npair, j = k - cs_r * npair;
-                    const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
+                    const int jn = j + 1 == npair ? 0 : j + 1;
+                    const int csn = jn == 0 ? cs + 1 : cs;
                     if (j == pf_j && cs + 1 < cs_hi) prefetch_x(cs + 1);
                     build_pair(cs, j, bv);
                     const uint16_t *pcur = wptr16(cs, j);
@@ -364,6 +371,8 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                         open_slice(csn, t0, ntaps);
                         __syncthreads();
                     }
+                    cs = csn;
+                    j = jn;
                 }
             }
         }
@@ -410,11 +419,11 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
             __syncthreads();   // previous pass done with the tables
             open_slice(cs_lo, t0, ntaps);
             __syncthreads();
+            int cs = cs_lo, tg = 0;   // group k's (slice, tap group), advanced group by group
             for (int k = 0; k < ngroups; ++k) {
                 const bool more = k + 1 < ngroups;
-                const int cs_r = k / ngr, tg = k - cs_r * ngr;
-                const int csn_r = (k + 1) / ngr, tgn = k + 1 - csn_r * ngr;
-                const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
+                const int tgn = tg + 1 == ngr ? 0 : tg + 1;
+                const int csn = tgn == 0 ? cs + 1 : cs;
                 acc4 bq[4][PB];
                 build_group(cs, tg, ntaps, bq);
                 const int nt = min(4, ntaps - tg * 4);
@@ -433,6 +442,8 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                     open_slice(csn, t0, ntaps);
                     __syncthreads();
                 }
+                cs = csn;
+                tg = tgn;
             }
         }
     } else if (use16_flag) {
@@ -455,23 +466,25 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
             // the next slice's X window is requested PF steps before it is needed (memory
             // latency exceeds one step's MFMAs), or at the slice's first step when shorter
             const int pf_tl = max(ntaps - PF, 0);
+            int cs = cs_lo, tl = 0;   // step k's (slice, tap), advanced step by step
             for (int k = 0; k < nsteps; ++k) {
                 const bool more = k + 1 < nsteps;
-                const int kn = k + 1, csn_r = kn / ntaps, tln = kn - csn_r * ntaps;
-                const int cs_r = k / ntaps;
-                const int cs = cs_lo + cs_r, csn = cs_lo + csn_r;
+                const int tln = tl + 1 == ntaps ? 0 : tl + 1;
+                const int csn = tln == 0 ? cs + 1 : cs;
                 const bool new_slice = more && tln == 0;
-                if (k - cs_r * ntaps == pf_tl && cs + 1 < cs_hi) prefetch_x(cs + 1);
+                if (tl == pf_tl && cs + 1 < cs_hi) prefetch_x(cs + 1);
                 if (more && !new_slice) build_b(csn, tln, bnxt);
-                mfma_step(bcur, wa, more ? wptr(csn, t0 + tln) : wptr(cs, t0 + k - cs_r * ntaps));
+                mfma_step(bcur, wa, more ? wptr(csn, t0 + tln) : wptr(cs, t0 + tl));
                 if (new_slice) {
                     __syncthreads();   // every wave done reading the current window
                     open_slice(csn, t0, ntaps);
                     __syncthreads();
                     build_b(csn, 0, bnxt);
                 }
-    #pragma unroll
+#pragma unroll
                 for (int pb = 0; pb < PB; ++pb) bcur[pb] = bnxt[pb];
+                cs = csn;
+                tl = tln;
             }
         }
     }
