@@ -1260,8 +1260,8 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
     t.npiece = dtype == kF32 ? 3 : 1;
     // 1D / 2D passes of nine taps: the K loop's weight blocks staged in LDS when the window
     // keeps a margin of min(R, 4) cells beside the buffers (3D: short K loops, and the window
-    // needs the room; passes of fewer taps: measured slower, a step's MFMAs then cover too
-    // little of the next block's load and barrier)
+    // needs the room; five-tap 1D passes ran slower staged, with two buffers or with three
+    // and each block requested two steps ahead, so shorter passes keep the direct loads)
     t.wstage = 0;
     if (dim < 3 && t.cells > 0 && t.tpp == WIN_TMAX) {
         const int stage = 2 * t.tpp * t.npiece * 1024;
