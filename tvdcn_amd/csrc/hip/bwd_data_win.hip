@@ -724,6 +724,26 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
         }
 
         // ---- epilogue: every wave walks its own pixels tap by tap, no barriers -------
+        // 2D offset / mask gradients: the next (tap, pixel block)'s record and corner X (fast
+        // records; a clamped cell otherwise) are read from LDS at the end of the current one,
+        // so their latency overlaps its reductions and atomics (cfg2 data gradient -2%; 1D,
+        // whose epilogue is a tenth of the kernel, measured 0.6% slower with it)
+        constexpr bool XPF = DIM == 2 && COORD;
+        constexpr int NFX = DIM == 2 ? 4 : 2;
+        acc4 rn = acc4{0.f, 0.f, 0.f, 0.f};
+        acc4 xn[XPF ? NFX : 1];
+        auto x_prefetch = [&](int tl, int pb) {
+            if constexpr (XPF) {
+                rn = geo[tl * BPX + wave * (PB * 16) + pb * 16 + (lane & 15)];
+                const int f = max(rec_fast_cell<DIM>(rn), 0);
+#pragma unroll
+                for (int k = 0; k < NFX; ++k) {
+                    const int cell = f + (k & 1) + (k >> 1) * wt.WE[2];
+                    xn[k] = *reinterpret_cast<const acc4 *>(xwin + cell * XS + mq);
+                }
+            }
+        };
+        if constexpr (XPF) x_prefetch(0, 0);
         for (int tl = 0; tl < ntaps; ++tl) {
             const int t = t0 + tl;
             acc4 gt[PB];
@@ -745,7 +765,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 #pragma unroll
             for (int pb = 0; pb < PB; ++pb) {
                 const int i = wave * (PB * 16) + pb * 16 + (lane & 15);
-                const acc4 r = geo[tl * BPX + i];
+                const acc4 r = XPF ? rn : geo[tl * BPX + i];
                 const float mk = rec_mask<DIM>(r);
                 const acc4 gv = gt[pb];
                 const int fc = rec_fast_cell<DIM>(r);
@@ -837,7 +857,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                         float gk[NF];
 #pragma unroll
                         for (int k = 0; k < NF; ++k) {
-                            const acc4 x = *reinterpret_cast<const acc4 *>(xwin + cell[k] * XS + mq);
+                            const acc4 x = XPF ? xn[XPF ? k : 0] : *reinterpret_cast<const acc4 *>(xwin + cell[k] * XS + mq);
                             gk[k] = gv[0] * x[0] + gv[1] * x[1] + gv[2] * x[2] + gv[3] * x[3];
                         }
                         if constexpr (DIM == 2) {
@@ -950,6 +970,12 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     }
                 }
 
+                if constexpr (XPF) {
+                    if (pb + 1 < PB)
+                        x_prefetch(tl, pb + 1);
+                    else if (tl + 1 < ntaps)
+                        x_prefetch(tl + 1, 0);
+                }
                 if constexpr (COORD) {
 #pragma unroll
                     for (int a = 0; a <= DIM; ++a) {
