@@ -439,3 +439,17 @@ def test_large_fp32_operands_take_the_fp32_loop(what):
     for name, gr, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
         e = rel_err(gr, r)
         assert e < TOL[torch.float32][1], f"grad_{name} rel err {e}"
+
+
+@pytest.mark.parametrize("dim,transposed,dtype", [(1, False, torch.float32), (1, True, torch.float32),
+                                                  (1, False, torch.float16), (2, False, torch.bfloat16)])
+def test_staged_weight_blocks_nine_tap_passes(dim, transposed, dtype):
+    """Nine-tap passes stage the data gradient's weight blocks in LDS (double-buffered, one
+    barrier per 32-channel step): several steps, a GEMM side off the step size (zero rows),
+    the conv backward and the transposed forward (scatter-only plan)."""
+    kernel = [9] if dim == 1 else [3, 3]
+    in_size = [200] if dim == 1 else [20, 18]
+    case = make_case(dim, transposed, batch=2, cin=48, cout=80, kernel=kernel, stride=[1] * dim,
+                     padding=[k // 2 for k in kernel], dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim,
+                     seed=610 + dim + 2 * transposed, offset_scale=2.0)
+    check(case, dtype)
