@@ -309,12 +309,58 @@ __global__ void __launch_bounds__(256) weight_reduce_kernel(const A *__restrict_
     }
 }
 
+// The same sum for Cg % 4 == 0 and 16-byte aligned partials: a block holds 4 rows (grp, t, m) of
+// 64 threads, each thread 4 consecutive channels per 16-byte load; the row's split range is
+// formed once per row (no per-element index divisions)
+template <typename T, typename A>
+__global__ void __launch_bounds__(256) weight_reduce4_kernel(const A *__restrict__ part, T *__restrict__ gw,
+                                                             int k_splits, int G, int Kn, int Mg, int Cg, int ups,
+                                                             int n_sp, int tpp, bool accumulate) {
+    const int rows = G * Kn * Mg;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int m = r % Mg;
+    const int t = (r / Mg) % Kn;
+    const int grp = r / (Mg * Kn);
+    int ks0 = 0, ks1 = k_splits;
+    if (ups > 0) {
+        const unsigned pass = (unsigned)(t / tpp);
+        ks0 = (int)(pass * (unsigned)n_sp / (unsigned)ups);
+        ks1 = min(k_splits, (int)(((pass + 1u) * (unsigned)n_sp - 1u) / (unsigned)ups) + 1);
+    }
+    const size_t per_split = (size_t)rows * Cg;
+    const A *src = part + (size_t)r * Cg;   // layout [ks][grp][t][m][c]: row r = (grp * Kn + t) * Mg + m
+    T *dst = gw + ((size_t)grp * Mg + m) * Cg * Kn + t;
+    for (int c = 4 * (threadIdx.x & 63); c < Cg; c += 256) {
+        Vec4<A> sum{A(0), A(0), A(0), A(0)};
+        for (int ks = ks0; ks < ks1; ++ks) {
+            const Vec4<A> v = *reinterpret_cast<const Vec4<A> *>(src + ks * per_split + c);
+            sum.x += v.x;
+            sum.y += v.y;
+            sum.z += v.z;
+            sum.w += v.w;
+        }
+        const A sv[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            T *o = dst + (size_t)(c + j) * Kn;
+            *o = from_acc<T, A>(accumulate ? to_acc<A>(*o) + sv[j] : sv[j]);
+        }
+    }
+}
+
 template <typename T, typename A>
 hipError_t launch_reduce(const Geo &g, int k_splits, const void *part, void *gw, bool accumulate, hipStream_t s, int ups,
                          int n_sp, int tpp) {
     if (ups > 0 && (n_sp <= 0 || tpp <= 0)) return hipErrorInvalidValue;
     const size_t n = (size_t)g.G * g.Kn * g.Mg * g.Cg;
     if (n > (size_t)INT_MAX) return hipErrorInvalidValue;
+    if (g.Cg % 4 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0) {
+        const unsigned blocks = (unsigned)(((size_t)g.G * g.Kn * g.Mg + 3) / 4);
+        hipLaunchKernelGGL((weight_reduce4_kernel<T, A>), dim3(blocks), dim3(256), 0, s, static_cast<const A *>(part),
+                           static_cast<T *>(gw), k_splits, g.G, g.Kn, g.Mg, g.Cg, ups, n_sp, tpp, accumulate);
+        return hipGetLastError();
+    }
     const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL((weight_reduce_kernel<T, A>), dim3(blocks), dim3(256), 0, s, static_cast<const A *>(part),
                        static_cast<T *>(gw), k_splits, g.G, g.Kn, g.Mg, g.Cg, ups, n_sp, tpp, accumulate);

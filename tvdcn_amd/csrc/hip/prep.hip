@@ -202,10 +202,17 @@ struct FillSet {
 };
 __global__ void __launch_bounds__(256) fill_zero_multi_kernel(const FillSet f) {
     const size_t total = f.start[f.n];
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-        int k = 0;
-        while (k + 1 < f.n && i >= f.start[k + 1]) ++k;
-        f.body[k][i - f.start[k]] = uint4{0u, 0u, 0u, 0u};
+    const size_t nt = (size_t)gridDim.x * blockDim.x;
+    // four 16-byte stores per thread and round (a grid of a few thousand blocks)
+    for (size_t i0 = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i0 < total; i0 += 4 * nt) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const size_t i = i0 + u * nt;
+            if (i >= total) break;
+            int k = 0;
+            while (k + 1 < f.n && i >= f.start[k + 1]) ++k;
+            f.body[k][i - f.start[k]] = uint4{0u, 0u, 0u, 0u};
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x < 2 * kFillMax * 8) {
         const int e = threadIdx.x >> 3, j = threadIdx.x & 7;
@@ -340,7 +347,8 @@ hipError_t launch_fill_zero_multi(const FillItem *items, int n, hipStream_t s) {
     }
     if (f.n == 0) return hipSuccess;
     f.start[f.n] = total;
-    hipLaunchKernelGGL(fill_zero_multi_kernel, dim3(grid_for(total > 0 ? total : 1)), dim3(256), 0, s, f);
+    const size_t blocks = std::min<size_t>(std::max<size_t>((total + 1023) / 1024, 1), 4096);
+    hipLaunchKernelGGL(fill_zero_multi_kernel, dim3((unsigned)blocks), dim3(256), 0, s, f);
     return hipGetLastError();
 }
 
