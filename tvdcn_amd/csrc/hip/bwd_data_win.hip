@@ -128,12 +128,14 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
                                               uint16_t *__restrict__ zs, int *flag, int G, int Mg, int Pn, int ms32,
                                               int pblocks, bool zvec) {
     float(*tile)[65] = reinterpret_cast<float(*)[65]>(smem);   // [32][65]
-    const int pb = (int)(bid % pblocks);
-    const long long bgs = bid / pblocks;   // (b * G + grp) * ms32 + step
-    const int st = (int)(bgs % ms32);
-    const long long bg = bgs / ms32;
-    const int grp = (int)(bg % G);
-    const long long b = bg / G;
+    // (the block index is a grid index: 32-bit division, not the 64-bit sequence)
+    const unsigned ub = (unsigned)bid;
+    const int pb = (int)(ub % (unsigned)pblocks);
+    const unsigned bgs = ub / (unsigned)pblocks;   // (b * G + grp) * ms32 + step
+    const int st = (int)(bgs % (unsigned)ms32);
+    const unsigned bg = bgs / (unsigned)ms32;
+    const int grp = (int)(bg % (unsigned)G);
+    const unsigned b = bg / (unsigned)G;
     const int p0 = pb * 64;
     const T *src = z + ((size_t)b * G + grp) * (size_t)Mg * Pn;
     if (zvec) {

@@ -520,10 +520,11 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
 template <typename T>
 __device__ __forceinline__ void fwd_weight_f32(const T *__restrict__ w, float *__restrict__ wp, int G, int Mg, int Cg,
                                                int Kn, int slices, int Mg_pad) {
-    const size_t total = (size_t)G * slices * Kn * Mg_pad * BC;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    // 32-bit index arithmetic (the launcher refuses layouts of 2^31 elements or more)
+    const unsigned total = (unsigned)G * slices * Kn * Mg_pad * BC;
+    for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
         const int ci = (int)(i % BC);
-        size_t r = i / BC;
+        unsigned r = i / BC;
         const int m = (int)(r % Mg_pad);   // row blocks of 16 are consecutive: m = block * 16 + row
         r /= Mg_pad;
         const int t = (int)(r % Kn);
@@ -553,11 +554,11 @@ __global__ void __launch_bounds__(256)
 fwd_w16_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, int G, int Mg, int Cg, int Kn, int slices,
                int nmb, int tpp, int hp, int pp, float *__restrict__ wp) {
     if (wp != nullptr) fwd_weight_f32<T>(w, wp, G, Mg, Cg, Kn, slices, nmb * 16);
-    const size_t total = (size_t)G * slices * pp * nmb * 64;
+    const unsigned total = (unsigned)G * slices * pp * nmb * 64;
     bool bad = false;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
         const int l = (int)(i & 63);
-        size_t r = i >> 6;
+        unsigned r = i >> 6;
         const int mb = (int)(r % nmb);
         r /= nmb;
         const int pq = (int)(r % pp);
@@ -681,6 +682,8 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     f.hp = (wt.tpp + 1) / 2;
     f.pp = (g.Kn + wt.tpp - 1) / wt.tpp * f.hp;
     f.w16_elems = dim < 3 ? (size_t)g.G * slices * f.pp * (f.Mg_pad / 16) * f.npiece * 512 : 0;
+    // the layout kernels index in 32 bits
+    if ((size_t)g.G * slices * g.Kn * f.Mg_pad * BC > (size_t)INT_MAX || f.w16_elems / 8 > (size_t)INT_MAX) return f;
     f.ok = true;
     return f;
 }
