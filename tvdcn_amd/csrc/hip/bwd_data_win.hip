@@ -254,7 +254,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
         if (!xg) fill_xwin(g, wt, tile, xb, xwin, tid, NT);
     }
     if constexpr (SCATTER) {
-        for (int i = tid; i < BC * cst; i += NT) iwin[i] = 0;
+        // 16-byte stores: BC * cst is a multiple of 64 words and the window is 16-byte aligned
+        for (int i = tid; i < BC * cst / 4; i += NT) reinterpret_cast<uint4 *>(iwin)[i] = uint4{0u, 0u, 0u, 0u};
         if (tid < BC) {
             bmax[tid] = 0;
             bexp[tid] = 0u;
