@@ -405,7 +405,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
-              f"(the path would shard over the batch, see DESIGN.md)", file=sys.stderr)
+              f"(the path would shard over the batch: independent images, one all-reduce of the weight and "
+              f"bias gradients)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
