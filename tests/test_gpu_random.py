@@ -94,3 +94,14 @@ def test_random_medium_problem_fp32(seed):
         if r is not None:
             e = rel_err(gr, r)
             assert e < 1e-3 if name == "offset" else e < 2e-4, f"grad_{name} rel err {e}"
+
+
+@pytest.mark.parametrize("seed", [6391, 11239, 12803])
+def test_random_problem_without_a_window_fp32(seed):
+    """3D transposed problems on tiny input grids (an axis of 1 or 2 cells): the 256-pixel tile box
+    stretches along the long axis and no window fits its footprint. Such plans take the unwindowed
+    kernels (a zero-cell window still counted a corner at its origin cell as inside and read LDS that
+    was never filled)."""
+    dim, transposed, params = random_case(seed)
+    print(f"seed {seed}: dim {dim} transposed {transposed} {params}", flush=True)
+    check(make_case(dim, transposed, **params), torch.float32)

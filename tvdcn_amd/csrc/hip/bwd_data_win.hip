@@ -1308,7 +1308,9 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
     t.ms32 = (g.Mg + 31) / 32;
     t.zs_elems = (size_t)g.B * g.G * t.ms32 * g.Pn * t.npiece * 32;
     t.ws_elems = (size_t)g.G * t.c_tiles * t.ms32 * g.Kn * t.npiece * 512;
-    t.ok = true;
+    // no window at all (the footprint does not fit): a unit-extent window would still place a
+    // corner at its origin cell "inside" it, so these problems take the unwindowed kernels
+    t.ok = t.cells > 0;
     return t;
 }
 

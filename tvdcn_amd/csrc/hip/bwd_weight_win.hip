@@ -472,7 +472,7 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     w.ok = false;
     // needs the windowed tiling; GEMM sides up to 128 rows take 64-row tiles with the taps
     // split between two wave groups, larger ones 256-row tiles
-    if (!wt.ok || g.Mg < 16 || weight_win_fixed_bytes(g, dim, wt.tpp) + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
+    if (!wt.ok || wt.cells == 0 || g.Mg < 16 || weight_win_fixed_bytes(g, dim, wt.tpp) + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
         return w;
     w.tg = g.Mg <= 128 ? 2 : 1;
     const int rows = w.tg == 2 ? rows_of<1, 2>() : rows_of<2, 1>();

@@ -175,6 +175,9 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl, int64_t batch) {
     pl.wn_s = plan_data_win(g, pl.dtype, pl.dim, true, true);
     pl.wn_x = plan_data_win(g, pl.dtype, pl.dim, true, false);
     pl.wn_c = plan_data_win(g, pl.dtype, pl.dim, false, true);
+    // the launches use all three sizes of the windowed plan (and the operand layouts prepared for
+    // wn_s): one without a window disables them all
+    if (!pl.wn_s.ok || !pl.wn_x.ok || !pl.wn_c.ok) pl.wn_s.ok = pl.wn_x.ok = pl.wn_c.ok = false;
     // a margin under 2 cells loses a large share of the corners to global atomics
     // (3D: the window grows with the cube of its extent); two launches recompute the
     // grad-columns contraction but each gets about twice the window

@@ -648,6 +648,7 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     // (3D: one more cell, the zero cell)
     const int zc = dim == 3 ? 1 : 0;
     wt = win_resize(base, g, dim, (size_t)(GEO_WORDS + zc * XS) * sizeof(float), XS * sizeof(float), max_cells - zc);
+    if (wt.cells == 0) return f;   // no window fits: the unwindowed forward
     // 1D / 2D: two staging buffers of the 16-bit loop's weight blocks (8 row blocks x npiece KB
     // each: one step of 128-row tiles or two of 64-row tiles) when the window keeps a margin of
     // min(R, 4) cells beside them (a smaller window sends samples to global memory)
