@@ -1,5 +1,6 @@
 """Shared test helpers: case construction, norm-wise error metrics, the C ABI descriptor."""
 import ctypes
+import itertools
 
 import torch
 
@@ -64,6 +65,52 @@ def make_case(dim, transposed=False, batch=2, cin=4, cout=6, groups=1, og=1, mg=
     return dict(dim=dim, transposed=transposed, input=cast(x), weight=cast(w), offset=cast(off), mask=cast(msk),
                 bias=cast(b), stride=stride, padding=padding, dilation=dilation, output_padding=out_pad,
                 groups=groups, out_shape=[batch, cout] + o)
+
+
+def position_type(dtype):
+    """The float type in which the kernels form a sampling position `base + offset` for inputs of
+    `dtype`: the reference's own arithmetic for float32 and float16 (an integer base plus a scalar_t
+    offset, one rounding to scalar_t: cpu/deform_conv2d_common_kernels.cpp:407-411,
+    cuda/deform_conv2d_common_kernels.cu:170-178); float32 for bfloat16, which the reference lacks;
+    None for float64 (the oracle's own precision)."""
+    return {torch.float32: torch.float32, torch.float16: torch.float16, torch.bfloat16: torch.float32}.get(dtype)
+
+
+def rounded_position_offsets(case, offset, ptype):
+    """Offsets (float64) that put the float64 oracle's sampling positions where `ptype` arithmetic
+    puts them: base + offset rounded once to `ptype`, base = p * stride - padding + tap * dilation on
+    each axis of the column grid. The gradient reported for an offset is the one at that position.
+    Where the exact position lies within half a unit in the last place of an integer, the rounded
+    one is that integer: the sample then takes the other cell, and the offset gradient the other
+    one-sided derivative, as the reference's float path does."""
+    dim = case["dim"]
+    ks = list(case["weight"].shape[2:])
+    grid = list(offset.shape[2:])
+    B, ch = offset.shape[:2]
+    kn = 1
+    for k in ks:
+        kn *= k
+    og = ch // (dim * kn)
+    taps = torch.tensor(list(itertools.product(*[range(k) for k in ks])))   # (kn, dim)
+    pos = offset.double().reshape(B, og, kn, dim, *grid).clone()
+    for a in range(dim):
+        shape = [1] * dim
+        shape[a] = grid[a]
+        p = torch.arange(grid[a], dtype=torch.float64).reshape(shape)
+        base = p * case["stride"][a] - case["padding"][a] + \
+            taps[:, a].double().reshape([kn] + [1] * dim) * case["dilation"][a]   # (kn, *grid)
+        exact = pos[:, :, :, a] + base
+        pos[:, :, :, a] = exact.to(ptype).double() - base
+    return pos.reshape(offset.shape)
+
+
+def oracle_offsets(case, offset, dtype):
+    """The offsets to hand the float64 oracle for a run of the kernels in `dtype` (see
+    rounded_position_offsets); float64 offsets unchanged."""
+    ptype = position_type(dtype)
+    if offset is None or ptype is None:
+        return offset
+    return rounded_position_offsets(case, offset, ptype)
 
 
 class OracleDeformConv(torch.autograd.Function):

@@ -18,7 +18,7 @@ import torch.nn.functional as F
 
 import tvdcn
 from oracle import oracle
-from helpers import make_case, rel_err
+from helpers import make_case, oracle_offsets, rel_err
 
 NAMES = ("input", "weight", "offset", "mask", "bias")
 TOL = {torch.float64: (1e-10, 1e-10), torch.float32: (1e-5, 1e-4), torch.float16: (1e-2, 1e-2),
@@ -45,15 +45,9 @@ def run_cpu(case, dtype, grad_out=None):
     return out, [t.grad if t is not None else None for t in ts], grad_out
 
 
-def half_positions(case, offset):
-    from test_gpu_parity import half_position_offsets
-    return half_position_offsets(case, offset)
-
-
 def run_oracle(case, grad_out, dtype):
     args = [None if case[n] is None else case[n].to(dtype).double() for n in NAMES]
-    if dtype == torch.float16 and args[2] is not None:
-        args[2] = half_positions(case, args[2])
+    args[2] = oracle_offsets(case, args[2], dtype)
     kw = dict(stride=case["stride"], padding=case["padding"], dilation=case["dilation"], groups=case["groups"],
               transposed=case["transposed"], output_padding=case["output_padding"])
     return oracle.forward(case["dim"], *args, **kw), oracle.backward(case["dim"], grad_out.to(dtype).double(),

@@ -12,8 +12,8 @@ import torch
 
 import tvdcn
 from tvdcn.ops.deform_conv import _deform_conv_mask_activation
-from helpers import make_case, mask_activation_f64, oracle_conv, rel_err
-from test_gpu_parity import TOL, half_position_offsets
+from helpers import make_case, mask_activation_f64, oracle_conv, oracle_offsets, rel_err
+from test_gpu_parity import TOL
 
 pytestmark = pytest.mark.gpu
 
@@ -25,9 +25,10 @@ def _oracle_activated(case, dim, transposed, vals, activation, scale):
     """float64 reference on CPU leaves; returns (out, leaves)"""
     leaves = [None if v is None else v.detach().double().cpu().requires_grad_(True) for v in vals]
     x, w, o, logits, b = leaves
-    if o is not None and vals[2].dtype == torch.float16:
-        # float16 sampling positions are rounded to half precision (as the reference's c10::Half)
-        o = o + (half_position_offsets(case, o.detach()) - o.detach())
+    if o is not None:
+        # sampling positions rounded as the kernels form them (float16: to half precision, as the
+        # reference's c10::Half; float32 / bfloat16: to float32)
+        o = o + (oracle_offsets(case, o.detach(), vals[2].dtype) - o.detach())
     kn = 1
     for k in w.shape[2:]:
         kn *= k

@@ -3,8 +3,9 @@ tvdcn's CPU algorithm, itself pinned to the reference build and the golden fixtu
 
 Tolerances (norm-wise, see helpers.rel_err): float64 1e-9; float32 forward 1e-5 and
 backward 1e-4 (atomic ordering); float16 / bfloat16 1e-2 against the oracle run on
-the same rounded inputs (float16: and sampling positions rounded to half precision, as the
-reference's c10::Half arithmetic rounds them).
+the same rounded inputs. The oracle samples at the positions the kernels form: base + offset
+rounded once to float32 (float32, bfloat16) or to half precision (float16), as the reference's
+own float32 and c10::Half arithmetic rounds them (helpers.rounded_position_offsets).
 """
 import itertools
 
@@ -13,7 +14,7 @@ import torch
 
 import tvdcn
 from oracle import oracle
-from helpers import make_case, rel_err
+from helpers import make_case, oracle_offsets, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -42,37 +43,10 @@ def run_gpu(case, dtype, grad_out=None):
     return out, [t.grad if t is not None else None for t in ts], grad_out
 
 
-def half_position_offsets(case, offset):
-    """Offsets that put the float64 oracle's sampling positions where float16 arithmetic puts them:
-    base + offset rounded once to half precision, as the reference forms `y + offset` in c10::Half
-    (cpu/deform_conv2d_common_kernels.cpp:407-411, cuda/deform_conv2d_common_kernels.cu:170-178) and the
-    kernels do for float16 inputs. The gradient reported for an offset is the one at that position."""
-    dim = case["dim"]
-    ks = list(case["weight"].shape[2:])
-    grid = list(offset.shape[2:])
-    B, ch = offset.shape[:2]
-    kn = 1
-    for k in ks:
-        kn *= k
-    og = ch // (dim * kn)
-    taps = torch.tensor(list(__import__("itertools").product(*[range(k) for k in ks])))   # (kn, dim)
-    pos = offset.reshape(B, og, kn, dim, *grid).clone()
-    for a in range(dim):
-        shape = [1] * dim
-        shape[a] = grid[a]
-        p = torch.arange(grid[a], dtype=torch.float64).reshape(shape)
-        base = p * case["stride"][a] - case["padding"][a] + \
-            taps[:, a].double().reshape([kn] + [1] * dim) * case["dilation"][a]   # (kn, *grid)
-        exact = pos[:, :, :, a] + base
-        pos[:, :, :, a] = exact.to(torch.float16).double() - base
-    return pos.reshape(offset.shape)
-
-
 def run_oracle(case, grad_out, dtype):
     cast = (lambda t: None if t is None else t.to(dtype).double())
     args = [cast(case[n]) for n in ("input", "weight", "offset", "mask", "bias")]
-    if dtype == torch.float16 and args[2] is not None:
-        args[2] = half_position_offsets(case, args[2])
+    args[2] = oracle_offsets(case, args[2], dtype)
     kw = dict(stride=case["stride"], padding=case["padding"], dilation=case["dilation"], groups=case["groups"],
               transposed=case["transposed"], output_padding=case["output_padding"])
     out = oracle.forward(case["dim"], *args, **kw)

@@ -7,8 +7,8 @@ import random
 import pytest
 import torch
 
-from helpers import make_case, rel_err
-from test_gpu_parity import check, run_gpu, run_oracle
+from helpers import make_case
+from test_gpu_parity import check
 
 pytestmark = pytest.mark.gpu
 
@@ -81,19 +81,9 @@ def test_random_medium_problem_fp32(seed):
                   padding=[k // 2] * dim, dilation=[1] * dim, out_pad=[1 if transposed else 0] * dim,
                   in_size=size, seed=seed, offset_scale=rnd.choice((1.0, 3.0)))
     print(f"seed {seed}: dim {dim} transposed {transposed} {params}", flush=True)
-    case = make_case(dim, transposed, **params)
-    # Sampling positions of up to ~700 (1D grids): a float32 position (integer base + offset,
-    # rounded once, as the reference's fp32 kernels compute it) is off by up to half an ulp,
-    # 3e-5 at 512..1024, which moves bilinear weights by that much against the float64 oracle.
-    # Structural mistakes show as errors of 1e-3 and more; the bound below leaves room for the
-    # rounding only.
-    out, grads, gout = run_gpu(case, torch.float32)
-    ref_out, ref_grads = run_oracle(case, gout, torch.float32)
-    assert rel_err(out, ref_out) < 1e-4, "forward"
-    for name, gr, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
-        if r is not None:
-            e = rel_err(gr, r)
-            assert e < 1e-3 if name == "offset" else e < 2e-4, f"grad_{name} rel err {e}"
+    # (sampling positions up to ~700 on the 1D grids: the oracle samples at their float32 roundings,
+    # as the kernels and the reference form them)
+    check(make_case(dim, transposed, **params), torch.float32)
 
 
 @pytest.mark.parametrize("seed", [6391, 11239, 12803])
@@ -105,3 +95,81 @@ def test_random_problem_without_a_window_fp32(seed):
     dim, transposed, params = random_case(seed)
     print(f"seed {seed}: dim {dim} transposed {transposed} {params}", flush=True)
     check(make_case(dim, transposed, **params), torch.float32)
+
+
+# Problems from wider random sweeps (random_case above, and a generator of larger kernels: up to 11
+# taps in 1D, 5 x 5 in 2D) that once failed, with the parameters they were drawn with. Each is
+# checked at the full bounds: the oracle samples at the float32 positions the kernels and the
+# reference form (a position within half a float32 step of a cell boundary takes the other cell and
+# the other one-sided offset derivative), and the transposed forward's scatter keeps float32 accuracy
+# on many-tap problems.
+SWEEP_CASES = [
+    # many-tap 3D transposed forwards (48 and 64 taps on few channels)
+    (11069, "float32", 3, True, {'batch': 2, 'cin': 4, 'cout': 64, 'groups': 2, 'og': 4, 'mg': 1, 'deformable': True,
+                                 'modulated': True, 'bias': False, 'kernel': [4, 4, 4], 'stride': [1, 3, 1],
+                                 'padding': [2, 0, 2], 'dilation': [1, 1, 1], 'out_pad': [0, 2, 0],
+                                 'in_size': [7, 4, 7], 'seed': 11069, 'offset_scale': 2.0}),
+    (37015, "float32", 3, True, {'batch': 1, 'cin': 16, 'cout': 48, 'groups': 1, 'og': 1, 'mg': 2, 'deformable': True,
+                                 'modulated': False, 'bias': True, 'kernel': [4, 3, 4], 'stride': [1, 3, 2],
+                                 'padding': [2, 0, 1], 'dilation': [2, 1, 1], 'out_pad': [1, 1, 1],
+                                 'in_size': [4, 7, 6], 'seed': 37015, 'offset_scale': 0.5}),
+    # a 3D transposed problem on a 1-cell axis (no window fits its footprint)
+    (10836, "bfloat16", 3, True, {'batch': 1, 'cin': 16, 'cout': 48, 'groups': 1, 'og': 1, 'mg': 2,
+                                  'deformable': True, 'modulated': False, 'bias': False, 'kernel': [2, 2, 3],
+                                  'stride': [3, 3, 3], 'padding': [0, 0, 1], 'dilation': [1, 1, 1],
+                                  'out_pad': [0, 2, 1], 'in_size': [5, 4, 1], 'seed': 10836, 'offset_scale': 0.5}),
+    # bfloat16 2D problems with larger kernels
+    (35764, "bfloat16", 2, False, {'batch': 1, 'cin': 16, 'cout': 4, 'groups': 1, 'og': 2, 'mg': 2,
+                                   'deformable': True, 'modulated': False, 'bias': True, 'kernel': [2, 2],
+                                   'stride': [2, 1], 'padding': [0, 2], 'dilation': [1, 1], 'out_pad': [0, 0],
+                                   'in_size': [9, 14], 'seed': 35764, 'offset_scale': 0.5}),
+    (40692, "bfloat16", 2, False, {'batch': 1, 'cin': 64, 'cout': 48, 'groups': 1, 'og': 2, 'mg': 1, 'kernel': [3, 5],
+                                   'stride': [2, 2], 'padding': [1, 4], 'dilation': [1, 2], 'out_pad': [0, 0],
+                                   'in_size': [18, 26], 'seed': 40692, 'offset_scale': 0.5, 'modulated': False,
+                                   'bias': False}),
+    (41412, "bfloat16", 2, False, {'batch': 2, 'cin': 64, 'cout': 16, 'groups': 1, 'og': 2, 'mg': 1, 'kernel': [5, 4],
+                                   'stride': [1, 1], 'padding': [4, 1], 'dilation': [2, 1], 'out_pad': [0, 0],
+                                   'in_size': [25, 28], 'seed': 41412, 'offset_scale': 5.0, 'modulated': True,
+                                   'bias': False}),
+    # float32 positions on cell boundaries (single offset-gradient elements against the exact positions)
+    (14539, "float32", 2, False, {'batch': 1, 'cin': 32, 'cout': 80, 'groups': 1, 'og': 2, 'mg': 1, 'kernel': [5, 4],
+                                  'stride': [1, 1], 'padding': [4, 1], 'dilation': [2, 1], 'out_pad': [0, 0],
+                                  'in_size': [22, 22], 'seed': 14539, 'offset_scale': 0.5, 'modulated': True,
+                                  'bias': True}),
+    (40039, "float32", 1, False, {'batch': 2, 'cin': 32, 'cout': 32, 'groups': 1, 'og': 2, 'mg': 1, 'kernel': [10],
+                                  'stride': [1], 'padding': [4], 'dilation': [1], 'out_pad': [0], 'in_size': [123],
+                                  'seed': 40039, 'offset_scale': 0.5, 'modulated': True, 'bias': True}),
+    (40271, "float32", 1, False, {'batch': 1, 'cin': 64, 'cout': 32, 'groups': 1, 'og': 2, 'mg': 2, 'kernel': [11],
+                                  'stride': [2], 'padding': [10], 'dilation': [2], 'out_pad': [0], 'in_size': [273],
+                                  'seed': 40271, 'offset_scale': 2.0, 'modulated': True, 'bias': False}),
+    (40573, "float32", 3, False, {'batch': 2, 'cin': 48, 'cout': 48, 'groups': 1, 'og': 1, 'mg': 1,
+                                  'kernel': [3, 2, 2], 'stride': [1, 1, 1], 'padding': [1, 0, 0],
+                                  'dilation': [1, 1, 1], 'out_pad': [0, 0, 0], 'in_size': [5, 11, 12], 'seed': 40573,
+                                  'offset_scale': 5.0, 'modulated': False, 'bias': False}),
+    (40615, "float32", 2, True, {'batch': 2, 'cin': 64, 'cout': 80, 'groups': 1, 'og': 1, 'mg': 1, 'kernel': [4, 5],
+                                 'stride': [2, 2], 'padding': [3, 4], 'dilation': [2, 2], 'out_pad': [1, 1],
+                                 'in_size': [9, 21], 'seed': 40615, 'offset_scale': 0.5, 'modulated': False,
+                                 'bias': False}),
+    (41309, "float32", 1, False, {'batch': 2, 'cin': 32, 'cout': 80, 'groups': 1, 'og': 2, 'mg': 2, 'kernel': [8],
+                                  'stride': [2], 'padding': [3], 'dilation': [1], 'out_pad': [0], 'in_size': [211],
+                                  'seed': 41309, 'offset_scale': 2.0, 'modulated': True, 'bias': False}),
+    (7219, "float32", 2, True, {'batch': 2, 'cin': 16, 'cout': 80, 'groups': 1, 'og': 1, 'mg': 1, 'kernel': [4, 3],
+                                'stride': [1, 2], 'padding': [1, 2], 'dilation': [1, 2], 'out_pad': [0, 0],
+                                'in_size': [13, 27], 'seed': 7219, 'offset_scale': 0.5, 'modulated': True,
+                                'bias': True}),
+    (6097, "float32", 2, True, {'batch': 2, 'cin': 16, 'cout': 4, 'groups': 1, 'og': 4, 'mg': 4, 'deformable': True,
+                                'modulated': False, 'bias': True, 'kernel': [3, 2], 'stride': [1, 3],
+                                'padding': [2, 1], 'dilation': [2, 1], 'out_pad': [0, 0], 'in_size': [6, 13],
+                                'seed': 6097, 'offset_scale': 0.5}),
+    (6391, "float32", 3, True, {'batch': 2, 'cin': 32, 'cout': 48, 'groups': 2, 'og': 2, 'mg': 1, 'deformable': True,
+                                'modulated': True, 'bias': True, 'kernel': [4, 1, 4], 'stride': [2, 1, 1],
+                                'padding': [1, 0, 1], 'dilation': [1, 1, 2], 'out_pad': [1, 0, 0],
+                                'in_size': [7, 1, 5], 'seed': 6391, 'offset_scale': 6.0}),
+]
+
+
+@pytest.mark.parametrize("seed,dtype,dim,transposed,params", SWEEP_CASES, ids=[str(c[0]) for c in SWEEP_CASES])
+def test_sweep_case(seed, dtype, dim, transposed, params):
+    dtype = getattr(torch, dtype)
+    print(f"seed {seed}: {dtype} dim {dim} transposed {transposed} {params}", flush=True)
+    check(make_case(dim, transposed, **params), dtype)

@@ -15,7 +15,7 @@ import torch
 
 import tvdcn
 from oracle import oracle
-from helpers import make_case, rel_err
+from helpers import make_case, oracle_offsets, rel_err
 from test_gpu_parity import TOL, check, run_gpu, run_oracle
 
 pytestmark = pytest.mark.gpu
@@ -238,56 +238,15 @@ def test_forward_copy_kept_for_backward(dim):
         assert rel_err(t.grad, r) < TOL[torch.float32][1], f"grad_{n} (oracle)"
 
 
-def _samples_on_cell_boundaries(case, tol=2e-5):
-    """Mask over grad_offset's elements: True where the sample's exact (float64) position lies
-    within tol of an integer on some axis. There the bilinear / trilinear coordinate derivative
-    jumps, and a float32 position (integer base + offset, rounded once, as the reference's fp32
-    kernels form it: cuda/deform_conv2d_common_kernels.cu:170-178) may fall on the other side
-    (half an ulp: 4e-6 at |position| < 64), so the float32 offset gradient there is the other
-    one-sided derivative. Conv (not transposed) geometry."""
-    dim = case["dim"]
-    k = list(case["weight"].shape[2:])
-    st, pad, dil = case["stride"], case["padding"], case["dilation"]
-    off = case["offset"].to(torch.float32).double()
-    B, out = off.shape[0], list(off.shape[2:])
-    K = 1
-    for v in k:
-        K *= v
-    og = off.shape[1] // (K * dim)
-    off = off.reshape(B, og, *k, dim, *out)
-    near = torch.zeros(B, og, *k, *out, dtype=torch.bool)
-    for a in range(dim):
-        o = torch.arange(out[a], dtype=torch.float64) * st[a] - pad[a]
-        kk = torch.arange(k[a], dtype=torch.float64) * dil[a]
-        kshape = [1] * (2 + dim) + [1] * dim
-        kshape[2 + a] = k[a]
-        oshape = [1] * (2 + dim) + [1] * dim
-        oshape[2 + dim + a] = out[a]
-        pos = kk.reshape(kshape) + o.reshape(oshape) + off.select(2 + dim, a)
-        near |= (pos - pos.round()).abs() < tol
-    return near.unsqueeze(2 + dim).expand(B, og, *k, dim, *out).reshape(case["offset"].shape)
-
-
 def test_weight_splits_across_pass_boundaries_fp32():
     """3D, 27 taps (three passes) over 135 spatial tiles: the windowed weight gradient's splits
     run over (pass, tile) units two at a time, so split 67 holds the last tile of pass 0 and
     the first of pass 1, and the reduction sums per tap only the splits that meet its pass.
-    Every other quantity at the usual bounds; the offset gradient away from the (about 1e-4 of
-    all) samples that sit on a cell boundary, where its value is one-sided."""
+    Every quantity at the usual bounds (the oracle samples at the float32 positions, so the
+    samples that round onto a cell boundary take the same one-sided offset derivative)."""
     case = make_case(3, False, batch=3, cin=16, cout=32, kernel=[3, 3, 3], stride=[1, 1, 1], padding=[1, 1, 1],
                      dilation=[1, 1, 1], in_size=[12, 24, 40], out_pad=[0, 0, 0], seed=590)
-    out, grads, gout = run_gpu(case, torch.float32)
-    ref_out, ref_grads = run_oracle(case, gout, torch.float32)
-    assert rel_err(out, ref_out) < 1e-5
-    near = _samples_on_cell_boundaries(case)
-    print(f"offset-gradient elements on cell boundaries: {int(near.sum())} of {near.numel()}", flush=True)
-    assert float(near.double().mean()) < 1e-3
-    for name, g, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
-        g = g.double().cpu()
-        if name == "offset":
-            g = torch.where(near, r, g)
-        e = rel_err(g, r)
-        assert e < 1e-4, f"grad_{name} rel err {e}"
+    check(case, torch.float32)
 
 
 def test_channels_last_1d_input():
@@ -342,6 +301,32 @@ def scatter_magnitude(case, gout, dtype):
     op = [S[i] - ((P[i] - 1) * s[i] - 2 * p[i] + d[i] * (k[i] - 1) + 1) for i in range(dim)]
     return oracle.forward(dim, X, sel, off, msk, None, stride=s, padding=p, dilation=d, groups=1,
                           transposed=True, output_padding=op)
+
+
+def transposed_forward_magnitude(case, dtype):
+    """A[b, c, s] = sum over the scatter terms landing on output element (b, c, s) of the transposed
+    forward of |cols * mask| * corner weight, cols = W^T input (groups 1): the float64 oracle's transposed
+    forward of |cols| through a selection weight (channel c * K + t -> output channel c at tap t)"""
+    from oracle import oracle
+    dim = case["dim"]
+    w = case["weight"].to(dtype).double()   # (Cin, Cout, k...)
+    M, C = w.shape[:2]
+    k = list(w.shape[2:])
+    K = w[0, 0].numel()
+    x = case["input"].to(dtype).double()
+    B, P = x.shape[0], list(x.shape[2:])
+    cols = torch.einsum("mck,bmp->bckp", w.reshape(M, C, K), x.reshape(B, M, -1))   # (B, C, K, P)
+    X = cols.abs().reshape(B, C * K, *P)
+    sel = torch.zeros(C * K, C, K, dtype=torch.float64)
+    idx = torch.arange(C)
+    for t in range(K):
+        sel[idx * K + t, idx, t] = 1.0
+    sel = sel.reshape(C * K, C, *k)
+    off = oracle_offsets(case, case["offset"].to(dtype).double(), dtype)
+    msk = case["mask"].to(dtype).double().abs() if case["mask"] is not None else None
+    return oracle.forward(dim, X, sel, off, msk, None, stride=case["stride"], padding=case["padding"],
+                          dilation=case["dilation"], groups=1, transposed=True,
+                          output_padding=case["output_padding"])
 
 
 def elementwise_err(a, ref, mag):
@@ -453,3 +438,34 @@ def test_staged_weight_blocks_nine_tap_passes(dim, transposed, dtype):
                      padding=[k // 2 for k in kernel], dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim,
                      seed=610 + dim + 2 * transposed, offset_scale=2.0)
     check(case, dtype)
+
+
+@pytest.mark.skipif(not oracle.have_reference(), reason="reference CPU build (oracle/_ref) not available")
+@pytest.mark.parametrize("dim", [2, 3])
+def test_transposed_forward_elementwise_fp32(dim):
+    """The transposed forward is the scatter-only plan of the data-gradient kernel: its output accumulates
+    in the LDS fixed-point window. With many taps (2D 5 x 5 at stride 2; 3D 4 x 4 x 4 on few channels,
+    64 taps) the unit of a window tied to the summed bound of its tile lost float32 accuracy (forward
+    rel err 1e-5 .. 2.3e-5 on 48 / 64-tap 3D problems); the unit follows the largest kept term of the pass
+    instead. Each element against the float64 oracle, relative to the summed magnitude of its own terms
+    plus that of a typical element (elementwise_err), within 4x the reference's own float32 path on the
+    same inputs (oracle/_ref) + 1e-6; norm-wise within the float32 forward bound."""
+    if dim == 2:
+        case = make_case(2, True, batch=2, cin=32, cout=48, kernel=[5, 5], stride=[2, 2], padding=[2, 2],
+                         dilation=[1, 1], in_size=[20, 18], out_pad=[1, 1], seed=611, offset_scale=2.0)
+    else:
+        case = make_case(3, True, batch=2, cin=16, cout=32, kernel=[4, 4, 4], stride=[1, 2, 1], padding=[2, 1, 2],
+                         dilation=[1, 1, 1], in_size=[7, 6, 7], out_pad=[0, 1, 0], seed=612, offset_scale=2.0)
+    out, _, _ = run_gpu(case, torch.float32)
+    ref_out, _ = run_oracle(case, torch.zeros(case["out_shape"], dtype=torch.float64), torch.float32)
+    mag = transposed_forward_magnitude(case, torch.float32)
+    e = elementwise_err(out, ref_out, mag)
+    args = [case[n].float() if case[n] is not None else None for n in ("input", "weight", "offset", "mask", "bias")]
+    params = [case["stride"], case["padding"], case["output_padding"], case["dilation"], case["groups"]]
+    ref32 = oracle.run_reference([{"op": f"deform_conv_transpose{dim}d", "args": args + params}])
+    e_ref = elementwise_err(ref32[0], ref_out, mag)
+    n = rel_err(out, ref_out)
+    print(f"dim {dim}: transposed forward elementwise error {e:.2e} (reference float32 path {e_ref:.2e}), "
+          f"norm-wise {n:.2e}", flush=True)
+    assert n < TOL[torch.float32][0]
+    assert e <= 4 * e_ref + 1e-6

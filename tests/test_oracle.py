@@ -18,7 +18,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import oracle
-from helpers import make_case, rel_err
+from helpers import make_case, rel_err, rounded_position_offsets
 
 GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
 NAMES = ("input", "weight", "offset", "mask", "bias")
@@ -53,8 +53,16 @@ def test_oracle_matches_reference_fixtures(path):
         args = [a.unsqueeze(0) if (a is not None and i in (0, 2, 3)) else a for i, a in enumerate(args)]
         gout = gout.unsqueeze(0)
     dtype = t["input"].dtype
+    if dtype != torch.float64 and args[2] is not None:
+        # The reference forms each sample position y + offset in the input's type (c10::Half or
+        # float arithmetic, cpu/deform_conv2d_common_kernels.cpp:407-411): floor() can then land on
+        # the neighbouring cell (its own fp16 grad_offset is ~13% (L2) from the value at the exact
+        # positions on the float16 fixture); the oracle samples at the same rounded positions
+        geo = dict(dim=dim, weight=args[1], stride=kw["stride"], padding=kw["padding"], dilation=kw["dilation"])
+        args[2] = rounded_position_offsets(geo, args[2], dtype)
+    args = [None if a is None else a.double() for a in args]
     out = oracle.forward(dim, *args, **kw)
-    grads = oracle.backward(dim, gout, *args, **kw)
+    grads = oracle.backward(dim, gout.double(), *args, **kw)
     tf, tb = tol_for(dtype)
     ref_out = t["out"].unsqueeze(0) if unb else t["out"]
     assert rel_err(out, ref_out) < tf
@@ -63,15 +71,6 @@ def test_oracle_matches_reference_fixtures(path):
             assert gname not in t
             continue
         ref = t[gname].unsqueeze(0) if (unb and gname in ("g_input", "g_offset", "g_mask")) else t[gname]
-        if dtype == torch.float16 and gname == "g_offset":
-            # The reference evaluates the sample position y + offset in half precision
-            # (c10::Half arithmetic, cpu/deform_conv2d_common_kernels.cpp:407-411), so
-            # floor() can land on a neighbouring pixel and the coordinate weights jump;
-            # its own fp16 grad_offset deviates ~13% (L2) from the exact value on this
-            # fixture. Only a coarse L2 agreement is meaningful here.
-            l2 = float((g - ref.double()).norm() / ref.double().norm())
-            assert l2 < 0.25, gname
-            continue
         assert rel_err(g, ref) < tb, gname
 
 
@@ -96,6 +95,53 @@ def test_oracle_matches_reference_build_random(dim, transposed):
     assert rel_err(oracle.forward(dim, x, w, o, m, b, **kw), ref) < 1e-12
     for g, r in zip(oracle.backward(dim, gout, x, w, o, m, b, **kw), rg):
         assert rel_err(g, r) < 1e-12
+
+
+def _near_integer_offsets(shape, seed):
+    """float32 offsets one float32 step from an integer (k = -2 .. 2), on the side of k - 1 or k + 1: a
+    position base + offset then lies within half a float32 step of the integer base + k, so its float32
+    rounding is that integer while the exact value is not; a third of the offsets stay random"""
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randint(-2, 3, shape, generator=g).float()
+    side = torch.where(torch.rand(shape, generator=g) < 0.5, k - 1, k + 1)
+    near = torch.nextafter(k, side)
+    rand = (torch.rand(shape, generator=g) - 0.5) * 4
+    return torch.where(torch.rand(shape, generator=g) < 1 / 3, rand, near)
+
+
+@pytest.mark.skipif(not os.path.exists(oracle.REF_LIB), reason="reference CPU build (oracle/_ref) not built")
+@pytest.mark.parametrize("dim,transposed", [(1, False), (2, False), (3, False), (1, True), (2, True), (3, True)])
+def test_float32_position_model_matches_reference_build(dim, transposed):
+    """The reference's float32 path forms a sampling position as integer base + float offset, rounded
+    once to float32 (cpu/deform_conv2d_common_kernels.cpp:407-411; the CUDA twin
+    cuda/deform_conv2d_common_kernels.cu:170-178). Offsets one float32 step from an integer put most
+    positions within half a step of a cell boundary: rounded, they sit on the boundary and take the other
+    cell and the other one-sided offset derivative. The float64 oracle sampling at those rounded positions
+    (helpers.rounded_position_offsets, what the GPU parity tests hand the oracle for float32 runs) must
+    match the reference's own float32 results at float32 accuracy, and the oracle at the exact positions
+    must not (the model is what closes the gap)."""
+    case = make_case(dim, transposed, batch=2, cin=8, cout=6, groups=1, og=2, mg=1, seed=131 + dim,
+                     in_size={1: [23], 2: [9, 11], 3: [5, 6, 7]}[dim], dtype=torch.float32)
+    case["offset"] = _near_integer_offsets(case["offset"].shape, 17 + dim)
+    x, w, o, m, b = (case[n] for n in NAMES)
+    s, p, d, op, G = case["stride"], case["padding"], case["dilation"], case["output_padding"], case["groups"]
+    gout = torch.rand(case["out_shape"], generator=torch.Generator().manual_seed(5)).float()
+    name = f"deform_conv_transpose{dim}d" if transposed else f"deform_conv{dim}d"
+    params = [s, p, op, d, G] if transposed else [s, p, d, G]
+    ref, rg = oracle.run_reference([{"op": name, "args": [x, w, o, m, b] + params},
+                                    {"op": f"_{name}_backward", "args": [gout, x, w, o, m, b] + params}])
+    kw = dict(stride=s, padding=p, dilation=d, groups=G, transposed=transposed, output_padding=op)
+    x64, w64, m64, b64, g64 = (t.double() for t in (x, w, m, b, gout))
+    o_model = rounded_position_offsets(case, o.double(), torch.float32)
+    moved = float((o_model != o.double()).double().mean())
+    assert moved > 0.3, f"only {moved:.2f} of the positions round onto a boundary"
+    out = oracle.forward(dim, x64, w64, o_model, m64, b64, **kw)
+    grads = oracle.backward(dim, g64, x64, w64, o_model, m64, b64, **kw)
+    assert rel_err(out, ref) < 1e-5
+    for gname, gr, r in zip(GNAMES, grads, rg):
+        assert rel_err(gr, r) < 1e-4, gname
+    exact = oracle.backward(dim, g64, x64, w64, o.double(), m64, b64, **kw)
+    assert rel_err(exact[2], rg[2]) > 1e-2, "the exact positions should take other one-sided derivatives"
 
 
 CONV = {1: F.conv1d, 2: F.conv2d, 3: F.conv3d}

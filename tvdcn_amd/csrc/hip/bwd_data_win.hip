@@ -74,6 +74,13 @@ constexpr int BM = 16;            // GEMM-side channels per K step
 // on the same banks).
 __host__ __device__ constexpr int fix_stride(int cells) { return ((cells + 11) & ~15) + 4; }
 constexpr int FIX_BITS = 29;      // fixed-point headroom: |cell sum| * 2^s_c < 2^29
+// Scatter-only plans (transposed forward; the scatter launch of a split conv backward): the unit
+// follows the largest term the window keeps, |term| * 2^s_c < 2^PREC_BITS, and the cells sum
+// modulo 2^32. An add whose returned old value lies outside [-WRAP_K, WRAP_K) may have wrapped
+// (|add| <= 2^PREC_BITS < 2^31 - WRAP_K); a wrap found there sends the wrapped 2^32 units to
+// global memory, so the held value plus what went out stays the exact integer sum.
+constexpr int PREC_BITS = 26;
+constexpr unsigned WRAP_K = 0x78000000u;   // 2^31 - 2^27
 static_assert(NW * PB * 16 == BPX, "one tile of pixels per workgroup");
 static_assert(NT == BC * 32, "window rescale: 32 threads per channel");
 
@@ -108,6 +115,13 @@ __device__ __forceinline__ int fixed_round(float x) {
     int r;
     asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(x));
     return r;
+}
+
+// 2^32 units of scale 2^s in the direction of the add v when old + v wrapped past +-2^31, else 0
+__device__ __forceinline__ float wrap_spill(unsigned old, int v, int s) {
+    const unsigned nw = old + (unsigned)v;
+    if ((int)((old ^ nw) & ((unsigned)v ^ nw)) >= 0) return 0.f;
+    return ldexpf(v > 0 ? 1.f : -1.f, 32 - s);
 }
 
 // Sum over the four 16-lane rows of the wave (lanes l, l ^ 16, l ^ 32, l ^ 48), every lane
@@ -208,6 +222,8 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     float *__restrict__ goff, float *__restrict__ gmask) {
     constexpr int NC = 1 << DIM;
     constexpr int TMAX = WIN_TMAX;
+    // scatter-only: the unit follows the largest kept term, cells sum modulo 2^32 (PREC_BITS)
+    constexpr bool PREC = SCATTER && !COORD;
 
     extern __shared__ float smem[];
     acc4 *geo = reinterpret_cast<acc4 *>(smem);                // [TMAX][BPX] sampling table (window.h)
@@ -216,8 +232,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                                                // flag [BC] and the spike flag [BC + 1]
     float *btot = bsum + NW * BC + BC + 4;                     // [BC] bound of what the window holds
     int *shift = reinterpret_cast<int *>(btot + BC);           // [BC] rescale of the window for a pass
-    // [BC] spike thresholds of a pass with spikes, read before its rescale shifts are written
-    float *thr = reinterpret_cast<float *>(shift);
+    // [BC] spike thresholds of a pass with spikes, read before its rescale shifts are written (PREC
+    // sets both in one step and keeps no bound: the thresholds take the bound's words)
+    float *thr = PREC ? btot : reinterpret_cast<float *>(shift);
     int *bmax = shift + BC;                                    // [BC] largest |G * mask| (float bits, >= 0)
     unsigned *bexp = reinterpret_cast<unsigned *>(bmax + BC);  // [BC] exponent sums + (counts << 20)
     // (xg: the offset / mask gradients read X from global memory; no X window)
@@ -655,6 +672,27 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 }
                 if (tid == 0) scl[BC] = bad != 0ull;
             };
+            // PREC: the scale of the pass from the largest term the window keeps (kmax; a pass
+            // with spikes keeps the terms up to their threshold), coarsened to what the window
+            // holds; bc (the sum of every term) only tells whether the pass is finite. A pass that
+            // skips the window (not finite; 3D with spikes: skip) leaves the held scale as it is:
+            // the window's flush reads it.
+            auto set_scale_prec = [&](float kmax, float bc, bool skip) {
+                const unsigned long long bad = __ballot(!isfinite(bc));
+                int e = 0;
+                if (kmax > 0.f) frexpf(kmax, &e);   // kmax < 2^e
+                int sc = PREC_BITS - e;
+                shift[tid] = 0;
+                if (bad == 0ull && !skip) {
+                    if (win_data) {
+                        const int held = scl[tid];
+                        sc = min(sc, held);
+                        shift[tid] = held - sc;
+                    }
+                    scl[tid] = sc;
+                }
+                if (tid == 0) scl[BC] = bad != 0ull;
+            };
             const float no_lim[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
             bound_sweep(no_lim, true);
             __syncthreads();
@@ -674,7 +712,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 const bool spike = isfinite(bc) && big > lim;
                 thr[tid] = spike ? lim : INFINITY;
                 const unsigned long long any = __ballot(spike);
-                if (any == 0ull) set_scale(bc);   // no spike: the bound is final
+                if constexpr (PREC)
+                    set_scale_prec(spike ? lim : big, bc, DIM == 3 && any != 0ull);
+                else if (any == 0ull)
+                    set_scale(bc);   // no spike: the bound is final
                 if (tid == 0) scl[BC + 1] = any != 0ull;
             }
             __syncthreads();
@@ -686,6 +727,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 // 3D: a pass with spikes skips the window (the branch-light 3D path has no
                 // per-channel routing)
                 no_window = no_window || spikes;
+            } else if (spikes && PREC) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) th[v] = thr[mq + v];
             } else if (spikes) {
                 // bound of the terms that stay in the window
 #pragma unroll
@@ -709,12 +753,13 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 spikes = false;
             } else {
                 if (win_data) {
-                    // rescale to nearest (halves up); a shift of 31 or more leaves under half a unit
+                    // rescale to nearest (halves up); a shift of 31 or more leaves at most a unit
+                    // (PREC: a held value may be anywhere in the 32-bit range)
                     const int c = tid >> 5, sh = shift[c];
                     if (sh > 0) {
                         for (int cell = tid & 31; cell < cst; cell += 32) {
-                            const int v = iwin[c * cst + cell];   // |v| < 2^29
-                            iwin[c * cst + cell] = sh >= 31 ? 0 : (v + (1 << (sh - 1))) >> sh;
+                            const int v = iwin[c * cst + cell];
+                            iwin[c * cst + cell] = sh >= 31 ? 0 : (v >> sh) + ((v >> (sh - 1)) & 1);
                         }
                     }
                     __syncthreads();
@@ -817,24 +862,72 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                         }
                         if constexpr (SCATTER) {
                             if (cq_ok) {
+                                // (PREC: mask * G scaled, the corner weight <= 1 applied after, so no
+                                // intermediate leaves the float range)
                                 float gsc[4];
 #pragma unroll
-                                for (int v = 0; v < 4; ++v) gsc[v] = ldexpf(gv[v], sexp[v]);
+                                for (int v = 0; v < 4; ++v) gsc[v] = ldexpf(PREC ? mk * gv[v] : gv[v], sexp[v]);
                                 float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+                                if constexpr (!PREC) {
 #pragma unroll
-                                for (int k = 0; k < 8; ++k) {
-                                    if (k > 0 && !deformable) break;
-                                    if (!cr.in_grid(k)) continue;
-                                    const float sw = mk * cr.weight(k);
-                                    if (cr.in_win(k)) {
-                                        unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + cr.cell(wt, k));
+                                    for (int k = 0; k < 8; ++k) {
+                                        if (k > 0 && !deformable) break;
+                                        if (!cr.in_grid(k)) continue;
+                                        const float sw = mk * cr.weight(k);
+                                        if (cr.in_win(k)) {
+                                            unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + cr.cell(wt, k));
 #pragma unroll
-                                        for (int v = 0; v < 4; ++v)
-                                            atomicAdd(dst + v * cst, (unsigned int)fixed_round(sw * gsc[v]));
-                                    } else {
-                                        float *dst = gdst + (size_t)cr.idx(g, k) * g.C;
+                                            for (int v = 0; v < 4; ++v)
+                                                atomicAdd(dst + v * cst, (unsigned int)fixed_round(sw * gsc[v]));
+                                        } else {
+                                            float *dst = gdst + (size_t)cr.idx(g, k) * g.C;
 #pragma unroll
-                                        for (int v = 0; v < 4; ++v) atomic_add(dst + v, sw * gv[v]);
+                                            for (int v = 0; v < 4; ++v) atomic_add(dst + v, sw * gv[v]);
+                                        }
+                                    }
+                                } else {
+                                    // the returned old values of four corners at a time are checked for a
+                                    // possible wrap, the adds recomputed where one is
+#pragma unroll
+                                    for (int h = 0; h < 2; ++h) {
+                                        if (h > 0 && !deformable) break;
+                                        unsigned near = 0u;
+                                        unsigned old[4][4];
+#pragma unroll
+                                        for (int j = 0; j < 4; ++j) {
+                                            const int k = 4 * h + j;
+                                            if (k > 0 && !deformable) break;
+                                            if (!cr.in_grid(k)) continue;
+                                            if (cr.in_win(k)) {
+                                                unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + cr.cell(wt, k));
+                                                const float sw = cr.weight(k);
+#pragma unroll
+                                                for (int v = 0; v < 4; ++v) {
+                                                    old[j][v] = atomicAdd(dst + v * cst, (unsigned int)fixed_round(sw * gsc[v]));
+                                                    near = max(near, old[j][v] + WRAP_K);
+                                                }
+                                            } else {
+                                                float *dst = gdst + (size_t)cr.idx(g, k) * g.C;
+                                                const float sw = mk * cr.weight(k);
+#pragma unroll
+                                                for (int v = 0; v < 4; ++v) atomic_add(dst + v, sw * gv[v]);
+                                            }
+                                        }
+                                        if (near >= 2u * WRAP_K) {
+                                            // some add may have wrapped: its 2^32 units go to global memory
+#pragma unroll
+                                            for (int j = 0; j < 4; ++j) {
+                                                const int k = 4 * h + j;
+                                                if (k > 0 && !deformable) break;
+                                                if (!cr.in_grid(k) || !cr.in_win(k)) continue;
+                                                const float sw = cr.weight(k);
+#pragma unroll
+                                                for (int v = 0; v < 4; ++v) {
+                                                    const float sp = wrap_spill(old[j][v], fixed_round(sw * gsc[v]), sexp[v]);
+                                                    if (sp != 0.f) atomic_add(gdst + (size_t)cr.idx(g, k) * g.C + v, sp);
+                                                }
+                                            }
+                                        }
                                     }
                                 }
                             }
@@ -883,25 +976,52 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     if constexpr (SCATTER) {
                         if (cq_ok) {
                             // mask-weighted corner weights; G pre-scaled to fixed point per channel
+                            // (PREC: mask * G scaled, plain corner weights <= 1 after)
+                            const float mw = PREC ? 1.f : mk;
                             float wm[NF];
                             if constexpr (DIM == 2) {
-                                const float a1 = mk * fy, a0 = mk - a1;
+                                const float a1 = mw * fy, a0 = mw - a1;
                                 wm[1] = a0 * fx;
                                 wm[0] = a0 - wm[1];
                                 wm[3] = a1 * fx;
                                 wm[2] = a1 - wm[3];
                             } else {
-                                wm[1] = mk * fx;
-                                wm[0] = mk - wm[1];
+                                wm[1] = mw * fx;
+                                wm[0] = mw - wm[1];
                             }
                             float gs[4];
 #pragma unroll
-                            for (int v = 0; v < 4; ++v) gs[v] = ldexpf(gv[v], sexp[v]);
+                            for (int v = 0; v < 4; ++v) gs[v] = ldexpf(PREC ? mk * gv[v] : gv[v], sexp[v]);
+                            unsigned near = 0u;
+                            unsigned old[NF][4];
 #pragma unroll
                             for (int k = 0; k < NF; ++k) {
                                 unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + cell[k]);
 #pragma unroll
-                                for (int v = 0; v < 4; ++v) atomicAdd(dst + v * cst, (unsigned int)fixed_round(wm[k] * gs[v]));
+                                for (int v = 0; v < 4; ++v) {
+                                    const int a = fixed_round(wm[k] * gs[v]);
+                                    if constexpr (PREC) {
+                                        old[k][v] = atomicAdd(dst + v * cst, (unsigned int)a);
+                                        near = max(near, old[k][v] + WRAP_K);
+                                    } else {
+                                        atomicAdd(dst + v * cst, (unsigned int)a);
+                                    }
+                                }
+                            }
+                            if (PREC && near >= 2u * WRAP_K) {
+                                // some add may have wrapped: its 2^32 units go to global memory
+                                // (window cells outside the grid hold what the flush drops)
+                                float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+#pragma unroll
+                                for (int k = 0; k < NF; ++k) {
+                                    const int gi = tile.cell_index(g, wt, cell[k]);
+                                    if (gi < 0) continue;
+#pragma unroll
+                                    for (int v = 0; v < 4; ++v) {
+                                        const float sp = wrap_spill(old[k][v], fixed_round(wm[k] * gs[v]), sexp[v]);
+                                        if (sp != 0.f) atomic_add(gdst + (size_t)gi * g.C + v, sp);
+                                    }
+                                }
                             }
                         }
                     }
@@ -950,6 +1070,12 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     if constexpr (SCATTER) {
                         if (cq_ok) {
                             float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+                            // (PREC: mask * G scaled once, the corner weight <= 1 applied after)
+                            float gs[4];
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) gs[v] = PREC ? ldexpf(mk * gv[v], sexp[v]) : 0.f;
+                            unsigned near = 0u;
+                            unsigned old[NC][4];
 #pragma unroll
                             for (int k = 0; k < NC; ++k) {
                                 if (gidx[k] < 0) continue;
@@ -958,15 +1084,32 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                     unsigned int *dst = reinterpret_cast<unsigned int *>(iwin + mq * cst + loc[k]);
 #pragma unroll
                                     for (int v = 0; v < 4; ++v) {
-                                        if (sp[v])
+                                        if (sp[v]) {
                                             atomic_add(gdst + (size_t)gidx[k] * g.C + v, s * gv[v]);
-                                        else
+                                        } else if constexpr (PREC) {
+                                            old[k][v] = atomicAdd(dst + v * cst, (unsigned int)fixed_round(w[k] * gs[v]));
+                                            near = max(near, old[k][v] + WRAP_K);
+                                        } else {
                                             atomicAdd(dst + v * cst, (unsigned int)fixed_round(ldexpf(s * gv[v], sexp[v])));
+                                        }
                                     }
                                 } else {
                                     float *dst = gdst + (size_t)gidx[k] * g.C;
 #pragma unroll
                                     for (int v = 0; v < 4; ++v) atomic_add(dst + v, s * gv[v]);
+                                }
+                            }
+                            if (PREC && near >= 2u * WRAP_K) {
+                                // some add may have wrapped: its 2^32 units go to global memory
+#pragma unroll
+                                for (int k = 0; k < NC; ++k) {
+                                    if (gidx[k] < 0 || !use_window || loc[k] < 0) continue;
+#pragma unroll
+                                    for (int v = 0; v < 4; ++v) {
+                                        if (sp[v]) continue;   // spike terms went to global memory
+                                        const float spl = wrap_spill(old[k][v], fixed_round(w[k] * gs[v]), sexp[v]);
+                                        if (spl != 0.f) atomic_add(gdst + (size_t)gidx[k] * g.C + v, spl);
+                                    }
                                 }
                             }
                         }
