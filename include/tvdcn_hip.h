@@ -119,6 +119,15 @@ size_t tvdcn_deform_conv_backward_workspace_size(const tvdcn_conv_desc *desc);
  * (ops/utils/parallel_helpers.h:7-16), counted in elements instead of images. */
 tvdcn_status tvdcn_set_max_block_elements(int64_t max_elements);
 
+/* Images per batch block of a call described by desc (0 for an empty batch), under the current
+ * limit. When the batch is split, the block is rounded down to a multiple of the image count m at
+ * which every batch-sized tensor's bytes reach a multiple of 16 (m <= 16), so that each block's
+ * pointers are as aligned as the caller's; when fewer than m images fit in a block, later blocks'
+ * pointers may be less aligned, which the kernels accept. Counterpart of the reference's
+ * n_parallel_imgs = get_greatest_divisor_below_bound(batch, kMaxParallelImgs)
+ * (ops/utils/parallel_helpers.h:7-16, ops/cuda/deform_conv2d_kernel.cpp:149), a query here. */
+tvdcn_status tvdcn_conv_batch_block(const tvdcn_conv_desc *desc, int64_t *images_per_block);
+
 /*
  * Forward of deform_conv{1,2,3}d / deform_conv_transpose{1,2,3}d.
  * Replaces the CUDA-key forward drivers ops/cuda/deform_conv2d_kernel.cpp:85-385,

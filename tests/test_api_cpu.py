@@ -11,6 +11,7 @@
 * the nn.Module wrappers and mask activations keep the reference's API and errors.
 """
 import ctypes
+import math
 import os
 import re
 
@@ -49,8 +50,6 @@ def test_c_abi_exports_every_declared_function(lib):
     assert len(names) >= 11
     for n in names:
         assert hasattr(lib, n), n
-
-
 
 
 def cfg2_desc(**over):
@@ -125,6 +124,57 @@ def test_c_abi_argument_errors(lib):
         st = lib.tvdcn_deform_conv_forward(ctypes.byref(d), None, None, ctypes.c_void_p(16), ctypes.c_void_p(16),
                                            None, None, None, ctypes.c_size_t(0), None)
         assert st == 1 and msg in lib.tvdcn_last_error()
+
+
+def test_batch_blocks_keep_pointers_aligned(lib):
+    """With a forced block limit the batch runs in blocks of images; for C = 3 on a 7 x 7 input every
+    batch-sized tensor's per-image bytes leave a remainder mod 16 (float32 input 588 B, offset 392 B x
+    18 / 9 ...), so the block is rounded down to a multiple of the image count m that makes all of them
+    multiples of 16: each block's pointers stay 16-byte aligned. With room for fewer than m images per
+    block the block is not rounded (the kernels accept less aligned block pointers)."""
+    lib.tvdcn_conv_batch_block.restype = ctypes.c_int
+    lib.tvdcn_set_max_block_elements.restype = ctypes.c_int
+    d = Desc(dim=2, transposed=0, dtype=0, batch=37, in_channels=3, out_channels=5, groups=1, offset_groups=1,
+             mask_groups=1)
+    for i in range(2):
+        d.in_size[i], d.kernel[i], d.stride[i], d.padding[i], d.dilation[i] = 7, 3, 1, 1, 1
+    es_of = {0: 4, 1: 8, 2: 2, 3: 2}
+    try:
+        for dtype in (0, 1, 2, 3):
+            d.dtype = dtype
+            es = es_of[dtype]
+            per_image = [3 * 49, 5 * 49, 18 * 49, 9 * 49]   # input, output, offset, mask
+            m = max(16 // math.gcd(n * es % 16, 16) if n * es % 16 else 1 for n in per_image)
+            for limit in (20 * 18 * 49, 18 * 49 * 3, 2 ** 31 - 1):
+                assert lib.tvdcn_set_max_block_elements(ctypes.c_int64(limit)) == 0
+                blk = ctypes.c_int64(0)
+                assert lib.tvdcn_conv_batch_block(ctypes.byref(d), ctypes.byref(blk)) == 0
+                raw = min(37, limit // (18 * 49))
+                if raw >= 37:
+                    assert blk.value == 37
+                elif raw >= m:
+                    assert blk.value == raw - raw % m and blk.value % m == 0
+                    for n in per_image:
+                        assert blk.value * n * es % 16 == 0
+                else:
+                    assert blk.value == raw
+    finally:
+        lib.tvdcn_set_max_block_elements(ctypes.c_int64(2 ** 31 - 1))
+
+
+def test_c_abi_rejects_misaligned_tensor_pointers(lib):
+    """The C ABI takes 16-byte aligned tensor pointers (a batch block's own pointers may be less
+    aligned; the caller's are checked at the entry, before any device work)."""
+    lib.tvdcn_deform_conv_forward.restype = ctypes.c_int
+    lib.tvdcn_deform_conv_backward.restype = ctypes.c_int
+    lib.tvdcn_last_error.restype = ctypes.c_char_p
+    d = cfg2_desc()
+    big = ctypes.c_size_t(1 << 40)
+    p, q = ctypes.c_void_p(1 << 20), ctypes.c_void_p((1 << 20) + 4)
+    st = lib.tvdcn_deform_conv_forward(ctypes.byref(d), p, p, q, p, None, p, p, big, None)
+    assert st == 1 and b"16-byte aligned" in lib.tvdcn_last_error()
+    st = lib.tvdcn_deform_conv_backward(ctypes.byref(d), p, p, p, p, p, p, p, p, q, None, p, big, None)
+    assert st == 1 and b"16-byte aligned" in lib.tvdcn_last_error()
 
 
 REF_SCHEMAS = {
@@ -449,6 +499,40 @@ def test_packed_modules_choose_the_fused_mask_activation():
     assert m._mask_fusion() == (0, 0.0)
     with pytest.raises(ValueError, match="scale must be positive"):
         m(meta(2, 4, 8, 8))
+
+
+@pytest.mark.parametrize("kind", ["hook", "pre_hook", "global_hook"])
+def test_mask_activation_hooks_run(kind):
+    """A forward hook or pre-hook on the mask activation (or a global one) runs as in the reference,
+    which calls the activation module: the fused mask load is not taken while one is registered, and
+    what the hook does to the mask shows in the output."""
+    torch.manual_seed(0)
+    m = tvdcn.PackedDeformConv2d(4, 6, 3, padding=1, modulated=True)
+    for gen in (m.offset_generator, m.mask_generator):
+        torch.nn.init.normal_(gen.weight, std=0.3)
+    x = torch.randn(2, 4, 7, 8)
+    calls = []
+    if kind == "hook":
+        h = m.mask_activation.register_forward_hook(lambda mod, inp, out: calls.append(1) or out * 0.25)
+    elif kind == "pre_hook":
+        h = m.mask_activation.register_forward_pre_hook(lambda mod, inp: calls.append(1) or (inp[0] - 3.0,))
+    else:
+        h = torch.nn.modules.module.register_module_forward_hook(
+            lambda mod, inp, out: (calls.append(1) or out * 0.25) if isinstance(mod, tvdcn.MaskSigmoid) else None)
+    try:
+        assert m._mask_fusion() == (0, 0.0)
+        y = m(x)
+    finally:
+        h.remove()
+    assert calls, "the hook did not run"
+    assert m._mask_fusion() == (1, 2.0)       # fused again once the hook is gone
+    offset = m.offset_generator(x)
+    logits = m.mask_generator(x)
+    mask = 2.0 * torch.sigmoid(logits - 3.0 if kind == "pre_hook" else logits)
+    if kind != "pre_hook":
+        mask = mask * 0.25
+    ref = tvdcn.deform_conv2d(x, m.weight, offset, mask, m.bias, padding=1)
+    assert torch.allclose(y, ref, rtol=1e-5, atol=1e-6)
 
 
 MODULES = [

@@ -15,7 +15,7 @@ import torch
 
 import tvdcn
 from helpers import make_case, rel_err
-from test_gpu_parity import check
+from test_gpu_parity import check, run_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -93,3 +93,39 @@ def test_problem_above_2_31_elements():
     # sums over 8.4M pixels per weight element in two float32 orders: the backward's 1e-4
     assert rel_err(gw, parts[0][0] + parts[1][0]) < 1e-4
     assert rel_err(gb, parts[0][1] + parts[1][1]) < 1e-4
+
+
+@pytest.mark.parametrize("images", [1, 3, 5])
+@pytest.mark.parametrize("transposed,dtype,channels_last", [
+    (False, torch.float32, False), (True, torch.float32, False), (False, torch.float16, False),
+    (True, torch.bfloat16, False), (False, torch.float32, True)])
+def test_forced_batch_blocks_with_unaligned_image_sizes(transposed, dtype, channels_last, images):
+    """C = 3 on a 7 x 7 grid: no batch-sized tensor's per-image bytes are a multiple of 16 (float32
+    input 588 B), so blocks of 1 or 3 images put later blocks' pointers off 16-byte boundaries (2- or
+    4-byte aligned), which every kernel accepts; blocks of 5 images round down to 4, a multiple of 16
+    bytes for every tensor. Batch 7: full blocks and a remainder, against the float64 oracle (float32
+    channels-last: the input sampled in place at the block's offset)."""
+    case = make_case(2, transposed, batch=7, cin=3, cout=5, kernel=[3, 3], stride=[1, 1], padding=[1, 1],
+                     dilation=[1, 1], in_size=[7, 7], out_pad=[0, 0], seed=830 + images)
+    lib = _lib()
+    print(f"blocks of {images} image(s): transposed {transposed} {dtype} channels_last {channels_last}", flush=True)
+    assert lib.tvdcn_set_max_block_elements(images * _per_image(case)) == 0
+    try:
+        if not channels_last:
+            check(case, dtype)
+            return
+        names = ("input", "weight", "offset", "mask", "bias")
+        ts = [case[n].to(DEV, dtype) for n in names]
+        ts[0] = ts[0].contiguous(memory_format=torch.channels_last)
+        ts = [t.requires_grad_(True) for t in ts]
+        y = tvdcn.deform_conv2d(*ts, stride=1, padding=1, dilation=1)
+        gout = torch.rand(y.shape, generator=torch.Generator().manual_seed(7), dtype=torch.float64)
+        y.backward(gout.to(DEV, dtype))
+        torch.cuda.synchronize()
+        assert ts[0].grad.is_contiguous(memory_format=torch.channels_last)
+        ref_out, ref_grads = run_oracle(case, gout, dtype)
+        assert rel_err(y, ref_out) < 1e-5
+        for n, t, r in zip(names, ts, ref_grads):
+            assert rel_err(t.grad, r) < 1e-4, n
+    finally:
+        assert lib.tvdcn_set_max_block_elements(2 ** 31 - 1) == 0

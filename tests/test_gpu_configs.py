@@ -47,7 +47,8 @@ def config(n):
         o = torch.randn(16, 20, 4096, generator=g) * 3
         logits = torch.randn(16, 20, 4096, generator=g)
         m = torch.softmax(logits.view(16, 4, 5, 4096), 2).view(16, 20, 4096)
-        return dict(dim=1, tr=False, x=x, w=w, o=o, m=m, b=None, s=[1], p=[2], d=[1], op=[0], G=1)
+        return dict(dim=1, tr=False, x=x, w=w, o=o, m=m, b=None, s=[1], p=[2], d=[1], op=[0], G=1, logits=logits,
+                    kn=5)
     if n == 4:
         x = torch.randn(2, 64, 16, 56, 56, generator=g)
         w = kaiming((64, 64, 3, 3, 3), 1728, g)
@@ -62,7 +63,8 @@ def config(n):
         o = torch.randn(8, 64, 32, 32, generator=g)
         logits = torch.randn(8, 32, 32, 32, generator=g)
         m = torch.softmax(logits.view(8, 2, 16, 32, 32), 2).view(8, 32, 32, 32)
-        return dict(dim=2, tr=True, x=x, w=w, o=o, m=m, b=None, s=[2, 2], p=[1, 1], d=[1, 1], op=[0, 0], G=1)
+        return dict(dim=2, tr=True, x=x, w=w, o=o, m=m, b=None, s=[2, 2], p=[1, 1], d=[1, 1], op=[0, 0], G=1,
+                    logits=logits, kn=16)
     raise ValueError(n)
 
 
@@ -119,6 +121,40 @@ def test_full_config_fp32_matches_reference(n):
             continue
         e = rel_err(gr, r)
         print(f"cfg{n} grad_{name} rel err {e:.2e}", flush=True)
+        assert e < 1e-4, name
+
+
+@pytest.mark.skipif(not HAVE_REF, reason="reference CPU build (oracle/_ref) not available")
+@pytest.mark.parametrize("n", [3, 5])
+def test_full_config_fused_softmax_matches_reference(n):
+    """Configs 3 and 5 as bench.py times them: the mask is the softmax of the logits over each mask
+    group's taps, applied in the kernels' mask load (tvdcn::deform_conv_mask_activation, what
+    PackedDeformConv*(mask_activation="softmax") runs), and its gradient flows to the logits. Against
+    the reference's CPU build run on mask = mask_softmax(logits) (its own composition), the mask
+    gradient carried to the logits through the softmax in float64: forward within 1e-5, every gradient
+    (the logits' included) within 1e-4."""
+    from tvdcn.ops.deform_conv import _deform_conv_mask_activation
+    c = config(n)
+    gout = upstream(c, n)
+    ref_out, ref_grads = reference(c, gout)
+    dim = c["dim"]
+    ts = [t.to(DEV).requires_grad_(True) if t is not None else None
+          for t in (c["x"], c["w"], c["o"], c["logits"], c["b"])]
+    out = _deform_conv_mask_activation(ts[0], ts[1], ts[2], ts[3], ts[4], c["s"], c["p"], c["op"], c["d"], c["G"],
+                                       c["tr"], 2, 0.0)
+    out.backward(gout.to(DEV))
+    torch.cuda.synchronize()
+    e = rel_err(out, ref_out)
+    print(f"cfg{n} fused softmax forward rel err {e:.2e}", flush=True)
+    assert e < 1e-5
+    # d loss / d logits = y * (g - sum_taps g * y), y = softmax over each group's taps (float64)
+    B, ch = c["logits"].shape[:2]
+    y = torch.softmax(c["logits"].double().view(B, ch // c["kn"], c["kn"], -1), 2)
+    gm = ref_grads[3].double().view(y.shape)
+    ref_glogits = (y * (gm - (gm * y).sum(2, keepdim=True))).view(c["logits"].shape)
+    for name, t, r in zip(("input", "weight", "offset", "logits"), ts, (*ref_grads[:3], ref_glogits)):
+        e = rel_err(t.grad, r)
+        print(f"cfg{n} fused softmax grad_{name} rel err {e:.2e}", flush=True)
         assert e < 1e-4, name
 
 

@@ -10,6 +10,8 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <numeric>
+#include <initializer_list>
 #include <vector>
 
 #include "../../../include/tvdcn_hip.h"
@@ -241,6 +243,20 @@ tvdcn_status batch_block(const tvdcn_conv_desc *d, int64_t &block, ImageElems *e
         return fail(TVDCN_STATUS_NOT_SUPPORTED, "one image's tensors exceed " + std::to_string(lim) +
                                                     " elements (the kernels index in 32 bits)");
     block = d->batch == 0 ? 0 : std::max<int64_t>(1, std::min<int64_t>(d->batch, lim / std::max<int64_t>(e.largest(), 1)));
+    if (block < d->batch) {
+        // a block of m images spans a multiple of 16 bytes of every user tensor, so a block that
+        // is a multiple of m keeps every block's pointers as aligned as the caller's (the layout
+        // copies then take their 16-byte paths); a block below m leaves them less aligned, which
+        // the kernels accept (they need 16-byte alignment only of what stays aligned anyway: a
+        // channels-last input with channels % 4 == 0, rows of 4-element quads)
+        const int64_t es = (int64_t)elem_size(d->dtype);
+        int64_t m = 1;
+        for (const int64_t n : {e.in, e.out, e.offset, e.mask}) {
+            const int64_t bytes = n * es % 16;
+            if (bytes != 0) m = std::max<int64_t>(m, 16 / std::gcd<int64_t>(bytes, 16));
+        }
+        if (block >= m) block -= block % m;
+    }
     return TVDCN_STATUS_SUCCESS;
 }
 
@@ -328,6 +344,13 @@ void *at(void *ws, size_t off) { return off == (size_t)-1 ? nullptr : static_cas
     } while (0)
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// the caller's tensor pointers (null: absent) are 16-byte aligned
+tvdcn_status check_aligned(std::initializer_list<const void *> ptrs) {
+    for (const void *p : ptrs)
+        if (p && !aligned16(p)) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "tensor pointers must be 16-byte aligned");
+    return TVDCN_STATUS_SUCCESS;
+}
 
 // ---------------------------------------------------------------------------
 // Optional per-kernel timing: HIP events recorded on the launch stream around
@@ -473,8 +496,8 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
     const Geo &g = pl.g;
     const Layout L = layout(pl, false);
     if (!input || !weight || !output) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
-    if (!aligned16(input) || !aligned16(workspace))
-        return fail(TVDCN_STATUS_INVALID_ARGUMENT, "input and workspace must be 16-byte aligned");
+    // (the caller's pointers are checked at the entry; a later block's may be less aligned)
+    if (!aligned16(workspace)) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int dt = pl.dtype;
     g_last_error.clear();
@@ -743,6 +766,13 @@ tvdcn_status scratch_of_current_device(void **out) {
 
 extern "C" {
 
+tvdcn_status tvdcn_conv_batch_block(const tvdcn_conv_desc *desc, int64_t *images_per_block) {
+    int64_t block = 0;
+    const tvdcn_status st = batch_block(desc, block);
+    if (st == TVDCN_STATUS_SUCCESS && images_per_block) *images_per_block = block;
+    return st;
+}
+
 tvdcn_status tvdcn_conv_output_size(const tvdcn_conv_desc *desc, int64_t out_size[3]) {
     int64_t tmp[3] = {1, 1, 1};
     tvdcn_status st = output_size(desc, tmp);
@@ -778,6 +808,8 @@ tvdcn_status tvdcn_deform_conv_forward(const tvdcn_conv_desc *desc, const void *
     if (desc->batch == 0) return TVDCN_STATUS_SUCCESS;   // empty batch: empty output, nothing to do
     st = check_forward_pointers(desc, offset, mask);
     if (st) return st;
+    st = check_aligned({input, weight, offset, mask, bias, output});
+    if (st) return st;
     if (workspace_bytes < workspace_bytes_of(desc, false))
         return fail(TVDCN_STATUS_WORKSPACE_TOO_SMALL, "workspace too small");
     return forward_blocks(desc, block, input, weight, offset, mask, bias, output, workspace, stream);
@@ -794,6 +826,8 @@ tvdcn_status tvdcn_deform_conv_forward_noalloc(const tvdcn_conv_desc *desc, cons
     if (st) return st;
     if (desc->batch == 0) return TVDCN_STATUS_SUCCESS;
     st = check_forward_pointers(desc, offset, mask);
+    if (st) return st;
+    st = check_aligned({input, weight, offset, mask, bias, output});
     if (st) return st;
     const size_t need = workspace_bytes_of(desc, false);
     if (need > (size_t)TVDCN_SCRATCH_BYTES)
@@ -843,6 +877,9 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
     if (!grad_out || !input || !weight || !grad_input || !grad_weight)
         return fail(TVDCN_STATUS_INVALID_ARGUMENT, "null tensor pointer");
     if (!aligned16(workspace)) return fail(TVDCN_STATUS_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    st = check_aligned({grad_out, input, weight, offset, mask, grad_input, grad_weight, grad_offset, grad_mask,
+                        grad_bias});
+    if (st) return st;
     if (!fits_int(desc->batch)) return fail(TVDCN_STATUS_NOT_SUPPORTED, "batch above 2^31 - 1");
     g_last_error.clear();
     // per image: X / grad_input and Z follow the op's input and output tensors

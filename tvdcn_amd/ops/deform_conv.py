@@ -103,11 +103,22 @@ def _deform_conv_mask_activation(input: Tensor, weight: Tensor, offset: Optional
                                                        scale)
 
 
+def _has_forward_hooks(module: nn.Module) -> bool:
+    """True when calling ``module`` would run forward (pre-)hooks: its own or torch's global ones."""
+    from torch.nn.modules import module as _module
+    return bool(module._forward_hooks or module._forward_pre_hooks or _module._global_forward_hooks or
+                _module._global_forward_pre_hooks)
+
+
 def _mask_fusion_of(activation: Optional[Callable], kernel_size: Tuple[int, ...]) -> Tuple[int, float]:
     """(code, scale) of a mask activation the kernels apply themselves; (0, 0.0) for any other.
 
-    Only the exact classes qualify (a subclass may change ``forward``). A non-positive sigmoid scale
-    is left to ``MaskSigmoid`` itself, which raises the reference's ``ValueError``."""
+    Only the exact classes qualify (a subclass may change ``forward``), and only while no forward
+    hook or pre-hook would run on the call (the reference calls the module, so a hook that reads or
+    edits the mask keeps running). A non-positive sigmoid scale is left to ``MaskSigmoid`` itself,
+    which raises the reference's ``ValueError``."""
+    if isinstance(activation, nn.Module) and _has_forward_hooks(activation):
+        return _FUSED_NONE, 0.0
     if type(activation) is MaskSigmoid:
         if activation.scale > 0:
             return _FUSED_SIGMOID, float(activation.scale)
