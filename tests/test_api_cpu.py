@@ -1,7 +1,9 @@
 """CPU tests of the drop-in boundary and the host logic (no GPU compute).
 
 * the C ABI library loads and exports every function declared in include/tvdcn_hip.h;
-  its host-only entry points (output size, workspace queries, argument checks) work;
+  its host-only entry points (output size, workspace and batch-block queries, argument checks) work;
+* the C++ API of include/tvdcn_ops.h: the reference's exported symbols, and a C++ caller built
+  against the header and linked with _C.so gets the Python API's results;
 * the operator schemas match the reference's (names, argument order, defaults);
 * shape inference and validation run on meta tensors, with the reference's error
   texts (checked side by side with the reference build when oracle/_ref exists);
@@ -724,3 +726,82 @@ def test_c_abi_batch_blocks_beyond_32_bit_indexing(lib):
     finally:
         assert lib.tvdcn_set_max_block_elements(2 ** 31 - 1) == 0
     assert lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(big)) == fw
+
+
+CPP_CALLER = os.path.join(ROOT, "tests", "cpp", "cpp_api_caller.cpp")
+
+
+@pytest.fixture(scope="module")
+def cpp_caller_output(tmp_path_factory):
+    """builds tests/cpp/cpp_api_caller.cpp against include/tvdcn_ops.h and tvdcn_amd/_C.so (g++, torch's
+    headers and libraries), runs it, returns {name: values}"""
+    import subprocess
+    from tvdcn_amd import _build
+    tdir, incs = _build._torch_paths()
+    libdir = os.path.join(tdir, "lib")
+    exe = str(tmp_path_factory.mktemp("cpp_api") / "caller")
+    cmd = ["g++", "-O1", "-std=c++17", f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           "-I", os.path.join(ROOT, "include")]
+    for i in incs:
+        cmd += ["-isystem", i]
+    cmd += [CPP_CALLER, "-o", exe, os.path.join(ROOT, "tvdcn_amd", "_C.so"), "-L", libdir, "-lc10", "-ltorch",
+            "-ltorch_cpu",
+            f"-Wl,-rpath,{libdir}", f"-Wl,-rpath,{os.path.join(ROOT, 'tvdcn_amd')}"]
+    subprocess.run(cmd, check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    proc = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    out = {}
+    for line in proc.stdout.splitlines():
+        name, *vals = line.split()
+        out[name] = vals
+    return out
+
+
+def _filled(shape, phase):
+    n = 1
+    for v in shape:
+        n *= v
+    return torch.sin(torch.arange(n, dtype=torch.float32) * 0.37 + phase).reshape(shape)
+
+
+def test_cpp_api_exports_the_reference_symbols():
+    """The C++ API's functions have the reference's mangled names (namespace, name, argument types):
+    every public tvdcn:: function the reference's own build exports (its CPU kernels' internals aside),
+    _C.so exports too, so C++ code linked against the reference links against this library."""
+    import subprocess
+    if not oracle.have_reference():
+        pytest.skip("reference CPU build (oracle/_ref) not available")
+
+    def exported(path):
+        out = subprocess.run(["nm", "-D", "--defined-only", path], stdout=subprocess.PIPE, text=True,
+                             check=True).stdout
+        return {ln.split()[-1] for ln in out.splitlines() if ln.split() and ln.split()[-1].startswith("_ZN5tvdcn")}
+
+    ref = {s for s in exported(oracle.REF_LIB) if not s.startswith("_ZN5tvdcn3ops3cpu")}
+    ours = exported(os.path.join(ROOT, "tvdcn_amd", "_C.so"))
+    assert len(ref) == 26
+    assert ref <= ours, sorted(ref - ours)
+
+
+def test_cpp_api_caller(cpp_caller_output):
+    """A C++ program calling tvdcn::ops (include/tvdcn_ops.h) on host tensors gets what the Python API
+    computes from the same inputs: forward (int and SymInt argument forms), the backward schema, a
+    transposed op with output_padding, default arguments, and the library information."""
+    out = cpp_caller_output
+    val = lambda name: torch.tensor([float(v) for v in out[name]], dtype=torch.float64)
+    assert int(out["cuda_version"][0]) == tvdcn.cuda_version()
+    assert out["cuda_arch_flags"] == tvdcn.cuda_arch_list()
+    x, w, b = _filled((2, 4, 5, 6), 0.1), _filled((3, 4, 3, 3), 0.2), _filled((3,), 0.3)
+    off, msk = _filled((2, 36, 5, 6), 0.4) * 1.5, _filled((2, 9, 5, 6), 0.5).abs()
+    y = tvdcn.deform_conv2d(x, w, off, msk, b, stride=1, padding=1, dilation=1)
+    close = lambda name, t: torch.allclose(val(name), t.detach().double().flatten(), rtol=1e-6, atol=1e-6)
+    assert close("conv2d", y) and close("conv2d_symint", y)
+    gy = _filled(tuple(y.shape), 0.6)
+    grads = torch.ops.tvdcn._deform_conv2d_backward(gy, x, w, off, msk, b, [1, 1], [1, 1], [1, 1], 1)
+    for name, g in zip(("input", "weight", "offset", "mask", "bias"), grads):
+        assert close(f"conv2d_grad_{name}", g), name
+    x1, w1, off1 = _filled((2, 4, 7), 0.7), _filled((4, 2, 3), 0.8), _filled((2, 3, 7), 0.9)
+    assert close("transpose1d", tvdcn.deform_conv_transpose1d(x1, w1, off1, None, None, stride=2, padding=1,
+                                                                output_padding=1))
+    x3, w3, off3 = _filled((1, 2, 3, 4, 4), 1.0), _filled((2, 2, 2, 2, 2), 1.1), _filled((1, 24, 2, 3, 3), 1.2)
+    assert close("conv3d_defaults", tvdcn.deform_conv3d(x3, w3, off3))

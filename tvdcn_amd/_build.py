@@ -6,7 +6,8 @@ Two shared objects are produced next to this file:
   ``include/tvdcn_hip.h`` (hipcc, one object per ``csrc/hip/*.hip``).
 * ``_C.so`` -- the PyTorch operator layer (``csrc/torch/ops.cpp``) that registers
   the ``tvdcn`` ops and calls the C ABI (links against ``libtvdcn_hip.so``), with the
-  host-tensor (CPU key) kernels of ``csrc/torch/cpu_kernels.cpp``.
+  host-tensor (CPU key) kernels of ``csrc/torch/cpu_kernels.cpp`` and the C++ API of
+  ``include/tvdcn_ops.h`` (``csrc/torch/cpp_api.cpp``).
 
 Run ``python -m tvdcn_amd._build`` (or ``__graft_entry__.build()``). Objects go to
 ``tvdcn_amd/_build/`` and are rebuilt when their sources (or shared headers) change.
@@ -22,6 +23,7 @@ ROOT = os.path.dirname(HERE)
 HIP_DIR = os.path.join(HERE, "csrc", "hip")
 TORCH_SRC = os.path.join(HERE, "csrc", "torch", "ops.cpp")
 CPU_SRC = os.path.join(HERE, "csrc", "torch", "cpu_kernels.cpp")
+CPP_API_SRC = os.path.join(HERE, "csrc", "torch", "cpp_api.cpp")
 INCLUDE = os.path.join(ROOT, "include")
 OBJ_DIR = os.path.join(HERE, "_build")
 HIP_LIB = os.path.join(HERE, "libtvdcn_hip.so")
@@ -104,7 +106,7 @@ def build_torch(force=False, verbose=False):
     os.makedirs(OBJ_DIR, exist_ok=True)
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
     objs = []
-    for src, extra in ((TORCH_SRC, []), (CPU_SRC, ["-O3", "-fopenmp"])):
+    for src, extra in ((TORCH_SRC, []), (CPU_SRC, ["-O3", "-fopenmp"]), (CPP_API_SRC, [])):
         obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + "_torch.o")
         objs.append(obj)
         if force or _stale(obj, [src] + _headers() + _torch_headers()):

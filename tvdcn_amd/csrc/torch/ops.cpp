@@ -1091,7 +1091,9 @@ std::string arch_flags() { return tvdcn_arch_flags(); }
     "Tensor? mask=None, Tensor? bias=None, SymInt[" #D "] stride=1, SymInt[" #D "] padding=0, SymInt[" #D      \
     "] output_padding=0, SymInt[" #D "] dilation=1, SymInt groups=1) -> (Tensor, Tensor, Tensor, Tensor, Tensor)"
 
-TORCH_LIBRARY(tvdcn, m) {
+// a fragment (as the reference registers each op file, ops/deform_conv2d.cpp:117): other libraries
+// may add operators to the namespace
+TORCH_LIBRARY_FRAGMENT(tvdcn, m) {
     m.def(TVDCN_CONV_SCHEMA(1));
     m.def(TVDCN_CONV_BWD_SCHEMA(1));
     m.def(TVDCN_CONV_SCHEMA(2));
