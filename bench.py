@@ -39,14 +39,16 @@ PEAK_16BIT_MFMA = 2.5e15       # MI355X dense fp16 / bf16 matrix, FLOP/s
 
 def mfma_path(family, dtype=torch.float32, dim=2):
     """(MFMA instruction, MFMA products per algorithmic product, its dense peak) of a kernel family's
-    K loop: 16x16x32 MFMAs in the 1D/2D kernels and the data gradient, fp32 operands as three bf16
-    pieces of which six cross products are summed (fp32-accurate), fp16/bf16 operands as they are;
-    the 3D forward and weight gradient run fp32 16x16x4 MFMAs (operands widened). A launch whose fp32
-    operands were flagged (not finite, or too large for the pieces) runs the fp32 loop instead."""
+    K loop: 16x16x32 MFMAs in the 1D/2D kernels and the data gradient, fp32 operands as two fp16
+    pieces at a per-tensor power-of-two scale, of which three cross products are summed
+    (fp32-accurate), fp16/bf16 operands as they are; the 3D forward and weight gradient run fp32
+    16x16x4 MFMAs (operands widened). A launch whose fp32 operands were flagged (not finite) runs the
+    fp32 loop instead. The fp32 path's own ceiling is the 16-bit peak over the products per product
+    (2.5 PFLOP/s / 3 = 833 TFLOP/s fp32-equivalent), above the fp32 MFMA peak."""
     if dim == 3 and family in ("gather_gemm", "weight_grad"):
         return "v_mfma_f32_16x16x4_f32", 1, PEAK_FP32_MFMA
     if dtype == torch.float32:
-        return "v_mfma_f32_16x16x32_bf16 (3 bf16 pieces per fp32 value, 6 products)", 6, PEAK_16BIT_MFMA
+        return "v_mfma_f32_16x16x32_f16 (2 fp16 pieces per fp32 value, 3 products)", 3, PEAK_16BIT_MFMA
     return f"v_mfma_f32_16x16x32_{'f16' if dtype == torch.float16 else 'bf16'}", 1, PEAK_16BIT_MFMA
 FAMILIES = ["layout", "gather_gemm", "data_grad", "weight_grad", "bias_grad", "mask_softmax"]
 
@@ -166,8 +168,11 @@ def family_rooflines(kern, contraction_flops, grad_out_bytes, mask_bytes=0, dtyp
                              achieved=round(achieved / scale, 2), peak=round(peak / scale, 1), unit=unit,
                              frac=round(achieved / peak, 4))
             if bound == "mfma":
+                # hw_frac: the instruction's use of its own dense peak, which is also the fraction of
+                # the path's ceiling (hw_peak / products in algorithmic FLOP/s)
                 instr, products, hw_peak = mfma_path(name, dtype, dim)
-                out[name].update(mfma=instr, hw_frac=round(products * achieved / hw_peak, 4))
+                out[name].update(mfma=instr, hw_frac=round(products * achieved / hw_peak, 4),
+                                 ceiling=round(hw_peak / products / scale, 1))
         else:
             # layout family: several small launches (channels-last copies, weight re-layouts, zero fills)
             out[name] = dict(avg_ms=round(k["avg_ms"], 4), launches=k["launches"], total_ms=round(k["total_ms"], 4))
@@ -271,7 +276,7 @@ def run_suite_case(n, dtype, steps, warmup, cpu=False):
     roof = family_rooflines(kern, F, es * gout.numel(), mask_bytes, dtype=dtype, dim=dim)
     row = {
         "case": c["name"], "dtype": str(dtype).replace("torch.", ""),
-        "compute": ("fp32-accurate: bf16 pieces on 16x16x32 MFMAs, fp32 accumulate" if dtype == torch.float32 else
+        "compute": ("fp32-accurate: scaled fp16 pieces on 16x16x32 MFMAs, fp32 accumulate" if dtype == torch.float32 else
                     f"{str(dtype).replace('torch.', '')} operands on 16x16x32 MFMAs, fp32 accumulate") +
                    ("; 3D forward and weight gradient: fp32 16x16x4 MFMAs" if dim == 3 else ""),
         "mask": "softmax of logits in the mask load" if logits is not None else "given",
@@ -432,7 +437,8 @@ def main():
     dom = max(mfma, key=lambda k: kern[k]["total_ms"])
     d = roof[dom]
     roofline = dict(kernel=dom, bound=d["bound"], achieved=d["achieved"], peak=d["peak"], unit=d["unit"],
-                    frac=d["frac"], traffic=load_traffic(dom), mfma=d.get("mfma"), hw_frac=d.get("hw_frac"))
+                    frac=d["frac"], traffic=load_traffic(dom), mfma=d.get("mfma"), hw_frac=d.get("hw_frac"),
+                    ceiling=d.get("ceiling"))
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -76,7 +76,7 @@ def test_c_abi_host_queries(lib):
     fw = lib.tvdcn_deform_conv_forward_workspace_size(ctypes.byref(d))
     bw = lib.tvdcn_deform_conv_backward_workspace_size(ctypes.byref(d))
     # forward: channels-last copy of the input (33.5 MB) + the re-laid-out weight, fp32 (2.4 MB) and
-    # as the 16-bit MFMA operand (three bf16 pieces: 3.5 MB)
+    # as the 16-bit MFMA operand (two fp16 pieces: 2.4 MB)
     assert 8 * 256 * 64 * 64 * 4 <= fw < 8 * 256 * 64 * 64 * 4 + 8 * 2**20
     assert bw > fw
     # transposed output size (cfg5): 32 -> 64 with k4 s2 p1

@@ -401,9 +401,9 @@ def test_saved_input_version_check_by_default():
 
 @pytest.mark.parametrize("what", ["input", "mask", "grad_out"])
 def test_large_fp32_operands_take_the_fp32_loop(what):
-    """fp32 operands go into the 16-bit MFMA loops as three bf16 pieces only when the pieces cannot
-    overflow: an input at or above 2^96, a plain mask at or above 2^30 or a grad_out past the bf16
-    range sets the device flag, and the kernels run their fp32 MFMA loops. Results against the
+    """fp32 operands go into the 16-bit MFMA loops as scaled fp16 pieces only when their products and
+    scales stay in the float range: an input at or above 2^96, a plain mask at or above 2^30 or a
+    grad_out past the bf16 range sets the device flag, and the kernels run their fp32 MFMA loops. Results against the
     float64 oracle at the fp32 tolerances (forward and every gradient)."""
     case = make_case(2, False, batch=2, cin=32, cout=32, kernel=[3, 3], stride=[1, 1], padding=[1, 1],
                      dilation=[1, 1], in_size=[14, 12], out_pad=[0, 0], seed=560)

@@ -20,12 +20,12 @@
 //     consecutive channels of one pixel per (tap, 16-pixel block). It runs on
 //     16x16x32 MFMAs, 32 channels per step, from 16-bit operands laid out by
 //     data_prep_kernel (Z and weight splits, one launch): fp16 and bf16 tensors as they are, fp32
-//     tensors as three bf16 pieces each, of whose nine cross products the six with
-//     i + j <= 2 are summed (the rest are below 2^-25 of the product, under fp32's own
-//     rounding; 6 MFMAs at 16 cycles against 8 fp32 16x16x4 MFMAs at 32 cycles per 32
-//     channels). An fp32 operand that is not finite or would round past the bf16
-//     range (a device flag set by the layout kernels) sends the launch down the fp32
-//     loop (16x16x4 MFMAs, 16 channels per step), which keeps the reference's inf/nan
+//     tensors as two fp16 pieces each at a per-tensor power-of-two scale, of whose four cross
+//     products the three with i + j <= 1 are summed (the rest are within fp32's own rounding;
+//     3 MFMAs at 16 cycles against 8 fp32 16x16x4 MFMAs at 32 cycles per 32 channels), the
+//     sums scaled back after the K loop. An fp32 operand that is not finite or would round
+//     past the bf16 range (a device flag set by the layout kernels) sends the launch down the
+//     fp32 loop (16x16x4 MFMAs, 16 channels per step), which keeps the reference's inf/nan
 //     propagation.
 //   * Epilogue per tap: the geometry of the 256 pixels (one per thread) goes to an
 //     LDS table. The offset/mask gradients are formed in the MFMA layout (4
@@ -142,6 +142,7 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
                                               uint16_t *__restrict__ zs, int *flag, int G, int Mg, int Pn, int ms32,
                                               int pblocks, bool zvec) {
     float(*tile)[65] = reinterpret_cast<float(*)[65]>(smem);   // [32][65]
+    const int sz = NP == 2 ? operand_scale(flag, AMAX_Z) : 0;   // (every lane: before any returns)
     // (the block index is a grid index: 32-bit division, not the 64-bit sequence)
     const unsigned ub = (unsigned)bid;
     const int pb = (int)(ub % (unsigned)pblocks);
@@ -183,11 +184,11 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
         bad = bad || bf16_split_bad(v[e]);
     }
     uint4 out[NP];
-    pack8_16<T, NP>(v, out);
+    pack8_16<T, NP>(v, sz, out);
     uint16_t *dst = zs + ((size_t)bgs * Pn + p) * (NP * 32) + q * 8;
 #pragma unroll
     for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + k * 32) = out[k];
-    if (NP == 3 && bad) atomicOr(flag, 1);
+    if (NP == 2 && bad) atomicOr(flag, 1);
 }
 
 // Reduction over each row of 16 lanes (the lanes of one channel quad's 16 pixels), the
@@ -578,6 +579,16 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 kloop16s();
             else
                 kloop16();
+            if constexpr (npiece_of<T>() == 2) {
+                // the pieces' scales back out: G = acc 2^-(s_W + s_Z)
+                const int back = -(operand_scale(flag, AMAX_W) + operand_scale(flag, AMAX_Z));
+#pragma unroll
+                for (int tp = 0; tp < TMAX; ++tp)
+#pragma unroll
+                    for (int pb = 0; pb < PB; ++pb)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) acc[tp][pb][v] = ldexpf(acc[tp][pb][v], back);
+            }
         } else {
             const bool mpad = g.Mg % BM != 0;
             if (ntaps == TMAX && !mpad)
@@ -1209,6 +1220,7 @@ __device__ __forceinline__ void weight_split_block(int L, float *smem, const T *
     }
     __syncthreads();
     uint16_t *dst = out + ((((size_t)grp * c_tiles + ct) * ms32 + st) * Kn + t0) * (NP * 512);
+    const int sw = NP == 2 ? operand_scale(flag, AMAX_W) : 0;
     bool bad = false;
     for (int u = threadIdx.x; u < nt * 64; u += blockDim.x) {
         const int tt = u >> 6, l = u & 63, q = l >> 4, c = l & 15;
@@ -1219,11 +1231,11 @@ __device__ __forceinline__ void weight_split_block(int L, float *smem, const T *
             bad = bad || bf16_split_bad(v[e]);
         }
         uint4 o[NP];
-        pack8_16<T, NP>(v, o);
+        pack8_16<T, NP>(v, sw, o);
 #pragma unroll
         for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + (size_t)tt * (NP * 512) + k * 512 + l * 8) = o[k];
     }
-    if (NP == 3 && bad) atomicOr(flag, 1);
+    if (NP == 2 && bad) atomicOr(flag, 1);
 }
 
 // The data gradient's operand layouts in one launch: blocks [0, nz) split Z (z_split_block),
@@ -1429,7 +1441,7 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
     t = win_resize(base, g, dim, fixed, cell);
     const int npass = (g.Kn + WIN_TMAX - 1) / WIN_TMAX;
     t.tpp = (g.Kn + npass - 1) / npass;
-    t.npiece = dtype == kF32 ? 3 : 1;
+    t.npiece = dtype == kF32 ? 2 : 1;
     // 1D / 2D passes of nine taps: the K loop's weight blocks staged in LDS when the window
     // keeps a margin of min(R, 4) cells beside the buffers (3D: short K loops, and the window
     // needs the room; five-tap 1D passes ran slower staged, with two buffers or with three

@@ -98,6 +98,10 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     const int mrow = mt * BMW + (wave % (NW / TG)) * (MB * 16);   // first row of this wave
     constexpr bool use16 = USE16 && DIM < 3;
     if (flag != nullptr && (*flag == 0) != use16) return;   // the other instantiation's launch
+    // fp32 as fp16 pieces: the scales of Z and of the sampled columns, and the one back out
+    const int s_z = use16 ? operand_scale(flag, AMAX_Z) : 0;
+    const int s_s = use16 ? sampled_scale(g, flag, mask != nullptr) : 0;
+    const int s_back = npiece_of<T>() == 2 && use16 ? -(s_z + s_s) : 0;
 
     if constexpr (DIM == 3) {
         if (tid < XS) xwin[wt.cells * XS + tid] = 0.f;   // zero cell of the 3D corner reads
@@ -266,7 +270,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 #pragma unroll
                         for (int v = 0; v < 4; ++v) {
                             uint16_t pc[NP];
-                            split_one16<T, NP>(sv[v], pc);
+                            split_one16<T, NP>(sv[v], s_s, pc);
 #pragma unroll
                             for (int kk = 0; kk < NP; ++kk)
                                 s16[((size_t)kk * TM * BC + tl * BC + 4 * sq + v) * SS16 + sj] = pc[kk];
@@ -323,7 +327,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                     for (int kb = 0; kb < KB; ++kb) {
                         uint4 za16[MB][NP];
 #pragma unroll
-                        for (int mb = 0; mb < MB; ++mb) pack8_16<T, NP>(zc[kb][mb], za16[mb]);
+                        for (int mb = 0; mb < MB; ++mb) pack8_16<T, NP>(zc[kb][mb], s_z, za16[mb]);
 #pragma unroll
                         for (int tp = 0; tp < TM; ++tp) {
                             if ((FULL || tp < ntaps) && (TG == 1 || tp % TG == tg)) {
@@ -397,7 +401,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int m = mrow + mb * 16 + 4 * q + v;
-                    if (m < g.Mg) dst[(size_t)m * g.Cg + c] = acc[mb][tp][v];
+                    if (m < g.Mg) dst[(size_t)m * g.Cg + c] = s_back != 0 ? ldexpf(acc[mb][tp][v], s_back) : acc[mb][tp][v];
                 }
         }
     }

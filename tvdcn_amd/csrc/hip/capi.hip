@@ -289,7 +289,7 @@ Layout layout(const Plan &pl, bool backward) {
     const size_t SENTINEL = (size_t)-1;
     L.xcl = L.wf = L.wd = L.cl_acc = L.wpart = L.goff_acc = L.gmask_acc = L.yacc = SENTINEL;
     L.zs = L.wsplit = L.w16 = L.flag = SENTINEL;
-    L.flag = take(align_up(sizeof(int)));
+    L.flag = take(align_up(sizeof(int) * OPERAND_FLAG_WORDS));   // the flag and the operands' largest magnitudes
     // windowed data gradient (conv backward, transposed forward and backward): split operands
     auto take_split = [&]() {
         if (!pl.wn_s.ok) return;
@@ -461,9 +461,10 @@ tvdcn_status check_forward_pointers(const tvdcn_conv_desc *desc, const void *off
 // tvdcn_deform_conv_forward_noalloc (the per-device scratch array). Every workspace byte the
 // kernels read is written first in the same call (the zero-filled accumulator by a fill kernel),
 // so the workspace may hold anything on entry.
-// The sampled side of the 16-bit forward loop: mask * bilinear(X) in bf16 pieces (fp32) needs
-// |X| < SAMPLED_LIMIT and |mask| < MASK_LIMIT (checked on the device into *flag); a sigmoid mask
-// activation bounds the mask by its scale, a softmax by 1.
+// The sampled side of the 16-bit forward loop: mask * bilinear(X) in scaled fp16 pieces (fp32) needs
+// |X| < SAMPLED_LIMIT and |mask| < MASK_LIMIT (checked on the device into *flag: the product and its
+// scale stay in the float range); a sigmoid mask activation bounds the mask by its scale, a softmax
+// by 1.
 bool sampled16_host_ok(const Plan &pl, const tvdcn_conv_desc *desc) {
     if (pl.dtype != kF32) return true;
     if (desc->flags & TVDCN_FLAG_MASK_SIGMOID) return std::fabs(desc->mask_scale) < (double)MASK_LIMIT;
@@ -476,6 +477,22 @@ const void *mask_to_check(const Plan &pl, const tvdcn_conv_desc *desc, const voi
     return mask;
 }
 size_t mask_numel(const Geo &g) { return (size_t)g.B * g.mg * g.Kn * g.Pn; }
+
+// float32: the largest magnitudes of the 16-bit MFMA operands (their pieces' scales) -- the weight,
+// the sampled tensor X, a mask given as values (an activated mask's bound is known), the GEMM-side
+// tensor Z -- into the words after the zeroed operand flag (null pointers: not needed)
+hipError_t operand_amax(const Plan &pl, const tvdcn_conv_desc *desc, const void *weight, const void *x,
+                        const void *mask, const void *z, int *flag, hipStream_t s) {
+    const Geo &g = pl.g;
+    if (pl.dtype != kF32) return hipSuccess;
+    const bool plain_mask = !(desc->flags & (TVDCN_FLAG_MASK_SIGMOID | TVDCN_FLAG_MASK_SOFTMAX));
+    const AmaxItem items[4] = {
+        {static_cast<const float *>(weight), (size_t)g.M * g.Cg * g.Kn, AMAX_SLOT_W},
+        {static_cast<const float *>(x), (size_t)g.B * g.C * g.Sn, AMAX_SLOT_X},
+        {plain_mask ? static_cast<const float *>(mask) : nullptr, mask_numel(g), AMAX_SLOT_M},
+        {static_cast<const float *>(z), (size_t)g.B * g.M * g.Pn, AMAX_SLOT_Z}};
+    return launch_amax(items, 4, flag, s);
+}
 
 hipError_t check_sampled(const Plan &pl, const tvdcn_conv_desc *desc, const void *x_in_place, const void *mask,
                          int *flag, hipStream_t s) {
@@ -507,18 +524,25 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
         void *w16 = pl.fw.ok && sampled16_host_ok(pl, desc) ? at(workspace, L.w16) : nullptr;
         // the flag and (split channel slices) the fp32 accumulator zeroed by one launch
         void *y32 = pl.fw.ok && pl.fw.ksplit > 1 ? (dt == kF32 ? output : at(workspace, L.yacc)) : nullptr;
-        const FillItem fills[2] = {{flag, 4}, {y32, y32 ? (size_t)g.B * g.M * g.Pn * 4 : 0}};
+        const FillItem fills[2] = {{flag, 4 * OPERAND_FLAG_WORDS}, {y32, y32 ? (size_t)g.B * g.M * g.Pn * 4 : 0}};
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero_multi(fills, 2, s));
         const void *x_in_place = nullptr;
-        // the 16-bit loop's mask range check rides on the input's layout copy when there is one
+        // the 16-bit loop's mask range check and (fp32) its operands' largest magnitudes ride on the
+        // input's layout copy when there is one
         const void *mchk = w16 != nullptr ? mask_to_check(pl, desc, mask) : nullptr;
-        if (!(desc->flags & TVDCN_FLAG_CHANNELS_LAST))
+        if (!(desc->flags & TVDCN_FLAG_CHANNELS_LAST)) {
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, input, xcl, g.B, g.C, g.Sn, s, flag, mchk,
-                                                                         mask_numel(g), MASK_LIMIT));
-        else if (acc_is_storage(dt))
-            x_in_place = xcl = const_cast<void *>(input);   // already the kernels' layout and type
-        else
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, input, xcl, (size_t)g.B * g.Sn * g.C, s));
+                                                                         mask_numel(g), MASK_LIMIT,
+                                                                         w16 != nullptr ? weight : nullptr,
+                                                                         (size_t)g.M * g.Cg * g.Kn));
+        } else {
+            if (acc_is_storage(dt))
+                x_in_place = xcl = const_cast<void *>(input);   // already the kernels' layout and type
+            else
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, input, xcl, (size_t)g.B * g.Sn * g.C, s));
+            if (w16 != nullptr)
+                TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, operand_amax(pl, desc, weight, input, mask, nullptr, flag, s));
+        }
         if (pl.fw.ok) {
             if (w16 != nullptr) {
                 // both weight layouts (16-bit pieces and the fp32 loop's) in one launch
@@ -540,9 +564,10 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
         }
     } else {
         void *wd = at(workspace, L.wd), *ycl = at(workspace, L.cl_acc);
-        const FillItem fills[2] = {{flag, 4}, {ycl, (size_t)g.B * g.Sn * g.C * acc_size(dt)}};
+        const FillItem fills[2] = {{flag, 4 * OPERAND_FLAG_WORDS}, {ycl, (size_t)g.B * g.Sn * g.C * acc_size(dt)}};
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero_multi(fills, 2, s));
         if (pl.wn_s.ok) {
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, operand_amax(pl, desc, weight, nullptr, nullptr, input, flag, s));
             void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_prep(dt, g, pl.wn_s, input, weight, zs, wsp, wd, flag, s));
             TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, input, wd, zs,
@@ -562,8 +587,8 @@ tvdcn_status forward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const 
 // bias gradient; the weight gradient is written (first block) or added (accumulate_weight).
 tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const void *grad_out, const void *input,
                               const void *weight, const void *offset, const void *mask, void *grad_input,
-                              void *grad_weight, void *grad_offset, void *grad_mask, void *workspace, void *stream,
-                              bool accumulate_weight) {
+                              void *grad_weight, void *grad_offset, void *grad_mask, void *grad_bias, void *workspace,
+                              void *stream, bool accumulate_weight) {
     const Geo &g = pl.g;
     const Layout L = layout(pl, true);
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -589,18 +614,22 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         // the offset / mask gradient accumulators, the operand flag and grad_input zeroed by one launch
         const FillItem fills[4] = {{goff, goff ? n_goff * ab : 0},
                                    {gmask, gmask ? n_gmask * ab : 0},
-                                   {flag, 4},
+                                   {flag, 4 * OPERAND_FLAG_WORDS},
                                    {gx_cl, gx_cl ? (size_t)g.B * g.Sn * g.C * ab : 0}};
         TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero_multi(fills, 4, s));
         const bool coord = offset != nullptr || mask != nullptr;
         // the 16-bit loops of the sampled side (weight gradient; transposed: input gradient)
         const bool sampled16 = sampled16_host_ok(pl, desc) && (pl.ww.ok || (pl.transposed && pl.fw.ok));
         const void *x_in_place = nullptr;
+        // (fp32) the 16-bit MFMA operands' largest magnitudes: the weight and X ride on X's layout
+        // copy, Z = grad_out on the bias gradient (this block's, accumulated over the blocks),
+        // whatever else on a launch of its own
         if (!cl_in) {
             // the mask's range check rides on the layout copy
             const void *mchk = sampled16 ? mask_to_check(pl, desc, mask) : nullptr;
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_to_channels_last(dt, X, xcl, g.B, g.C, g.Sn, s, flag, mchk,
-                                                                         mask_numel(g), MASK_LIMIT));
+                                                                         mask_numel(g), MASK_LIMIT, weight,
+                                                                         (size_t)g.M * g.Cg * g.Kn));
         } else {
             if (direct)
                 x_in_place = xcl = const_cast<void *>(X);   // already the kernels' layout and type
@@ -608,6 +637,17 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_storage_to_acc(dt, X, xcl, (size_t)g.B * g.Sn * g.C, s));
             if (sampled16) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, check_sampled(pl, desc, x_in_place, mask, flag, s));
         }
+        // grad_out (B, Cout, *out_size): conv Cout = M on the column grid, transposed Cout = C on the
+        // sampled grid
+        if (!pl.transposed)
+            TVDCN_LAUNCH(TVDCN_KERNEL_BIAS_GRAD, s, launch_bias_grad(dt, grad_out, grad_bias, g.B, g.M, g.Pn, s,
+                                                                     accumulate_weight, flag));
+        else
+            TVDCN_LAUNCH(TVDCN_KERNEL_BIAS_GRAD, s, launch_bias_grad(dt, grad_out, grad_bias, g.B, g.C, g.Sn, s,
+                                                                     accumulate_weight));
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, operand_amax(pl, desc, cl_in ? weight : nullptr, cl_in ? X : nullptr,
+                                                          cl_in ? mask : nullptr, pl.transposed ? Z : nullptr, flag,
+                                                          s));
         void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
         if (pl.wn_s.ok)
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_prep(dt, g, pl.wn_s, Z, weight, zs, wsp, wd, flag, s));
@@ -896,17 +936,9 @@ tvdcn_status tvdcn_deform_conv_backward(const tvdcn_conv_desc *desc, const void 
         if (st) return st;
         st = backward_planned(nb == block ? pl : bp, desc, adv(grad_out, b0 * out_b), adv(input, b0 * in_b), weight,
                               adv(offset, b0 * off_b), adv(mask, b0 * mask_b), adv(grad_input, b0 * in_b),
-                              grad_weight, adv(grad_offset, b0 * off_b), adv(grad_mask, b0 * mask_b), workspace, stream,
-                              b0 > 0);
+                              grad_weight, adv(grad_offset, b0 * off_b), adv(grad_mask, b0 * mask_b), grad_bias,
+                              workspace, stream, b0 > 0);
         if (st) return st;
-    }
-    if (grad_bias) {
-        // grad_out is (B, Cout, *out_size) over the whole batch (the kernel indexes in 64 bits):
-        // conv Cout = M on the column grid, transposed Cout = C on the sampled grid
-        const int Cout = (int)desc->out_channels;
-        const int So = pl.transposed ? g.Sn : g.Pn;
-        TVDCN_LAUNCH(TVDCN_KERNEL_BIAS_GRAD, s,
-                     launch_bias_grad(dt, grad_out, grad_bias, (int)desc->batch, Cout, So, s));
     }
     return TVDCN_STATUS_SUCCESS;
 }

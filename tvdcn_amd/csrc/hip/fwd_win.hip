@@ -71,6 +71,9 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     const int slices = (g.Cg + BC - 1) / BC;
     // the 16-bit loop (1D / 2D) when its weight was laid out and (fp32) no operand was flagged
     const bool use16_flag = DIM < 3 && w16 != nullptr && (flag == nullptr || *flag == 0);
+    // fp32 as fp16 pieces: the sampled columns' scale, and the one back out (the weight's with it)
+    const int s_b = npiece_of<T>() == 2 && use16_flag ? sampled_scale(g, flag, mask != nullptr) : 0;
+    const int s_back = npiece_of<T>() == 2 && use16_flag ? -(s_b + operand_scale(flag, AMAX_W)) : 0;
     const int cs_lo = ks * fw.slices_per, cs_hi = min(slices, cs_lo + fw.slices_per);
 
     Tile tile;
@@ -242,7 +245,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 for (int pb = 0; pb < PB; ++pb) {
                     const float v[8] = {b0[pb][0], b0[pb][1], b0[pb][2], b0[pb][3],
                                         b1[pb][0], b1[pb][1], b1[pb][2], b1[pb][3]};
-                    pack8_16<T, NP>(v, bp[pb]);
+                    pack8_16<T, NP>(v, s_b, bp[pb]);
                 }
             };
             if constexpr (STAGE) {
@@ -503,7 +506,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 const int m = mt * BMR + mb * 16 + 4 * q + v;
                 if (m < g.Mg) {
                     const int mg_glob = grp * g.Mg + m;
-                    float r = acc[mb][pb][v];
+                    float r = s_back != 0 ? ldexpf(acc[mb][pb][v], s_back) : acc[mb][pb][v];
                     if (bias != nullptr && ks == 0) r += to_acc<float>(bias[mg_glob]);
                     const size_t o = ((size_t)tile.b * g.M + mg_glob) * g.Pn + p;
                     if (fw.ksplit == 1)
@@ -547,7 +550,8 @@ __global__ void fwd_win_weight_kernel(const T *__restrict__ w, float *__restrict
 // weight (M, Cg, Kn) -> W16[G][slices][pp][Mg_pad / 16][NP][64 lanes][8]: per (slice, tap pair j
 // of pass p, 16-row block) the 16x16x32 A fragments: lane l = m % 16 + 16 q holds at e = 0..7
 // W[m][slice * 16 + 4 q + e % 4] at tap p * tpp + 2 j + e / 4 (zero past the pass, Mg, Cg); fp32
-// as three bf16 pieces (*flag set for a value bad for the split), fp16 / bf16 as they are
+// as two fp16 pieces at the weight's scale (*flag set for a value bad for the split), fp16 / bf16
+// as they are
 // (wp: when not null, the fp32 layout of fwd_win_weight_kernel is written by the same launch)
 template <typename T, int NP>
 __global__ void __launch_bounds__(256)
@@ -555,6 +559,7 @@ fwd_w16_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, i
                int nmb, int tpp, int hp, int pp, float *__restrict__ wp) {
     if (wp != nullptr) fwd_weight_f32<T>(w, wp, G, Mg, Cg, Kn, slices, nmb * 16);
     const unsigned total = (unsigned)G * slices * pp * nmb * 64;
+    const int sw = NP == 2 ? operand_scale(flag, AMAX_W) : 0;
     bool bad = false;
     for (unsigned i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
         const int l = (int)(i & 63);
@@ -576,12 +581,12 @@ fwd_w16_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, i
             bad = bad || bf16_split_bad(v[e]);
         }
         uint4 o[NP];
-        pack8_16<T, NP>(v, o);
+        pack8_16<T, NP>(v, sw, o);
         uint16_t *dst = out + ((((size_t)grp * slices + cs) * pp + pq) * nmb + mb) * (NP * 512) + l * 8;
 #pragma unroll
         for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + k * 512) = o[k];
     }
-    if (NP == 3 && bad) atomicOr(flag, 1);
+    if (NP == 2 && bad) atomicOr(flag, 1);
 }
 
 template <int DIM, typename T, int MB, bool STAGE>
@@ -723,9 +728,9 @@ hipError_t launch_fwd_win_layout16(int dtype, const Geo &g, const FwdWin &fw, co
                        fw.hp, fw.pp, static_cast<float *>(wp));                                                        \
     return hipGetLastError();
     switch (dtype) {
-        case kF32: { TVDCN_FW16(float, 3) }
-        case kF16: { TVDCN_FW16(__half, 1) }
-        case kBF16: { TVDCN_FW16(__hip_bfloat16, 1) }
+        case kF32: { TVDCN_FW16(float, npiece_of<float>()) }
+        case kF16: { TVDCN_FW16(__half, npiece_of<__half>()) }
+        case kBF16: { TVDCN_FW16(__hip_bfloat16, npiece_of<__hip_bfloat16>()) }
     }
 #undef TVDCN_FW16
     return hipErrorInvalidValue;

@@ -61,10 +61,11 @@ struct WinTiles {
     int tpp;             // taps per pass (<= WIN_TMAX)
     size_t chunk_elems;  // floats of the re-laid-out weight
     // 16-bit MFMA operands of the data gradient (16x16x32 MFMAs over 32 GEMM-side channels per
-    // step): fp32 tensors split into three bf16 pieces each, fp16 / bf16 tensors as they are
+    // step): fp32 tensors split into two fp16 pieces each (per-tensor power-of-two scale), fp16 /
+    // bf16 tensors as they are
     int xglobal;         // 3D only: offset / mask gradients read X from global memory, no X window
     int ms32;            // 32-channel steps of the GEMM side (zero padded)
-    int npiece;          // 16-bit pieces per value: 3 (fp32), 1 (fp16 / bf16)
+    int npiece;          // 16-bit pieces per value: 2 (fp32), 1 (fp16 / bf16)
     size_t zs_elems;     // 16-bit elements of the split Z: [B][G][ms32][Pn][npiece][32]
     size_t ws_elems;     // 16-bit elements of the split weight: [G][c_tiles][ms32][Kn][npiece][512]
     int wstage;          // bytes of LDS staging the 16-bit K loop's weight blocks (double-buffered
@@ -122,10 +123,12 @@ WeightTiles plan_weight(const Geo &g, int dtype);
 // layout / elementwise helpers (prep.hip)
 // (flag: when not null, fp32 values not below SAMPLED_LIMIT in magnitude set *flag; chk: when not
 // null, an fp32 tensor of chk_n values range-checked against chk_limit into *flag by the same
-// launch, as launch_check_range does)
+// launch, as launch_check_range does, its largest magnitude into the mask slot after *flag;
+// amax_w: fp32 only, when not null, the largest magnitudes of amax_w's amax_w_n values (the
+// weight slot) and of the copied values (the sampled-tensor slot), by the same launch)
 hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s,
                                    int *flag = nullptr, const void *chk = nullptr, size_t chk_n = 0,
-                                   float chk_limit = 0.f);
+                                   float chk_limit = 0.f, const void *amax_w = nullptr, size_t amax_w_n = 0);
 // 16-bit MFMA operands of the sampled side (forward, weight gradient): the sampled values are
 // mask * bilinear(X), below 2^126 (and so within bf16's range) when |X| < SAMPLED_LIMIT and
 // |mask| < MASK_LIMIT; larger or non-finite values send the launch to its fp32 MFMA loop.
@@ -148,6 +151,25 @@ struct FillItem {
     size_t bytes;
 };
 hipError_t launch_fill_zero_multi(const FillItem *items, int n, hipStream_t s);
+// The fp32 path's 16-bit MFMA operands are fp16 pieces at a per-tensor power-of-two scale: the
+// workspace's operand flag (one int) is followed by the largest magnitudes of the operands (float
+// bits; slots: weight, sampled tensor, mask, GEMM-side tensor), zeroed with it. Each slot is spread
+// over AMAX_SPREAD sub-slots, one per 64-byte line (AMAX_STRIDE words apart): producing blocks raise
+// sub-slot (block index % AMAX_SPREAD), so that their atomics do not all meet on one address, and a
+// consumer takes the largest of the sub-slots.
+constexpr int AMAX_SLOT_W = 0, AMAX_SLOT_X = 1, AMAX_SLOT_M = 2, AMAX_SLOT_Z = 3, AMAX_SLOTS = 4;
+constexpr int AMAX_SPREAD = 64, AMAX_STRIDE = 16;
+constexpr int OPERAND_FLAG_WORDS = AMAX_STRIDE + AMAX_SLOTS * AMAX_SPREAD * AMAX_STRIDE;
+// word (after the flag's first) of sub-slot k of slot
+__host__ __device__ constexpr int amax_word(int slot, int k) { return AMAX_STRIDE + (slot * AMAX_SPREAD + k) * AMAX_STRIDE; }
+struct AmaxItem {
+    const float *p;   // nullptr / n == 0: skipped
+    size_t n;
+    int slot;
+};
+// raises slot `slot` of the words after *flag to the largest |p[i]| of every item (up to 4, one
+// launch; nan values are passed over: the layout kernels' checks flag them)
+hipError_t launch_amax(const AmaxItem *items, int n, int *flag, hipStream_t s);
 hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n, hipStream_t s);
 hipError_t launch_storage_to_acc(int dtype, const void *x, void *acc, size_t n, hipStream_t s);   // elementwise widening
 // gmask_acc (accumulation type) *= d(scale * sigmoid(logit)) / d(logit), elementwise
@@ -157,7 +179,10 @@ hipError_t launch_mask_softmax_logit_grad(int dtype, const void *logits, void *g
                                           hipStream_t s);
 hipError_t launch_mask_sigmoid_grad(int dtype, const void *logits, void *gmask_acc, double scale, size_t n,
                                     hipStream_t s);
-hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s);
+// gbias (when not null) = (accumulate: gbias +) sum over batch and space of gout; flag (fp32, when not
+// null): gout's largest magnitude into the GEMM-side slot after *flag, by the same launch
+hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s,
+                            bool accumulate = false, int *flag = nullptr);
 
 // the three GEMM families
 hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTiles &t, const void *xcl,
@@ -165,7 +190,7 @@ hipError_t launch_fwd_gather_gemm(int dtype, int dim, const Geo &g, const FwdTil
                                   hipStream_t s);
 // weight -> the windowed forward's fragment-major layout (fwd_win.hip)
 hipError_t launch_fwd_win_layout(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *wp, hipStream_t s);
-// the weight as W16 (fp32: three bf16 pieces; *flag set for a value bad for the split)
+// the weight as W16 (fp32: two fp16 pieces at the weight's scale; *flag set for a value bad for the split)
 // (wp: when not null, also the fp32 layout of launch_fwd_win_layout, in the same launch)
 hipError_t launch_fwd_win_layout16(int dtype, const Geo &g, const FwdWin &fw, const void *w, void *w16, int *flag,
                                    hipStream_t s, void *wp = nullptr);

@@ -13,22 +13,66 @@ namespace {
 
 constexpr int TT = 64;   // transpose tile
 
-// x [B][C][S] (T) -> xcl [B][S][C] (A); 64 x 64 tile through LDS, 256 threads. With chk, the
-// grid holds one more z slice whose blocks range-check chk[0 .. chk_n) into *flag instead (one
-// launch for the copy and the check of another operand, e.g. the mask).
+// Raises sub-slot (linear block index % AMAX_SPREAD) of amax slot `slot` after *flag to the block's
+// largest m (every thread of a 256-thread block calls it): one atomic per block, on one of
+// AMAX_SPREAD lines (atomics on one address serialise)
+__device__ __forceinline__ void block_amax(float m, int *flag, int slot) {
+    __shared__ float wmax[4];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        const unsigned blk = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        if (m > 0.f)
+            atomicMax(reinterpret_cast<unsigned *>(flag) + amax_word(slot, (int)(blk % AMAX_SPREAD)),
+                      __float_as_uint(m));
+    }
+}
+
+// The extra jobs of a channels-last copy launch, in the z slices past the batch: the mask's range
+// check against chk_limit (into *flag) and its largest magnitude, the weight's largest magnitude;
+// with amax_x the copy itself records the copied values' largest magnitude (fp32 path pieces)
+struct CopyJobs {
+    const float *chk;
+    size_t chk_n;
+    float chk_limit;
+    const float *w;
+    size_t w_n;
+    bool amax_x;
+};
+__device__ __forceinline__ int copy_extra_slices(const CopyJobs &j) { return (j.chk != nullptr) + (j.w != nullptr); }
+
+// slice k of the extra z slices (blocks of that slice stride over the tensor)
+__device__ __forceinline__ void copy_extra_job(const CopyJobs &j, int k, int *flag) {
+    const bool is_chk = j.chk != nullptr && k == 0;
+    const float *v = is_chk ? j.chk : j.w;
+    const size_t n = is_chk ? j.chk_n : j.w_n;
+    const size_t nb = (size_t)gridDim.x * gridDim.y;
+    bool bad = false;
+    float m = 0.f;
+    for (size_t i = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += nb * blockDim.x) {
+        const float a = fabsf(v[i]);
+        bad = bad || !(a < j.chk_limit);
+        m = fmaxf(m, a);
+    }
+    if (is_chk && bad) atomicOr(flag, 1);
+    block_amax(m, flag, is_chk ? AMAX_SLOT_M : AMAX_SLOT_W);
+}
+
+// x [B][C][S] (T) -> xcl [B][S][C] (A); 64 x 64 tile through LDS, 256 threads. The z slices past the
+// batch run the launch's other jobs (CopyJobs: one launch for the copy and the checks of other
+// operands, e.g. the mask).
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) to_cl_kernel(const T *__restrict__ x, A *__restrict__ xcl, int C, int S,
-                                                    int *flag, const float *__restrict__ chk, size_t chk_n,
-                                                    float chk_limit) {
+                                                    int *flag, const CopyJobs jobs) {
     __shared__ A tile[TT][TT + 1];
     const int b = blockIdx.z;
-    if (chk != nullptr && b == (int)gridDim.z - 1) {
-        bool bad = false;
-        const size_t nb = (size_t)gridDim.x * gridDim.y;
-        for (size_t i = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < chk_n;
-             i += nb * blockDim.x)
-            bad = bad || !(fabsf(chk[i]) < chk_limit);
-        if (bad) atomicOr(flag, 1);
+    const int nextra = flag != nullptr ? copy_extra_slices(jobs) : 0;
+    if (b >= (int)gridDim.z - nextra) {
+        copy_extra_job(jobs, b - ((int)gridDim.z - nextra), flag);
         return;
     }
     const int s0 = blockIdx.x * TT, c0 = blockIdx.y * TT;
@@ -36,13 +80,20 @@ __global__ void __launch_bounds__(256) to_cl_kernel(const T *__restrict__ x, A *
     A *ob = xcl + (size_t)b * C * S;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     bool big = false;
+    float m = 0.f;
     for (int r = ty; r < TT; r += 4) {
         const int c = c0 + r, s = s0 + tx;
         const A v = (c < C && s < S) ? to_acc<A>(xb[(size_t)c * S + s]) : A(0);
-        if constexpr (std::is_same<A, float>::value) big = big || !(fabsf(v) < SAMPLED_LIMIT);
+        if constexpr (std::is_same<A, float>::value) {
+            big = big || !(fabsf(v) < SAMPLED_LIMIT);
+            m = fmaxf(m, fabsf(v));
+        }
         tile[r][tx] = v;
     }
     if (flag != nullptr && big) atomicOr(flag, 1);
+    if constexpr (std::is_same<A, float>::value) {
+        if (flag != nullptr && jobs.amax_x) block_amax(m, flag, AMAX_SLOT_X);
+    }
     __syncthreads();
     for (int r = ty; r < TT; r += 4) {
         const int s = s0 + r, c = c0 + tx;
@@ -52,19 +103,14 @@ __global__ void __launch_bounds__(256) to_cl_kernel(const T *__restrict__ x, A *
 
 // float32 x [B][C][S] -> xcl [B][S][C] with 16-byte accesses on both sides (C % 4 == 0 and
 // S % 4 == 0: a quad is wholly inside or outside the tensor): 64 x 64 tile through LDS, 256
-// threads; a load quad runs along s, a store quad along c. Same chk / flag jobs as to_cl_kernel.
+// threads; a load quad runs along s, a store quad along c. Same jobs as to_cl_kernel.
 __global__ void __launch_bounds__(256) to_cl4_kernel(const float *__restrict__ x, float *__restrict__ xcl, int C,
-                                                     int S, int *flag, const float *__restrict__ chk, size_t chk_n,
-                                                     float chk_limit) {
+                                                     int S, int *flag, const CopyJobs jobs) {
     __shared__ float tile[TT][TT + 1];   // [c][s]
     const int b = blockIdx.z;
-    if (chk != nullptr && b == (int)gridDim.z - 1) {
-        bool bad = false;
-        const size_t nb = (size_t)gridDim.x * gridDim.y;
-        for (size_t i = ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < chk_n;
-             i += nb * blockDim.x)
-            bad = bad || !(fabsf(chk[i]) < chk_limit);
-        if (bad) atomicOr(flag, 1);
+    const int nextra = flag != nullptr ? copy_extra_slices(jobs) : 0;
+    if (b >= (int)gridDim.z - nextra) {
+        copy_extra_job(jobs, b - ((int)gridDim.z - nextra), flag);
         return;
     }
     const int s0 = blockIdx.x * TT, c0 = blockIdx.y * TT;
@@ -72,6 +118,7 @@ __global__ void __launch_bounds__(256) to_cl4_kernel(const float *__restrict__ x
     float *ob = xcl + (size_t)b * C * S;
     const int u = threadIdx.x & 15, r0 = threadIdx.x >> 4;
     bool big = false;
+    float m = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int cl = r0 + 16 * k, c = c0 + cl, s = s0 + 4 * u;
@@ -79,12 +126,14 @@ __global__ void __launch_bounds__(256) to_cl4_kernel(const float *__restrict__ x
         if (c < C && s < S) v = *reinterpret_cast<const float4 *>(xb + (size_t)c * S + s);
         big = big || !(fabsf(v.x) < SAMPLED_LIMIT) || !(fabsf(v.y) < SAMPLED_LIMIT) ||
               !(fabsf(v.z) < SAMPLED_LIMIT) || !(fabsf(v.w) < SAMPLED_LIMIT);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         tile[cl][4 * u] = v.x;
         tile[cl][4 * u + 1] = v.y;
         tile[cl][4 * u + 2] = v.z;
         tile[cl][4 * u + 3] = v.w;
     }
     if (flag != nullptr && big) atomicOr(flag, 1);
+    if (flag != nullptr && jobs.amax_x) block_amax(m, flag, AMAX_SLOT_X);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -254,31 +303,50 @@ __global__ void storage_to_acc_kernel(const T *__restrict__ x, A *__restrict__ a
 // in a fixed order, then a fixed reduction tree (deterministic)
 template <typename T, typename A>
 __global__ void __launch_bounds__(1024) bias_grad_kernel(const T *__restrict__ gout, T *__restrict__ gb, int B, int C,
-                                                         int S) {
+                                                         int S, bool accumulate, int *flag) {
     __shared__ A red[16];
+    __shared__ float mx[16];
     const int c = blockIdx.x;
     const int tid = threadIdx.x;
     const bool vec = sizeof(T) <= 4 && S % 4 == 0;
     A acc = A(0);
+    float m = 0.f;
     for (int b = 0; b < B; ++b) {
         const T *row = gout + ((size_t)b * C + c) * S;
         if (vec) {
             for (int s4 = tid; s4 < S / 4; s4 += 1024) {
                 const Vec4<A> v = load4_t<A, T>(row + 4 * s4);
                 acc += (v.x + v.y) + (v.z + v.w);
+                m = fmaxf(m, (float)fmax(fmax(fabs(v.x), fabs(v.y)), fmax(fabs(v.z), fabs(v.w))));
             }
         } else {
-            for (int s = tid; s < S; s += 1024) acc += to_acc<A>(row[s]);
+            for (int s = tid; s < S; s += 1024) {
+                const A v = to_acc<A>(row[s]);
+                acc += v;
+                m = fmaxf(m, (float)fabs(v));
+            }
         }
     }
 #pragma unroll
-    for (int m = 32; m > 0; m >>= 1) acc += __shfl_xor(acc, m);
-    if ((tid & 63) == 0) red[tid >> 6] = acc;
+    for (int o = 32; o > 0; o >>= 1) {
+        acc += __shfl_xor(acc, o);
+        m = fmaxf(m, __shfl_xor(m, o));
+    }
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = acc;
+        mx[tid >> 6] = m;
+    }
     __syncthreads();
     if (tid == 0) {
         A sum = A(0);
-        for (int w = 0; w < 16; ++w) sum += red[w];
-        gb[c] = from_acc<T, A>(sum);
+        float big = 0.f;
+        for (int w = 0; w < 16; ++w) {
+            sum += red[w];
+            big = fmaxf(big, mx[w]);
+        }
+        if (gb != nullptr) gb[c] = from_acc<T, A>(accumulate ? to_acc<A>(gb[c]) + sum : sum);
+        if (flag != nullptr && big > 0.f)
+            atomicMax(reinterpret_cast<unsigned *>(flag) + amax_word(AMAX_SLOT_Z, c % AMAX_SPREAD), __float_as_uint(big));
     }
 }
 
@@ -302,23 +370,85 @@ hipError_t by_dtype(int dtype, F &&f) {
     return hipErrorInvalidValue;
 }
 
+// largest |value| of up to four fp32 tensors: blockIdx.y = item, a grid-stride loop over the item
+// (16-byte loads when vec: the pointer 16-byte aligned and n % 4 == 0), one atomicMax of the
+// wave's largest per wave (float bits: non-negative floats order as their patterns). fmaxf passes
+// over nan.
+struct AmaxSet {
+    const float *p[4];
+    size_t n[4];
+    int slot[4];
+    bool vec[4];
+};
+__global__ void __launch_bounds__(256) amax_kernel(const AmaxSet set, int *flag) {
+    const int it = blockIdx.y;
+    const float *p = set.p[it];
+    const size_t n = set.n[it];
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    float m = 0.f;
+    if (set.vec[it]) {
+        const size_t n4 = n / 4;
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+            const float4 v = reinterpret_cast<const float4 *>(p)[i];
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) m = fmaxf(m, fabsf(p[i]));
+    }
+    block_amax(m, flag, set.slot[it]);
+}
+
 }  // namespace
 
+hipError_t launch_amax(const AmaxItem *items, int n, int *flag, hipStream_t s) {
+    AmaxSet set{};
+    int k = 0;
+    size_t most = 0;
+    for (int i = 0; i < n; ++i) {
+        if (items[i].p == nullptr || items[i].n == 0) continue;
+        if (k == 4 || items[i].slot < 0 || items[i].slot >= AMAX_SLOTS) return hipErrorInvalidValue;
+        set.p[k] = items[i].p;
+        set.n[k] = items[i].n;
+        set.slot[k] = items[i].slot;
+        set.vec[k] = al16(items[i].p) && items[i].n % 4 == 0;
+        most = std::max(most, items[i].n);
+        ++k;
+    }
+    if (k == 0) return hipSuccess;
+    // about 16 values per thread on the largest item, at most 1024 blocks per item
+    const size_t blocks = std::min<size_t>(std::max<size_t>((most + 4095) / 4096, 1), 1024);
+    hipLaunchKernelGGL(amax_kernel, dim3((unsigned)blocks, (unsigned)k), dim3(256), 0, s, set, flag);
+    return hipGetLastError();
+}
+
 hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, int C, int Sn, hipStream_t s,
-                                   int *flag, const void *chk, size_t chk_n, float chk_limit) {
-    if (chk != nullptr && (flag == nullptr || chk_n == 0)) chk = nullptr;
+                                   int *flag, const void *chk, size_t chk_n, float chk_limit, const void *amax_w,
+                                   size_t amax_w_n) {
+    CopyJobs jobs{};
+    if (flag != nullptr) {
+        if (chk != nullptr && chk_n > 0) {
+            jobs.chk = static_cast<const float *>(chk);
+            jobs.chk_n = chk_n;
+            jobs.chk_limit = chk_limit;
+        }
+        if (dtype == kF32 && amax_w != nullptr && amax_w_n > 0) {
+            jobs.w = static_cast<const float *>(amax_w);
+            jobs.w_n = amax_w_n;
+            jobs.amax_x = true;
+        }
+    }
+    const int extra = (jobs.chk != nullptr) + (jobs.w != nullptr);
+    dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B + extra);
     if (dtype == kF32 && C % 4 == 0 && Sn % 4 == 0 && al16(x) && al16(xcl)) {
-        dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B + (chk != nullptr ? 1 : 0));
         hipLaunchKernelGGL(to_cl4_kernel, grid, dim3(256), 0, s, static_cast<const float *>(x), static_cast<float *>(xcl),
-                           C, Sn, flag, static_cast<const float *>(chk), chk_n, chk_limit);
+                           C, Sn, flag, jobs);
         return hipGetLastError();
     }
     return by_dtype(dtype, [&](auto tv, auto av) {
         using T = decltype(tv);
         using A = decltype(av);
-        dim3 grid((Sn + TT - 1) / TT, (C + TT - 1) / TT, B + (chk != nullptr ? 1 : 0));
         hipLaunchKernelGGL((to_cl_kernel<T, A>), grid, dim3(256), 0, s, static_cast<const T *>(x),
-                           static_cast<A *>(xcl), C, Sn, flag, static_cast<const float *>(chk), chk_n, chk_limit);
+                           static_cast<A *>(xcl), C, Sn, flag, jobs);
         return hipGetLastError();
     });
 }
@@ -474,12 +604,15 @@ hipError_t launch_storage_to_acc(int dtype, const void *x, void *acc, size_t n, 
     });
 }
 
-hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s) {
+hipError_t launch_bias_grad(int dtype, const void *gout, void *gbias, int B, int C, int Sn, hipStream_t s,
+                            bool accumulate, int *flag) {
+    if (dtype != kF32) flag = nullptr;
+    if (gbias == nullptr && flag == nullptr) return hipSuccess;
     return by_dtype(dtype, [&](auto tv, auto av) {
         using T = decltype(tv);
         using A = decltype(av);
         hipLaunchKernelGGL((bias_grad_kernel<T, A>), dim3(C), dim3(1024), 0, s, static_cast<const T *>(gout),
-                           static_cast<T *>(gbias), B, C, Sn);
+                           static_cast<T *>(gbias), B, C, Sn, accumulate, flag);
         return hipGetLastError();
     });
 }

@@ -527,32 +527,72 @@ __device__ __forceinline__ AxisW<DIM, float> record_weights(const Geo &g, const 
 
 
 // ---------------------------------------------------------------------------
-// 16-bit MFMA operands. v_mfma_f32_16x16x32_bf16 / _f16: lane l supplies K = 8 (l / 16) ..
+// 16-bit MFMA operands. v_mfma_f32_16x16x32_f16 / _bf16: lane l supplies K = 8 (l / 16) ..
 // + 7 of row (A) / column (B) l % 16 as eight 16-bit values in four dwords (the lower K in
 // the low half); the 16x16 result has the layout of the 16x16x4 fp32 MFMA. fp32 operands
-// go in as three bf16 pieces each: p0 = bf16(v), p1 = bf16(v - p0), p2 = bf16(v - p0 - p1)
-// (nearest, ties to even; the residuals are exact in fp32), so v = p0 + p1 + p2 + r with
-// |r| <= 2^-27 |v|. Of the nine cross products p_i q_j, the six with i + j <= 2 are summed;
-// the three left out and both residuals are below 2^-25 |v w| together, under fp32's own
-// rounding of one multiply-add. An fp32 value is bad for this when it is not finite or
-// rounds past the largest bf16; fp16 / bf16 operands go in as they are.
+// go in as two fp16 pieces each, of the value scaled by a power of two 2^s that puts the
+// operand's largest magnitude in [2^14, 2^15): p0 = fp16(v 2^s), p1 = fp16(v 2^s - p0) (nearest,
+// ties to even; the residual is exact in fp32), so v 2^s = p0 + p1 + r with |r| <= 2^-24 |v 2^s|
+// while p1 stays a normal fp16 (|v| >= 2^-17 of the operand's largest; below that the error is
+// at most 2^-25 of a unit, 2^-40 of the largest). Of the four cross products p_i q_j the three
+// with i + j <= 1 are summed (exact products, fp32 accumulation); the one left out and the
+// residuals are below 3 2^-24 |v w|, fp32's own rounding of a few multiply-adds; the sum is
+// scaled back by 2^-(s_a + s_b). An fp32 value is bad for this when it is not finite (or rounds
+// past the largest bf16: the range checks of the sampled operands); fp16 / bf16 operands go in
+// as they are.
 // ---------------------------------------------------------------------------
-template <typename T> constexpr int npiece_of() { return std::is_same<T, float>::value ? 3 : 1; }
+template <typename T> constexpr int npiece_of() { return std::is_same<T, float>::value ? 2 : 1; }
 
 __device__ __forceinline__ bool bf16_split_bad(float v) {
     return (__float_as_uint(v) & 0x7FFFFFFFu) >= 0x7F7F8000u;
 }
 
-// the pieces of two values, packed two per dword (v_cvt_pk_bf16_f32)
-__device__ __forceinline__ void split3_pk(float a, float b, uint32_t (&w)[3]) {
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+// Largest magnitudes of the fp32 path's operands (float bits, raised with atomicMax: non-negative
+// floats order as their bit patterns), in the words after the operand flag (kernels.h: amax_word)
+enum { AMAX_W = AMAX_SLOT_W, AMAX_X = AMAX_SLOT_X, AMAX_M = AMAX_SLOT_M, AMAX_Z = AMAX_SLOT_Z };
+// the largest of a slot's sub-slots; every lane of the wave calls it (each loads one sub-slot)
+__device__ __forceinline__ float operand_amax(const int *flag, int slot) {
+    static_assert(AMAX_SPREAD == 64, "one sub-slot per lane");
+    const unsigned *w = reinterpret_cast<const unsigned *>(flag);
+    float m = __uint_as_float(w[amax_word(slot, threadIdx.x & 63)]);
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const b2 h = {(__bf16)a, (__bf16)b};
-        w[k] = __builtin_bit_cast(uint32_t, h);
-        a -= (float)h[0];
-        b -= (float)h[1];
-    }
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    return m;
+}
+// e with |v| < 2^e for every value of a magnitude bound a (0 for a zero, non-finite or absent bound)
+__device__ __forceinline__ int bound_exp(float a) {
+    int e = 0;
+    if (a > 0.f && a <= 3.402823466e38f) frexpf(a, &e);   // a < 2^e
+    return e;
+}
+// scale exponent of an operand whose values lie below 2^e: the largest lands in [2^14, 2^15)
+__device__ __forceinline__ int piece_scale(int e) { return 15 - e; }
+// the sampled operand mask * bilinear(X): below (largest |X|) x (largest |mask|): the mask's bound
+// is its tensor's largest value, mask_scale (sigmoid) or 1 (softmax, no mask). Every lane of the
+// wave calls it.
+__device__ __forceinline__ int sampled_scale(const Geo &g, const int *flag, bool has_mask) {
+    if (flag == nullptr) return 0;
+    const float mm = operand_amax(flag, AMAX_M);
+    const float mbound = !has_mask ? 1.f
+                         : g.mask_act == MASK_ACT_SIGMOID ? (float)g.mask_scale
+                         : g.mask_act == MASK_ACT_SOFTMAX ? 1.f
+                                                          : mm;
+    return piece_scale(bound_exp(operand_amax(flag, AMAX_X)) + bound_exp(mbound));
+}
+// every lane of the wave calls it
+__device__ __forceinline__ int operand_scale(const int *flag, int slot) {
+    return flag == nullptr ? 0 : piece_scale(bound_exp(operand_amax(flag, slot)));
+}
+
+// two values as their fp16 pieces at scale 2^s, packed two per dword
+__device__ __forceinline__ void split2_pk(float a, float b, int s, uint32_t (&w)[2]) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    a = ldexpf(a, s);
+    b = ldexpf(b, s);
+    const h2 h0 = {(_Float16)a, (_Float16)b};
+    w[0] = __builtin_bit_cast(uint32_t, h0);
+    const h2 h1 = {(_Float16)(a - (float)h0[0]), (_Float16)(b - (float)h0[1])};
+    w[1] = __builtin_bit_cast(uint32_t, h1);
 }
 
 // two values rounded to the 16-bit type T (fp16 or bf16), packed
@@ -568,16 +608,15 @@ template <typename T> __device__ __forceinline__ uint32_t pack2_16(float a, floa
     }
 }
 
-// one value as its NP 16-bit pieces (fp32) or as T (fp16 / bf16)
+// one value as its NP 16-bit pieces at scale 2^s (fp32) or as T (fp16 / bf16; s unused)
 template <typename T, int NP>
-__device__ __forceinline__ void split_one16(float v, uint16_t (&p)[NP]) {
-    if constexpr (NP == 3) {
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            const __bf16 h = (__bf16)v;
-            p[k] = __builtin_bit_cast(uint16_t, h);
-            v -= (float)h;
-        }
+__device__ __forceinline__ void split_one16(float v, int s, uint16_t (&p)[NP]) {
+    static_assert(NP == npiece_of<T>(), "pieces per value of T");
+    if constexpr (NP == 2) {
+        v = ldexpf(v, s);
+        const _Float16 h = (_Float16)v;
+        p[0] = __builtin_bit_cast(uint16_t, h);
+        p[1] = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
     } else if constexpr (std::is_same<T, __half>::value) {
         p[0] = __builtin_bit_cast(uint16_t, (_Float16)v);
     } else {
@@ -585,17 +624,19 @@ __device__ __forceinline__ void split_one16(float v, uint16_t (&p)[NP]) {
     }
 }
 
-// eight values of a lane as NP 16-bit operand fragments (pieces for fp32, T's values otherwise)
+// eight values of a lane as NP 16-bit operand fragments (pieces at scale 2^s for fp32, T's
+// values otherwise)
 template <typename T, int NP>
-__device__ __forceinline__ void pack8_16(const float (&v)[8], uint4 (&out)[NP]) {
+__device__ __forceinline__ void pack8_16(const float (&v)[8], int s, uint4 (&out)[NP]) {
+    static_assert(NP == npiece_of<T>(), "pieces per value of T");
     uint32_t w[NP][4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
-        if constexpr (NP == 3) {
-            uint32_t p[3];
-            split3_pk(v[e], v[e + 1], p);
-#pragma unroll
-            for (int k = 0; k < 3; ++k) w[k][e >> 1] = p[k];
+        if constexpr (NP == 2) {
+            uint32_t p[2];
+            split2_pk(v[e], v[e + 1], s, p);
+            w[0][e >> 1] = p[0];
+            w[1][e >> 1] = p[1];
         } else {
             w[0][e >> 1] = pack2_16<T>(v[e], v[e + 1]);
         }
@@ -604,9 +645,10 @@ __device__ __forceinline__ void pack8_16(const float (&v)[8], uint4 (&out)[NP]) 
     for (int k = 0; k < NP; ++k) out[k] = uint4{w[k][0], w[k][1], w[k][2], w[k][3]};
 }
 
-// D += A * B on one 16x16x32 MFMA: fp16 operands for T = fp16, bf16 otherwise
+// D += A * B on one 16x16x32 MFMA: fp16 operands for T = fp16 and for the pieces of fp32, bf16
+// otherwise
 template <typename T> __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uint4 b, f32x4 c) {
-    if constexpr (std::is_same<T, __half>::value) {
+    if constexpr (std::is_same<T, __half>::value || std::is_same<T, float>::value) {
         typedef _Float16 h8 __attribute__((ext_vector_type(8)));
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
     } else {
@@ -616,14 +658,12 @@ template <typename T> __device__ __forceinline__ f32x4 mfma16x16x32(uint4 a, uin
     }
 }
 
-// acc += the split product of A and B fragments (NP pieces each): the six products with
-// i + j <= 2, smallest first, for fp32; the one product otherwise
+// acc += the split product of A and B fragments (NP pieces each): the three products with
+// i + j <= 1, smallest first, for fp32; the one product otherwise
 template <typename T, int NP>
 __device__ __forceinline__ f32x4 mfma16x16x32_np(const uint4 (&a)[NP], const uint4 (&b)[NP], f32x4 c) {
-    if constexpr (NP == 3) {
-        c = mfma16x16x32<T>(a[2], b[0], c);
-        c = mfma16x16x32<T>(a[1], b[1], c);
-        c = mfma16x16x32<T>(a[0], b[2], c);
+    static_assert(NP == npiece_of<T>(), "pieces per value of T");
+    if constexpr (NP == 2) {
         c = mfma16x16x32<T>(a[1], b[0], c);
         c = mfma16x16x32<T>(a[0], b[1], c);
     }
