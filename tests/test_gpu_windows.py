@@ -469,3 +469,39 @@ def test_transposed_forward_elementwise_fp32(dim):
           f"norm-wise {n:.2e}", flush=True)
     assert n < TOL[torch.float32][0]
     assert e <= 4 * e_ref + 1e-6
+
+
+@pytest.mark.parametrize("kind", ["tiny", "large", "wide", "transposed_tiny"])
+def test_fp32_pieces_scaled_per_tensor(kind):
+    """fp32 operands enter the 16-bit MFMA loops as two fp16 pieces of the value times a per-tensor
+    power of two that puts the tensor's largest magnitude in [2^14, 2^15): magnitudes far outside
+    fp16's range (tiny: inputs near 1e-6 and an upstream gradient near 1e-8, whose unscaled fp16
+    pieces would underflow; large: inputs near 1e4 with weights near 1e-4) and a wide range inside
+    one tensor (input magnitudes log-uniform over 1e-4 .. 1e2) keep float32 accuracy: forward and
+    every gradient against the float64 oracle at the float32 bounds."""
+    transposed = kind.startswith("transposed")
+    case = make_case(2, transposed, batch=2, cin=32, cout=48, kernel=[3, 3], stride=[1, 1] if not transposed else [2, 2],
+                     padding=[1, 1], dilation=[1, 1], in_size=[14, 12], out_pad=[1, 1] if transposed else [0, 0],
+                     seed=620)
+    g = torch.Generator().manual_seed(621)
+    gout = torch.randn(case["out_shape"], generator=g, dtype=torch.float64)
+    if kind in ("tiny", "transposed_tiny"):
+        case["input"] = case["input"] * 1e-6
+        gout = gout * 1e-8
+    elif kind == "large":
+        case["input"] = case["input"] * 1e4
+        case["weight"] = case["weight"] * 1e-4
+    else:
+        mag = torch.exp(torch.empty(case["input"].shape, dtype=torch.float64).uniform_(
+            float(torch.log(torch.tensor(1e-4))), float(torch.log(torch.tensor(1e2))), generator=g))
+        case["input"] = torch.where(torch.rand(case["input"].shape, generator=g) < 0.5, -mag, mag)
+    out, grads, _ = run_gpu(case, torch.float32, grad_out=gout)
+    ref_out, ref_grads = run_oracle(case, gout, torch.float32)
+    e = rel_err(out, ref_out)
+    print(f"{kind}: forward rel err {e:.2e}", flush=True)
+    assert e < TOL[torch.float32][0]
+    for name, gr, r in zip(("input", "weight", "offset", "mask", "bias"), grads, ref_grads):
+        if r is not None:
+            e = rel_err(gr, r)
+            print(f"{kind}: grad_{name} rel err {e:.2e}", flush=True)
+            assert e < TOL[torch.float32][1], name
