@@ -69,8 +69,8 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     const int grp = L / n_sp;
     const bool deformable = offset != nullptr;
     const int slices = (g.Cg + BC - 1) / BC;
-    // the 16-bit loop (1D / 2D) when its weight was laid out and (fp32) no operand was flagged
-    const bool use16_flag = DIM < 3 && w16 != nullptr && (flag == nullptr || *flag == 0);
+    // the 16-bit loop when its weight was laid out and (fp32) no operand was flagged
+    const bool use16_flag = w16 != nullptr && (flag == nullptr || *flag == 0);
     // fp32 as fp16 pieces: the sampled columns' scale, and the one back out (the weight's with it)
     const int s_b = npiece_of<T>() == 2 && use16_flag ? sampled_scale(g, flag, mask != nullptr) : 0;
     const int s_back = npiece_of<T>() == 2 && use16_flag ? -(s_b + operand_scale(flag, AMAX_W)) : 0;
@@ -406,47 +406,117 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 for (int j = 0; j < 4; ++j) bq[j][pb] = sv[j];
             }
         };
-        for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
-            const int ntaps = min(wt.tpp, g.Kn - t0);
-            const int ngr = (ntaps + 3) >> 2;   // tap groups per slice
-            const int ngroups = (cs_hi - cs_lo) * ngr;
-            geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
-
-            // group k = (slice cs_lo + k / ngr, taps 4 * (k % ngr) ..): its B fragments are
-            // built at its start (the sampling's LDS latency is covered by the other wave of
-            // the SIMD), then its steps run; wa holds the weight fragments of the next step.
-            // The X window of a slice is loaded at the slice switch (the registers a prefetch
-            // would hold across the steps are taken by the group's B fragments).
-            acc4 wa[MB];
-            load_w(wptr(cs_lo, t0), wa);
-            __syncthreads();   // previous pass done with the tables
-            open_slice(cs_lo, t0, ntaps);
-            __syncthreads();
-            int cs = cs_lo, tg = 0;   // group k's (slice, tap group), advanced group by group
-            for (int k = 0; k < ngroups; ++k) {
-                const bool more = k + 1 < ngroups;
-                const int tgn = tg + 1 == ngr ? 0 : tg + 1;
-                const int csn = tgn == 0 ? cs + 1 : cs;
-                acc4 bq[4][PB];
-                build_group(cs, tg, ntaps, bq);
-                const int nt = min(4, ntaps - tg * 4);
-                const int tb = t0 + tg * 4;
+        if (use16_flag) {
+            // 16x16x32 steps: a group's four taps are two tap pairs, each pair's B fragment its
+            // two sampled quads (the 16-bit loop's K order, W16 below), split into pieces (fp32)
+            // or rounded to T; the pair's A fragments come from global memory, each row block's
+            // loaded one block ahead
+            constexpr int NP = npiece_of<T>();
+            const int nmb = fw.Mg_pad / 16;
+            const uint16_t *wl = w16 + (size_t)mt * MB * (NP * 512);
+            auto load_w16g = [&](const uint16_t *p, uint4 (&f)[NP]) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (j < nt) {
-                        // weight fragments of the step after this one (this step's own at the end)
-                        const float *pn = j + 1 < nt ? wptr(cs, tb + j + 1)
-                                                     : (more ? wptr(csn, t0 + tgn * 4) : wptr(cs, tb + j));
-                        mfma_step(bq[j], wa, pn);
+                for (int k = 0; k < NP; ++k) f[k] = *reinterpret_cast<const uint4 *>(p + lane * 8 + k * 512);
+            };
+            static_assert(MB % 2 == 0, "row blocks in pairs: the next step's block 0 lands in slot 0");
+            for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
+                const int ntaps = min(wt.tpp, g.Kn - t0);
+                const int ngr = (ntaps + 3) >> 2;
+                const int ngroups = (cs_hi - cs_lo) * ngr;
+                geo_og = geo_mg = -1;
+                const int pp0 = (t0 / wt.tpp) * fw.hp;
+                auto wptr16 = [&](int cs, int j) {
+                    return wl + (((size_t)grp * slices + cs) * fw.pp + pp0 + j) * nmb * (NP * 512);
+                };
+                uint4 wa[2][NP];
+                load_w16g(wptr16(cs_lo, 0), wa[0]);
+                __syncthreads();   // previous pass done with the tables
+                open_slice(cs_lo, t0, ntaps);
+                __syncthreads();
+                int cs = cs_lo, tg = 0;
+                for (int k = 0; k < ngroups; ++k) {
+                    const bool more = k + 1 < ngroups;
+                    const int tgn = tg + 1 == ngr ? 0 : tg + 1;
+                    const int csn = tgn == 0 ? cs + 1 : cs;
+                    acc4 bq[4][PB];
+                    build_group(cs, tg, ntaps, bq);
+                    const int npr = (min(4, ntaps - tg * 4) + 1) >> 1;   // tap pairs of the group
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        if (h < npr) {
+                            uint4 bv[PB][NP];
+#pragma unroll
+                            for (int pb = 0; pb < PB; ++pb) {
+                                const float v[8] = {bq[2 * h][pb][0],     bq[2 * h][pb][1],     bq[2 * h][pb][2],
+                                                    bq[2 * h][pb][3],     bq[2 * h + 1][pb][0], bq[2 * h + 1][pb][1],
+                                                    bq[2 * h + 1][pb][2], bq[2 * h + 1][pb][3]};
+                                pack8_16<T, NP>(v, s_b, bv[pb]);
+                            }
+                            const uint16_t *pcur = wptr16(cs, 2 * tg + h);
+                            const uint16_t *pnext =
+                                h + 1 < npr ? wptr16(cs, 2 * tg + h + 1) : (more ? wptr16(csn, 2 * tgn) : pcur);
+#pragma unroll
+                            for (int mb = 0; mb < MB; ++mb) {
+                                load_w16g(mb + 1 < MB ? pcur + (size_t)(mb + 1) * (NP * 512) : pnext, wa[(mb + 1) & 1]);
+#pragma unroll
+                                for (int pb = 0; pb < PB; ++pb)
+                                    acc[mb][pb] = mfma16x16x32_np<T, NP>(wa[mb & 1], bv[pb], acc[mb][pb]);
+                                __builtin_amdgcn_sched_barrier(0);
+                            }
+                        }
                     }
+                    if (more && tgn == 0) {
+                        __syncthreads();   // every wave done reading the current window
+                        open_slice(csn, t0, ntaps);
+                        __syncthreads();
+                    }
+                    cs = csn;
+                    tg = tgn;
                 }
-                if (more && tgn == 0) {
-                    __syncthreads();   // every wave done reading the current window
-                    open_slice(csn, t0, ntaps);
-                    __syncthreads();
+            }
+        } else {
+            for (int t0 = 0; t0 < g.Kn; t0 += wt.tpp) {
+                const int ntaps = min(wt.tpp, g.Kn - t0);
+                const int ngr = (ntaps + 3) >> 2;   // tap groups per slice
+                const int ngroups = (cs_hi - cs_lo) * ngr;
+                geo_og = geo_mg = -1;   // a new pass of taps: the table must be rebuilt
+
+                // group k = (slice cs_lo + k / ngr, taps 4 * (k % ngr) ..): its B fragments are
+                // built at its start (the sampling's LDS latency is covered by the other wave of
+                // the SIMD), then its steps run; wa holds the weight fragments of the next step.
+                // The X window of a slice is loaded at the slice switch (the registers a prefetch
+                // would hold across the steps are taken by the group's B fragments).
+                acc4 wa[MB];
+                load_w(wptr(cs_lo, t0), wa);
+                __syncthreads();   // previous pass done with the tables
+                open_slice(cs_lo, t0, ntaps);
+                __syncthreads();
+                int cs = cs_lo, tg = 0;   // group k's (slice, tap group), advanced group by group
+                for (int k = 0; k < ngroups; ++k) {
+                    const bool more = k + 1 < ngroups;
+                    const int tgn = tg + 1 == ngr ? 0 : tg + 1;
+                    const int csn = tgn == 0 ? cs + 1 : cs;
+                    acc4 bq[4][PB];
+                    build_group(cs, tg, ntaps, bq);
+                    const int nt = min(4, ntaps - tg * 4);
+                    const int tb = t0 + tg * 4;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (j < nt) {
+                            // weight fragments of the step after this one (this step's own at the end)
+                            const float *pn = j + 1 < nt ? wptr(cs, tb + j + 1)
+                                                         : (more ? wptr(csn, t0 + tgn * 4) : wptr(cs, tb + j));
+                            mfma_step(bq[j], wa, pn);
+                        }
+                    }
+                    if (more && tgn == 0) {
+                        __syncthreads();   // every wave done reading the current window
+                        open_slice(csn, t0, ntaps);
+                        __syncthreads();
+                    }
+                    cs = csn;
+                    tg = tgn;
                 }
-                cs = csn;
-                tg = tgn;
             }
         }
     } else if (use16_flag) {
@@ -682,12 +752,12 @@ FwdWin plan_fwd_win(const Geo &g, const WinTiles &base, int dim, WinTiles &wt) {
     // 3D samples taps in groups of four: passes of eight taps fill their groups (27 taps:
     // 8, 8, 8, 3 = seven groups, where passes of nine would take nine)
     if (dim == 3 && g.Kn > WIN_TMAX) wt.tpp = 8;
-    // 16-bit weight fragments (1D / 2D)
+    // 16-bit weight fragments
     f.npiece = base.npiece;
     f.tpp = wt.tpp;
     f.hp = (wt.tpp + 1) / 2;
     f.pp = (g.Kn + wt.tpp - 1) / wt.tpp * f.hp;
-    f.w16_elems = dim < 3 ? (size_t)g.G * slices * f.pp * (f.Mg_pad / 16) * f.npiece * 512 : 0;
+    f.w16_elems = (size_t)g.G * slices * f.pp * (f.Mg_pad / 16) * f.npiece * 512;
     // the layout kernels index in 32 bits
     if ((size_t)g.G * slices * g.Kn * f.Mg_pad * BC > (size_t)INT_MAX || f.w16_elems / 8 > (size_t)INT_MAX) return f;
     f.ok = true;
