@@ -59,7 +59,7 @@ size_t fixed_words(const Geo &g, int tpp) {
 }
 
 // FULL: every pass uses all TM tap slots (no per-tap guards). USE16: the instantiation with the
-// 16x16x32 MFMA chunks (1D / 2D); it runs when the operand flag is clear and the fp32 one when it
+// 16x16x32 MFMA chunks; it runs when the operand flag is clear and the fp32 one when it
 // is set (both are launched; each returns at once when the flag selects the other), so that
 // neither loop's registers weigh on the other's.
 template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV, bool USE16>
@@ -96,7 +96,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     const bool deformable = offset != nullptr;
     const int tg = wave / (NW / TG);                     // this wave's tap group
     const int mrow = mt * BMW + (wave % (NW / TG)) * (MB * 16);   // first row of this wave
-    constexpr bool use16 = USE16 && DIM < 3;
+    constexpr bool use16 = USE16;
     if (flag != nullptr && (*flag == 0) != use16) return;   // the other instantiation's launch
     // fp32 as fp16 pieces: the scales of Z and of the sampled columns, and the one back out
     const int s_z = use16 ? operand_scale(flag, AMAX_Z) : 0;
@@ -180,9 +180,9 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                         const acc4 r = geo[tl * BPX + i];
                         acc4 sv[4];
                         if (nq == 4)
-                            sample3_all<true, true>(g, wt, tile, xwin, xb, 4, r, deformable, sv);
+                            sample3_all_fix<true>(g, wt, tile, xwin, xb, 4, r, deformable, sv);
                         else
-                            sample3_all<false, true>(g, wt, tile, xwin, xb, nq, r, deformable, sv);
+                            sample3_all_fix<false>(g, wt, tile, xwin, xb, nq, r, deformable, sv);
                         float *row = dst + tl * BC * SS + sj;
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
@@ -265,6 +265,29 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                 uint16_t *s16 = reinterpret_cast<uint16_t *>(sbuf);
                 auto build_s16 = [&](int k) {
                     const int i = k * KP + sj;
+                    if constexpr (DIM == 3) {
+                        // 3D: one item per (chunk pixel, tap) for all 16 channels, as in build_s
+                        const int nq = min(4, (g.Cg - tile.c0) >> 2);
+                        for (int tl = tid / KP; tl < ntaps; tl += NT / KP) {
+                            const acc4 r = geo[tl * BPX + i];
+                            acc4 sv[4];
+                            if (nq == 4)
+                                sample3_all_fix<true>(g, wt, tile, xwin, xb, 4, r, deformable, sv);
+                            else
+                                sample3_all_fix<false>(g, wt, tile, xwin, xb, nq, r, deformable, sv);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) {
+                                    uint16_t pc[NP];
+                                    split_one16<T, NP>(sv[j][v], s_s, pc);
+#pragma unroll
+                                    for (int kk = 0; kk < NP; ++kk)
+                                        s16[((size_t)kk * TM * BC + tl * BC + 4 * j + v) * SS16 + sj] = pc[kk];
+                                }
+                        }
+                        return;
+                    }
                     for (int tl = st0; tl < ntaps; tl += SSTEP) {
                         const acc4 sv = sample_quad(tl, i);
 #pragma unroll
@@ -429,16 +452,12 @@ template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, const int *flag, hipStream_t s) {
     if (wt.tpp > TMV) return hipErrorInvalidValue;   // a pass must fit the tap slots
-    if constexpr (DIM < 3) {
-        if (flag != nullptr) {
-            const hipError_t e = launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, true>(g, wt, ww, z, xcl, offset, mask, part,
-                                                                                  flag, s);
-            if (e != hipSuccess) return e;
-        }
+    if (flag != nullptr) {
+        const hipError_t e = launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, true>(g, wt, ww, z, xcl, offset, mask, part,
+                                                                              flag, s);
+        if (e != hipSuccess) return e;
     }
-    // (3D has no 16-bit instantiation: its fp32 one runs whatever the flag)
-    return launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, false>(g, wt, ww, z, xcl, offset, mask, part,
-                                                             DIM < 3 ? flag : nullptr, s);
+    return launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, false>(g, wt, ww, z, xcl, offset, mask, part, flag, s);
 }
 
 template <typename T>
