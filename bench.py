@@ -39,14 +39,11 @@ PEAK_16BIT_MFMA = 2.5e15       # MI355X dense fp16 / bf16 matrix, FLOP/s
 
 def mfma_path(family, dtype=torch.float32, dim=2):
     """(MFMA instruction, MFMA products per algorithmic product, its dense peak) of a kernel family's
-    K loop: 16x16x32 MFMAs in the 1D/2D kernels and the data gradient, fp32 operands as two fp16
-    pieces at a per-tensor power-of-two scale, of which three cross products are summed
-    (fp32-accurate), fp16/bf16 operands as they are; the 3D forward and weight gradient run fp32
-    16x16x4 MFMAs (operands widened). A launch whose fp32 operands were flagged (not finite) runs the
-    fp32 loop instead. The fp32 path's own ceiling is the 16-bit peak over the products per product
-    (2.5 PFLOP/s / 3 = 833 TFLOP/s fp32-equivalent), above the fp32 MFMA peak."""
-    if dim == 3 and family in ("gather_gemm", "weight_grad"):
-        return "v_mfma_f32_16x16x4_f32", 1, PEAK_FP32_MFMA
+    K loop: 16x16x32 MFMAs in every rank, fp32 operands as two fp16 pieces at a per-tensor
+    power-of-two scale, of which three cross products are summed (fp32-accurate), fp16/bf16 operands
+    as they are. A launch whose fp32 operands were flagged (not finite) runs the fp32 loop instead.
+    The fp32 path's own ceiling is the 16-bit peak over the products per product (2.5 PFLOP/s / 3 =
+    833 TFLOP/s fp32-equivalent), above the fp32 MFMA peak."""
     if dtype == torch.float32:
         return "v_mfma_f32_16x16x32_f16 (2 fp16 pieces per fp32 value, 3 products)", 3, PEAK_16BIT_MFMA
     return f"v_mfma_f32_16x16x32_{'f16' if dtype == torch.float16 else 'bf16'}", 1, PEAK_16BIT_MFMA
@@ -277,8 +274,7 @@ def run_suite_case(n, dtype, steps, warmup, cpu=False):
     row = {
         "case": c["name"], "dtype": str(dtype).replace("torch.", ""),
         "compute": ("fp32-accurate: scaled fp16 pieces on 16x16x32 MFMAs, fp32 accumulate" if dtype == torch.float32 else
-                    f"{str(dtype).replace('torch.', '')} operands on 16x16x32 MFMAs, fp32 accumulate") +
-                   ("; 3D forward and weight gradient: fp32 16x16x4 MFMAs" if dim == 3 else ""),
+                    f"{str(dtype).replace('torch.', '')} operands on 16x16x32 MFMAs, fp32 accumulate"),
         "mask": "softmax of logits in the mask load" if logits is not None else "given",
         "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(step_ms - fwd_ms, 4), "fwd_bwd_ms": round(step_ms, 4),
         "gflop_fwd": round(F / 1e9, 3), "gflop_bwd": round(nb * F / 1e9, 3),
