@@ -23,9 +23,9 @@
 //     tensors as two fp16 pieces each at a per-tensor power-of-two scale, of whose four cross
 //     products the three with i + j <= 1 are summed (the rest are within fp32's own rounding;
 //     3 MFMAs at 16 cycles against 8 fp32 16x16x4 MFMAs at 32 cycles per 32 channels), the
-//     sums scaled back after the K loop. An fp32 operand that is not finite or would round
-//     past the bf16 range (a device flag set by the layout kernels) sends the launch down the
-//     fp32 loop (16x16x4 MFMAs, 16 channels per step), which keeps the reference's inf/nan
+//     sums scaled back after the K loop. An fp32 operand that is not finite (or at least
+//     0x1.ffp127 in magnitude: a device flag set by the layout kernels) sends the launch down
+//     the fp32 loop (16x16x4 MFMAs, 16 channels per step), which keeps the reference's inf/nan
 //     propagation.
 //   * Epilogue per tap: the geometry of the 256 pixels (one per thread) goes to an
 //     LDS table. The offset/mask gradients are formed in the MFMA layout (4
@@ -181,7 +181,7 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         v[e] = tile[q * 8 + e][pl];
-        bad = bad || bf16_split_bad(v[e]);
+        bad = bad || split_bad(v[e]);
     }
     uint4 out[NP];
     pack8_16<T, NP>(v, sz, out);
@@ -1228,7 +1228,7 @@ __device__ __forceinline__ void weight_split_block(int L, float *smem, const T *
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             v[e] = tile[tt][c][q * 8 + e];
-            bad = bad || bf16_split_bad(v[e]);
+            bad = bad || split_bad(v[e]);
         }
         uint4 o[NP];
         pack8_16<T, NP>(v, sw, o);

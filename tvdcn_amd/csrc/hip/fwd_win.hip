@@ -648,7 +648,7 @@ fwd_w16_kernel(const T *__restrict__ w, uint16_t *__restrict__ out, int *flag, i
         for (int e = 0; e < 8; ++e) {
             const int tl = 2 * j + (e >> 2), c = cs * BC + 4 * q + (e & 3);
             v[e] = (tl < ntp && m < Mg && c < Cg) ? to_acc<float>(w[(((size_t)grp * Mg + m) * Cg + c) * Kn + tf + tl]) : 0.f;
-            bad = bad || bf16_split_bad(v[e]);
+            bad = bad || split_bad(v[e]);
         }
         uint4 o[NP];
         pack8_16<T, NP>(v, sw, o);

@@ -130,8 +130,8 @@ hipError_t launch_to_channels_last(int dtype, const void *x, void *xcl, int B, i
                                    int *flag = nullptr, const void *chk = nullptr, size_t chk_n = 0,
                                    float chk_limit = 0.f, const void *amax_w = nullptr, size_t amax_w_n = 0);
 // 16-bit MFMA operands of the sampled side (forward, weight gradient): the sampled values are
-// mask * bilinear(X), below 2^126 (and so within bf16's range) when |X| < SAMPLED_LIMIT and
-// |mask| < MASK_LIMIT; larger or non-finite values send the launch to its fp32 MFMA loop.
+// mask * bilinear(X), below 2^126 (finite, with a finite piece scale) when |X| < SAMPLED_LIMIT
+// and |mask| < MASK_LIMIT; larger or non-finite values send the launch to its fp32 MFMA loop.
 constexpr float SAMPLED_LIMIT = 0x1p96f;
 constexpr float MASK_LIMIT = 0x1p30f;
 // *flag |= some fp32 value of v[0 .. n) is not below limit in magnitude (or is nan)
@@ -204,7 +204,7 @@ hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t,
 // Z (the GEMM-side tensor, (B, M, Pn)) and the weight as the data gradient's 16-bit MFMA operands
 // (zs, wsplit), and the weight's fp32-loop chunks (wd: [G][c_tiles][m_steps][Kn][16 c][16 m]; skipped
 // when null), in one launch. For fp32 tensors, *flag (zeroed by the caller first) is set
-// when a value is not finite or would round past the bf16 range: the data gradient then runs its
+// when a value is not finite or at least 0x1.ffp127 in magnitude: the data gradient then runs its
 // fp32 MFMA loop.
 hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs,
                                 void *wsplit, void *wd, int *flag, hipStream_t s);

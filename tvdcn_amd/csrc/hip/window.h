@@ -635,18 +635,18 @@ __device__ __forceinline__ AxisW<DIM, float> record_weights(const Geo &g, const 
 // the low half); the 16x16 result has the layout of the 16x16x4 fp32 MFMA. fp32 operands
 // go in as two fp16 pieces each, of the value scaled by a power of two 2^s that puts the
 // operand's largest magnitude in [2^14, 2^15): p0 = fp16(v 2^s), p1 = fp16(v 2^s - p0) (nearest,
-// ties to even; the residual is exact in fp32), so v 2^s = p0 + p1 + r with |r| <= 2^-24 |v 2^s|
+// ties to even; the residual is exact in fp32), so v 2^s = p0 + p1 + r with |r| <= 2^-23 |v 2^s|
 // while p1 stays a normal fp16 (|v| >= 2^-17 of the operand's largest; below that the error is
 // at most 2^-25 of a unit, 2^-40 of the largest). Of the four cross products p_i q_j the three
-// with i + j <= 1 are summed (exact products, fp32 accumulation); the one left out and the
-// residuals are below 3 2^-24 |v w|, fp32's own rounding of a few multiply-adds; the sum is
-// scaled back by 2^-(s_a + s_b). An fp32 value is bad for this when it is not finite (or rounds
-// past the largest bf16: the range checks of the sampled operands); fp16 / bf16 operands go in
-// as they are.
+// with i + j <= 1 are summed (exact products, fp32 accumulation); the one left out (|p1 q1| <=
+// 2^-22 |v w|) and the residuals' terms (<= 2^-23 |v w| each) stay below 2^-21 |v w|, the
+// rounding fp32 itself accumulates over a few multiply-adds; the sum is scaled back by
+// 2^-(s_a + s_b). An fp32 value is bad for this (split_bad) when it is not finite or at least
+// 0x1.ffp127 in magnitude; fp16 / bf16 operands go in as they are.
 // ---------------------------------------------------------------------------
 template <typename T> constexpr int npiece_of() { return std::is_same<T, float>::value ? 2 : 1; }
 
-__device__ __forceinline__ bool bf16_split_bad(float v) {
+__device__ __forceinline__ bool split_bad(float v) {
     return (__float_as_uint(v) & 0x7FFFFFFFu) >= 0x7F7F8000u;
 }
 
