@@ -74,6 +74,9 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
     // fp32 as fp16 pieces: the sampled columns' scale, and the one back out (the weight's with it)
     const int s_b = npiece_of<T>() == 2 && use16_flag ? sampled_scale(g, flag, mask != nullptr) : 0;
     const int s_back = npiece_of<T>() == 2 && use16_flag ? -(s_b + operand_scale(flag, AMAX_W)) : 0;
+    // the sampling table's masks carry 2^s_b, so that the B fragments come out of the sampling at
+    // their pieces' scale
+    const float mscale_b = ldexpf(1.f, s_b);
     const int cs_lo = ks * fw.slices_per, cs_hi = min(slices, cs_lo + fw.slices_per);
 
     Tile tile;
@@ -207,7 +210,8 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
         if (og_s != geo_og || mg_s != geo_mg) {
             tile.ogu = og_s;
             tile.mgu = mg_s;
-            fill_geo<DIM, T, 3>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
+            // (the sampled values' piece scale folded into the records' masks)
+            fill_geo<DIM, T, 3>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT, mscale_b);
             geo_og = og_s;
             geo_mg = mg_s;
         }
@@ -245,7 +249,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                 for (int pb = 0; pb < PB; ++pb) {
                     const float v[8] = {b0[pb][0], b0[pb][1], b0[pb][2], b0[pb][3],
                                         b1[pb][0], b1[pb][1], b1[pb][2], b1[pb][3]};
-                    pack8_16<T, NP>(v, s_b, bp[pb]);
+                    pack8_16<T, NP>(v, 0, bp[pb]);   // (already at scale 2^s_b)
                 }
             };
             if constexpr (STAGE) {
@@ -450,7 +454,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
                                 const float v[8] = {bq[2 * h][pb][0],     bq[2 * h][pb][1],     bq[2 * h][pb][2],
                                                     bq[2 * h][pb][3],     bq[2 * h + 1][pb][0], bq[2 * h + 1][pb][1],
                                                     bq[2 * h + 1][pb][2], bq[2 * h + 1][pb][3]};
-                                pack8_16<T, NP>(v, s_b, bv[pb]);
+                                pack8_16<T, NP>(v, 0, bv[pb]);   // (already at scale 2^s_b)
                             }
                             const uint16_t *pcur = wptr16(cs, 2 * tg + h);
                             const uint16_t *pnext =

@@ -407,10 +407,13 @@ __device__ __forceinline__ void transpose_rows4(acc4 (&b)[4]) {
 }
 
 // RPT = records per thread per batch (WIN_TMAX * BPX / 512 = 4.5: one batch at 5); a
-// caller short of registers passes fewer.
+// caller short of registers passes fewer. mscale (a power of two) multiplies every record's
+// mask, after its activation: a caller whose sampled values are wanted at a scale folds it in
+// here, once per record, rather than once per sampled value.
 template <int DIM, typename T, int RPT = 5>
 __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const Tile &tile, const T *__restrict__ offset,
-                                         const T *__restrict__ mask, int t0, int ntaps, acc4 *geo, int tid, int nthreads) {
+                                         const T *__restrict__ mask, int t0, int ntaps, acc4 *geo, int tid, int nthreads,
+                                         float mscale = 1.f) {
     // records e = tid, tid + nthreads, ...: every global load of a batch is issued
     // before any is consumed (one memory latency per batch, not one per record)
     const bool deformable = offset != nullptr;
@@ -460,7 +463,8 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
                     pt.pos[a] = round_position<T, float>((float)pt.base[a] + ov[j][a]);
                     r[a] = pt.pos[a];
                 }
-                mk = mv[j];
+                // (an activated mask is scaled after its activation, below)
+                mk = mask != nullptr && g.mask_act != 0 ? mv[j] : mv[j] * mscale;
                 if (DIM < 3 && wt.cells > 0) {
                     const AxisW<DIM, float> aw = axis_weights<DIM, float>(g, pt, deformable);
                     bool fast = true;
@@ -504,7 +508,7 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
         for (int e = tid; e < n; e += nthreads) {
             if (tile.pixel(g, wt, e % BPX) < 0) continue;
             float *m = reinterpret_cast<float *>(geo + e) + (DIM == 3 ? 3 : DIM);
-            *m = mask_activate<float>(g, *m);
+            *m = mask_activate<float>(g, *m) * mscale;
         }
     } else if (mask != nullptr && g.mask_act == MASK_ACT_SOFTMAX) {
         // a pixel's records of the pass were written by other threads (record e belongs to
@@ -518,7 +522,7 @@ __device__ __forceinline__ void fill_geo(const Geo &g, const WinTiles &wt, const
             mask_softmax_norm<float, T>(g, mask, tile.b, tile.mgu, p, mx, inv);
             for (int tl = 0; tl < ntaps; ++tl) {
                 float *m = reinterpret_cast<float *>(geo + tl * BPX + i) + (DIM == 3 ? 3 : DIM);
-                *m = expf(*m - mx) * inv;
+                *m = expf(*m - mx) * inv * mscale;
             }
         }
     }
