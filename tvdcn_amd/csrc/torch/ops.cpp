@@ -301,6 +301,202 @@ void set_mask_activation(Problem &pr, int64_t activation, double mask_scale) {
 hipStream_t current_stream(const Tensor &t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
 
 // ---------------------------------------------------------------------------
+// One image above the kernels' 32-bit indexing (the C ABI refuses it with
+// TVDCN_STATUS_NOT_SUPPORTED; the reference indexes such images in 64 bits,
+// tvdcn/csrc/ops/utils/dispatch.h:52-60): the problem runs as sub-problems over channel ranges,
+// each of whose tensors fits. A sub-problem is one conv group's range of s sampled-side channels
+// (conv: input channels; transposed: output channels) times a range of t GEMM-side channels
+// (conv: output; transposed: input), with the offset / mask groups of its sampled channels. The
+// results that sum over ranges — the output over the ranges it contracts (conv: sampled side;
+// transposed: GEMM side), grad_input over the other side's, grad_offset / grad_mask over all — are
+// added in float32 (float64 for float64) in a fixed order; the weight gradient is written block by
+// block; the bias and its gradient go with the first range of the contracted side.
+// ---------------------------------------------------------------------------
+struct ChannelSplit {
+    int64_t G, Cg, Mg;   // groups, sampled / GEMM-side channels per group
+    int64_t cpo, cpm;    // sampled channels per offset / mask group (0: no offset / mask)
+    int64_t kn;          // kernel taps
+    int64_t s, t;        // channels per sampled / GEMM-side range
+};
+
+bool image_too_large(const tvdcn_conv_desc &d) {
+    int64_t images = 0;
+    return d.batch > 0 && tvdcn_conv_batch_block(&d, &images) == TVDCN_STATUS_NOT_SUPPORTED;
+}
+
+// first offset / mask group of sampled channels [c0, c0 + s) and their count (a range lies inside one
+// group or covers whole groups)
+void range_groups(int64_t c0, int64_t s, int64_t per, int64_t &first, int64_t &count) {
+    first = c0 / per;
+    count = s > per ? s / per : 1;
+}
+
+tvdcn_conv_desc range_desc(const Problem &pr, const ChannelSplit &sp, int64_t c0) {
+    tvdcn_conv_desc d = pr.desc;
+    d.flags &= ~TVDCN_FLAG_CHANNELS_LAST;   // the ranges are copied to NC<spatial> order
+    d.groups = 1;
+    d.in_channels = pr.transposed ? sp.t : sp.s;
+    d.out_channels = pr.transposed ? sp.s : sp.t;
+    int64_t first = 0, count = 0;
+    if (sp.cpo) {
+        range_groups(c0, sp.s, sp.cpo, first, count);
+        d.offset_groups = count;
+    }
+    if (sp.cpm) {
+        range_groups(c0, sp.s, sp.cpm, first, count);
+        d.mask_groups = count;
+    }
+    return d;
+}
+
+// a range size s of the sampled side is usable when it divides the group's channels and each range
+// lies inside one offset (mask) group or covers whole ones that do not straddle conv groups
+bool range_fits_groups(int64_t s, int64_t Cg, int64_t per) {
+    if (Cg % s) return false;
+    if (per == 0) return true;
+    return per % s == 0 || (s % per == 0 && Cg % per == 0);
+}
+
+ChannelSplit plan_channel_split(const Problem &pr, const char *name) {
+    const tvdcn_conv_desc &d = pr.desc;
+    ChannelSplit sp{};
+    sp.G = d.groups;
+    const int64_t Cs = pr.transposed ? d.out_channels : d.in_channels;
+    const int64_t Cm = pr.transposed ? d.in_channels : d.out_channels;
+    sp.Cg = Cs / sp.G;
+    sp.Mg = Cm / sp.G;
+    sp.cpo = d.offset_groups ? Cs / d.offset_groups : 0;
+    sp.cpm = d.mask_groups ? Cs / d.mask_groups : 0;
+    sp.kn = 1;
+    for (int i = 0; i < d.dim; ++i) sp.kn *= d.kernel[i];
+    // the largest usable sampled-side range with a one-channel GEMM-side range, then the largest
+    // GEMM-side range beside it
+    auto fits = [&](int64_t s, int64_t t) {
+        ChannelSplit c = sp;
+        c.s = s;
+        c.t = t;
+        int64_t images = 0;
+        const tvdcn_conv_desc rd = range_desc(pr, c, 0);
+        return tvdcn_conv_batch_block(&rd, &images) == TVDCN_STATUS_SUCCESS;
+    };
+    for (int64_t s = sp.Cg; s >= 1 && sp.s == 0; --s)
+        if (range_fits_groups(s, sp.Cg, sp.cpo) && range_fits_groups(s, sp.Cg, sp.cpm) && fits(s, 1)) sp.s = s;
+    TORCH_CHECK(sp.s > 0, name, ": one image's tensors exceed 2^31 - 1 elements even for one channel (its offset, ",
+                "mask or spatial extent alone is too large for the kernels' 32-bit indexing)");
+    for (int64_t t = sp.Mg; t >= 1 && sp.t == 0; --t)
+        if (sp.Mg % t == 0 && fits(sp.s, t)) sp.t = t;
+    TORCH_CHECK(sp.t > 0, name, ": one image's tensors exceed 2^31 - 1 elements even for one channel");
+    return sp;
+}
+
+// the tensors of range (g, i, j): sampled channels c0 = g * Cg + i * s, GEMM-side m0 = g * Mg + j * t
+struct RangeOperands {
+    int64_t c0, m0;
+    bool first;   // the first range of the contracted side: takes the bias
+    tvdcn_conv_desc desc;
+    Tensor input, weight, offset, mask, bias;
+};
+
+RangeOperands range_operands(const Problem &pr, const ChannelSplit &sp, int64_t g, int64_t i, int64_t j) {
+    RangeOperands r;
+    r.c0 = g * sp.Cg + i * sp.s;
+    r.m0 = g * sp.Mg + j * sp.t;
+    r.first = pr.transposed ? j == 0 : i == 0;
+    r.desc = range_desc(pr, sp, r.c0);
+    r.input = aligned((pr.transposed ? pr.input.narrow(1, r.m0, sp.t) : pr.input.narrow(1, r.c0, sp.s)).contiguous());
+    // conv weight (Cout, Cin / G, k...), transposed weight (Cin, Cout / G, k...): GEMM-side rows, the
+    // group's sampled channels as columns in both
+    r.weight = aligned(pr.weight.narrow(0, r.m0, sp.t).narrow(1, i * sp.s, sp.s).contiguous());
+    int64_t first = 0, count = 0;
+    if (sp.cpo) {
+        range_groups(r.c0, sp.s, sp.cpo, first, count);
+        const int64_t per = sp.kn * pr.dim;
+        r.offset = aligned(pr.offset.narrow(1, first * per, count * per).contiguous());
+    }
+    if (sp.cpm) {
+        range_groups(r.c0, sp.s, sp.cpm, first, count);
+        r.mask = aligned(pr.mask.narrow(1, first * sp.kn, count * sp.kn).contiguous());
+    }
+    if (pr.bias.defined() && r.first)
+        r.bias = aligned((pr.transposed ? pr.bias.narrow(0, r.c0, sp.s) : pr.bias.narrow(0, r.m0, sp.t)).contiguous());
+    return r;
+}
+
+at::ScalarType sum_type(const Tensor &t) { return t.scalar_type() == at::kDouble ? at::kDouble : at::kFloat; }
+
+Tensor forward_channel_split(const Problem &pr, const char *name) {
+    const ChannelSplit sp = plan_channel_split(pr, name);
+    Tensor acc = at::zeros(out_shape(pr), pr.input.options().dtype(sum_type(pr.input)));
+    Tensor ws;
+    for (int64_t g = 0; g < sp.G; ++g)
+        for (int64_t i = 0; i < sp.Cg / sp.s; ++i)
+            for (int64_t j = 0; j < sp.Mg / sp.t; ++j) {
+                RangeOperands r = range_operands(pr, sp, g, i, j);
+                Tensor part = pr.transposed ? acc.narrow(1, r.c0, sp.s) : acc.narrow(1, r.m0, sp.t);
+                Tensor y = at::empty(part.sizes(), pr.input.options());
+                const size_t ws_bytes = tvdcn_deform_conv_forward_workspace_size(&r.desc);
+                TORCH_CHECK(ws_bytes > 0, name, ": ", tvdcn_last_error());
+                if (!ws.defined() || (size_t)ws.numel() < ws_bytes)
+                    ws = at::empty({(int64_t)ws_bytes}, pr.input.options().dtype(at::kByte));
+                check_status(tvdcn_deform_conv_forward(&r.desc, r.input.data_ptr(), r.weight.data_ptr(),
+                                                       ptr_or_null(r.offset), ptr_or_null(r.mask), ptr_or_null(r.bias),
+                                                       y.data_ptr(), ws.data_ptr(), ws_bytes, current_stream(y)),
+                             name);
+                part.add_(y);
+            }
+    return acc.to(pr.input.scalar_type());
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_channel_split(const Problem &pr, const Tensor &grad,
+                                                                          const char *name) {
+    const ChannelSplit sp = plan_channel_split(pr, name);
+    const auto sums = pr.input.options().dtype(sum_type(pr.input));
+    Tensor gi = at::zeros(pr.input.sizes(), sums);
+    Tensor gw = at::empty_like(pr.weight);
+    Tensor go = pr.offset.defined() ? at::zeros(pr.offset.sizes(), sums) : Tensor();
+    Tensor gm = pr.mask.defined() ? at::zeros(pr.mask.sizes(), sums) : Tensor();
+    Tensor gb = pr.bias.defined() ? at::empty({pr.desc.out_channels}, pr.input.options()) : Tensor();
+    Tensor ws;
+    for (int64_t g = 0; g < sp.G; ++g)
+        for (int64_t i = 0; i < sp.Cg / sp.s; ++i)
+            for (int64_t j = 0; j < sp.Mg / sp.t; ++j) {
+                RangeOperands r = range_operands(pr, sp, g, i, j);
+                Tensor gr = aligned((pr.transposed ? grad.narrow(1, r.c0, sp.s) : grad.narrow(1, r.m0, sp.t)).contiguous());
+                Tensor r_gi = at::empty_like(r.input), r_gw = at::empty_like(r.weight);
+                Tensor r_go = r.offset.defined() ? at::empty_like(r.offset) : Tensor();
+                Tensor r_gm = r.mask.defined() ? at::empty_like(r.mask) : Tensor();
+                Tensor r_gb = r.bias.defined() ? at::empty_like(r.bias) : Tensor();
+                const size_t ws_bytes = tvdcn_deform_conv_backward_workspace_size(&r.desc);
+                TORCH_CHECK(ws_bytes > 0, name, ": ", tvdcn_last_error());
+                if (!ws.defined() || (size_t)ws.numel() < ws_bytes)
+                    ws = at::empty({(int64_t)ws_bytes}, pr.input.options().dtype(at::kByte));
+                check_status(tvdcn_deform_conv_backward(&r.desc, gr.data_ptr(), r.input.data_ptr(), r.weight.data_ptr(),
+                                                        ptr_or_null(r.offset), ptr_or_null(r.mask), r_gi.data_ptr(),
+                                                        r_gw.data_ptr(), mut_ptr_or_null(r_go), mut_ptr_or_null(r_gm),
+                                                        mut_ptr_or_null(r_gb), ws.data_ptr(), ws_bytes,
+                                                        current_stream(r_gi)),
+                             name);
+                (pr.transposed ? gi.narrow(1, r.m0, sp.t) : gi.narrow(1, r.c0, sp.s)).add_(r_gi);
+                gw.narrow(0, r.m0, sp.t).narrow(1, i * sp.s, sp.s).copy_(r_gw);
+                int64_t first = 0, count = 0;
+                if (r_go.defined()) {
+                    range_groups(r.c0, sp.s, sp.cpo, first, count);
+                    go.narrow(1, first * sp.kn * pr.dim, count * sp.kn * pr.dim).add_(r_go);
+                }
+                if (r_gm.defined()) {
+                    range_groups(r.c0, sp.s, sp.cpm, first, count);
+                    gm.narrow(1, first * sp.kn, count * sp.kn).add_(r_gm);
+                }
+                if (r_gb.defined())
+                    (pr.transposed ? gb.narrow(0, r.c0, sp.s) : gb.narrow(0, r.m0, sp.t)).copy_(r_gb);
+            }
+    Tensor grad_input = at::empty_like(pr.input);   // (keeps a channels-last input's order)
+    grad_input.copy_(gi);
+    return {grad_input, gw, go.defined() ? go.to(pr.input.scalar_type()) : go,
+            gm.defined() ? gm.to(pr.input.scalar_type()) : gm, gb};
+}
+
+// ---------------------------------------------------------------------------
 // forward / backward, CUDA (HIP) key
 // ---------------------------------------------------------------------------
 Tensor forward_hip(int dim, bool transposed, const Tensor &input, const Tensor &weight,
@@ -315,7 +511,9 @@ Tensor forward_hip(int dim, bool transposed, const Tensor &input, const Tensor &
     pr.desc.dtype = dtype_code(pr.input.scalar_type());
     set_mask_activation(pr, activation, mask_scale);
     Tensor output = at::empty(out_shape(pr), pr.input.options());
-    if (output.numel() > 0) {
+    if (output.numel() > 0 && image_too_large(pr.desc)) {
+        output = forward_channel_split(pr, name);
+    } else if (output.numel() > 0) {
         const size_t ws_bytes = tvdcn_deform_conv_forward_workspace_size(&pr.desc);
         TORCH_CHECK(ws_bytes > 0 || pr.desc.batch == 0, name, ": ", tvdcn_last_error());
         Tensor ws = at::empty({(int64_t)std::max<size_t>(ws_bytes, 1)}, pr.input.options().dtype(at::kByte));
@@ -349,6 +547,15 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backward_hip(
                 at::IntArrayRef(out_shape(pr)));
     TORCH_CHECK(g.scalar_type() == pr.input.scalar_type(), name, ": grad dtype must match input dtype");
 
+    if (image_too_large(pr.desc)) {
+        auto [grad_input, grad_weight, grad_offset, grad_mask, grad_bias] = backward_channel_split(pr, g, name);
+        if (pr.unbatched) {
+            grad_input = grad_input.squeeze(0);
+            if (grad_offset.defined()) grad_offset = grad_offset.squeeze(0);
+            if (grad_mask.defined()) grad_mask = grad_mask.squeeze(0);
+        }
+        return {grad_input, grad_weight, grad_offset, grad_mask, grad_bias};
+    }
     Tensor grad_input = at::empty_like(pr.input);
     Tensor grad_weight = at::empty_like(pr.weight);
     Tensor grad_offset = pr.offset.defined() ? at::empty_like(pr.offset) : Tensor();
