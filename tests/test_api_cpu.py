@@ -47,6 +47,19 @@ def test_native_library_loaded():
     assert tvdcn.cuda_version() > 60000000
 
 
+def test_operator_library_found_by_the_extension_finder():
+    """The operator library is located as the reference locates its _C (tvdcn/extension.py:19-51): the
+    import system's extension finder over the package directory, so _C + any of the interpreter's
+    extension suffixes is taken; a name without a library raises ImportError."""
+    import importlib.machinery
+    path = extension._get_extension_path("_C")
+    assert os.path.dirname(path) == os.path.dirname(extension.__file__)
+    base = os.path.basename(path)
+    assert base.startswith("_C") and base[2:] in importlib.machinery.EXTENSION_SUFFIXES
+    with pytest.raises(ImportError):
+        extension._get_extension_path("_no_such_library")
+
+
 def test_c_abi_exports_every_declared_function(lib):
     names = declared_functions()
     assert len(names) >= 11

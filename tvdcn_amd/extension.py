@@ -2,7 +2,10 @@
 
 Mirrors tvdcn/extension.py (``has_ops``, ``with_cuda``, ``cuda_version``,
 ``cuda_arch_list``, ``_assert_has_ops``; tvdcn/extension.py:61-188). The library
-is ``tvdcn_amd/_C.so``, built in-tree by ``tvdcn_amd/_build.py``; it registers the
+is ``tvdcn_amd/_C.so``, built in-tree by ``tvdcn_amd/_build.py`` and found as the
+reference finds its ``_C`` (tvdcn/extension.py:19-51): the import system's extension
+finder over this directory, so ``_C`` + any extension suffix of the interpreter
+(``.cpython-*.so``, ``.abi3.so``, ``.so``) is taken; it registers the
 ``torch.ops.tvdcn`` operators (the reference's namespace and schemas) and links
 ``libtvdcn_hip.so`` (the gfx950 HIP kernels behind the C ABI in
 ``include/tvdcn_hip.h``). There is no fallback: if the library is missing every op
@@ -12,14 +15,25 @@ raises.
 (as tvdcn/extension.py:55-82 does), so that TorchScript can compile
 ``_assert_has_ops`` into scripted modules.
 """
+import importlib.machinery
 import os
 from typing import List
 
 import torch
 
 _LIB_DIR = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_LIB_DIR, "_C.so")
 HIP_LIB_PATH = os.path.join(_LIB_DIR, "libtvdcn_hip.so")
+
+
+def _get_extension_path(lib_name: str) -> str:
+    """Path of library ``lib_name`` in this package's directory under any of the interpreter's
+    extension-module suffixes (the import system's own file finder); ImportError when absent."""
+    finder = importlib.machinery.FileFinder(
+        _LIB_DIR, (importlib.machinery.ExtensionFileLoader, importlib.machinery.EXTENSION_SUFFIXES))
+    spec = finder.find_spec(lib_name)
+    if spec is None or spec.origin is None:
+        raise ImportError(f"no {lib_name} library in {_LIB_DIR}")
+    return spec.origin
 
 _HAS_OPS = False
 _LOAD_ERROR = None
@@ -39,13 +53,10 @@ def _load() -> bool:
     if _HAS_OPS:
         return True
     try:
-        if os.path.exists(_LIB_PATH):
-            torch.ops.load_library(_LIB_PATH)
-            _HAS_OPS = True
-            _has_ops = _has_ops_loaded
-            _LOAD_ERROR = None
-        else:
-            _LOAD_ERROR = f"{_LIB_PATH} does not exist"
+        torch.ops.load_library(_get_extension_path("_C"))
+        _HAS_OPS = True
+        _has_ops = _has_ops_loaded
+        _LOAD_ERROR = None
     except (ImportError, OSError, RuntimeError) as e:  # pragma: no cover - reported by _assert_has_ops
         _LOAD_ERROR = str(e)
     return _HAS_OPS
