@@ -37,9 +37,9 @@ PEAK_HBM = 8.0e12              # MI355X HBM3E, B/s
 PEAK_16BIT_MFMA = 2.5e15       # MI355X dense fp16 / bf16 matrix, FLOP/s
 
 
-def mfma_path(family, dtype=torch.float32, dim=2):
-    """(MFMA instruction, MFMA products per algorithmic product, its dense peak) of a kernel family's
-    K loop: 16x16x32 MFMAs in every rank, fp32 operands as two fp16 pieces at a per-tensor
+def mfma_path(dtype=torch.float32):
+    """(MFMA instruction, MFMA products per algorithmic product, its dense peak) of the MFMA kernel
+    families' K loops: 16x16x32 MFMAs in every rank, fp32 operands as two fp16 pieces at a per-tensor
     power-of-two scale, of which three cross products are summed (fp32-accurate), fp16/bf16 operands
     as they are. A launch whose fp32 operands were flagged (not finite) runs the fp32 loop instead.
     The fp32 path's own ceiling is the 16-bit peak over the products per product (2.5 PFLOP/s / 3 =
@@ -141,7 +141,7 @@ def gpu_bench(inp, steps, warmup):
     return time_path(params, fwd, gout, steps, warmup)
 
 
-def family_rooflines(kern, contraction_flops, grad_out_bytes, mask_bytes=0, dtype=torch.float32, dim=2):
+def family_rooflines(kern, contraction_flops, grad_out_bytes, mask_bytes=0, dtype=torch.float32):
     """Algorithmic work per launch of each kernel family against the bound that applies: each of
     the three MFMA families performs one contraction of `contraction_flops` per launch (its fraction
     taken of the fp32 MFMA peak, the arithmetic the path delivers; `mfma` names the instruction its
@@ -167,7 +167,7 @@ def family_rooflines(kern, contraction_flops, grad_out_bytes, mask_bytes=0, dtyp
             if bound == "mfma":
                 # hw_frac: the instruction's use of its own dense peak, which is also the fraction of
                 # the path's ceiling (hw_peak / products in algorithmic FLOP/s)
-                instr, products, hw_peak = mfma_path(name, dtype, dim)
+                instr, products, hw_peak = mfma_path(dtype)
                 out[name].update(mfma=instr, hw_frac=round(products * achieved / hw_peak, 4),
                                  ceiling=round(hw_peak / products / scale, 1))
         else:
@@ -270,7 +270,7 @@ def run_suite_case(n, dtype, steps, warmup, cpu=False):
     nb = 3 if c["tr"] else 2
     es = torch.finfo(dtype).bits // 8
     mask_bytes = es * (logits.numel() if logits is not None else 0)
-    roof = family_rooflines(kern, F, es * gout.numel(), mask_bytes, dtype=dtype, dim=dim)
+    roof = family_rooflines(kern, F, es * gout.numel(), mask_bytes, dtype=dtype)
     row = {
         "case": c["name"], "dtype": str(dtype).replace("torch.", ""),
         "compute": ("fp32-accurate: scaled fp16 pieces on 16x16x32 MFMAs, fp32 accumulate" if dtype == torch.float32 else
