@@ -383,6 +383,47 @@ def test_scatter_elementwise_under_gradient_spikes_fp32(dim, spike, dense):
         assert rel_err(gr, r) < TOL[torch.float32][1], name
 
 
+@pytest.mark.skipif(not oracle.have_reference(), reason="reference CPU build (oracle/_ref) not available")
+@pytest.mark.parametrize("dim", [1, 2, 3])
+def test_scatter_elementwise_graded_grad_out_fp32(dim):
+    """grad_input element by element when grad_out falls smoothly from 1 to 1e-3 across every 256-pixel
+    tile of the data-gradient kernel (log-linear along the tile's last axis): the quiet end of a tile
+    accumulates in the same fixed-point window, at a unit set by the tile's bound, as its loud end. Error
+    of an element as in the spike test: |x - x64| / (A + median A), bound 4x the reference's own float32
+    path (oracle/_ref) + 1e-5. Also printed: the error relative to the element's own magnitude A alone
+    over the quietest tenth of the elements, ours and the reference's."""
+    in_size = {1: [600], 2: [40, 36], 3: [8, 16, 16]}[dim]
+    case = make_case(dim, False, batch=2, cin=16 if dim == 3 else 32, cout=64, kernel=[3] * dim,
+                     stride=[1] * dim, padding=[1] * dim, dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim,
+                     seed=545 + dim)
+    case["offset"] = (case["offset"] * 256).round() / 256
+    g = torch.Generator().manual_seed(546)
+    gout = torch.randn(case["out_shape"], generator=g, dtype=torch.float64)
+    span = {1: 256, 2: 16, 3: 8}[dim]   # the tile's extent along the last axis
+    n = case["out_shape"][-1]
+    u = (torch.arange(n, dtype=torch.float64) % span) / (span - 1)
+    gout = gout * torch.pow(10.0, -3.0 * u)
+    _, grads, _ = run_gpu(case, torch.float32, grad_out=gout)
+    _, ref = run_oracle(case, gout, torch.float32)
+    mag = scatter_magnitude(case, gout, torch.float32)
+    e = elementwise_err(grads[0], ref[0], mag)
+    args = [case[n].float() if case[n] is not None else None for n in ("input", "weight", "offset", "mask", "bias")]
+    params = [case["stride"], case["padding"], case["dilation"], case["groups"]]
+    ref32 = oracle.run_reference([{"op": f"_deform_conv{dim}d_backward", "args": [gout.float()] + args + params}])
+    e_ref = elementwise_err(ref32[0][0], ref[0], mag)
+    quiet = (mag > 0) & (mag <= mag[mag > 0].quantile(0.1))
+
+    def own(a):
+        return float(((a.detach().double().cpu() - ref[0]).abs()[quiet] / mag[quiet]).max())
+
+    print(f"dim {dim} graded grad_out: grad_input elementwise error {e:.2e} (reference float32 path {e_ref:.2e}); "
+          f"quietest tenth, relative to their own magnitude: {own(grads[0]):.2e} "
+          f"(reference {own(ref32[0][0]):.2e})", flush=True)
+    assert e <= 4 * e_ref + 1e-5
+    for name, gr, r in zip(("weight", "offset", "mask", "bias"), grads[1:], ref[1:]):
+        assert rel_err(gr, r) < TOL[torch.float32][1], name
+
+
 def test_saved_input_version_check_by_default():
     """By default the autograd node saves the input itself, as the reference does
     (autograd/deform_conv2d_kernel.cpp:35): changing it in place after the forward makes the backward
