@@ -447,7 +447,7 @@ hipError_t launch_k1(const Geo &g, const WinTiles &wt, const WeightWin &ww, cons
     return hipGetLastError();
 }
 
-// the fp32 instantiation, and (1D / 2D, with an operand flag) the 16-bit one beside it
+// the fp32 instantiation, and (with an operand flag) the 16-bit one beside it
 template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
                     const void *offset, const void *mask, void *part, const int *flag, hipStream_t s) {

@@ -611,12 +611,17 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         const bool cl_in = (desc->flags & TVDCN_FLAG_CHANNELS_LAST) != 0;   // conv only
         // conv: the channels-last grad_input of the accumulation type, accumulated in place
         void *gx_cl = pl.transposed ? nullptr : cl_in && direct ? grad_input : at(workspace, L.cl_acc);
-        // the offset / mask gradient accumulators, the operand flag and grad_input zeroed by one launch
-        const FillItem fills[4] = {{goff, goff ? n_goff * ab : 0},
+        // transposed, input gradient on the split forward plan: its fp32 accumulator
+        void *y32 = pl.transposed && pl.fw.ok && pl.fw.ksplit > 1 ? (dt == kF32 ? grad_input : at(workspace, L.yacc))
+                                                                   : nullptr;
+        // the offset / mask gradient accumulators, the operand flag, grad_input (conv) or the split
+        // accumulator (transposed) zeroed by one launch
+        const FillItem fills[5] = {{goff, goff ? n_goff * ab : 0},
                                    {gmask, gmask ? n_gmask * ab : 0},
                                    {flag, 4 * OPERAND_FLAG_WORDS},
-                                   {gx_cl, gx_cl ? (size_t)g.B * g.Sn * g.C * ab : 0}};
-        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero_multi(fills, 4, s));
+                                   {gx_cl, gx_cl ? (size_t)g.B * g.Sn * g.C * ab : 0},
+                                   {y32, y32 ? (size_t)g.B * g.M * g.Pn * 4 : 0}};
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero_multi(fills, 5, s));
         const bool coord = offset != nullptr || mask != nullptr;
         // the 16-bit loops of the sampled side (weight gradient; transposed: input gradient)
         const bool sampled16 = sampled16_host_ok(pl, desc) && (pl.ww.ok || (pl.transposed && pl.fw.ok));
@@ -687,11 +692,6 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
                     TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout16(dt, g, pl.fw, weight, w16, flag, s, wf));
                 else
                     TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fwd_win_layout(dt, g, pl.fw, weight, wf, s));
-                void *y32 = nullptr;
-                if (pl.fw.ksplit > 1) {
-                    y32 = dt == kF32 ? grad_input : at(workspace, L.yacc);
-                    TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_fill_zero(4, y32, (size_t)g.B * g.M * g.Pn, s));
-                }
                 TVDCN_LAUNCH(TVDCN_KERNEL_GATHER_GEMM, s,
                              launch_fwd_win(dt, pl.dim, g, pl.wn_f, pl.fw, xcl, wf, w16, flag, offset, mask, nullptr,
                                             grad_input, y32, s));
@@ -726,10 +726,10 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
     if (gmask && (desc->flags & TVDCN_FLAG_MASK_SOFTMAX))
         TVDCN_LAUNCH(TVDCN_KERNEL_MASK_SOFTMAX, s,
                      launch_mask_softmax_logit_grad(dt, mask, gmask, (int64_t)g.B * g.mg, g.Kn, g.Pn, s));
-    if (!direct) {
-        if (goff) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, goff, grad_offset, n_goff, s));
-        if (gmask) TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_acc_to_storage(dt, gmask, grad_mask, n_gmask, s));
-    }
+    if (!direct && (goff || gmask))
+        TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                     launch_acc_to_storage2(dt, goff, grad_offset, goff ? n_goff : 0, gmask, grad_mask,
+                                            gmask ? n_gmask : 0, s));
     return TVDCN_STATUS_SUCCESS;
 }
 

@@ -171,6 +171,9 @@ struct AmaxItem {
 // launch; nan values are passed over: the layout kernels' checks flag them)
 hipError_t launch_amax(const AmaxItem *items, int n, int *flag, hipStream_t s);
 hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n, hipStream_t s);
+// the same for two tensors in one launch (acc0 -> out0, n0 elements; acc1 -> out1, n1 elements)
+hipError_t launch_acc_to_storage2(int dtype, const void *acc0, void *out0, size_t n0, const void *acc1, void *out1,
+                                  size_t n1, hipStream_t s);
 hipError_t launch_storage_to_acc(int dtype, const void *x, void *acc, size_t n, hipStream_t s);   // elementwise widening
 // gmask_acc (accumulation type) *= d(scale * sigmoid(logit)) / d(logit), elementwise
 // gmask_acc (accumulation type) <- y * (gmask_acc - sum_k gmask_acc_k * y_k), y = softmax over K of the

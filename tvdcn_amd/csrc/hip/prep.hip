@@ -275,6 +275,18 @@ __global__ void acc_to_storage_kernel(const A *__restrict__ a, T *__restrict__ o
         o[i] = from_acc<T, A>(a[i]);
 }
 
+// two conversions in one launch: elements [0, n0) of the first pair, then [0, n1) of the second
+template <typename T, typename A>
+__global__ void acc_to_storage2_kernel(const A *__restrict__ a0, T *__restrict__ o0, size_t n0,
+                                       const A *__restrict__ a1, T *__restrict__ o1, size_t n1) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n0 + n1; i += (size_t)gridDim.x * blockDim.x) {
+        if (i < n0)
+            o0[i] = from_acc<T, A>(a0[i]);
+        else
+            o1[i - n0] = from_acc<T, A>(a1[i - n0]);
+    }
+}
+
 // Mask gradient of logits: the kernels accumulate d(loss)/d(mask value) per (b, group, tap,
 // pixel); with mask value m = scale * sigmoid(logit), d(m)/d(logit) = m * (1 - m / scale)
 // depends on that element only, so it scales the accumulated sum once.
@@ -561,6 +573,20 @@ hipError_t launch_acc_to_storage(int dtype, const void *acc, void *out, size_t n
         using A = decltype(av);
         hipLaunchKernelGGL((acc_to_storage_kernel<T, A>), dim3(grid_for(n)), dim3(256), 0, s,
                            static_cast<const A *>(acc), static_cast<T *>(out), n);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_acc_to_storage2(int dtype, const void *acc0, void *out0, size_t n0, const void *acc1, void *out1,
+                                  size_t n1, hipStream_t s) {
+    if (n0 == 0) return launch_acc_to_storage(dtype, acc1, out1, n1, s);
+    if (n1 == 0) return launch_acc_to_storage(dtype, acc0, out0, n0, s);
+    return by_dtype(dtype, [&](auto tv, auto av) {
+        using T = decltype(tv);
+        using A = decltype(av);
+        hipLaunchKernelGGL((acc_to_storage2_kernel<T, A>), dim3(grid_for(n0 + n1)), dim3(256), 0, s,
+                           static_cast<const A *>(acc0), static_cast<T *>(out0), n0, static_cast<const A *>(acc1),
+                           static_cast<T *>(out1), n1);
         return hipGetLastError();
     });
 }
