@@ -139,8 +139,8 @@ __device__ __forceinline__ float row_sum4(float v) {
 // (zvec: Pn % 4 == 0 and z aligned to 4 elements: the tile is read in 4-pixel vectors)
 template <typename T, int NP>
 __device__ __forceinline__ void z_split_block(long long bid, float *smem, const T *__restrict__ z,
-                                              uint16_t *__restrict__ zs, int *flag, int G, int Mg, int Pn, int ms32,
-                                              int pblocks, bool zvec) {
+                                              uint16_t *__restrict__ zs, uint16_t *__restrict__ zw, int *flag, int G,
+                                              int Mg, int Pn, int ms32, int pblocks, bool zvec, size_t zw_plane) {
     float(*tile)[65] = reinterpret_cast<float(*)[65]>(smem);   // [32][65]
     const int sz = NP == 2 ? operand_scale(flag, AMAX_Z) : 0;   // (every lane: before any returns)
     // (the block index is a grid index: 32-bit division, not the 64-bit sequence)
@@ -174,6 +174,21 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
         }
     }
     __syncthreads();
+    if (NP == 2 && zw != nullptr) {
+        // the same values in Z's own layout (8 consecutive pixels of one row per thread; Pn % 8 == 0)
+        const int ml = threadIdx.x >> 3, px = 8 * (threadIdx.x & 7);
+        const int m = st * 32 + ml, pw = p0 + px;
+        if (m < Mg && pw < Pn) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = tile[ml][px + e];
+            uint4 out[NP];
+            pack8_16<T, NP>(v, sz, out);
+            uint16_t *dst = zw + ((size_t)bg * Mg + m) * Pn + pw;
+#pragma unroll
+            for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + k * zw_plane) = out[k];
+        }
+    }
     const int pl = threadIdx.x >> 2, q = threadIdx.x & 3, p = p0 + pl;
     if (p >= Pn) return;
     float v[8];
@@ -1245,11 +1260,12 @@ template <typename T, int NP>
 __global__ void __launch_bounds__(256)
 data_prep_kernel(const T *__restrict__ z, uint16_t *__restrict__ zs, const T *__restrict__ w, uint16_t *__restrict__ wsp,
                  float *__restrict__ wd, int *flag, int G, int Mg, int Cg, int Pn, int Kn, int c_tiles, int ms32,
-                 int m_steps, int pblocks, long long nz, int nws, bool zvec) {
+                 int m_steps, int pblocks, long long nz, int nws, bool zvec, uint16_t *__restrict__ zw,
+                 size_t zw_plane) {
     __shared__ float smem[WL_TK * BC * 33];
     long long L = blockIdx.x;
     if (L < nz) {
-        z_split_block<T, NP>(L, smem, z, zs, flag, G, Mg, Pn, ms32, pblocks, zvec);
+        z_split_block<T, NP>(L, smem, z, zs, zw, flag, G, Mg, Pn, ms32, pblocks, zvec, zw_plane);
         return;
     }
     L -= nz;
@@ -1315,7 +1331,8 @@ hipError_t launch_d(int dim, const Geo &g, const WinTiles &tl, bool scatter, boo
 
 template <typename T>
 hipError_t launch_prep(const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs, void *wsp, void *wd,
-                       int *flag, hipStream_t s) {
+                       int *flag, hipStream_t s, void *zw) {
+    if (zw != nullptr && (npiece_of<T>() != 2 || z == nullptr || g.Pn % 8 != 0)) return hipErrorInvalidValue;
     constexpr int NP = npiece_of<T>();
     const int pblocks = (g.Pn + 63) / 64;
     const int tchunks = (g.Kn + WL_TK - 1) / WL_TK;
@@ -1329,7 +1346,8 @@ hipError_t launch_prep(const Geo &g, const WinTiles &t, const void *z, const voi
                        static_cast<uint16_t *>(zs), static_cast<const T *>(w), static_cast<uint16_t *>(wsp),
                        static_cast<float *>(wd), flag, g.G, g.Mg, g.Cg, g.Pn, g.Kn, t.c_tiles, t.ms32, t.m_steps,
                        pblocks, zblocks, (int)wblocks,
-                       g.Pn % 4 == 0 && reinterpret_cast<uintptr_t>(z) % (4 * sizeof(T)) == 0);
+                       g.Pn % 4 == 0 && reinterpret_cast<uintptr_t>(z) % (4 * sizeof(T)) == 0,
+                       static_cast<uint16_t *>(zw), (size_t)g.B * g.M * g.Pn);
     return hipGetLastError();
 }
 
@@ -1470,11 +1488,11 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
 }
 
 hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs,
-                                void *wsplit, void *wd, int *flag, hipStream_t s) {
+                                void *wsplit, void *wd, int *flag, hipStream_t s, void *zw) {
     switch (dtype) {
-        case kF32: return launch_prep<float>(g, t, z, w, zs, wsplit, wd, flag, s);
-        case kF16: return launch_prep<__half>(g, t, z, w, zs, wsplit, wd, flag, s);
-        case kBF16: return launch_prep<__hip_bfloat16>(g, t, z, w, zs, wsplit, wd, flag, s);
+        case kF32: return launch_prep<float>(g, t, z, w, zs, wsplit, wd, flag, s, zw);
+        case kF16: return launch_prep<__half>(g, t, z, w, zs, wsplit, wd, flag, s, zw);
+        case kBF16: return launch_prep<__hip_bfloat16>(g, t, z, w, zs, wsplit, wd, flag, s, zw);
     }
     return hipErrorInvalidValue;
 }

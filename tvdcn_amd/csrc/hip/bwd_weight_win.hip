@@ -66,7 +66,7 @@ template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV, bool
 __global__ void __launch_bounds__(NT)
 bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const T *__restrict__ z,
                       const float *__restrict__ xcl, const T *__restrict__ offset, const T *__restrict__ mask,
-                      float *__restrict__ part, const int *flag) {
+                      float *__restrict__ part, const int *flag, const uint16_t *__restrict__ zw) {
     using SH = WShape<TMV, KPV>;
     constexpr int TM = SH::TM, KP = SH::KP, NCH = SH::NCH, NH = SH::NH, SS = SH::SS;
     constexpr int GEO_WORDS = SH::GEO_WORDS, SBUF_WORDS = SH::SBUF_WORDS;
@@ -201,17 +201,20 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 
             // A operand: Z[m][4 consecutive chunk pixels], m = mrow + mb * 16 + lane % 16
             const T *zrow[MB];
+            size_t zoff[MB];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int m = min(mrow + mb * 16 + (lane & 15), g.Mg - 1);
-                zrow[mb] = z + ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
+                zoff[mb] = ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
+                zrow[mb] = z + zoff[mb];
             }
             // quad path: a 16-pixel half chunk lies within one row of the box (box_x >= 16) and
             // P_x % 4 == 0, so the lane's 4 pixels are consecutive and all inside or all outside
             // the grid; in a tile wholly inside the grid every quad is inside
             const bool quad = ww.z_vec && wt.box[2] >= 16;
-            const bool full = quad && tile.p0[0] + wt.box[0] <= g.P[0] && tile.p0[1] + wt.box[1] <= g.P[1] &&
-                              tile.p0[2] + wt.box[2] <= g.P[2];
+            const bool tile_in = tile.p0[0] + wt.box[0] <= g.P[0] && tile.p0[1] + wt.box[1] <= g.P[1] &&
+                                 tile.p0[2] + wt.box[2] <= g.P[2];
+            const bool full = quad && tile_in;
             // Z of half h of chunk k (pixels k * KP + 16 h + 4 * (lane / 16) .. + 3); pixels
             // outside the grid stay 0 (never loaded, so that a non-finite value there cannot
             // leak into the sums)
@@ -333,24 +336,49 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                             for (int u = 0; u < 8; ++u) za[mb][u] = pu[u] >= 0 ? to_acc<float>(zrow[mb][pu[u]]) : 0.f;
                     }
                 };
-                float zc[KB][MB][8], zn[KB][MB][8];
+                // A fragments of K block kb of chunk k: with zw (Z as 16-bit values in its own layout:
+                // fp16 / bf16 Z itself, the pieces of an fp32 Z), 8 pixels of a row per 16-byte load;
+                // else loaded as fp32 and split here. Pixels outside the grid stay 0.
+                const bool zdirect = zw != nullptr && ww.z8;
+                const size_t zplane = (size_t)g.B * g.M * g.Pn;
+                auto load_frag = [&](int k, int kb, uint4 (&za)[MB][NP]) {
+                    if (zdirect) {
+                        const int i0 = k * KP + 32 * kb + 8 * q;
+                        const int iz = i0 >> wt.lbxy, iy = (i0 >> wt.lbx) & (wt.box[1] - 1), ix = i0 & (wt.box[2] - 1);
+                        const int pz = tile.p0[0] + iz, py = tile.p0[1] + iy, px = tile.p0[2] + ix;
+                        const int p = (pz * g.P[1] + py) * g.P[2] + px;
+                        // (the 8 pixels lie in one row of the box, px % 8 == 0 and P_x % 8 == 0: all
+                        // inside the grid or all outside)
+                        const bool ok = tile_in || (pz < g.P[0] && py < g.P[1] && px < g.P[2]);
 #pragma unroll
-                for (int kb = 0; kb < KB; ++kb) load_a8(0, kb, zc[kb]);
+                        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                            for (int kk = 0; kk < NP; ++kk) {
+                                za[mb][kk] = uint4{0u, 0u, 0u, 0u};
+                                if (ok) za[mb][kk] = *reinterpret_cast<const uint4 *>(zw + kk * zplane + zoff[mb] + p);
+                            }
+                    } else {
+                        float v[MB][8];
+                        load_a8(k, kb, v);
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb) pack8_16<T, NP>(v[mb], s_z, za[mb]);
+                    }
+                };
+                uint4 zc[KB][MB][NP], zn[KB][MB][NP];
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) load_frag(0, kb, zc[kb]);
                 for (int k = 0; k < NCH; ++k) {
                     __syncthreads();   // every wave done with the previous chunk's S16 tile
                     build_s16(k);
                     const bool more = k + 1 < NCH;
                     if (more) {
 #pragma unroll
-                        for (int kb = 0; kb < KB; ++kb) load_a8(k + 1, kb, zn[kb]);
+                        for (int kb = 0; kb < KB; ++kb) load_frag(k + 1, kb, zn[kb]);
                     }
                     __syncthreads();
                     const uint16_t *sb = s16 + (size_t)(lane & 15) * SS16 + 8 * q;
 #pragma unroll
                     for (int kb = 0; kb < KB; ++kb) {
-                        uint4 za16[MB][NP];
-#pragma unroll
-                        for (int mb = 0; mb < MB; ++mb) pack8_16<T, NP>(zc[kb][mb], s_z, za16[mb]);
 #pragma unroll
                         for (int tp = 0; tp < TM; ++tp) {
                             if ((FULL || tp < ntaps) && (TG == 1 || tp % TG == tg)) {
@@ -360,7 +388,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                                     bf[kk] = *reinterpret_cast<const uint4 *>(sb + ((size_t)kk * TM * BC + tp * BC) * SS16 + 32 * kb);
 #pragma unroll
                                 for (int mb = 0; mb < MB; ++mb)
-                                    acc[mb][tp] = mfma16x16x32_np<T, NP>(za16[mb], bf, acc[mb][tp]);
+                                    acc[mb][tp] = mfma16x16x32_np<T, NP>(zc[kb][mb], bf, acc[mb][tp]);
                             }
                         }
                     }
@@ -370,7 +398,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 #pragma unroll
                             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-                                for (int e = 0; e < 8; ++e) zc[kb][mb][e] = zn[kb][mb][e];
+                                for (int kk = 0; kk < NP; ++kk) zc[kb][mb][kk] = zn[kb][mb][kk];
                     }
                 }
             } else {
@@ -432,7 +460,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 
 template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV, bool USE16>
 hipError_t launch_k1(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
-                     const void *offset, const void *mask, void *part, const int *flag, hipStream_t s) {
+                     const void *offset, const void *mask, void *part, const int *flag, const void *zw, hipStream_t s) {
     using SH = WShape<TMV, KPV>;
     auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG, TMV, KPV, USE16>;
     const size_t lds =
@@ -443,38 +471,39 @@ hipError_t launch_k1(const Geo &g, const WinTiles &wt, const WeightWin &ww, cons
     const long long blocks = (long long)g.G * ww.n_split * ww.m_tiles * wt.c_tiles;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NT), lds, s, g, wt, ww, static_cast<const T *>(z),
                        static_cast<const float *>(xcl), static_cast<const T *>(offset), static_cast<const T *>(mask),
-                       static_cast<float *>(part), flag);
+                       static_cast<float *>(part), flag, USE16 ? static_cast<const uint16_t *>(zw) : nullptr);
     return hipGetLastError();
 }
 
 // the fp32 instantiation, and (with an operand flag) the 16-bit one beside it
 template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
 hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
-                    const void *offset, const void *mask, void *part, const int *flag, hipStream_t s) {
+                    const void *offset, const void *mask, void *part, const int *flag, const void *zw,
+                    hipStream_t s) {
     if (wt.tpp > TMV) return hipErrorInvalidValue;   // a pass must fit the tap slots
     if (flag != nullptr) {
         const hipError_t e = launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, true>(g, wt, ww, z, xcl, offset, mask, part,
-                                                                              flag, s);
+                                                                              flag, zw, s);
         if (e != hipSuccess) return e;
     }
-    return launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, false>(g, wt, ww, z, xcl, offset, mask, part, flag, s);
+    return launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, false>(g, wt, ww, z, xcl, offset, mask, part, flag, nullptr, s);
 }
 
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
-                    const void *offset, const void *mask, void *part, const int *flag, hipStream_t s) {
+                    const void *offset, const void *mask, void *part, const int *flag, const void *zw, hipStream_t s) {
     const bool small = small_shape(g, wt.tpp);
     const int tm = small ? SMALL_TM : WIN_TMAX;
     const bool full = wt.tpp == tm && g.Kn % tm == 0;
     auto pick = [&](auto dim_tag) -> hipError_t {
         constexpr int D = decltype(dim_tag)::value;
-        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, s)
-                                    : launch_k<D, T, false, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, s);
+        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s)
+                                    : launch_k<D, T, false, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s);
         if (small)
-            return full ? launch_k<D, T, true, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, flag, s)
-                        : launch_k<D, T, false, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, flag, s);
-        return full ? launch_k<D, T, true, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, s)
-                    : launch_k<D, T, false, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, s);
+            return full ? launch_k<D, T, true, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s)
+                        : launch_k<D, T, false, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s);
+        return full ? launch_k<D, T, true, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s)
+                    : launch_k<D, T, false, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s);
     };
     switch (dim) {
         case 1: return pick(std::integral_constant<int, 1>());
@@ -512,6 +541,7 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     w.units_per_split = (int)std::max<long long>(1, (units + splits - 1) / splits);
     w.n_split = (int)std::max<long long>(1, (units + w.units_per_split - 1) / w.units_per_split);
     w.z_vec = g.P[2] % 4 == 0 && wt.box[2] >= 4;
+    w.z8 = g.P[2] % 8 == 0 && wt.box[2] >= 8;
     w.part_elems = (size_t)w.n_split * g.G * g.Kn * g.Mg * g.Cg;
     w.ok = g.B > 0;
     return w;
@@ -519,12 +549,16 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
 
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
-                                 void *gw, bool accumulate, const int *flag, hipStream_t s) {
+                                 void *gw, bool accumulate, const int *flag, hipStream_t s, const void *zw) {
+    // the 16-bit loop's A fragments straight from 16-bit values: the pieces of an fp32 Z (zw), or a
+    // 16-bit Z itself when its rows are 16-byte aligned
+    if (!ww.z8) zw = nullptr;
+    if (dtype != kF32) zw = reinterpret_cast<uintptr_t>(z) % 16 == 0 && ww.z8 ? z : nullptr;
     hipError_t e = hipErrorInvalidValue;
     switch (dtype) {
-        case kF32: e = launch_d<float>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, s); break;
-        case kF16: e = launch_d<__half>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, s); break;
-        case kBF16: e = launch_d<__hip_bfloat16>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, s); break;
+        case kF32: e = launch_d<float>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, zw, s); break;
+        case kF16: e = launch_d<__half>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, zw, s); break;
+        case kBF16: e = launch_d<__hip_bfloat16>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, zw, s); break;
     }
     if (e != hipSuccess) return e;
     return launch_weight_reduce(dtype, g, ww.n_split, part, gw, accumulate, s, ww.units_per_split, ww.n_spatial,

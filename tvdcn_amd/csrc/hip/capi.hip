@@ -264,6 +264,7 @@ tvdcn_status batch_block(const tvdcn_conv_desc *d, int64_t &block, ImageElems *e
 struct Layout {
     size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, wpart = 0, goff_acc = 0, gmask_acc = 0, yacc = 0;
     size_t zs = 0, wsplit = 0;   // the windowed data gradient's 16-bit MFMA operands
+    size_t zw = 0;               // (fp32) Z's pieces in its own layout, for the weight gradient's 16-bit loop
     size_t w16 = 0;              // the windowed forward's 16-bit weight
     size_t flag = 0;             // operand flag: some fp32 operand too large or not finite for them
     size_t total = 0;
@@ -288,7 +289,7 @@ Layout layout(const Plan &pl, bool backward) {
     };
     const size_t SENTINEL = (size_t)-1;
     L.xcl = L.wf = L.wd = L.cl_acc = L.wpart = L.goff_acc = L.gmask_acc = L.yacc = SENTINEL;
-    L.zs = L.wsplit = L.w16 = L.flag = SENTINEL;
+    L.zs = L.wsplit = L.w16 = L.flag = L.zw = SENTINEL;
     L.flag = take(align_up(sizeof(int) * OPERAND_FLAG_WORDS));   // the flag and the operands' largest magnitudes
     // windowed data gradient (conv backward, transposed forward and backward): split operands
     auto take_split = [&]() {
@@ -318,6 +319,9 @@ Layout layout(const Plan &pl, bool backward) {
         L.xcl = take(cl_bytes);
         L.wd = take(wd_bytes);
         take_split();
+        // written beside the data gradient's split of Z (same launch), read by the weight gradient
+        if (pl.dtype == kF32 && pl.wn_s.ok && pl.ww.ok && pl.ww.z8)
+            L.zw = take(align_up((size_t)g.B * g.M * g.Pn * 2 * sizeof(uint16_t)));
         if (pl.transposed) {
             L.wf = take(wf_bytes);
             take_w16();
@@ -654,8 +658,11 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
                                                           cl_in ? mask : nullptr, pl.transposed ? Z : nullptr, flag,
                                                           s));
         void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
+        // (fp32, 16-bit weight-gradient loop) Z's pieces in its own layout, from the same launch
+        void *zw = sampled16 && pl.wn_s.ok ? at(workspace, L.zw) : nullptr;
         if (pl.wn_s.ok)
-            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_data_win_prep(dt, g, pl.wn_s, Z, weight, zs, wsp, wd, flag, s));
+            TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
+                         launch_data_win_prep(dt, g, pl.wn_s, Z, weight, zs, wsp, wd, flag, s, zw));
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s, launch_weight_data_layout(dt, g, weight, wd, pl.dt.Mg_pad, pl.dt.Cg_pad, s));
         if (!pl.transposed) {
@@ -713,7 +720,8 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         if (pl.ww.ok)
             TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight_win(dt, pl.dim, g, pl.wn_w, pl.ww, Z, xcl, offset,
                                                                             mask, at(workspace, L.wpart), grad_weight,
-                                                                            accumulate_weight, sampled16 ? flag : nullptr, s));
+                                                                            accumulate_weight, sampled16 ? flag : nullptr, s,
+                                                                            zw));
         else
             TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight(dt, pl.dim, g, pl.wt, Z, xcl, offset, mask,
                                                                         at(workspace, L.wpart), grad_weight,

@@ -84,6 +84,9 @@ struct WeightWin {
     // whatever the number of passes
     int units_per_split, n_split;
     bool z_vec;          // 4 consecutive tile pixels are contiguous and 16-byte aligned
+    bool z8;             // 8 consecutive tile pixels are contiguous in every row (P_x % 8 == 0 and
+                         // the box's rows at least 8 wide): the 16-bit loop can read its A fragments
+                         // as 16-bit values, 8 per 16-byte load
     size_t part_elems;   // workspace floats for the split partials
 };
 
@@ -209,16 +212,19 @@ hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t,
 // when null), in one launch. For fp32 tensors, *flag (zeroed by the caller first) is set
 // when a value is not finite or at least 0x1.ffp127 in magnitude: the data gradient then runs its
 // fp32 MFMA loop.
+// zw (fp32 only, may be null): Z again as two fp16 pieces at its scale in Z's own layout, piece k
+// at zw + k * B * M * Pn, for the weight gradient's 16-bit loop (needs WeightWin::z8)
 hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs,
-                                void *wsplit, void *wd, int *flag, hipStream_t s);
+                                void *wsplit, void *wd, int *flag, hipStream_t s, void *zw = nullptr);
 hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
                                const void *z, const void *wchunks, const void *zs, const void *wsplit,
                                const int *flag, const void *xcl, const void *offset, const void *mask, void *gx_cl,
                                void *goff, void *gmask, hipStream_t s);
-// flag: the operand flag (null: the fp32 MFMA loop; set: the same)
+// flag: the operand flag (null: the fp32 MFMA loop; set: the same). zw: the fp32 Z's pieces
+// written by launch_data_win_prep (null: the kernel splits Z in registers)
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
-                                 void *gw, bool accumulate, const int *flag, hipStream_t s);
+                                 void *gw, bool accumulate, const int *flag, hipStream_t s, const void *zw = nullptr);
 // gw (storage type, layout (M, Cg, Kn)) = sum over k_splits of part[ks][G][Kn][Mg][Cg]
 // dW = sum over splits of the partials; with units_per_split > 0 (windowed kernel) tap t sums only
 // the splits whose unit range meets its pass (t / tpp) over n_spatial tiles
