@@ -691,15 +691,28 @@ __device__ __forceinline__ int operand_scale(const int *flag, int slot) {
     return flag == nullptr ? 0 : piece_scale(bound_exp(operand_amax(flag, slot)));
 }
 
-// two values as their fp16 pieces at scale 2^s, packed two per dword
+// a - (float)h, h the low (HI = false) or high half of the fp16 pair w: one v_fma_mix_f32
+// (-h * 1 + a, its fp16 operand taken as it is, so exactly the subtraction a - (float)h)
+// where the compiler forms two conversions back to fp32 and two subtractions per pair
+template <bool HI> __device__ __forceinline__ float sub_half(float a, uint32_t w) {
+    float r;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(a));
+    else
+        asm("v_fma_mix_f32 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(a));
+    return r;
+}
+
+// two values as their fp16 pieces at scale 2^s, packed two per dword: hi = RN16(v), lo =
+// RN16(v - hi)
 __device__ __forceinline__ void split2_pk(float a, float b, int s, uint32_t (&w)[2]) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
     a = ldexpf(a, s);
     b = ldexpf(b, s);
-    const h2 h0 = {(_Float16)a, (_Float16)b};
-    w[0] = __builtin_bit_cast(uint32_t, h0);
-    const h2 h1 = {(_Float16)(a - (float)h0[0]), (_Float16)(b - (float)h0[1])};
-    w[1] = __builtin_bit_cast(uint32_t, h1);
+    w[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, h2));
+    const f2 r = {sub_half<false>(a, w[0]), sub_half<true>(b, w[0])};
+    w[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, h2));
 }
 
 // two values rounded to the 16-bit type T (fp16 or bf16), packed
@@ -721,9 +734,8 @@ __device__ __forceinline__ void split_one16(float v, int s, uint16_t (&p)[NP]) {
     static_assert(NP == npiece_of<T>(), "pieces per value of T");
     if constexpr (NP == 2) {
         v = ldexpf(v, s);
-        const _Float16 h = (_Float16)v;
-        p[0] = __builtin_bit_cast(uint16_t, h);
-        p[1] = __builtin_bit_cast(uint16_t, (_Float16)(v - (float)h));
+        p[0] = __builtin_bit_cast(uint16_t, (_Float16)v);
+        p[1] = __builtin_bit_cast(uint16_t, (_Float16)sub_half<false>(v, p[0]));
     } else if constexpr (std::is_same<T, __half>::value) {
         p[0] = __builtin_bit_cast(uint16_t, (_Float16)v);
     } else {
