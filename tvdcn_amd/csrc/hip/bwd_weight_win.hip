@@ -364,16 +364,13 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                         for (int mb = 0; mb < MB; ++mb) pack8_16<T, NP>(v[mb], s_z, za[mb]);
                     }
                 };
-                uint4 zc[KB][MB][NP], zn[KB][MB][NP];
-#pragma unroll
-                for (int kb = 0; kb < KB; ++kb) load_frag(0, kb, zc[kb]);
-                for (int k = 0; k < NCH; ++k) {
+                // chunk k on the A fragments in cur, those of chunk k + 1 loaded into nxt
+                auto chunk = [&](int k, const uint4 (&cur)[KB][MB][NP], uint4 (&nxt)[KB][MB][NP]) {
                     __syncthreads();   // every wave done with the previous chunk's S16 tile
                     build_s16(k);
-                    const bool more = k + 1 < NCH;
-                    if (more) {
+                    if (k + 1 < NCH) {
 #pragma unroll
-                        for (int kb = 0; kb < KB; ++kb) load_frag(k + 1, kb, zn[kb]);
+                        for (int kb = 0; kb < KB; ++kb) load_frag(k + 1, kb, nxt[kb]);
                     }
                     __syncthreads();
                     const uint16_t *sb = s16 + (size_t)(lane & 15) * SS16 + 8 * q;
@@ -388,18 +385,19 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                                     bf[kk] = *reinterpret_cast<const uint4 *>(sb + ((size_t)kk * TM * BC + tp * BC) * SS16 + 32 * kb);
 #pragma unroll
                                 for (int mb = 0; mb < MB; ++mb)
-                                    acc[mb][tp] = mfma16x16x32_np<T, NP>(zc[kb][mb], bf, acc[mb][tp]);
+                                    acc[mb][tp] = mfma16x16x32_np<T, NP>(cur[kb][mb], bf, acc[mb][tp]);
                             }
                         }
                     }
-                    if (more) {
+                };
+                // chunks in pairs, the fragment sets alternating (no copies between chunks)
+                static_assert(NCH % 2 == 0, "an even number of chunks per tile");
+                uint4 za[KB][MB][NP], zb[KB][MB][NP];
 #pragma unroll
-                        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                                for (int kk = 0; kk < NP; ++kk) zc[kb][mb][kk] = zn[kb][mb][kk];
-                    }
+                for (int kb = 0; kb < KB; ++kb) load_frag(0, kb, za[kb]);
+                for (int k = 0; k < NCH; k += 2) {
+                    chunk(k, za, zb);
+                    chunk(k + 1, zb, za);
                 }
             } else {
                 acc4 za[NH][MB], zn[NH][MB];
