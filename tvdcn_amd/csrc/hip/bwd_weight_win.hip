@@ -111,6 +111,9 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
     // (3D: chunk pixel j, taps tid / KP, + NT / KP, ..., all 16 channels)
     const int sj = tid % KP, sq = (tid / KP) & 3, st0 = tid / (KP * 4);
     constexpr int SSTEP = NT / (KP * 4);   // tap stride of the items
+    // (16-bit S tile, 1D / 2D: chunk pixel pair pj, channel quad pq, taps pt0, pt0 + PSTEP, ...)
+    const int pj = tid % (KP / 2), pq = (tid / (KP / 2)) & 3, pt0 = tid / (KP * 2);
+    constexpr int PSTEP = NT / (KP * 2);
 
     for (int pass = (int)(u_beg / n_sp); (long long)pass * n_sp < u_end; ++pass) {
         const int t0 = pass * wt.tpp;
@@ -128,21 +131,21 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
             Tile tile;
             tile.init(g, wt, s, ct, grp);
             const float *xb = xcl + (size_t)tile.b * g.Sn * g.C + tile.cg0;
-            const bool cq_ok = tile.c0 + 4 * sq < g.Cg;
             __syncthreads();   // previous tile done with the tables
             fill_geo<DIM, T>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
             fill_xwin(g, wt, tile, xb, xwin, tid, NT);
             __syncthreads();
 
-            // mask * sampled value of channels 4 sq .. + 3 at (tap tl, tile pixel i) (1D / 2D)
-            auto sample_quad = [&](int tl, int i) -> acc4 {
+            // mask * sampled value of channels 4 sqv .. + 3 at (tap tl, tile pixel i) (1D / 2D)
+            auto sample_quad = [&](int tl, int i, int sqv) -> acc4 {
+                const bool cq_ok = tile.c0 + 4 * sqv < g.Cg;
                 const acc4 r = geo[tl * BPX + i];
                 const int fc = fast_cell<DIM>(r);
                 const float mk = rec_mask<DIM>(r);
                 acc4 sv;
                 if (fc >= 0) {
                     // every corner cell is in the window (zeros outside the grid)
-                    sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * sq, r, mk);
+                    sv = window_sample_masked<DIM>(wt, xwin, fc, 4 * sqv, r, mk);
                 } else {
                     const AxisW<DIM, float> aw = record_weights<DIM>(g, r, deformable);
                     sv = acc4{0.f, 0.f, 0.f, 0.f};
@@ -156,10 +159,10 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                             const int cell = tile.corner_cell<DIM>(wt, aw, kk);
                             // LDS read unconditional (clamped), global read in its own branch:
                             // the two address spaces are never merged into one pointer
-                            acc4 x = *reinterpret_cast<const acc4 *>(xwin + max(cell, 0) * XS + 4 * sq);
+                            acc4 x = *reinterpret_cast<const acc4 *>(xwin + max(cell, 0) * XS + 4 * sqv);
                             if (cell < 0) {
                                 x = acc4{0.f, 0.f, 0.f, 0.f};
-                                if (cq_ok) x = *reinterpret_cast<const acc4 *>(xb + (size_t)idx * g.C + 4 * sq);
+                                if (cq_ok) x = *reinterpret_cast<const acc4 *>(xb + (size_t)idx * g.C + 4 * sqv);
                             }
                             sv += corner_weight<DIM, float>(aw, kk) * x;
                         }
@@ -192,7 +195,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                     return;
                 }
                 for (int tl = st0; tl < ntaps; tl += SSTEP) {
-                    const acc4 sv = sample_quad(tl, i);
+                    const acc4 sv = sample_quad(tl, i, sq);
                     float *row = dst + (tl * BC + 4 * sq) * SS + sj;
 #pragma unroll
                     for (int v = 0; v < 4; ++v) row[v * SS] = sv[v];
@@ -291,15 +294,23 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                         }
                         return;
                     }
-                    for (int tl = st0; tl < ntaps; tl += SSTEP) {
-                        const acc4 sv = sample_quad(tl, i);
+                    // 1D / 2D: item = (two consecutive chunk pixels, channel quad, tap), so that each
+                    // (row, piece) takes one 32-bit LDS store of the two pixels' values, and the fp32
+                    // split runs on the pair (packed conversions)
+                    const int i0 = k * KP + 2 * pj;
+                    for (int tl = pt0; tl < ntaps; tl += PSTEP) {
+                        const acc4 s0 = sample_quad(tl, i0, pq), s1 = sample_quad(tl, i0 + 1, pq);
 #pragma unroll
                         for (int v = 0; v < 4; ++v) {
-                            uint16_t pc[NP];
-                            split_one16<T, NP>(sv[v], s_s, pc);
+                            uint32_t w[NP];
+                            if constexpr (NP == 2)
+                                split2_pk(s0[v], s1[v], s_s, w);
+                            else
+                                w[0] = pack2_16<T>(s0[v], s1[v]);
 #pragma unroll
                             for (int kk = 0; kk < NP; ++kk)
-                                s16[((size_t)kk * TM * BC + tl * BC + 4 * sq + v) * SS16 + sj] = pc[kk];
+                                *reinterpret_cast<uint32_t *>(s16 + ((size_t)kk * TM * BC + tl * BC + 4 * pq + v) * SS16 +
+                                                              2 * pj) = w[kk];
                         }
                     }
                 };
