@@ -19,6 +19,11 @@
 // half of the chunk:
 //   A = Z[m][px] (4 consecutive pixels per lane, one 16-byte load when contiguous),
 //   B = S[px][c] of one tap, D = dW[m][c] of that tap.
+// The 16-bit loop (16x16x32 MFMAs, 32-pixel K blocks) keeps a single 16-bit S tile per
+// chunk, built from pixel pairs (one 32-bit LDS store per row and piece), and reads its A
+// fragments as 16-bit values: 8 pixels of a row per 16-byte load, from fp16 / bf16 Z itself
+// or, for fp32, from Z's fp16 pieces in Z's own layout (written by the data gradient's
+// operand-prep launch); the chunks run in pairs with alternating fragment sets.
 // At the end of each pass of the run the block is stored to the split's slot of the
 // workspace; per tap, the splits whose runs meet its pass are summed in a fixed order
 // (deterministic).
