@@ -546,3 +546,19 @@ def test_fp32_pieces_scaled_per_tensor(kind):
             e = rel_err(gr, r)
             print(f"{kind}: grad_{name} rel err {e:.2e}", flush=True)
             assert e < TOL[torch.float32][1], name
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim,transposed,in_size", [
+    (2, False, [20, 24]), (2, False, [20, 22]), (1, False, [320]), (1, False, [322]),
+    (3, False, [6, 8, 16]), (3, False, [6, 8, 12]), (2, True, [16, 16])])
+def test_weight_gradient_a_fragments(dim, transposed, in_size, dtype):
+    """The weight gradient's 16-bit loop reads its A fragments (Z, 8 pixels of a row) as 16-bit values
+    when the column grid's rows are a multiple of 8 wide (fp32: Z's pieces written beside the data
+    gradient's split; fp16 / bf16: Z itself), and forms them from fp32 loads otherwise: both widths,
+    every rank, conv and transposed, against the float64 oracle."""
+    k = [5] if dim == 1 else [3] * dim
+    case = make_case(dim, transposed, batch=2, cin=32, cout=48, kernel=k, stride=[1] * dim,
+                     padding=[kk // 2 for kk in k], dilation=[1] * dim, in_size=in_size, out_pad=[0] * dim,
+                     seed=630 + dim + 3 * transposed + in_size[-1])
+    check(case, dtype)
