@@ -133,8 +133,9 @@ __device__ __forceinline__ float row_sum4(float v) {
     return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
-// Z (B, G * Mg, Pn) -> zs [B][G][ms32][Pn][NP][32]: per pixel and 32-channel step, the NP pieces
-// of its 32 channels (zero past Mg), each as 4 lane groups of 8 (the 16x16x32 B-operand layout).
+// Z (B, G * Mg, Pn) -> zs [B][G][ms32][NP][Pn][32]: per 32-channel step and piece, every pixel's
+// 32 channels (zero past Mg) as 4 lane groups of 8 (the 16x16x32 B-operand layout), so that a
+// wave's fragment load of one piece for 16 consecutive pixels reads 1 KB of whole lines.
 // Block = 64 pixels of one (image, group, step), transposed through LDS.
 // (zvec: Pn % 4 == 0 and z aligned to 4 elements: the tile is read in 4-pixel vectors)
 template <typename T, int NP>
@@ -200,9 +201,9 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
     }
     uint4 out[NP];
     pack8_16<T, NP>(v, sz, out);
-    uint16_t *dst = zs + ((size_t)bgs * Pn + p) * (NP * 32) + q * 8;
+    uint16_t *dst = zs + ((size_t)bgs * NP * Pn + p) * 32 + q * 8;
 #pragma unroll
-    for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + k * 32) = out[k];
+    for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + (size_t)k * Pn * 32) = out[k];
     if (NP == 2 && bad) atomicOr(flag, 1);
 }
 
@@ -457,7 +458,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
             const uint16_t *zl[PB];
 #pragma unroll
             for (int pb = 0; pb < PB; ++pb)
-                zl[pb] = zs + ((size_t)(b * g.G + grp) * ms32 * g.Pn + (zp[pb] < 0 ? 0 : zp[pb])) * (NP * 32) + q * 8;
+                zl[pb] = zs + ((size_t)(b * g.G + grp) * ms32 * NP * g.Pn + (zp[pb] < 0 ? 0 : zp[pb])) * 32 + q * 8;
             const uint16_t *wl = wsplit + ((size_t)(grp * wt.c_tiles + ct) * ms32 * g.Kn + t0) * (NP * 512) + lane * 8;
             auto wfrag = [&](int st, int tl, uint4 (&f)[NP]) {
                 const uint16_t *pw = wl + ((size_t)min(st, ms32 - 1) * g.Kn + tl) * (NP * 512);
@@ -469,7 +470,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                 for (int pb = 0; pb < PB; ++pb)
 #pragma unroll
                     for (int k = 0; k < NP; ++k)
-                        f[pb][k] = *reinterpret_cast<const uint4 *>(zl[pb] + (size_t)st * zstep + k * 32);
+                        f[pb][k] = *reinterpret_cast<const uint4 *>(zl[pb] + (size_t)st * zstep + (size_t)k * g.Pn * 32);
             };
             uint4 zc[PB][NP], zn[PB][NP], wr[3][NP];
             zfrag(0, zc);
@@ -530,13 +531,13 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
             const uint16_t *zl[PB];
 #pragma unroll
             for (int pb = 0; pb < PB; ++pb)
-                zl[pb] = zs + ((size_t)(b * g.G + grp) * ms32 * g.Pn + (zp[pb] < 0 ? 0 : zp[pb])) * (NP * 32) + q * 8;
+                zl[pb] = zs + ((size_t)(b * g.G + grp) * ms32 * NP * g.Pn + (zp[pb] < 0 ? 0 : zp[pb])) * 32 + q * 8;
             auto zfrag = [&](int st, uint4 (&f)[PB][NP]) {
 #pragma unroll
                 for (int pb = 0; pb < PB; ++pb)
 #pragma unroll
                     for (int k = 0; k < NP; ++k)
-                        f[pb][k] = *reinterpret_cast<const uint4 *>(zl[pb] + (size_t)st * zstep + k * 32);
+                        f[pb][k] = *reinterpret_cast<const uint4 *>(zl[pb] + (size_t)st * zstep + (size_t)k * g.Pn * 32);
             };
             const uint16_t *wblk = wsplit + ((size_t)(grp * wt.c_tiles + ct) * ms32 * g.Kn + t0) * (NP * 512);
             const int blk = wt.tpp * (NP * 512);   // buffer stride (16-bit values)

@@ -66,7 +66,7 @@ struct WinTiles {
     int xglobal;         // 3D only: offset / mask gradients read X from global memory, no X window
     int ms32;            // 32-channel steps of the GEMM side (zero padded)
     int npiece;          // 16-bit pieces per value: 2 (fp32), 1 (fp16 / bf16)
-    size_t zs_elems;     // 16-bit elements of the split Z: [B][G][ms32][Pn][npiece][32]
+    size_t zs_elems;     // 16-bit elements of the split Z: [B][G][ms32][npiece][Pn][32]
     size_t ws_elems;     // 16-bit elements of the split weight: [G][c_tiles][ms32][Kn][npiece][512]
     int wstage;          // bytes of LDS staging the 16-bit K loop's weight blocks (double-buffered
                          // [2][tpp][npiece][512]); 0: fragments straight from global memory
