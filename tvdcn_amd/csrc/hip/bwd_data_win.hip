@@ -176,8 +176,11 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
     }
     __syncthreads();
     if (NP == 2 && zw != nullptr) {
-        // the same values in Z's own layout (8 consecutive pixels of one row per thread; Pn % 8 == 0)
-        const int ml = threadIdx.x >> 3, px = 8 * (threadIdx.x & 7);
+        // the same values for the weight gradient, in 8-pixel column blocks: element (image b, row
+        // m of Z's M, pixel p) at ((b * Pn / 8 + p / 8) * M + m) * 8 + p % 8 of each piece's plane
+        // (Pn % 8 == 0), so that a wave's A fragment (16 rows x 4 blocks of 8 pixels) reads whole
+        // lines. Thread = (row ml, 8-pixel block px / 8): consecutive threads, consecutive rows.
+        const int ml = threadIdx.x & 31, px = 8 * (threadIdx.x >> 5);
         const int m = st * 32 + ml, pw = p0 + px;
         if (m < Mg && pw < Pn) {
             float v[8];
@@ -185,7 +188,8 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
             for (int e = 0; e < 8; ++e) v[e] = tile[ml][px + e];
             uint4 out[NP];
             pack8_16<T, NP>(v, sz, out);
-            uint16_t *dst = zw + ((size_t)bg * Mg + m) * Pn + pw;
+            const size_t M = (size_t)G * Mg;
+            uint16_t *dst = zw + ((size_t)b * (Pn / 8) + pw / 8) * M * 8 + ((size_t)grp * Mg + m) * 8;
 #pragma unroll
             for (int k = 0; k < NP; ++k) *reinterpret_cast<uint4 *>(dst + k * zw_plane) = out[k];
         }

@@ -22,8 +22,9 @@
 // The 16-bit loop (16x16x32 MFMAs, 32-pixel K blocks) keeps a single 16-bit S tile per
 // chunk, built from pixel pairs (one 32-bit LDS store per row and piece), and reads its A
 // fragments as 16-bit values: 8 pixels of a row per 16-byte load, from fp16 / bf16 Z itself
-// or, for fp32, from Z's fp16 pieces in Z's own layout (written by the data gradient's
-// operand-prep launch); the chunks run in pairs with alternating fragment sets.
+// or, for fp32, from Z's fp16 pieces in 8-pixel column blocks (a fragment's 16 rows x 4 blocks
+// are whole lines; written by the data gradient's operand-prep launch); the chunks run in
+// pairs with alternating fragment sets.
 // At the end of each pass of the run the block is stored to the split's slot of the
 // workspace; per tap, the splits whose runs meet its pass are summed in a fixed order
 // (deterministic).
@@ -209,11 +210,12 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 
             // A operand: Z[m][4 consecutive chunk pixels], m = mrow + mb * 16 + lane % 16
             const T *zrow[MB];
-            size_t zoff[MB];
+            size_t zoff[MB], zblk[MB];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int m = min(mrow + mb * 16 + (lane & 15), g.Mg - 1);
                 zoff[mb] = ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
+                zblk[mb] = (size_t)tile.b * g.M * g.Pn + ((size_t)tile.grp * g.Mg + m) * 8;
                 zrow[mb] = z + zoff[mb];
             }
             // quad path: a 16-pixel half chunk lies within one row of the box (box_x >= 16) and
@@ -371,7 +373,14 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 #pragma unroll
                             for (int kk = 0; kk < NP; ++kk) {
                                 za[mb][kk] = uint4{0u, 0u, 0u, 0u};
-                                if (ok) za[mb][kk] = *reinterpret_cast<const uint4 *>(zw + kk * zplane + zoff[mb] + p);
+                                if (ok) {
+                                    // fp32: the pieces in 8-pixel column blocks (data_prep_kernel);
+                                    // fp16 / bf16: Z's own rows
+                                    const size_t at = npiece_of<T>() == 2
+                                                          ? zblk[mb] + (size_t)(p >> 3) * (g.M * 8) + kk * zplane
+                                                          : zoff[mb] + p;
+                                    za[mb][kk] = *reinterpret_cast<const uint4 *>(zw + at);
+                                }
                             }
                     } else {
                         float v[MB][8];

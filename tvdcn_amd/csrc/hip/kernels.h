@@ -212,8 +212,8 @@ hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t,
 // when null), in one launch. For fp32 tensors, *flag (zeroed by the caller first) is set
 // when a value is not finite or at least 0x1.ffp127 in magnitude: the data gradient then runs its
 // fp32 MFMA loop.
-// zw (fp32 only, may be null): Z again as two fp16 pieces at its scale in Z's own layout, piece k
-// at zw + k * B * M * Pn, for the weight gradient's 16-bit loop (needs WeightWin::z8)
+// zw (fp32 only, may be null): Z again as two fp16 pieces at its scale, piece k at zw + k * B * M * Pn,
+// in 8-pixel column blocks [B][Pn / 8][M][8], for the weight gradient's 16-bit loop (needs WeightWin::z8)
 hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs,
                                 void *wsplit, void *wd, int *flag, hipStream_t s, void *zw = nullptr);
 hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
