@@ -175,7 +175,7 @@ __device__ __forceinline__ void z_split_block(long long bid, float *smem, const 
         }
     }
     __syncthreads();
-    if (NP == 2 && zw != nullptr) {
+    if (zw != nullptr) {
         // the same values for the weight gradient, in 8-pixel column blocks: element (image b, row
         // m of Z's M, pixel p) at ((b * Pn / 8 + p / 8) * M + m) * 8 + p % 8 of each piece's plane
         // (Pn % 8 == 0), so that a wave's A fragment (16 rows x 4 blocks of 8 pixels) reads whole
@@ -1337,7 +1337,7 @@ hipError_t launch_d(int dim, const Geo &g, const WinTiles &tl, bool scatter, boo
 template <typename T>
 hipError_t launch_prep(const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs, void *wsp, void *wd,
                        int *flag, hipStream_t s, void *zw) {
-    if (zw != nullptr && (npiece_of<T>() != 2 || z == nullptr || g.Pn % 8 != 0)) return hipErrorInvalidValue;
+    if (zw != nullptr && (z == nullptr || g.Pn % 8 != 0)) return hipErrorInvalidValue;
     constexpr int NP = npiece_of<T>();
     const int pblocks = (g.Pn + 63) / 64;
     const int tchunks = (g.Kn + WL_TK - 1) / WL_TK;

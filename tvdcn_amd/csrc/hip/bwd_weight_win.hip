@@ -21,10 +21,10 @@
 //   B = S[px][c] of one tap, D = dW[m][c] of that tap.
 // The 16-bit loop (16x16x32 MFMAs, 32-pixel K blocks) keeps a single 16-bit S tile per
 // chunk, built from pixel pairs (one 32-bit LDS store per row and piece), and reads its A
-// fragments as 16-bit values: 8 pixels of a row per 16-byte load, from fp16 / bf16 Z itself
-// or, for fp32, from Z's fp16 pieces in 8-pixel column blocks (a fragment's 16 rows x 4 blocks
-// are whole lines; written by the data gradient's operand-prep launch); the chunks run in
-// pairs with alternating fragment sets.
+// fragments as 16-bit values: 8 pixels of a row per 16-byte load,
+// from Z's 16-bit values (fp16 / bf16 as they are, fp32 as fp16 pieces) in 8-pixel column
+// blocks (a fragment's 16 rows x 4 blocks are whole lines; written by the data gradient's
+// operand-prep launch); the chunks run in pairs with alternating fragment sets.
 // At the end of each pass of the run the block is stored to the split's slot of the
 // workspace; per tap, the splits whose runs meet its pass are summed in a fixed order
 // (deterministic).
@@ -210,13 +210,12 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 
             // A operand: Z[m][4 consecutive chunk pixels], m = mrow + mb * 16 + lane % 16
             const T *zrow[MB];
-            size_t zoff[MB], zblk[MB];
+            size_t zblk[MB];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int m = min(mrow + mb * 16 + (lane & 15), g.Mg - 1);
-                zoff[mb] = ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
                 zblk[mb] = (size_t)tile.b * g.M * g.Pn + ((size_t)tile.grp * g.Mg + m) * 8;
-                zrow[mb] = z + zoff[mb];
+                zrow[mb] = z + ((size_t)tile.b * g.M + (size_t)tile.grp * g.Mg + m) * g.Pn;
             }
             // quad path: a 16-pixel half chunk lies within one row of the box (box_x >= 16) and
             // P_x % 4 == 0, so the lane's 4 pixels are consecutive and all inside or all outside
@@ -373,14 +372,10 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
 #pragma unroll
                             for (int kk = 0; kk < NP; ++kk) {
                                 za[mb][kk] = uint4{0u, 0u, 0u, 0u};
-                                if (ok) {
-                                    // fp32: the pieces in 8-pixel column blocks (data_prep_kernel);
-                                    // fp16 / bf16: Z's own rows
-                                    const size_t at = npiece_of<T>() == 2
-                                                          ? zblk[mb] + (size_t)(p >> 3) * (g.M * 8) + kk * zplane
-                                                          : zoff[mb] + p;
-                                    za[mb][kk] = *reinterpret_cast<const uint4 *>(zw + at);
-                                }
+                                // (Z's 16-bit values in 8-pixel column blocks, data_prep_kernel)
+                                if (ok)
+                                    za[mb][kk] = *reinterpret_cast<const uint4 *>(
+                                        zw + zblk[mb] + (size_t)(p >> 3) * (g.M * 8) + kk * zplane);
                             }
                     } else {
                         float v[MB][8];
@@ -573,10 +568,8 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
                                  void *gw, bool accumulate, const int *flag, hipStream_t s, const void *zw) {
-    // the 16-bit loop's A fragments straight from 16-bit values: the pieces of an fp32 Z (zw), or a
-    // 16-bit Z itself when its rows are 16-byte aligned
+    // the 16-bit loop's A fragments straight from Z's 16-bit values in column blocks (zw)
     if (!ww.z8) zw = nullptr;
-    if (dtype != kF32) zw = reinterpret_cast<uintptr_t>(z) % 16 == 0 && ww.z8 ? z : nullptr;
     hipError_t e = hipErrorInvalidValue;
     switch (dtype) {
         case kF32: e = launch_d<float>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, zw, s); break;

@@ -264,7 +264,7 @@ tvdcn_status batch_block(const tvdcn_conv_desc *d, int64_t &block, ImageElems *e
 struct Layout {
     size_t xcl = 0, wf = 0, wd = 0, cl_acc = 0, wpart = 0, goff_acc = 0, gmask_acc = 0, yacc = 0;
     size_t zs = 0, wsplit = 0;   // the windowed data gradient's 16-bit MFMA operands
-    size_t zw = 0;               // (fp32) Z's pieces in its own layout, for the weight gradient's 16-bit loop
+    size_t zw = 0;               // Z's 16-bit values in column blocks, for the weight gradient's 16-bit loop
     size_t w16 = 0;              // the windowed forward's 16-bit weight
     size_t flag = 0;             // operand flag: some fp32 operand too large or not finite for them
     size_t total = 0;
@@ -320,8 +320,8 @@ Layout layout(const Plan &pl, bool backward) {
         L.wd = take(wd_bytes);
         take_split();
         // written beside the data gradient's split of Z (same launch), read by the weight gradient
-        if (pl.dtype == kF32 && pl.wn_s.ok && pl.ww.ok && pl.ww.z8)
-            L.zw = take(align_up((size_t)g.B * g.M * g.Pn * 2 * sizeof(uint16_t)));
+        if ((pl.dtype == kF32 || pl.dtype == kF16 || pl.dtype == kBF16) && pl.wn_s.ok && pl.ww.ok && pl.ww.z8)
+            L.zw = take(align_up((size_t)g.B * g.M * g.Pn * (pl.dtype == kF32 ? 2 : 1) * sizeof(uint16_t)));
         if (pl.transposed) {
             L.wf = take(wf_bytes);
             take_w16();
@@ -658,7 +658,7 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
                                                           cl_in ? mask : nullptr, pl.transposed ? Z : nullptr, flag,
                                                           s));
         void *zs = at(workspace, L.zs), *wsp = at(workspace, L.wsplit);
-        // (fp32, 16-bit weight-gradient loop) Z's pieces in its own layout, from the same launch
+        // (16-bit weight-gradient loop) Z's 16-bit values in column blocks, from the same launch
         void *zw = sampled16 && pl.wn_s.ok ? at(workspace, L.zw) : nullptr;
         if (pl.wn_s.ok)
             TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,

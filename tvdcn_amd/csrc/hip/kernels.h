@@ -212,16 +212,17 @@ hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t,
 // when null), in one launch. For fp32 tensors, *flag (zeroed by the caller first) is set
 // when a value is not finite or at least 0x1.ffp127 in magnitude: the data gradient then runs its
 // fp32 MFMA loop.
-// zw (fp32 only, may be null): Z again as two fp16 pieces at its scale, piece k at zw + k * B * M * Pn,
-// in 8-pixel column blocks [B][Pn / 8][M][8], for the weight gradient's 16-bit loop (needs WeightWin::z8)
+// zw (may be null): Z again as 16-bit values (fp32: two fp16 pieces at its scale, piece k at
+// zw + k * B * M * Pn) in 8-pixel column blocks [B][Pn / 8][M][8], for the weight gradient's
+// 16-bit loop (needs WeightWin::z8)
 hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs,
                                 void *wsplit, void *wd, int *flag, hipStream_t s, void *zw = nullptr);
 hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
                                const void *z, const void *wchunks, const void *zs, const void *wsplit,
                                const int *flag, const void *xcl, const void *offset, const void *mask, void *gx_cl,
                                void *goff, void *gmask, hipStream_t s);
-// flag: the operand flag (null: the fp32 MFMA loop; set: the same). zw: the fp32 Z's pieces
-// written by launch_data_win_prep (null: the kernel splits Z in registers)
+// flag: the operand flag (null: the fp32 MFMA loop; set: the same). zw: Z's 16-bit values
+// written by launch_data_win_prep (null: the kernel forms them in registers)
 hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
                                  const void *z, const void *xcl, const void *offset, const void *mask, void *part,
                                  void *gw, bool accumulate, const int *flag, hipStream_t s, const void *zw = nullptr);
