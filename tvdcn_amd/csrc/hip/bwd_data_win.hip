@@ -240,7 +240,7 @@ __global__ void __launch_bounds__(NT)
 bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wchunks, const uint16_t *zs,
                     const uint16_t *wsplit, const int *flag, const float *__restrict__ xcl,
                     const T *__restrict__ offset, const T *__restrict__ mask, float *__restrict__ gx_cl,
-                    float *__restrict__ goff, float *__restrict__ gmask) {
+                    float *__restrict__ goff, float *__restrict__ gmask, const int gx_nchw) {
     constexpr int NC = 1 << DIM;
     constexpr int TMAX = WIN_TMAX;
     // scatter-only: the unit follows the largest kept term, cells sum modulo 2^32 (PREC_BITS)
@@ -285,6 +285,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
     const int use16_flag = zs != nullptr && (flag == nullptr || *flag == 0);
     const bool cq_ok = c0 + mq < g.Cg;           // Cg % 4 == 0: a channel quad is all in or all out
     const float *xb = xcl + (size_t)b * g.Sn * g.C + cg0;
+    // grad_input's strides per channel and per pixel: channels-last (B, S, C) or, gx_nchw, the
+    // caller's (B, C, S) float32 tensor itself
+    const size_t gcs = gx_nchw ? (size_t)g.Sn : 1, gps = gx_nchw ? 1 : (size_t)g.C;
+    float *const gxb = gx_cl + (size_t)b * g.Sn * g.C;
 
     // ---- per-tile LDS state: X window (read by the offset/mask gradients), zeroed
     //      fixed-point window (scatter)
@@ -341,19 +345,22 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 
     // ---- the fixed-point window accumulates over every pass of the tile and is flushed
     //      once, at the end (or before a pass whose bound is not finite): one float atomic
-    //      per non-zero (cell, channel), 16 consecutive channels per cell
+    //      per non-zero (cell, channel), 16 consecutive channels per cell (channels-last) or
+    //      32 consecutive cells per channel (gx_nchw)
     bool win_data = false;   // the window holds accumulated values (uniform)
-    // thread = (channel tid % 16, cells tid / 16, + 32, ...); FB cells' values are read before
-    // any is used (one LDS latency per batch). keep: the window is used again (cleared as
-    // read, barrier at the end); at the end of the workgroup neither is needed.
+    // thread = (channel tid % 16, cells tid / 16, + 32, ...) or, gx_nchw, (channel tid / 32, cells
+    // tid % 32, + 32, ...); FB cells' values are read before any is used (one LDS latency per
+    // batch). keep: the window is used again (cleared as read, barrier at the end); at the end
+    // of the workgroup neither is needed.
     auto flush_window = [&](bool keep) {
         constexpr int FB = 8;
         constexpr int STEP = NT / 16;
-        const int c = tid & 15;
+        static_assert(STEP == 32 && NT / 32 == BC, "both thread maps step 32 cells per channel");
+        const int c = gx_nchw ? tid >> 5 : tid & 15;
         const int se = scl[c];
         const bool c_ok = c0 + c < g.Cg;
-        float *gbase = gx_cl + (size_t)b * g.Sn * g.C + cg0 + c;
-        const int first = tid >> 4;
+        float *gbase = gxb + (size_t)(cg0 + c) * gcs;
+        const int first = gx_nchw ? tid & 31 : tid >> 4;
         // cell walker (no divisions per cell), as in for_cells
         int lx = first % wt.WE[2];
         int rr = first / wt.WE[2];
@@ -387,7 +394,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
             for (int j = 0; j < FB; ++j) {
                 if (iv[j] == 0) continue;
                 if (keep) iwin[c * cst + cell0 + j * STEP] = 0;   // cleared for what follows
-                if (si[j] >= 0) atomic_add(gbase + (size_t)si[j] * g.C, ldexpf((float)iv[j], -se));
+                if (si[j] >= 0) atomic_add(gbase + (size_t)si[j] * gps, ldexpf((float)iv[j], -se));
             }
         }
         if (keep) __syncthreads();
@@ -898,7 +905,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                 float gsc[4];
 #pragma unroll
                                 for (int v = 0; v < 4; ++v) gsc[v] = ldexpf(PREC ? mk * gv[v] : gv[v], sexp[v]);
-                                float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+                                float *gdst = gxb + (size_t)(cg0 + mq) * gcs;
                                 if constexpr (!PREC) {
 #pragma unroll
                                     for (int k = 0; k < 8; ++k) {
@@ -911,9 +918,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                             for (int v = 0; v < 4; ++v)
                                                 atomicAdd(dst + v * cst, (unsigned int)fixed_round(sw * gsc[v]));
                                         } else {
-                                            float *dst = gdst + (size_t)cr.idx(g, k) * g.C;
+                                            float *dst = gdst + (size_t)cr.idx(g, k) * gps;
 #pragma unroll
-                                            for (int v = 0; v < 4; ++v) atomic_add(dst + v, sw * gv[v]);
+                                            for (int v = 0; v < 4; ++v) atomic_add(dst + v * gcs, sw * gv[v]);
                                         }
                                     }
                                 } else {
@@ -938,10 +945,10 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                                     near = max(near, old[j][v] + WRAP_K);
                                                 }
                                             } else {
-                                                float *dst = gdst + (size_t)cr.idx(g, k) * g.C;
+                                                float *dst = gdst + (size_t)cr.idx(g, k) * gps;
                                                 const float sw = mk * cr.weight(k);
 #pragma unroll
-                                                for (int v = 0; v < 4; ++v) atomic_add(dst + v, sw * gv[v]);
+                                                for (int v = 0; v < 4; ++v) atomic_add(dst + v * gcs, sw * gv[v]);
                                             }
                                         }
                                         if (near >= 2u * WRAP_K) {
@@ -955,7 +962,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 #pragma unroll
                                                 for (int v = 0; v < 4; ++v) {
                                                     const float sp = wrap_spill(old[j][v], fixed_round(sw * gsc[v]), sexp[v]);
-                                                    if (sp != 0.f) atomic_add(gdst + (size_t)cr.idx(g, k) * g.C + v, sp);
+                                                    if (sp != 0.f) atomic_add(gdst + (size_t)cr.idx(g, k) * gps + v * gcs, sp);
                                                 }
                                             }
                                         }
@@ -1042,7 +1049,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                             if (PREC && near >= 2u * WRAP_K) {
                                 // some add may have wrapped: its 2^32 units go to global memory
                                 // (window cells outside the grid hold what the flush drops)
-                                float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+                                float *gdst = gxb + (size_t)(cg0 + mq) * gcs;
 #pragma unroll
                                 for (int k = 0; k < NF; ++k) {
                                     const int gi = tile.cell_index(g, wt, cell[k]);
@@ -1050,7 +1057,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 #pragma unroll
                                     for (int v = 0; v < 4; ++v) {
                                         const float sp = wrap_spill(old[k][v], fixed_round(wm[k] * gs[v]), sexp[v]);
-                                        if (sp != 0.f) atomic_add(gdst + (size_t)gi * g.C + v, sp);
+                                        if (sp != 0.f) atomic_add(gdst + (size_t)gi * gps + v * gcs, sp);
                                     }
                                 }
                             }
@@ -1100,7 +1107,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                     }
                     if constexpr (SCATTER) {
                         if (cq_ok) {
-                            float *gdst = gx_cl + (size_t)b * g.Sn * g.C + cg0 + mq;
+                            float *gdst = gxb + (size_t)(cg0 + mq) * gcs;
                             // (PREC: mask * G scaled once, the corner weight <= 1 applied after)
                             float gs[4];
 #pragma unroll
@@ -1116,7 +1123,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
 #pragma unroll
                                     for (int v = 0; v < 4; ++v) {
                                         if (sp[v]) {
-                                            atomic_add(gdst + (size_t)gidx[k] * g.C + v, s * gv[v]);
+                                            atomic_add(gdst + (size_t)gidx[k] * gps + v * gcs, s * gv[v]);
                                         } else if constexpr (PREC) {
                                             old[k][v] = atomicAdd(dst + v * cst, (unsigned int)fixed_round(w[k] * gs[v]));
                                             near = max(near, old[k][v] + WRAP_K);
@@ -1125,9 +1132,9 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                         }
                                     }
                                 } else {
-                                    float *dst = gdst + (size_t)gidx[k] * g.C;
+                                    float *dst = gdst + (size_t)gidx[k] * gps;
 #pragma unroll
-                                    for (int v = 0; v < 4; ++v) atomic_add(dst + v, s * gv[v]);
+                                    for (int v = 0; v < 4; ++v) atomic_add(dst + v * gcs, s * gv[v]);
                                 }
                             }
                             if (PREC && near >= 2u * WRAP_K) {
@@ -1139,7 +1146,7 @@ bwd_data_win_kernel(const Geo g, const WinTiles wt, const T *z, const float *wch
                                     for (int v = 0; v < 4; ++v) {
                                         if (sp[v]) continue;   // spike terms went to global memory
                                         const float spl = wrap_spill(old[k][v], fixed_round(w[k] * gs[v]), sexp[v]);
-                                        if (spl != 0.f) atomic_add(gdst + (size_t)gidx[k] * g.C + v, spl);
+                                        if (spl != 0.f) atomic_add(gdst + (size_t)gidx[k] * gps + v * gcs, spl);
                                     }
                                 }
                             }
@@ -1291,7 +1298,7 @@ template <bool SCATTER, bool COORD> size_t lds_bytes(const WinTiles &t) {
 template <int DIM, typename T, bool SCATTER, bool COORD>
 hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void *wchunks, const void *zs,
                     const void *wsplit, const int *flag, const void *xcl, const void *offset, const void *mask,
-                    void *gx_cl, void *goff, void *gmask, hipStream_t s) {
+                    void *gx_cl, void *goff, void *gmask, hipStream_t s, bool gx_nchw) {
     auto kern = bwd_data_win_kernel<DIM, T, SCATTER, COORD>;
     const size_t lds = lds_bytes<SCATTER, COORD>(tl);
     static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
@@ -1302,34 +1309,38 @@ hipError_t launch_k(const Geo &g, const WinTiles &tl, const void *z, const void 
                        static_cast<const float *>(wchunks), static_cast<const uint16_t *>(zs),
                        static_cast<const uint16_t *>(wsplit), flag, static_cast<const float *>(xcl),
                        static_cast<const T *>(offset), static_cast<const T *>(mask), static_cast<float *>(gx_cl),
-                       static_cast<float *>(goff), static_cast<float *>(gmask));
+                       static_cast<float *>(goff), static_cast<float *>(gmask), gx_nchw ? 1 : 0);
     return hipGetLastError();
 }
 
 template <int DIM, typename T>
 hipError_t launch_f(const Geo &g, const WinTiles &tl, bool scatter, bool coord, const void *z, const void *wc,
                     const void *zs, const void *wsp, const int *flag, const void *xcl, const void *offset,
-                    const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
+                    const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s, bool nchw) {
     if (scatter && coord)
-        return launch_k<DIM, T, true, true>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+        return launch_k<DIM, T, true, true>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s, nchw);
     if (scatter)
-        return launch_k<DIM, T, true, false>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+        return launch_k<DIM, T, true, false>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s, nchw);
     if (coord)
-        return launch_k<DIM, T, false, true>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+        return launch_k<DIM, T, false, true>(g, tl, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s, nchw);
     return hipSuccess;
 }
 
 template <typename T>
 hipError_t launch_d(int dim, const Geo &g, const WinTiles &tl, bool scatter, bool coord, const void *z,
                     const void *wc, const void *zs, const void *wsp, const int *flag, const void *xcl,
-                    const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s) {
+                    const void *offset, const void *mask, void *gx_cl, void *goff, void *gmask, hipStream_t s,
+                    bool nchw) {
     switch (dim) {
         case 1:
-            return launch_f<1, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+            return launch_f<1, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s,
+                                  nchw);
         case 2:
-            return launch_f<2, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+            return launch_f<2, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s,
+                                  nchw);
         case 3:
-            return launch_f<3, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s);
+            return launch_f<3, T>(g, tl, scatter, coord, z, wc, zs, wsp, flag, xcl, offset, mask, gx_cl, goff, gmask, s,
+                                  nchw);
     }
     return hipErrorInvalidValue;
 }
@@ -1505,17 +1516,17 @@ hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, cons
 hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
                                const void *z, const void *wchunks, const void *zs, const void *wsplit,
                                const int *flag, const void *xcl, const void *offset, const void *mask, void *gx_cl,
-                               void *goff, void *gmask, hipStream_t s) {
+                               void *goff, void *gmask, hipStream_t s, bool gx_nchw) {
     switch (dtype) {
         case kF32:
             return launch_d<float>(dim, g, t, scatter, coord, z, wchunks, zs, wsplit, flag, xcl, offset, mask, gx_cl,
-                                   goff, gmask, s);
+                                   goff, gmask, s, gx_nchw);
         case kF16:
             return launch_d<__half>(dim, g, t, scatter, coord, z, wchunks, zs, wsplit, flag, xcl, offset, mask, gx_cl,
-                                    goff, gmask, s);
+                                    goff, gmask, s, gx_nchw);
         case kBF16:
             return launch_d<__hip_bfloat16>(dim, g, t, scatter, coord, z, wchunks, zs, wsplit, flag, xcl, offset, mask,
-                                            gx_cl, goff, gmask, s);
+                                            gx_cl, goff, gmask, s, gx_nchw);
     }
     return hipErrorInvalidValue;
 }

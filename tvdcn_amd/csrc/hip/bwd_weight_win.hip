@@ -53,15 +53,21 @@ template <int TMV, int KPV> struct WShape {
     static constexpr int NH = KP / 16;      // 16-pixel MFMA K blocks per chunk
     static constexpr int SS = KP + 4;       // S tile row stride (rows = (tap, channel))
     static constexpr int GEO_WORDS = TM * BPX * 4;
-    static constexpr int SBUF_WORDS = 2 * TM * BC * SS;
+    static constexpr int SBUF_WORDS = 2 * TM * BC * SS;   // the fp32 loop's S tiles, double-buffered
+    static constexpr int SS16 = KP + 8;                   // 16-bit S tile row stride
+    // the 16-bit loop's S tile, per piece (a multiple of 4 words: the X window stays 16-byte aligned)
+    static constexpr int S16_WORDS = TM * BC * SS16 / 2;
+    static_assert(S16_WORDS % 4 == 0 && S16_WORDS * 2 <= SBUF_WORDS, "S16 tile words");
+    // S words of an instantiation: the 16-bit loop (np pieces) needs less, and the X window takes the rest
+    static constexpr int sbuf_words(bool use16, int np) { return use16 ? np * S16_WORDS : SBUF_WORDS; }
 };
 constexpr int SMALL_TM = 5;
 // the (5, 64) shape serves 256-row tiles (GEMM sides above 128 rows); 64-row tiles split the
 // taps between two wave groups and keep (9, 32)
 bool small_shape(const Geo &g, int tpp) { return tpp <= SMALL_TM && g.Mg > 128; }
-size_t fixed_words(const Geo &g, int tpp) {
-    return small_shape(g, tpp) ? WShape<SMALL_TM, 64>::GEO_WORDS + WShape<SMALL_TM, 64>::SBUF_WORDS
-                               : WShape<WIN_TMAX, 32>::GEO_WORDS + WShape<WIN_TMAX, 32>::SBUF_WORDS;
+size_t fixed_words(const Geo &g, int tpp, bool use16, int np) {
+    return small_shape(g, tpp) ? WShape<SMALL_TM, 64>::GEO_WORDS + WShape<SMALL_TM, 64>::sbuf_words(use16, np)
+                               : WShape<WIN_TMAX, 32>::GEO_WORDS + WShape<WIN_TMAX, 32>::sbuf_words(use16, np);
 }
 
 // FULL: every pass uses all TM tap slots (no per-tap guards). USE16: the instantiation with the
@@ -75,12 +81,12 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                       float *__restrict__ part, const int *flag, const uint16_t *__restrict__ zw) {
     using SH = WShape<TMV, KPV>;
     constexpr int TM = SH::TM, KP = SH::KP, NCH = SH::NCH, NH = SH::NH, SS = SH::SS;
-    constexpr int GEO_WORDS = SH::GEO_WORDS, SBUF_WORDS = SH::SBUF_WORDS;
+    constexpr int GEO_WORDS = SH::GEO_WORDS, SBUF_WORDS = SH::sbuf_words(USE16, npiece_of<T>());
     constexpr int NC = 1 << DIM;
     constexpr int BMW = rows_of<MB, TG>();
     extern __shared__ float smem[];
     acc4 *geo = reinterpret_cast<acc4 *>(smem);         // [TM][BPX]
-    float *sbuf = smem + GEO_WORDS;                     // [2][TM * BC][SS]
+    float *sbuf = smem + GEO_WORDS;                     // [2][TM * BC][SS] (16-bit loop: [NP][TM * BC][SS16])
     float *xwin = smem + GEO_WORDS + SBUF_WORDS;        // [cells][XS]
 
     const int tid = threadIdx.x;
@@ -271,9 +277,9 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
                 //      32-pixel K block, A = Z[m][8 consecutive pixels of lane group q] (pieces
                 //      formed in registers), B = S16[tap][c][the same pixels]
                 constexpr int NP = npiece_of<T>();
-                constexpr int SS16 = KP + 8;
+                constexpr int SS16 = SH::SS16;
                 constexpr int KB = KP / 32;
-                static_assert(NP * TM * BC * SS16 * 2 <= SBUF_WORDS * 4, "the S16 tile fits the fp32 S buffers");
+                static_assert(NP * TM * BC * SS16 * 2 <= SBUF_WORDS * 4, "the S16 tile fits its buffer");
                 uint16_t *s16 = reinterpret_cast<uint16_t *>(sbuf);
                 auto build_s16 = [&](int k) {
                     const int i = k * KP + sj;
@@ -481,8 +487,9 @@ hipError_t launch_k1(const Geo &g, const WinTiles &wt, const WeightWin &ww, cons
                      const void *offset, const void *mask, void *part, const int *flag, const void *zw, hipStream_t s) {
     using SH = WShape<TMV, KPV>;
     auto kern = bwd_weight_win_kernel<DIM, T, FULL, MB, TG, TMV, KPV, USE16>;
-    const size_t lds =
-        ((size_t)SH::GEO_WORDS + SH::SBUF_WORDS + (size_t)(wt.cells + (DIM == 3)) * XS) * sizeof(float);
+    const size_t lds = ((size_t)SH::GEO_WORDS + SH::sbuf_words(USE16, npiece_of<T>()) +
+                        (size_t)(wt.cells + (DIM == 3)) * XS) *
+                       sizeof(float);
     static std::atomic<unsigned long long> lds_raised{0};   // per device, see raise_lds_limit
     if (const hipError_t e = raise_lds_limit(reinterpret_cast<const void *>(kern), lds_raised); e != hipSuccess)
         return e;
@@ -495,12 +502,12 @@ hipError_t launch_k1(const Geo &g, const WinTiles &wt, const WeightWin &ww, cons
 
 // the fp32 instantiation, and (with an operand flag) the 16-bit one beside it
 template <int DIM, typename T, bool FULL, int MB, int TG, int TMV, int KPV>
-hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
-                    const void *offset, const void *mask, void *part, const int *flag, const void *zw,
-                    hipStream_t s) {
-    if (wt.tpp > TMV) return hipErrorInvalidValue;   // a pass must fit the tap slots
+hipError_t launch_k(const Geo &g, const WinTiles &wt, const WinTiles &wt16, const WeightWin &ww, const void *z,
+                    const void *xcl, const void *offset, const void *mask, void *part, const int *flag,
+                    const void *zw, hipStream_t s) {
+    if (wt.tpp > TMV || wt16.tpp != wt.tpp) return hipErrorInvalidValue;   // a pass must fit the tap slots
     if (flag != nullptr) {
-        const hipError_t e = launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, true>(g, wt, ww, z, xcl, offset, mask, part,
+        const hipError_t e = launch_k1<DIM, T, FULL, MB, TG, TMV, KPV, true>(g, wt16, ww, z, xcl, offset, mask, part,
                                                                               flag, zw, s);
         if (e != hipSuccess) return e;
     }
@@ -508,20 +515,21 @@ hipError_t launch_k(const Geo &g, const WinTiles &wt, const WeightWin &ww, const
 }
 
 template <typename T>
-hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww, const void *z, const void *xcl,
-                    const void *offset, const void *mask, void *part, const int *flag, const void *zw, hipStream_t s) {
+hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WinTiles &wt16, const WeightWin &ww, const void *z,
+                    const void *xcl, const void *offset, const void *mask, void *part, const int *flag, const void *zw,
+                    hipStream_t s) {
     const bool small = small_shape(g, wt.tpp);
     const int tm = small ? SMALL_TM : WIN_TMAX;
     const bool full = wt.tpp == tm && g.Kn % tm == 0;
     auto pick = [&](auto dim_tag) -> hipError_t {
         constexpr int D = decltype(dim_tag)::value;
-        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s)
-                                    : launch_k<D, T, false, 1, 2, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s);
+        if (ww.tg == 2) return full ? launch_k<D, T, true, 1, 2, WIN_TMAX, 32>(g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s)
+                                    : launch_k<D, T, false, 1, 2, WIN_TMAX, 32>(g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s);
         if (small)
-            return full ? launch_k<D, T, true, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s)
-                        : launch_k<D, T, false, 2, 1, SMALL_TM, 64>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s);
-        return full ? launch_k<D, T, true, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s)
-                    : launch_k<D, T, false, 2, 1, WIN_TMAX, 32>(g, wt, ww, z, xcl, offset, mask, part, flag, zw, s);
+            return full ? launch_k<D, T, true, 2, 1, SMALL_TM, 64>(g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s)
+                        : launch_k<D, T, false, 2, 1, SMALL_TM, 64>(g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s);
+        return full ? launch_k<D, T, true, 2, 1, WIN_TMAX, 32>(g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s)
+                    : launch_k<D, T, false, 2, 1, WIN_TMAX, 32>(g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s);
     };
     switch (dim) {
         case 1: return pick(std::integral_constant<int, 1>());
@@ -533,8 +541,8 @@ hipError_t launch_d(int dim, const Geo &g, const WinTiles &wt, const WeightWin &
 
 }  // namespace
 
-size_t weight_win_fixed_bytes(const Geo &g, int dim, int tpp) {
-    return (fixed_words(g, tpp) + (dim == 3 ? XS : 0)) * sizeof(float);
+size_t weight_win_fixed_bytes(const Geo &g, int dim, int tpp, int npiece) {
+    return (fixed_words(g, tpp, npiece > 0, npiece) + (dim == 3 ? XS : 0)) * sizeof(float);
 }
 
 WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
@@ -542,7 +550,7 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     w.ok = false;
     // needs the windowed tiling; GEMM sides up to 128 rows take 64-row tiles with the taps
     // split between two wave groups, larger ones 256-row tiles
-    if (!wt.ok || wt.cells == 0 || g.Mg < 16 || weight_win_fixed_bytes(g, dim, wt.tpp) + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
+    if (!wt.ok || wt.cells == 0 || g.Mg < 16 || weight_win_fixed_bytes(g, dim, wt.tpp, 0) + (size_t)wt.cells * XS * 4 > WIN_LDS_TARGET)
         return w;
     w.tg = g.Mg <= 128 ? 2 : 1;
     const int rows = w.tg == 2 ? rows_of<1, 2>() : rows_of<2, 1>();
@@ -565,16 +573,19 @@ WeightWin plan_weight_win(const Geo &g, const WinTiles &wt, int dim) {
     return w;
 }
 
-hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
-                                 const void *z, const void *xcl, const void *offset, const void *mask, void *part,
-                                 void *gw, bool accumulate, const int *flag, hipStream_t s, const void *zw) {
+hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WinTiles &wt16,
+                                 const WeightWin &ww, const void *z, const void *xcl, const void *offset,
+                                 const void *mask, void *part, void *gw, bool accumulate, const int *flag,
+                                 hipStream_t s, const void *zw) {
     // the 16-bit loop's A fragments straight from Z's 16-bit values in column blocks (zw)
     if (!ww.z8) zw = nullptr;
     hipError_t e = hipErrorInvalidValue;
     switch (dtype) {
-        case kF32: e = launch_d<float>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, zw, s); break;
-        case kF16: e = launch_d<__half>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, zw, s); break;
-        case kBF16: e = launch_d<__hip_bfloat16>(dim, g, wt, ww, z, xcl, offset, mask, part, flag, zw, s); break;
+        case kF32: e = launch_d<float>(dim, g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s); break;
+        case kF16: e = launch_d<__half>(dim, g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s); break;
+        case kBF16:
+            e = launch_d<__hip_bfloat16>(dim, g, wt, wt16, ww, z, xcl, offset, mask, part, flag, zw, s);
+            break;
     }
     if (e != hipSuccess) return e;
     return launch_weight_reduce(dtype, g, ww.n_split, part, gw, accumulate, s, ww.units_per_split, ww.n_spatial,

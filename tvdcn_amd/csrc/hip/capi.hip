@@ -75,10 +75,16 @@ struct Plan {
     bool data_split; // conv backward: scatter (wn_x) and offset/mask gradients (wn_c) as two
                      // launches, when the shared window of wn_s would be too small
     WeightTiles wt;
-    WinTiles wn_w;   // the wn_s tiling with the weight-gradient kernel's window margin
+    WinTiles wn_w;   // the wn_s tiling with the weight-gradient kernel's window margin (fp32 loop)
+    WinTiles wn_w16; // ... and with its 16-bit loop's (a smaller S tile leaves a larger window)
     WinTiles wn_f;   // the wn_s tiling with the forward kernel's window margin
     WeightWin ww;    // windowed weight-gradient plan (over wn_w)
     FwdWin fw;       // windowed forward plan (over wn_f)
+    // conv backward: grad_input accumulated in the caller's tensor, no channels-last accumulator
+    // (a channels-last input of the accumulation type, or float32 on the windowed data gradient,
+    // whose window flush and atomics address the (B, C, *S) tensor directly)
+    bool gx_in_place;
+    bool gx_nchw;    // ... and that tensor is (B, C, *S)
 };
 
 bool fits_int(int64_t v) { return v >= 0 && v <= (int64_t)INT_MAX; }
@@ -187,9 +193,26 @@ tvdcn_status make_plan(const tvdcn_conv_desc *d, Plan &pl, int64_t batch) {
     pl.wn_xg = pl.wn_x;
     pl.wn_xg.xglobal = 1;
     pl.wt = plan_weight(g, pl.dtype);
-    pl.wn_w = win_resize(pl.wn_s, g, pl.dim, weight_win_fixed_bytes(g, pl.dim, pl.wn_s.tpp), x_window_cell_bytes());
+    pl.wn_w = win_resize(pl.wn_s, g, pl.dim, weight_win_fixed_bytes(g, pl.dim, pl.wn_s.tpp, 0), x_window_cell_bytes());
+    // (only where the fp32 loop's window keeps a margin under 4 cells on some axis: a margin of 4
+    // already holds nearly every corner, and a larger window costs its fill -- cfg2 weight gradient
+    // +5% at margin 8 against 6, cfg5 fp16 -25% at margin 1 against -2)
+    pl.wn_w16 = pl.wn_w;
+    bool small_margin = false;
+    for (int e = 3 - pl.dim; e < 3; ++e) small_margin = small_margin || pl.wn_w.R[e] < 4;
+    if (small_margin)
+        pl.wn_w16 = win_resize(pl.wn_s, g, pl.dim,
+                               weight_win_fixed_bytes(g, pl.dim, pl.wn_s.tpp, pl.dtype == kF32 ? 2 : 1),
+                               x_window_cell_bytes());
     pl.ww = plan_weight_win(g, pl.wn_w, pl.dim);
     pl.fw = plan_fwd_win(g, pl.wn_s, pl.dim, pl.wn_f);
+    const bool cl_in = (d->flags & TVDCN_FLAG_CHANNELS_LAST) != 0;
+    // (1D only: there a window row is the tile's 256 pixels + margins, whole lines of each channel;
+    // 2D / 3D window rows are 10-26 cells, and the flush and out-of-window corners then reach
+    // 2-4x the memory transactions per wave instruction of the 16-channel cells of the
+    // channels-last order -- cfg2 data gradient +8%, cfg4 +86%)
+    pl.gx_nchw = !pl.transposed && !cl_in && pl.dtype == kF32 && pl.wn_s.ok && pl.dim == 1;
+    pl.gx_in_place = !pl.transposed && ((cl_in && acc_is_storage(pl.dtype)) || pl.gx_nchw);
     return TVDCN_STATUS_SUCCESS;
 }
 
@@ -326,7 +349,7 @@ Layout layout(const Plan &pl, bool backward) {
             L.wf = take(wf_bytes);
             take_w16();
             if (split_acc) L.yacc = take(yacc_bytes);
-        } else
+        } else if (!pl.gx_in_place)
             L.cl_acc = take(cl_bytes);
         L.wpart = take(align_up(pl.ww.ok ? pl.ww.part_elems * sizeof(float) : pl.wt.part_elems * a));
         if (!acc_is_storage(pl.dtype)) {
@@ -613,8 +636,9 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
         void *xcl = at(workspace, L.xcl), *wd = at(workspace, L.wd);
         int *flag = static_cast<int *>(at(workspace, L.flag));
         const bool cl_in = (desc->flags & TVDCN_FLAG_CHANNELS_LAST) != 0;   // conv only
-        // conv: the channels-last grad_input of the accumulation type, accumulated in place
-        void *gx_cl = pl.transposed ? nullptr : cl_in && direct ? grad_input : at(workspace, L.cl_acc);
+        // conv: grad_input accumulated in place (channels-last of the accumulation type, or the
+        // float32 (B, C, *S) tensor on the windowed data gradient), else a channels-last accumulator
+        void *gx_cl = pl.transposed ? nullptr : pl.gx_in_place ? grad_input : at(workspace, L.cl_acc);
         // transposed, input gradient on the split forward plan: its fp32 accumulator
         void *y32 = pl.transposed && pl.fw.ok && pl.fw.ksplit > 1 ? (dt == kF32 ? grad_input : at(workspace, L.yacc))
                                                                    : nullptr;
@@ -670,25 +694,26 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
                 // 3D: one launch on the scatter window, the offset / mask gradients reading X
                 // from global memory (cached), instead of two that each recompute the contraction
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_xg, true, true, Z, wd, zs, wsp,
-                                                                            flag, xcl, offset, mask, gx_cl, goff, gmask, s));
+                                                                            flag, xcl, offset, mask, gx_cl, goff, gmask, s,
+                                                                            pl.gx_nchw));
             } else if (pl.wn_s.ok && coord && pl.data_split) {
                 // two launches, each with the larger window its LDS share allows
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_x, true, false, Z, wd, zs, wsp,
                                                                             flag, xcl, offset, mask, gx_cl, nullptr, nullptr,
-                                                                            s));
+                                                                            s, pl.gx_nchw));
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, pl.wn_c, false, true, Z, wd, zs, wsp,
                                                                             flag, xcl, offset, mask, nullptr, goff, gmask, s));
             } else if (pl.wn_s.ok)
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data_win(dt, pl.dim, g, coord ? pl.wn_s : pl.wn_x, true, coord,
                                                                             Z, wd, zs, wsp, flag, xcl, offset, mask, gx_cl,
-                                                                            goff, gmask, s));
+                                                                            goff, gmask, s, pl.gx_nchw));
             else
                 TVDCN_LAUNCH(TVDCN_KERNEL_DATA_GRAD, s, launch_bwd_data(dt, pl.dim, g, pl.dt, true, coord, Z, wd, xcl, offset, mask,
                                                                         gx_cl, goff, gmask, s));
-            if (!cl_in)
+            if (!pl.gx_in_place && !cl_in)
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
                              launch_from_channels_last(dt, gx_cl, grad_input, nullptr, g.B, g.C, g.Sn, s));
-            else if (!direct)
+            else if (!pl.gx_in_place)
                 TVDCN_LAUNCH(TVDCN_KERNEL_LAYOUT, s,
                              launch_acc_to_storage(dt, gx_cl, grad_input, (size_t)g.B * g.Sn * g.C, s));
         } else {
@@ -718,7 +743,7 @@ tvdcn_status backward_planned(const Plan &pl, const tvdcn_conv_desc *desc, const
                                                                         nullptr, goff, gmask, s));
         }
         if (pl.ww.ok)
-            TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight_win(dt, pl.dim, g, pl.wn_w, pl.ww, Z, xcl, offset,
+            TVDCN_LAUNCH(TVDCN_KERNEL_WEIGHT_GRAD, s, launch_bwd_weight_win(dt, pl.dim, g, pl.wn_w, pl.wn_w16, pl.ww, Z, xcl, offset,
                                                                             mask, at(workspace, L.wpart), grad_weight,
                                                                             accumulate_weight, sampled16 ? flag : nullptr, s,
                                                                             zw));

@@ -117,8 +117,10 @@ WinTiles plan_data_win(const Geo &g, int dtype, int dim, bool scatter, bool coor
 // (cell_cap > 0: at most that many window cells)
 WinTiles win_resize(const WinTiles &base, const Geo &g, int dim, size_t fixed_bytes, size_t cell_bytes,
                     long long cell_cap = 0);
-// LDS of the windowed weight gradient besides its X window (its shape follows the pass length)
-size_t weight_win_fixed_bytes(const Geo &g, int dim, int tpp);
+// LDS of the windowed weight gradient besides its X window (its shape follows the pass length):
+// npiece 0 for its fp32 loop, else the 16-bit pieces per value of its 16-bit loop (whose S tile
+// is smaller, so that its X window can be larger)
+size_t weight_win_fixed_bytes(const Geo &g, int dim, int tpp, int npiece);
 size_t x_window_cell_bytes();
 DataTiles plan_data(const Geo &g, int dtype);
 WeightTiles plan_weight(const Geo &g, int dtype);
@@ -217,15 +219,19 @@ hipError_t launch_bwd_data(int dtype, int dim, const Geo &g, const DataTiles &t,
 // 16-bit loop (needs WeightWin::z8)
 hipError_t launch_data_win_prep(int dtype, const Geo &g, const WinTiles &t, const void *z, const void *w, void *zs,
                                 void *wsplit, void *wd, int *flag, hipStream_t s, void *zw = nullptr);
+// gx_nchw: gx_cl is grad_input as the caller's float32 (B, C, *S) tensor (zeroed), not the
+// channels-last accumulator
 hipError_t launch_bwd_data_win(int dtype, int dim, const Geo &g, const WinTiles &t, bool scatter, bool coord,
                                const void *z, const void *wchunks, const void *zs, const void *wsplit,
                                const int *flag, const void *xcl, const void *offset, const void *mask, void *gx_cl,
-                               void *goff, void *gmask, hipStream_t s);
+                               void *goff, void *gmask, hipStream_t s, bool gx_nchw = false);
 // flag: the operand flag (null: the fp32 MFMA loop; set: the same). zw: Z's 16-bit values
 // written by launch_data_win_prep (null: the kernel forms them in registers)
-hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WeightWin &ww,
-                                 const void *z, const void *xcl, const void *offset, const void *mask, void *part,
-                                 void *gw, bool accumulate, const int *flag, hipStream_t s, const void *zw = nullptr);
+// wt / wt16: the tiling with the fp32 loop's / the 16-bit loop's window (same tiles and passes)
+hipError_t launch_bwd_weight_win(int dtype, int dim, const Geo &g, const WinTiles &wt, const WinTiles &wt16,
+                                 const WeightWin &ww, const void *z, const void *xcl, const void *offset,
+                                 const void *mask, void *part, void *gw, bool accumulate, const int *flag,
+                                 hipStream_t s, const void *zw = nullptr);
 // gw (storage type, layout (M, Cg, Kn)) = sum over k_splits of part[ks][G][Kn][Mg][Cg]
 // dW = sum over splits of the partials; with units_per_split > 0 (windowed kernel) tap t sums only
 // the splits whose unit range meets its pass (t / tpp) over n_spatial tiles
