@@ -144,7 +144,7 @@ bwd_weight_win_kernel(const Geo g, const WinTiles wt, const WeightWin ww, const 
             tile.init(g, wt, s, ct, grp);
             const float *xb = xcl + (size_t)tile.b * g.Sn * g.C + tile.cg0;
             __syncthreads();   // previous tile done with the tables
-            fill_geo<DIM, T>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
+            fill_geo<DIM, T, 5, true>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT);
             fill_xwin(g, wt, tile, xb, xwin, tid, NT);
             __syncthreads();
 

@@ -211,7 +211,7 @@ fwd_win_kernel(const Geo g, const WinTiles wt, const FwdWin fw, const float *__r
             tile.ogu = og_s;
             tile.mgu = mg_s;
             // (the sampled values' piece scale folded into the records' masks)
-            fill_geo<DIM, T, 3>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT, mscale_b);
+            fill_geo<DIM, T, 3, true>(g, wt, tile, offset, mask, t0, ntaps, geo, tid, NT, mscale_b);
             geo_og = og_s;
             geo_mg = mg_s;
         }
